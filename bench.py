@@ -1,0 +1,174 @@
+"""Benchmark: Cut Cross-Entropy fwd+bwd on one MI355X.
+
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c3] [--filter on|off]
+
+A step is one forward + backward (dE and dC, dBias when the workload has a bias)
+of linear_cross_entropy over one batch of synthetic input already resident in
+HBM.  Default workload: c3, the Llama-3.1-8B head (N=8192 tokens, D=4096,
+V=128256, bf16), the configuration the headline metric is quoted on.
+
+Prints one JSON line.  `value` is tokens/s of the whole job; `roofline` is the
+forward kernel pair (tile kernel + lse combine, timed with HIP events on the
+stream they run on) against the bf16 MFMA peak; `cpu_baseline` is the float32
+torch-CPU restatement of the reference's materialised-logits path timed on a
+bounded slice of the same workload on this host.
+"""
+
+import argparse
+import json
+import math
+import os
+import re
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "mlx-cross-entropy_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "fwd+bwd tokens/sec and % bf16 MFMA roofline, Llama-3-8B head, 1 MI355X"
+PEAK_TFLOPS = {"bf16": 2500.0, "f16": 2500.0, "f32": 157.3}
+HBM_PEAK_GBS = 8000.0
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def traffic_from_profiles(workload, filter_mode):
+    """HBM bytes per forward launch from the committed rocprofv3 --pmc summary, if present."""
+    path = os.path.join(ROOT, "profiles", f"fwd_tile_{workload}_traffic.txt")
+    if not os.path.exists(path):
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", open(path).read())
+    return float(m.group(1)) if m else None
+
+
+def cpu_baseline(w, rows, budget_s):
+    from oracle import cpu_baseline as CB
+
+    N = w["N"]
+    rows = min(rows, N)
+    r = CB.time_tokens_per_s(w["e"].detach(), w["c"].detach(), w["targets"].detach(), w["bias"], w["reduction"],
+                             w["ignore_index"], rows=rows, budget_s=budget_s)
+    return {"value": r["value"], "unit": "tokens/s", "cores": r["cores"], "kind": "port",
+            "sample": (f"first {r['rows']} of {N} tokens of {w['name']} (full D={w['D']}, V={w['V']}), "
+                       f"float32 torch CPU, materialised logits + autograd (reference/_reference.py), "
+                       f"{r['reps']} reps in {r['seconds']:.1f} s")}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="c3", choices=["c1", "c2", "c3", "c4", "c5"])
+    ap.add_argument("--filter", default="on", choices=["on", "off"])
+    ap.add_argument("--cpu-baseline", default="on", choices=["on", "off"])
+    ap.add_argument("--cpu-rows", type=int, default=256)
+    ap.add_argument("--cpu-budget", type=float, default=20.0)
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({"error": f"this build measures one GPU only (asked for --gpus {args.gpus}, "
+                                   f"WORLD_SIZE={world}); run with --gpus 1"}))
+        log("bench.py: multi-GPU runs are not part of this build; use --gpus 1")
+        sys.exit(1)
+
+    import torch
+
+    import mlx_cce_amd as cce
+    import workloads
+    from mlx_cce_amd import _ext
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    log(f"bench: {_ext.version()} on {torch.cuda.get_device_name(dev)}; building {args.workload}")
+    w = workloads.make(args.workload, device=dev)
+    N, D, V = w["N"], w["D"], w["V"]
+    dt = {torch.bfloat16: "bf16", torch.float16: "f16", torch.float32: "f32"}[w["dtype"]]
+    e = w["e"].reshape(N, D).detach().requires_grad_(True)
+    c = w["c"].detach().requires_grad_(True)
+    b = w["bias"].detach().requires_grad_(True) if w["bias"] is not None else None
+    t = w["targets"].reshape(N)
+    red = w["reduction"]
+    feps = cce.FILTER_LOG_EPS if args.filter == "on" else None
+    up = torch.ones(N, device=dev) if red == "none" else None
+
+    def step():
+        e.grad = None
+        c.grad = None
+        if b is not None:
+            b.grad = None
+        loss = cce.linear_cross_entropy(e, c, t, b, reduction=red, ignore_index=w["ignore_index"], filter_eps=feps)
+        loss.backward(up)
+        return loss
+
+    torch.cuda.synchronize()
+    for i in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    log(f"bench: warmup {args.warmup} done")
+    kept, total = cce.last_tile_stats(dev)
+    skip = 1.0 - kept / total
+
+    torch.cuda.reset_peak_memory_stats(dev)
+    _ext.set_timing(True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    tm = _ext.timings_ms()
+    _ext.set_timing(False)
+    peak_mem = torch.cuda.max_memory_allocated(dev)
+    log(f"bench: {args.steps} steps in {elapsed:.3f} s")
+
+    ms = elapsed * 1e3 / args.steps
+    fwd_ms = statistics.mean(tm["forward"])
+    bwd_ms = statistics.mean(tm["backward"])
+    peak = PEAK_TFLOPS[dt]
+    fwd_flops = 2.0 * N * D * V
+    achieved = fwd_flops / (fwd_ms * 1e-3) / 1e12
+    step_flops = workloads.flops(N, D, V, skip)
+    dense_flops = workloads.flops(N, D, V, 0.0)
+
+    out = {
+        "metric": METRIC,
+        "value": N / (ms * 1e-3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": dt,
+        "data": "synthetic (seeded torch.Generator on device; random-init classifier rows)",
+        "config": {"workload": f"{w['name']}: {w['description']}", "N": N, "D": D, "V": V, "reduction": red,
+                   "bias": b is not None, "grads": "dE,dC" + (",dBias" if b is not None else ""),
+                   "filter": "2^-12 (128x128 tiles)" if feps is not None else "off"},
+        "roofline": {"bound": "mfma", "kernel": "cce forward (fwd_tile_kernel + lse_kernel)",
+                     "achieved": achieved, "peak": peak, "unit": "TFLOP/s", "frac": achieved / peak,
+                     "traffic": traffic_from_profiles(args.workload, args.filter),
+                     "flops_per_launch": fwd_flops, "avg_launch_ms": fwd_ms},
+        "step": {"fwd_ms": fwd_ms, "bwd_ms": bwd_ms, "tile_skip": skip, "kept_tiles": kept, "total_tiles": total,
+                 "algorithmic_flops": step_flops, "tflops": step_flops / (ms * 1e-3) / 1e12,
+                 "mfma_frac": step_flops / (ms * 1e-3) / 1e12 / peak,
+                 "dense_equiv_mfma_frac": dense_flops / (ms * 1e-3) / 1e12 / peak,
+                 "peak_mem_gb": peak_mem / 2 ** 30, "logits_bytes_if_materialised": 4.0 * N * V},
+        "cpu_baseline": None,
+    }
+    if args.cpu_baseline == "on":
+        log("bench: timing CPU baseline")
+        out["cpu_baseline"] = cpu_baseline(w, args.cpu_rows, args.cpu_budget)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

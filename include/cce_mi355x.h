@@ -1,0 +1,116 @@
+/*
+ * cce_mi355x.h — C ABI of the MI355X (gfx950) Cut Cross-Entropy library.
+ *
+ * loss_r = lse(E_r . C^T + b) - (E_r . C_{t_r} + b_{t_r}), computed without ever
+ * materialising the [N, V] logits.  Every entry point is asynchronous on the
+ * caller's HIP stream, never allocates, never synchronises, and returns 0 on
+ * success or a negative CCE_ERR_* code (message via cce_last_error()).
+ * No exception crosses this boundary.
+ *
+ * Layouts (all row-major, contiguous, 16-byte aligned base pointers):
+ *   e        [N, D]   dtype                 hidden states (the reference's "e")
+ *   c        [V, D]   dtype                 classifier rows (the reference's "c")
+ *   bias     [V]      dtype, nullable
+ *   targets  [N]      int64; rows equal to ignore_index (when has_ignore != 0) are masked
+ *   tile_max, tile_sum_exp  [num_vocab_tiles, N] fp32, vocab-tile major, tile width
+ *                      CCE_STAT_TILE (128) columns; num_vocab_tiles = ceil(V / 128)
+ *   neg_target_logit, lse, nll   [N] fp32
+ *
+ * Reference boundary replaced (sb1992/mlx-cross-entropy):
+ *   csrc/bindings.cpp:12-87 (nanobind module mlx_cce._ext) and the MLX primitives
+ *   CutCrossEntropy / CutCrossEntropyBwd in csrc/cce/cce.h:37-101, cce.cpp:31-454.
+ */
+#ifndef CCE_MI355X_H
+#define CCE_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* dtype codes (reference accepts float32 / float16 / bfloat16: csrc/cce/cce.cpp:222-227) */
+#define CCE_DTYPE_F32 0
+#define CCE_DTYPE_F16 1
+#define CCE_DTYPE_BF16 2
+
+/* error codes */
+#define CCE_OK 0
+#define CCE_ERR_INVALID_ARGUMENT (-1) /* reference: std::invalid_argument, cce.cpp:41-73 */
+#define CCE_ERR_UNSUPPORTED_DTYPE (-2) /* reference: runtime_error "unsupported dtype", cce.cpp:226 */
+#define CCE_ERR_WORKSPACE (-3)        /* workspace missing or smaller than cce_backward_workspace_size() */
+#define CCE_ERR_LAUNCH (-4)           /* a HIP launch failed */
+#define CCE_ERR_NO_DEVICE (-5)        /* no HIP device (reference: eval_cpu throws, cce.cpp:185-199) */
+
+/* Width (vocabulary columns) of one tile_max / tile_sum_exp statistic and of
+ * the backward filter tile.  Reference uses 32 (cce.metal:34, cce.cpp:76). */
+#define CCE_STAT_TILE 128
+/* Token rows per backward tile (reference: 32, cce.metal:168). */
+#define CCE_BWD_ROWS 128
+
+/* ln(2^-12): the reference's gradient-filter threshold FILTER_LOG_EPS
+ * (csrc/cce/cce.metal:143, reference/_fused_backward.py:17). */
+#define CCE_FILTER_LOG_EPS (-8.3177661667f)
+
+/* Message describing the last error returned on this thread ("" if none). */
+const char* cce_last_error(void);
+
+/* Library version string. */
+const char* cce_version(void);
+
+/* Tile geometry compiled into the library: forward workgroup tile (tokens x vocab),
+ * statistic tile width, backward tile (tokens x vocab). Any pointer may be NULL. */
+void cce_tile_config(int* fwd_tokens, int* fwd_vocab, int* stat_tile, int* bwd_tokens, int* bwd_vocab);
+
+/* Number of vocabulary statistic tiles: ceil(V / CCE_STAT_TILE). */
+int64_t cce_num_vocab_tiles(int64_t V);
+
+/*
+ * Forward pass.  Replaces cce_forward_raw (csrc/bindings.cpp:58-69, cce.cpp:123-145)
+ * and CutCrossEntropy::eval_gpu (cce.cpp:207-277): one fused tiled-MFMA kernel that
+ * writes per-(vocab tile, row) max and sum-exp plus the target logit, then one
+ * combine kernel (reference reduce_tile_to_lse, cce.metal:332-355) that writes
+ *   lse[r] = logsumexp_v(E_r . C_v + b_v)
+ *   nll[r] = lse[r] + neg_target_logit[r]     for rows kept by the ignore mask,
+ *            0                                for masked rows (mlx_cce/__init__.py:59-70),
+ *            NaN                              for kept rows whose target is outside [0, V).
+ * tile_sum_exp is required (it is the combine kernel's input).
+ */
+int cce_forward(int dtype, const void* e, const void* c, const void* bias,
+                const int64_t* targets, int64_t ignore_index, int has_ignore,
+                int64_t N, int64_t D, int64_t V,
+                float* tile_max, float* tile_sum_exp, float* neg_target_logit,
+                float* lse, float* nll, void* hip_stream);
+
+/* Bytes of device workspace cce_backward needs for these sizes and outputs. */
+size_t cce_backward_workspace_size(int dtype, int64_t N, int64_t D, int64_t V,
+                                   int want_dE, int want_dC, int want_dBias);
+
+/*
+ * Backward pass.  Replaces cce_backward_raw (csrc/bindings.cpp:71-86, cce.cpp:152-179),
+ * CutCrossEntropyBwd::eval_gpu (cce.cpp:283-375) and the full-gradient research
+ * kernel (reference/_fused_backward.py:1406-1655), whose dC/dBias semantics it follows.
+ *   G[r,v] = d_nll[r] * (softmax(E_r . C^T + b)[v] - [v == t_r])
+ *   dE = G . C,  dC = G^T . E,  dBias = sum_r G[r, :]
+ * A (128-row, 128-column) tile is skipped when no row in it with d_nll != 0 has its
+ * target inside the tile and every row's tile_max - lse < filter_log_eps
+ * (reference predicate: cce.metal:191-204).  filter_log_eps = -INFINITY keeps all tiles.
+ * dE/dC/dBias are written in `dtype`; pass NULL for any gradient not wanted.
+ * Accumulation is fp32 atomics into the workspace, then one cast pass.
+ * tile_stats (nullable, device int64[2]) receives {kept tiles, total tiles}.
+ */
+int cce_backward(int dtype, const void* e, const void* c, const void* bias,
+                 const int64_t* targets, int64_t ignore_index, int has_ignore,
+                 int64_t N, int64_t D, int64_t V,
+                 const float* lse, const float* tile_max, const float* d_nll,
+                 float filter_log_eps,
+                 void* dE, void* dC, void* dBias,
+                 void* workspace, size_t workspace_bytes,
+                 int64_t* tile_stats, void* hip_stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CCE_MI355X_H */

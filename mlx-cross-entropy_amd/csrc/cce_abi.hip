@@ -1,0 +1,232 @@
+// cce_abi.hip — the extern "C" boundary declared in include/cce_mi355x.h.
+//
+// Host-side validation mirrors the reference's checks (csrc/cce/cce.cpp:41-73:
+// ranks, D agreement, bias shape; :222-227 dtype) but reports them as negative
+// return codes plus a thread-local message instead of C++ exceptions.  The
+// reference's alignment precondition N%32 == 0, V%32 == 0 (cce.cpp:64-68) is
+// lifted: ragged N and V are masked inside the kernels.  Rows must be 16-byte
+// multiples (D % 8 == 0 for 16-bit dtypes, D % 4 == 0 for fp32); the reference
+// requires D % 8 == 0 for every dtype.
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "cce_launch.h"
+#include "cce_mi355x.h"
+
+namespace {
+
+thread_local char g_err[512] = {0};
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof g_err, fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+size_t elem_size(int dtype) { return dtype == CCE_DTYPE_F32 ? 4 : 2; }
+size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+const char* dtype_name(int dtype) {
+  switch (dtype) {
+    case CCE_DTYPE_F32:
+      return "float32";
+    case CCE_DTYPE_F16:
+      return "float16";
+    case CCE_DTYPE_BF16:
+      return "bfloat16";
+    default:
+      return "?";
+  }
+}
+
+int num_cus_current() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return -1;
+  static int cache[64] = {0};
+  if (dev >= 0 && dev < 64 && cache[dev] > 0) return cache[dev];
+  int cu = 0;
+  if (hipDeviceGetAttribute(&cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return -1;
+  if (dev >= 0 && dev < 64) cache[dev] = cu;
+  return cu;
+}
+
+// Shape / pointer checks common to both passes.
+int check_common(const char* fn, int dtype, const void* e, const void* c, const int64_t* targets, int64_t N,
+                 int64_t D, int64_t V) {
+  if (dtype != CCE_DTYPE_F32 && dtype != CCE_DTYPE_F16 && dtype != CCE_DTYPE_BF16)
+    return fail(CCE_ERR_UNSUPPORTED_DTYPE, "[%s] unsupported dtype code %d (expected float32, float16 or bfloat16)",
+                fn, dtype);
+  if (N <= 0 || D <= 0 || V <= 0)
+    return fail(CCE_ERR_INVALID_ARGUMENT, "[%s] N, D, V must be positive, got N=%lld D=%lld V=%lld", fn,
+                (long long)N, (long long)D, (long long)V);
+  const int64_t epc = 16 / (int64_t)elem_size(dtype);
+  if (D % epc != 0)
+    return fail(CCE_ERR_INVALID_ARGUMENT, "[%s] D must be a multiple of %lld for %s (16-byte rows), got D=%lld", fn,
+                (long long)epc, dtype_name(dtype), (long long)D);
+  if ((int64_t)elem_size(dtype) * D >= (int64_t)1 << 23)
+    return fail(CCE_ERR_INVALID_ARGUMENT, "[%s] row of %lld bytes exceeds the 8 MiB limit", fn,
+                (long long)(elem_size(dtype) * D));
+  if (N >= ((int64_t)1 << 31) - 256 || V >= ((int64_t)1 << 31) - 256)
+    return fail(CCE_ERR_INVALID_ARGUMENT, "[%s] N and V must be below 2^31", fn);
+  const int64_t tiles = ((N + cce::kBwdTokens - 1) / cce::kBwdTokens) * ((V + cce::kBwdVocab - 1) / cce::kBwdVocab);
+  if (tiles >= ((int64_t)1 << 31))
+    return fail(CCE_ERR_INVALID_ARGUMENT, "[%s] N*V/16384 must be below 2^31", fn);
+  if (!e || !c || !targets) return fail(CCE_ERR_INVALID_ARGUMENT, "[%s] e, c and targets must be non-null", fn);
+  if (!aligned(e, 16) || !aligned(c, 16))
+    return fail(CCE_ERR_INVALID_ARGUMENT, "[%s] e and c must be 16-byte aligned", fn);
+  if (!aligned(targets, 8)) return fail(CCE_ERR_INVALID_ARGUMENT, "[%s] targets must be 8-byte aligned", fn);
+  return CCE_OK;
+}
+
+struct WsLayout {
+  size_t de, dc, db, acc_end, flags, list, count, total;
+};
+
+WsLayout ws_layout(int64_t N, int64_t D, int64_t V, bool want_de, bool want_dc, bool want_db) {
+  WsLayout L{};
+  const size_t nvt = (size_t)((V + cce::kBwdVocab - 1) / cce::kBwdVocab);
+  const size_t nrb = (size_t)((N + cce::kBwdTokens - 1) / cce::kBwdTokens);
+  size_t off = 0;
+  L.de = off;
+  if (want_de) off += align256((size_t)N * (size_t)D * 4);
+  L.dc = off;
+  if (want_dc) off += align256((size_t)V * (size_t)D * 4);
+  L.db = off;
+  if (want_db) off += align256((size_t)V * 4);
+  L.acc_end = off;
+  L.flags = off;
+  off += align256(nvt * nrb);
+  L.list = off;
+  off += align256(nvt * nrb * 4);
+  L.count = off;
+  off += 256;
+  L.total = off;
+  return L;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* cce_last_error(void) { return g_err; }
+
+const char* cce_version(void) { return "cce-mi355x 0.1.0 (gfx950)"; }
+
+void cce_tile_config(int* fwd_tokens, int* fwd_vocab, int* stat_tile, int* bwd_tokens, int* bwd_vocab) {
+  if (fwd_tokens) *fwd_tokens = cce::kFwdTokens;
+  if (fwd_vocab) *fwd_vocab = cce::kFwdVocab;
+  if (stat_tile) *stat_tile = cce::kStatTile;
+  if (bwd_tokens) *bwd_tokens = cce::kBwdTokens;
+  if (bwd_vocab) *bwd_vocab = cce::kBwdVocab;
+}
+
+int64_t cce_num_vocab_tiles(int64_t V) { return V <= 0 ? 0 : (V + cce::kStatTile - 1) / cce::kStatTile; }
+
+int cce_forward(int dtype, const void* e, const void* c, const void* bias, const int64_t* targets,
+                int64_t ignore_index, int has_ignore, int64_t N, int64_t D, int64_t V, float* tile_max,
+                float* tile_sum_exp, float* neg_target_logit, float* lse, float* nll, void* hip_stream) {
+  g_err[0] = 0;
+  int rc = check_common("cce_forward", dtype, e, c, targets, N, D, V);
+  if (rc != CCE_OK) return rc;
+  if (!tile_max || !tile_sum_exp || !neg_target_logit || !lse || !nll)
+    return fail(CCE_ERR_INVALID_ARGUMENT,
+                "[cce_forward] tile_max, tile_sum_exp, neg_target_logit, lse and nll must be non-null");
+  if (bias && !aligned(bias, elem_size(dtype)))
+    return fail(CCE_ERR_INVALID_ARGUMENT, "[cce_forward] bias is not aligned to its element size");
+  if (num_cus_current() <= 0) return fail(CCE_ERR_NO_DEVICE, "[cce_forward] no HIP device is available");
+
+  cce::FwdArgs a{};
+  a.e = e;
+  a.c = c;
+  a.bias = bias;
+  a.targets = targets;
+  a.ignore_index = ignore_index;
+  a.has_ignore = has_ignore ? 1 : 0;
+  a.N = N;
+  a.D = D;
+  a.V = V;
+  a.tile_max = tile_max;
+  a.tile_sum_exp = tile_sum_exp;
+  a.neg_target_logit = neg_target_logit;
+  a.lse = lse;
+  a.nll = nll;
+  hipError_t err = cce::launch_forward(dtype, a, reinterpret_cast<hipStream_t>(hip_stream));
+  if (err != hipSuccess)
+    return fail(CCE_ERR_LAUNCH, "[cce_forward] kernel launch failed: %s", hipGetErrorString(err));
+  return CCE_OK;
+}
+
+size_t cce_backward_workspace_size(int dtype, int64_t N, int64_t D, int64_t V, int want_dE, int want_dC,
+                                   int want_dBias) {
+  (void)dtype;
+  if (N <= 0 || D <= 0 || V <= 0) return 0;
+  return ws_layout(N, D, V, want_dE != 0, want_dC != 0, want_dBias != 0).total;
+}
+
+int cce_backward(int dtype, const void* e, const void* c, const void* bias, const int64_t* targets,
+                 int64_t ignore_index, int has_ignore, int64_t N, int64_t D, int64_t V, const float* lse,
+                 const float* tile_max, const float* d_nll, float filter_log_eps, void* dE, void* dC, void* dBias,
+                 void* workspace, size_t workspace_bytes, int64_t* tile_stats, void* hip_stream) {
+  g_err[0] = 0;
+  int rc = check_common("cce_backward", dtype, e, c, targets, N, D, V);
+  if (rc != CCE_OK) return rc;
+  if (!lse || !tile_max || !d_nll)
+    return fail(CCE_ERR_INVALID_ARGUMENT, "[cce_backward] lse, tile_max and d_nll must be non-null");
+  if (dBias && !bias)
+    return fail(CCE_ERR_INVALID_ARGUMENT, "[cce_backward] dBias requested but bias is null");
+  if (bias && !aligned(bias, elem_size(dtype)))
+    return fail(CCE_ERR_INVALID_ARGUMENT, "[cce_backward] bias is not aligned to its element size");
+  if ((dE && !aligned(dE, 16)) || (dC && !aligned(dC, 16)) || (dBias && !aligned(dBias, 16)))
+    return fail(CCE_ERR_INVALID_ARGUMENT, "[cce_backward] gradient outputs must be 16-byte aligned");
+  if (std::isnan(filter_log_eps))
+    return fail(CCE_ERR_INVALID_ARGUMENT, "[cce_backward] filter_log_eps must not be NaN");
+  const WsLayout L = ws_layout(N, D, V, dE != nullptr, dC != nullptr, dBias != nullptr);
+  if (!workspace || workspace_bytes < L.total)
+    return fail(CCE_ERR_WORKSPACE, "[cce_backward] workspace of %zu bytes required, %zu given", L.total,
+                workspace ? workspace_bytes : (size_t)0);
+  if (!aligned(workspace, 256))
+    return fail(CCE_ERR_WORKSPACE, "[cce_backward] workspace must be 256-byte aligned");
+  const int cus = num_cus_current();
+  if (cus <= 0) return fail(CCE_ERR_NO_DEVICE, "[cce_backward] no HIP device is available");
+
+  hipStream_t s = reinterpret_cast<hipStream_t>(hip_stream);
+  char* ws = reinterpret_cast<char*>(workspace);
+  cce::BwdArgs a{};
+  a.e = e;
+  a.c = c;
+  a.bias = bias;
+  a.targets = targets;
+  a.ignore_index = ignore_index;
+  a.has_ignore = has_ignore ? 1 : 0;
+  a.N = N;
+  a.D = D;
+  a.V = V;
+  a.lse = lse;
+  a.tile_max = tile_max;
+  a.d_nll = d_nll;
+  a.filter_log_eps = filter_log_eps;
+  a.dE_acc = dE ? reinterpret_cast<float*>(ws + L.de) : nullptr;
+  a.dC_acc = dC ? reinterpret_cast<float*>(ws + L.dc) : nullptr;
+  a.dBias_acc = dBias ? reinterpret_cast<float*>(ws + L.db) : nullptr;
+  a.flags = reinterpret_cast<uint8_t*>(ws + L.flags);
+  a.list = reinterpret_cast<int*>(ws + L.list);
+  a.count = reinterpret_cast<int*>(ws + L.count);
+  a.tile_stats = tile_stats;
+  a.num_cus = cus;
+
+  hipError_t err = cce::launch_fill_zero(ws, L.acc_end, s);
+  if (err == hipSuccess) err = cce::launch_backward(dtype, a, s);
+  if (err == hipSuccess && dE) err = cce::launch_cast(dtype, a.dE_acc, dE, N * D, s);
+  if (err == hipSuccess && dC) err = cce::launch_cast(dtype, a.dC_acc, dC, V * D, s);
+  if (err == hipSuccess && dBias) err = cce::launch_cast(dtype, a.dBias_acc, dBias, V, s);
+  if (err != hipSuccess)
+    return fail(CCE_ERR_LAUNCH, "[cce_backward] kernel launch failed: %s", hipGetErrorString(err));
+  return CCE_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,197 @@
+"""mlx_cce_amd — Cut Cross-Entropy for AMD Instinct MI355X (gfx950), PyTorch-ROCm.
+
+Drop-in for the reference package ``mlx_cce`` (sb1992/mlx-cross-entropy):
+
+    from mlx_cce_amd import linear_cross_entropy
+    loss = linear_cross_entropy(hidden_states, classifier_weight, targets)
+
+loss = logsumexp(e @ c.T + bias) - (e @ c.T + bias)[target], computed by
+hand-written HIP kernels (``libcce_mi355x.so``) without materialising the
+[N, V] logits.  Gradients dE, dC and dBias are produced for every input that
+requires grad; vocabulary tiles whose softmax is below 2^-12 for every row of a
+128-row block are skipped in the backward (the reference's filter,
+csrc/cce/cce.metal:191-204).
+
+API mirrors (reference file:line):
+    linear_cross_entropy   mlx_cce/__init__.py:79-107 (+ shift/return_lse of reference/__init__.py:22-85)
+    cce_loss               mlx_cce/__init__.py:54-76
+    cut_cross_entropy      csrc/bindings.cpp:15-56
+    cce_forward_raw        csrc/bindings.cpp:58-69
+    cce_backward_raw       csrc/bindings.cpp:71-86
+    LinearCrossEntropy     reference/__init__.py:88-118
+"""
+
+__version__ = "0.1.0"
+
+import torch
+
+from . import _ext
+from ._ext import FILTER_LOG_EPS, cce_backward_raw, cce_forward_raw
+
+__all__ = [
+    "linear_cross_entropy",
+    "cce_loss",
+    "cut_cross_entropy",
+    "cce_forward_raw",
+    "cce_backward_raw",
+    "LinearCrossEntropy",
+    "FILTER_LOG_EPS",
+    "last_tile_stats",
+]
+
+_REDUCTIONS = ("none", "sum", "mean")
+_last_stats = {}
+
+
+def last_tile_stats(device=None):
+    """(kept, total) backward tiles of the most recent backward on `device` (synchronises)."""
+    dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+    t = _last_stats.get(dev)
+    if t is None:
+        return None
+    kept, total = t.tolist()
+    return int(kept), int(total)
+
+
+class _CCEFunction(torch.autograd.Function):
+    """Autograd glue: replaces the reference's mx.custom_function + vjp (mlx_cce/__init__.py:21-51)."""
+
+    @staticmethod
+    def forward(ctx, e, c, bias, targets, ignore_index, reduction, filter_eps, grad_c, grad_bias):
+        tile_max, _tse, _ntl, lse, nll = _ext.forward(e, c, targets, bias, ignore_index)
+        N = e.shape[0]
+        if reduction == "none":
+            loss = nll
+            scale = None
+        elif reduction == "sum":
+            loss = nll.sum()
+            scale = None
+        else:  # mean over valid rows, divided by max(count, 1) (mlx_cce/__init__.py:73-75)
+            if ignore_index is None:
+                count = torch.full((), float(N), dtype=torch.float32, device=e.device)
+            else:
+                count = (targets != ignore_index).sum().clamp_(min=1).to(torch.float32)
+            loss = nll.sum() / count
+            scale = count
+        ctx.save_for_backward(e, c, bias, targets, lse, tile_max, scale)
+        ctx.cce = (ignore_index, reduction, filter_eps, grad_c, grad_bias)
+        ctx.mark_non_differentiable(lse)
+        return loss, lse
+
+    @staticmethod
+    def backward(ctx, grad_loss, _grad_lse):
+        e, c, bias, targets, lse, tile_max, scale = ctx.saved_tensors
+        ignore_index, reduction, filter_eps, grad_c, grad_bias = ctx.cce
+        N = e.shape[0]
+        g = grad_loss.to(torch.float32)
+        if reduction == "none":
+            d_nll = g.reshape(N)
+        elif reduction == "sum":
+            d_nll = g.reshape(1).expand(N)
+        else:
+            d_nll = (g / scale).reshape(1).expand(N)
+        want_de = ctx.needs_input_grad[0]
+        want_dc = ctx.needs_input_grad[1] and grad_c
+        want_db = bias is not None and ctx.needs_input_grad[2] and grad_bias
+        if not (want_de or want_dc or want_db):
+            return None, None, None, None, None, None, None, None, None
+        stats = torch.empty((2,), dtype=torch.int64, device=e.device)
+        dE, dC, dB = _ext.backward(e, c, targets, lse, tile_max, d_nll, bias, ignore_index, filter_eps,
+                                   want_de, want_dc, want_db, tile_stats=stats)
+        _last_stats[e.device] = stats
+        return dE, dC, dB, None, None, None, None, None, None
+
+
+def _cce(e, c, targets, bias, reduction, ignore_index, filter_eps, grad_c=True, grad_bias=True):
+    if reduction not in _REDUCTIONS:
+        raise ValueError(f"Unknown reduction: {reduction!r}")
+    if bias is not None and bias.dtype != e.dtype:
+        bias = bias.to(e.dtype)
+    loss, lse = _CCEFunction.apply(e, c, bias, targets, ignore_index, reduction, filter_eps, grad_c, grad_bias)
+    return loss, lse
+
+
+def cce_loss(e, c, targets, bias=None, reduction="mean", ignore_index=-100, *, filter_eps=FILTER_LOG_EPS):
+    """Reference mlx_cce/__init__.py:54-76.  e [N, D], c [V, D], targets [N]; fp32 loss.
+
+    ignore_index=None treats every row as valid.  filter_eps (keyword-only, not in
+    the reference) sets the backward tile filter threshold; None disables it.
+    """
+    if e.dim() != 2:
+        raise ValueError(f"[cut_cross_entropy] e must be 2D [B, D], got {e.dim()}D")
+    loss, _ = _cce(e, c, targets, bias, reduction, ignore_index, filter_eps)
+    return loss
+
+
+def linear_cross_entropy(e, c, targets, bias=None, reduction="mean", ignore_index=-100, *, shift=0,
+                         return_lse=False, filter_eps=FILTER_LOG_EPS):
+    """Memory-efficient cross-entropy that never materializes [N, V] logits.
+
+    Reference mlx_cce/__init__.py:79-107; ``shift`` and ``return_lse`` follow the
+    research API reference/__init__.py:22-85 (reference/_ops.py:209-211,238-239).
+
+    Args:
+        e: hidden states [..., D] (flattened to [N, D])
+        c: classifier weights [V, D]
+        targets: target indices [...] (flattened to [N])
+        bias: optional classifier bias [V]
+        reduction: "mean", "sum" or "none"
+        ignore_index: target value to mask (-100 default); None disables masking
+        shift: drop the last `shift` positions of e and the first `shift` targets (causal LM)
+        return_lse: also return the per-token logsumexp [N] (fp32, no gradient)
+        filter_eps: backward tile-filter threshold (ln 2^-12); None disables filtering
+    Returns:
+        loss (fp32 scalar, or [...] for reduction="none"), optionally (loss, lse)
+    """
+    if shift:
+        e = e[..., :-shift, :]
+        targets = targets[..., shift:]
+    orig_shape = targets.shape
+    D = e.shape[-1]
+    e_flat = e.reshape(-1, D)
+    t_flat = targets.reshape(-1)
+    loss, lse = _cce(e_flat, c, t_flat, bias, reduction, ignore_index, filter_eps)
+    if reduction == "none":
+        loss = loss.reshape(orig_shape)
+    if return_lse:
+        return loss, lse
+    return loss
+
+
+def cut_cross_entropy(e, c, targets, bias=None, reduction="mean", ignore_index=-100, compute_all_grads=False,
+                      *, stream=None):
+    """Reference csrc/bindings.cpp:15-56 (one-shot native op).
+
+    compute_all_grads=False differentiates only e (the reference's LoRA /
+    frozen-head mode); True also produces dC and dBias.
+    """
+    ctx = torch.cuda.stream(stream) if stream is not None else _ext._nullctx()
+    with ctx:
+        loss, _ = _cce(e, c, targets, bias, reduction, ignore_index, FILTER_LOG_EPS,
+                       grad_c=compute_all_grads, grad_bias=compute_all_grads)
+    return loss
+
+
+class LinearCrossEntropy(torch.nn.Module):
+    """Drop-in module (reference/__init__.py:88-118)."""
+
+    def __init__(self, reduction="mean", ignore_index=-100, shift=0, compute_all_grads=True,
+                 filter_eps=FILTER_LOG_EPS):
+        super().__init__()
+        self.reduction = reduction
+        self.ignore_index = ignore_index
+        self.shift = shift
+        self.compute_all_grads = compute_all_grads
+        self.filter_eps = filter_eps
+
+    def forward(self, e, c, targets, bias=None):
+        if self.shift:
+            e = e[..., :-self.shift, :]
+            targets = targets[..., self.shift:]
+        orig_shape = targets.shape
+        e_flat = e.reshape(-1, e.shape[-1])
+        loss, _ = _cce(e_flat, c, targets.reshape(-1), bias, self.reduction, self.ignore_index, self.filter_eps,
+                       grad_c=self.compute_all_grads, grad_bias=self.compute_all_grads)
+        if self.reduction == "none":
+            loss = loss.reshape(orig_shape)
+        return loss

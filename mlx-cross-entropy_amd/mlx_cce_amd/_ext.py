@@ -1,0 +1,276 @@
+"""ctypes binding of ``libcce_mi355x.so`` — the C ABI declared in ``include/cce_mi355x.h``.
+
+This module is the PyTorch-side replacement of the reference's nanobind module
+``mlx_cce._ext`` (csrc/bindings.cpp:12-87).  It only moves pointers and the
+current HIP stream across the boundary; every FLOP runs in the HIP library.
+There is no fallback: if the library is missing or the tensors are not on a
+ROCm device, the call raises.
+"""
+
+import ctypes
+import math
+import os
+
+import torch
+
+from ._build import LIB_PATH
+
+FILTER_LOG_EPS = -8.3177661667  # ln(2^-12); reference csrc/cce/cce.metal:143
+STAT_TILE = 128
+
+CCE_OK = 0
+CCE_ERR_INVALID_ARGUMENT = -1
+CCE_ERR_UNSUPPORTED_DTYPE = -2
+CCE_ERR_WORKSPACE = -3
+CCE_ERR_LAUNCH = -4
+CCE_ERR_NO_DEVICE = -5
+
+DTYPE_CODES = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
+
+# Every symbol include/cce_mi355x.h declares, with (restype, argtypes).
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_INT = ctypes.c_int
+SIGNATURES = {
+    "cce_last_error": (ctypes.c_char_p, []),
+    "cce_version": (ctypes.c_char_p, []),
+    "cce_tile_config": (None, [_P, _P, _P, _P, _P]),
+    "cce_num_vocab_tiles": (_I64, [_I64]),
+    "cce_forward": (_INT, [_INT, _P, _P, _P, _P, _I64, _INT, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P]),
+    "cce_backward_workspace_size": (ctypes.c_size_t, [_INT, _I64, _I64, _I64, _INT, _INT, _INT]),
+    "cce_backward": (_INT, [_INT, _P, _P, _P, _P, _I64, _INT, _I64, _I64, _I64, _P, _P, _P, ctypes.c_float,
+                            _P, _P, _P, _P, ctypes.c_size_t, _P, _P]),
+}
+
+_lib = None
+
+# Opt-in timing: when enabled, every cce_forward / cce_backward call is bracketed
+# by HIP events recorded on the stream the kernels are launched on.
+_timing = {"on": False, "forward": [], "backward": []}
+
+
+def set_timing(on):
+    """Enable/disable event timing of the library calls and clear recorded events."""
+    _timing["on"] = bool(on)
+    _timing["forward"].clear()
+    _timing["backward"].clear()
+
+
+def timings_ms():
+    """{'forward': [ms...], 'backward': [ms...]} of the recorded calls (synchronises)."""
+    torch.cuda.synchronize()
+    return {k: [a.elapsed_time(b) for a, b in _timing[k]] for k in ("forward", "backward")}
+
+
+def _event_pair(kind):
+    if not _timing["on"]:
+        return None
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    _timing[kind].append((a, b))
+    return a, b
+
+
+def lib():
+    """Load the HIP library once (after torch, so it binds to torch's HIP runtime)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is missing. Build it with `python mlx-cross-entropy_amd/mlx_cce_amd/_build.py` "
+                "(hipcc, --offload-arch=gfx950).")
+        handle = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = handle
+    return _lib
+
+
+def version():
+    return lib().cce_version().decode()
+
+
+def tile_config():
+    vals = [ctypes.c_int() for _ in range(5)]
+    lib().cce_tile_config(*[ctypes.byref(v) for v in vals])
+    keys = ("fwd_tokens", "fwd_vocab", "stat_tile", "bwd_tokens", "bwd_vocab")
+    return {k: v.value for k, v in zip(keys, vals)}
+
+
+def _raise(rc, fn):
+    msg = lib().cce_last_error().decode() or f"{fn} failed with code {rc}"
+    if rc == CCE_ERR_INVALID_ARGUMENT or rc == CCE_ERR_WORKSPACE:
+        raise ValueError(msg)
+    raise RuntimeError(msg)
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _check_device(name, t, device):
+    if t.device.type != "cuda":
+        raise RuntimeError(
+            f"[cce] {name} is on {t.device}; this op runs only on a ROCm GPU (HIP) device "
+            "(the reference likewise has no CPU evaluation)")
+    if device is not None and t.device != device:
+        raise ValueError(f"[cce] {name} is on {t.device}, expected {device}")
+
+
+def _prep(e, c, targets, bias):
+    """Validate and normalise operands to the library's layout; returns dtype code."""
+    if e.dim() != 2:
+        raise ValueError(f"[cut_cross_entropy] e must be 2D [B, D], got {e.dim()}D")
+    if c.dim() != 2:
+        raise ValueError(f"[cut_cross_entropy] c must be 2D [V, D], got {c.dim()}D")
+    if targets.dim() != 1:
+        raise ValueError(f"[cut_cross_entropy] targets must be 1D [B], got {targets.dim()}D")
+    if c.shape[1] != e.shape[1]:
+        raise ValueError("[cut_cross_entropy] c.shape[1] must equal e.shape[1] (D)")
+    if targets.shape[0] != e.shape[0]:
+        raise ValueError("[cut_cross_entropy] targets.shape[0] must equal e.shape[0] (B)")
+    if bias is not None and (bias.dim() != 1 or bias.shape[0] != c.shape[0]):
+        raise ValueError("[cut_cross_entropy] bias must be 1D [V]")
+    if e.dtype not in DTYPE_CODES:
+        raise RuntimeError(f"CCE: unsupported dtype {e.dtype}")
+    if c.dtype != e.dtype or (bias is not None and bias.dtype != e.dtype):
+        raise TypeError(f"[cut_cross_entropy] e, c and bias must share one dtype, got {e.dtype}, {c.dtype}"
+                        + (f", {bias.dtype}" if bias is not None else ""))
+    dev = e.device
+    _check_device("e", e, None)
+    _check_device("c", c, dev)
+    _check_device("targets", targets, dev)
+    if bias is not None:
+        _check_device("bias", bias, dev)
+    return DTYPE_CODES[e.dtype]
+
+
+def forward(e, c, targets, bias=None, ignore_index=-100):
+    """Run the fused forward.  Returns (tile_max, tile_sum_exp, neg_target_logit, lse, nll).
+
+    tile_max / tile_sum_exp are [ceil(V/128), N] fp32 (vocab-tile major);
+    nll is the per-token loss, 0 on rows whose target equals ignore_index.
+    """
+    code = _prep(e, c, targets, bias)
+    e = e.contiguous()
+    c = c.contiguous()
+    targets = targets.to(torch.int64).contiguous()
+    if bias is not None:
+        bias = bias.contiguous()
+    N, D = e.shape
+    V = c.shape[0]
+    nvt = (V + STAT_TILE - 1) // STAT_TILE
+    f32 = dict(dtype=torch.float32, device=e.device)
+    tile_max = torch.empty((nvt, N), **f32)
+    tile_sum_exp = torch.empty((nvt, N), **f32)
+    neg_tl = torch.empty((N,), **f32)
+    lse = torch.empty((N,), **f32)
+    nll = torch.empty((N,), **f32)
+    has_ignore = ignore_index is not None
+    with torch.cuda.device(e.device):
+        stream = torch.cuda.current_stream(e.device).cuda_stream
+        ev = _event_pair("forward")
+        if ev:
+            ev[0].record()
+        rc = lib().cce_forward(code, _ptr(e), _ptr(c), _ptr(bias), _ptr(targets),
+                               int(ignore_index) if has_ignore else 0, 1 if has_ignore else 0,
+                               N, D, V, _ptr(tile_max), _ptr(tile_sum_exp), _ptr(neg_tl), _ptr(lse), _ptr(nll),
+                               ctypes.c_void_p(stream))
+        if ev:
+            ev[1].record()
+    if rc != CCE_OK:
+        _raise(rc, "cce_forward")
+    return tile_max, tile_sum_exp, neg_tl, lse, nll
+
+
+def workspace_size(e, c, want_de, want_dc, want_db):
+    N, D = e.shape
+    V = c.shape[0]
+    return int(lib().cce_backward_workspace_size(DTYPE_CODES.get(e.dtype, -1), N, D, V,
+                                                 int(want_de), int(want_dc), int(want_db)))
+
+
+def backward(e, c, targets, lse, tile_max, d_nll, bias=None, ignore_index=-100,
+             filter_eps=FILTER_LOG_EPS, want_de=True, want_dc=True, want_db=True, tile_stats=None):
+    """Run the filtered backward.  Returns (dE, dC, dBias), each None when not wanted.
+
+    d_nll is the fp32 cotangent of the per-token loss [N].  filter_eps=None or
+    -inf disables the 2^-12 tile filter.  tile_stats, if given, is a device
+    int64[2] tensor that receives (kept tiles, total tiles).
+    """
+    code = _prep(e, c, targets, bias)
+    e = e.contiguous()
+    c = c.contiguous()
+    targets = targets.to(torch.int64).contiguous()
+    if bias is not None:
+        bias = bias.contiguous()
+    want_db = bool(want_db and bias is not None)
+    N, D = e.shape
+    V = c.shape[0]
+    lse = lse.contiguous()
+    tile_max = tile_max.contiguous()
+    d_nll = d_nll.to(torch.float32).contiguous()
+    if d_nll.shape != (N,) or lse.shape != (N,):
+        raise ValueError("[cce_backward] lse and d_nll must be [N]")
+    dE = torch.empty_like(e) if want_de else None
+    dC = torch.empty_like(c) if want_dc else None
+    dB = torch.empty_like(bias) if want_db else None
+    ws_bytes = workspace_size(e, c, want_de, want_dc, want_db)
+    ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=e.device)
+    eps = -math.inf if filter_eps is None else float(filter_eps)
+    has_ignore = ignore_index is not None
+    with torch.cuda.device(e.device):
+        stream = torch.cuda.current_stream(e.device).cuda_stream
+        ev = _event_pair("backward")
+        if ev:
+            ev[0].record()
+        rc = lib().cce_backward(code, _ptr(e), _ptr(c), _ptr(bias), _ptr(targets),
+                                int(ignore_index) if has_ignore else 0, 1 if has_ignore else 0,
+                                N, D, V, _ptr(lse), _ptr(tile_max), _ptr(d_nll), ctypes.c_float(eps),
+                                _ptr(dE), _ptr(dC), _ptr(dB), _ptr(ws), ctypes.c_size_t(ws_bytes),
+                                _ptr(tile_stats), ctypes.c_void_p(stream))
+        if ev:
+            ev[1].record()
+    if rc != CCE_OK:
+        _raise(rc, "cce_backward")
+    return dE, dC, dB
+
+
+# --------------------------------------------------------------------------
+# Mirrors of the reference's native entry points (csrc/bindings.cpp:58-86).
+
+def cce_forward_raw(e, c, targets, bias=None, *, ignore_index=None, stream=None):
+    """Reference csrc/bindings.cpp:58-69: returns [tile_max, tile_sum_exp, neg_target_logit, lse].
+
+    Differences: statistics are per 128-column tile and laid out [num_vocab_tiles, N]
+    (the reference uses 32-column tiles, row major); targets may be any integer dtype.
+    """
+    ctx = torch.cuda.stream(stream) if stream is not None else _nullctx()
+    with ctx:
+        tm, ts, ntl, lse, _ = forward(e, c, targets, bias, ignore_index)
+    return [tm, ts, ntl, lse]
+
+
+def cce_backward_raw(e, c, lse, targets, d_nll, tile_max, bias=None, *, ignore_index=None,
+                     filter_eps=FILTER_LOG_EPS, compute_all_grads=False, stream=None):
+    """Reference csrc/bindings.cpp:71-86: returns dE (in e.dtype).
+
+    With compute_all_grads=True returns (dE, dC, dBias) — the semantics of the
+    reference's full-gradient kernel, reference/_fused_backward.py:1618-1655.
+    """
+    ctx = torch.cuda.stream(stream) if stream is not None else _nullctx()
+    with ctx:
+        dE, dC, dB = backward(e, c, targets, lse, tile_max, d_nll, bias, ignore_index, filter_eps,
+                              True, compute_all_grads, compute_all_grads)
+    if compute_all_grads:
+        return dE, dC, dB
+    return dE
+
+
+class _nullctx:
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        return False

@@ -1,0 +1,360 @@
+"""GPU parity: the HIP path (libcce_mi355x.so via the C ABI) against the float64 oracle.
+
+Tolerances (written per test):
+  * loss: 1e-3 relative (reference tests/test_correctness.py:34-40) — the fp32
+    path is checked at 1e-5;
+  * dE / dC / dBias: relative Frobenius error <= 1e-3 with the filter disabled for
+    fp32 inputs, <= 2e-2 for bf16 (measured values are
+    printed), cosine > 0.9999 for the reference's own dE test shapes
+    (tests/test_gradients.py:34-46);
+  * exact: target gather, tile max and the ignore mask on integer-valued inputs
+    (every product and sum is exact in fp32), and the kept-tile set recomputed
+    from the kernel's own fp32 statistics.
+"""
+
+import glob
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import workloads
+from oracle import cce_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = sorted(glob.glob(os.path.join(os.path.dirname(__file__), "golden", "*.npz")))
+
+
+@pytest.fixture(scope="module")
+def m(cuda):
+    import mlx_cce_amd
+    mlx_cce_amd._ext.lib()
+    return mlx_cce_amd
+
+
+def f64(t):
+    return None if t is None else t.detach().double().cpu().numpy()
+
+
+def run(m, e, c, t, bias=None, reduction="mean", ignore_index=-100, filter_eps=None, grads=True, upstream=None):
+    e = e.detach().clone().requires_grad_(grads)
+    c = c.detach().clone().requires_grad_(grads)
+    b = bias.detach().clone().requires_grad_(grads) if bias is not None else None
+    loss = m.linear_cross_entropy(e, c, t, b, reduction=reduction, ignore_index=ignore_index, filter_eps=filter_eps)
+    if grads:
+        g = torch.ones_like(loss) if upstream is None else upstream
+        loss.backward(g)
+    torch.cuda.synchronize()
+    return loss.detach(), (e.grad if grads else None), (c.grad if grads else None), (b.grad if (grads and b is not None) else None)
+
+
+def cosine(a, b):
+    a, b = np.ravel(a), np.ravel(b)
+    return float(np.dot(a, b) / (np.linalg.norm(a) * np.linalg.norm(b) + 1e-30))
+
+
+def normal_case(B, D, V, dtype, dev, seed=42, std=1.0):
+    g = torch.Generator(device=dev).manual_seed(seed)
+    e = torch.randn((B, D), generator=g, device=dev).to(dtype)
+    c = (torch.randn((V, D), generator=g, device=dev) * std).to(dtype)
+    t = torch.randint(0, V, (B,), generator=g, device=dev)
+    return e, c, t
+
+
+# ------------------------------------------------------------ golden fixtures
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("path", GOLDEN, ids=[os.path.basename(p)[:-4] for p in GOLDEN])
+def test_golden(m, cuda, path, dtype):
+    z = np.load(path)
+    e = torch.tensor(z["e"], device=cuda).to(dtype)
+    c = torch.tensor(z["c"], device=cuda).to(dtype)
+    b = torch.tensor(z["bias"], device=cuda).to(dtype) if "bias" in z else None
+    t = torch.tensor(z["targets"], device=cuda)
+    red = str(z["reduction"])
+    loss, dE, dC, dB = run(m, e, c, t, b, red, int(z["ignore_index"]))
+    tol_loss = 1e-5 if dtype == torch.float32 else 1e-3
+    np.testing.assert_allclose(f64(loss), z["loss"], rtol=tol_loss, atol=1e-6)
+    tol = 1e-4 if dtype == torch.float32 else 2e-2
+    for name, got, ref in (("dE", dE, z["dE"]), ("dC", dC, z["dC"])) + ((("dBias", dB, z["dBias"]),) if b is not None else ()):
+        err = O.rel_fro(f64(got), ref)
+        print(f"{os.path.basename(path)} {dtype} {name} rel_fro={err:.3e}")
+        assert err < tol, (name, err)
+
+
+def test_integer_inputs_exact(m, cuda):
+    """Integer inputs: every logit is exact in fp32, so the gather, tile max and mask must match bit for bit."""
+    z = np.load(os.path.join(os.path.dirname(__file__), "golden", "g_int_bias_none.npz"))
+    for dtype in (torch.float32, torch.bfloat16, torch.float16):
+        e = torch.tensor(z["e"], device=cuda).to(dtype)
+        c = torch.tensor(z["c"], device=cuda).to(dtype)
+        b = torch.tensor(z["bias"], device=cuda).to(dtype)
+        t = torch.tensor(z["targets"], device=cuda)
+        t[::7] = -100
+        tm, ts, ntl, lse = m.cce_forward_raw(e, c, t, b, ignore_index=-100)
+        torch.cuda.synchronize()
+        S = z["e"].astype(np.float64) @ z["c"].astype(np.float64).T + z["bias"]
+        tt = t.cpu().numpy()
+        valid = tt != -100
+        rows = np.nonzero(valid)[0]
+        np.testing.assert_array_equal(f64(ntl)[rows], -S[rows, tt[rows]])
+        tm_ref, _ = O.tile_stats(z["e"], z["c"], z["bias"])
+        np.testing.assert_array_equal(f64(tm), tm_ref)
+        _, _, _, _, nll = m._ext.forward(e, c, t, b, -100)
+        nll = f64(nll)
+        assert (nll[~valid] == 0.0).all()
+        np.testing.assert_allclose(nll[valid], O.per_token(z["e"], z["c"], tt, z["bias"])[0][valid], rtol=1e-5)
+
+
+# -------------------------------------------- the reference's own test suite
+SHAPES = [(32, 64, 1024), (64, 128, 4096), (128, 256, 32000), (32, 2048, 128256)]
+
+
+@pytest.mark.parametrize("B,D,V", SHAPES)
+def test_reference_shapes_loss_and_dE(m, cuda, B, D, V):
+    """tests/test_correctness.py:34-40 (loss rtol 1e-3) and tests/test_gradients.py:34-46 (dE cosine)."""
+    e, c, t = normal_case(B, D, V, torch.float32, cuda)
+    loss, dE, _, _ = run(m, e, c, t, filter_eps=m.FILTER_LOG_EPS)
+    ref = O.linear_cross_entropy(f64(e), f64(c), t.cpu().numpy(), None, "mean")
+    np.testing.assert_allclose(f64(loss), ref, rtol=1e-3)
+    rE, _, _ = O.grads(f64(e), f64(c), t.cpu().numpy(), None, "mean")
+    assert cosine(f64(dE), rE) > 0.9999
+
+
+@pytest.mark.parametrize("reduction", ["none", "sum", "mean"])
+def test_reduction_modes(m, cuda, reduction):
+    e, c, t = normal_case(32, 64, 1024, torch.float32, cuda)
+    loss, dE, dC, _ = run(m, e, c, t, reduction=reduction)
+    ref = O.linear_cross_entropy(f64(e), f64(c), t.cpu().numpy(), None, reduction)
+    np.testing.assert_allclose(f64(loss), ref, rtol=1e-5, atol=1e-5)
+    rE, rC, _ = O.grads(f64(e), f64(c), t.cpu().numpy(), None, reduction)
+    assert O.rel_fro(f64(dE), rE) < 1e-4 and O.rel_fro(f64(dC), rC) < 1e-4
+
+
+def test_ignore_index(m, cuda):
+    """tests/test_correctness.py:50-63 and tests/test_gradients.py:48-61."""
+    e, c, t = normal_case(32, 64, 1024, torch.float32, cuda)
+    tm = torch.where(torch.arange(32, device=cuda) < 16, t, torch.full_like(t, -100))
+    loss, dE, dC, _ = run(m, e, c, tm, ignore_index=-100)
+    full = O.linear_cross_entropy(f64(e), f64(c), t.cpu().numpy(), None, "none")
+    np.testing.assert_allclose(f64(loss), full[:16].sum() / 16.0, rtol=1e-5)
+    assert (f64(dE)[16:] == 0).all()
+
+
+def test_ignore_index_none(m, cuda):
+    e, c, t = normal_case(32, 64, 1024, torch.float32, cuda)
+    got = m.cce_loss(e, c, t, ignore_index=None)
+    ref = O.linear_cross_entropy(f64(e), f64(c), t.cpu().numpy(), None, "mean", ignore_index=None)
+    np.testing.assert_allclose(f64(got), ref, rtol=1e-5)
+
+
+def test_bias(m, cuda):
+    e, c, t = normal_case(32, 64, 1024, torch.float32, cuda)
+    b = torch.randn(1024, device=cuda)
+    loss, dE, dC, dB = run(m, e, c, t, b)
+    ref = O.linear_cross_entropy(f64(e), f64(c), t.cpu().numpy(), f64(b), "mean")
+    np.testing.assert_allclose(f64(loss), ref, rtol=1e-5)
+    rE, rC, rB = O.grads(f64(e), f64(c), t.cpu().numpy(), f64(b), "mean")
+    for got, r in ((dE, rE), (dC, rC), (dB, rB)):
+        assert O.rel_fro(f64(got), r) < 1e-4
+
+
+def test_batched_sequence(m, cuda):
+    """tests/test_correctness.py:82-96: e [4, 128, 256], V=4096."""
+    g = torch.Generator(device=cuda).manual_seed(42)
+    e = torch.randn((4, 128, 256), generator=g, device=cuda)
+    c = torch.randn((4096, 256), generator=g, device=cuda)
+    t = torch.randint(0, 4096, (4, 128), generator=g, device=cuda)
+    loss, dE, _, _ = run(m, e, c, t)
+    ref = O.linear_cross_entropy(f64(e), f64(c), t.cpu().numpy(), None, "mean")
+    np.testing.assert_allclose(f64(loss), ref, rtol=1e-3)
+    rE, _, _ = O.grads(f64(e).reshape(-1, 256), f64(c), t.cpu().numpy().reshape(-1), None, "mean")
+    assert cosine(f64(dE).reshape(-1, 256), rE) > 0.9999
+    none = m.linear_cross_entropy(e, c, t, reduction="none")
+    assert none.shape == (4, 128)
+
+
+def test_cut_cross_entropy_matches_cce_loss(m, cuda):
+    """tests/test_correctness.py:98-104 (rtol 1e-5)."""
+    e, c, t = normal_case(32, 64, 1024, torch.float32, cuda)
+    a = m.cut_cross_entropy(e, c, t)
+    b = m.cce_loss(e, c, t)
+    np.testing.assert_allclose(f64(a), f64(b), rtol=1e-5)
+
+
+def test_shift_and_return_lse(m, cuda):
+    g = torch.Generator(device=cuda).manual_seed(3)
+    e = torch.randn((2, 40, 64), generator=g, device=cuda)
+    c = torch.randn((500, 64), generator=g, device=cuda)
+    t = torch.randint(0, 500, (2, 40), generator=g, device=cuda)
+    loss, lse = m.linear_cross_entropy(e, c, t, reduction="none", shift=1, return_lse=True)
+    assert loss.shape == (2, 39) and lse.shape == (78,)
+    ref, rlse = O.linear_cross_entropy(f64(e), f64(c), t.cpu().numpy(), None, "none", shift=1, return_lse=True)
+    np.testing.assert_allclose(f64(loss), ref, rtol=1e-5)
+    np.testing.assert_allclose(f64(lse), rlse, rtol=1e-6)
+
+
+def test_float16(m, cuda):
+    e, c, t = normal_case(128, 256, 4000, torch.float16, cuda, std=0.1)
+    loss, dE, dC, _ = run(m, e, c, t)
+    ref = O.linear_cross_entropy(f64(e), f64(c), t.cpu().numpy(), None, "mean")
+    np.testing.assert_allclose(f64(loss), ref, rtol=1e-3)
+    rE, rC, _ = O.grads(f64(e), f64(c), t.cpu().numpy(), None, "mean")
+    assert O.rel_fro(f64(dE), rE) < 2e-2 and O.rel_fro(f64(dC), rC) < 2e-2
+
+
+# ------------------------------------------------------------------- edges
+@pytest.mark.parametrize("N,D,V", [(1, 8, 1), (3, 16, 5), (130, 40, 257), (300, 8, 129)])
+def test_ragged_shapes(m, cuda, N, D, V):
+    e, c, t = normal_case(N, D, V, torch.float32, cuda, seed=N + V)
+    b = torch.randn(V, device=cuda)
+    loss, dE, dC, dB = run(m, e, c, t, b, reduction="sum")
+    ref = O.linear_cross_entropy(f64(e), f64(c), t.cpu().numpy(), f64(b), "sum")
+    np.testing.assert_allclose(f64(loss), ref, rtol=1e-5, atol=1e-5)
+    rE, rC, rB = O.grads(f64(e), f64(c), t.cpu().numpy(), f64(b), "sum")
+    for got, r in ((dE, rE), (dC, rC), (dB, rB)):
+        assert O.rel_fro(f64(got), r) < 1e-4 or np.abs(f64(got) - r).max() < 1e-6
+
+
+def test_all_rows_ignored(m, cuda):
+    e, c, t = normal_case(64, 32, 300, torch.bfloat16, cuda)
+    t[:] = -100
+    loss, dE, dC, _ = run(m, e, c, t)
+    assert f64(loss) == 0.0
+    assert not f64(dE).any() and not f64(dC).any()
+
+
+def test_out_of_range_target_is_nan(m, cuda):
+    e, c, t = normal_case(16, 32, 100, torch.float32, cuda)
+    t[3] = 100
+    loss = m.linear_cross_entropy(e, c, t, reduction="none")
+    torch.cuda.synchronize()
+    assert math.isnan(float(loss[3])) and np.isfinite(f64(loss)[[0, 1, 2, 4]]).all()
+
+
+def test_only_dE_requested(m, cuda):
+    e, c, t = normal_case(64, 64, 1000, torch.bfloat16, cuda)
+    e.requires_grad_(True)
+    loss = m.linear_cross_entropy(e, c, t)
+    loss.backward()
+    torch.cuda.synchronize()
+    rE, _, _ = O.grads(f64(e), f64(c), t.cpu().numpy(), None, "mean")
+    assert O.rel_fro(f64(e.grad), rE) < 2e-2 and c.grad is None
+
+
+def test_upstream_gradient_none_reduction(m, cuda):
+    e, c, t = normal_case(96, 64, 700, torch.float32, cuda)
+    b = torch.randn(700, device=cuda)
+    up = torch.randn(96, device=cuda)
+    loss, dE, dC, dB = run(m, e, c, t, b, reduction="none", upstream=up)
+    rE, rC, rB = O.grads(f64(e), f64(c), t.cpu().numpy(), f64(b), "none", grad_out=f64(up))
+    for got, r in ((dE, rE), (dC, rC), (dB, rB)):
+        assert O.rel_fro(f64(got), r) < 1e-4
+
+
+# ------------------------------------------------------------------ filter
+def _peaked(dev, N=512, D=256, V=8192, boost=12.0, dtype=torch.bfloat16, seed=5):
+    g = torch.Generator(device=dev).manual_seed(seed)
+    c = (torch.randn((V, D), generator=g, device=dev) * 0.02).to(dtype)
+    t = workloads.zipf_targets(g, N, V, device=dev)
+    ct = c.float()[t]
+    e = (0.5 * torch.randn((N, D), generator=g, device=dev) + boost * ct / ct.pow(2).sum(1, keepdim=True)).to(dtype)
+    return e, c, t
+
+
+def test_filtered_backward_matches_filter_emulation(m, cuda):
+    """Kept-tile set is exact against the kernel's own fp32 statistics; gradients match the oracle over it."""
+    e, c, t = _peaked(cuda)
+    tm, _, _, lse, _ = m._ext.forward(e, c, t, None, -100)
+    N = e.shape[0]
+    d_nll = torch.full((N,), 1.0 / N, device=cuda)
+    stats = torch.zeros(2, dtype=torch.int64, device=cuda)
+    dE, dC, _ = m._ext.backward(e, c, t, lse, tm, d_nll, None, -100, m.FILTER_LOG_EPS, True, True, False,
+                                tile_stats=stats)
+    torch.cuda.synchronize()
+    tm_np, lse_np = tm.cpu().numpy(), lse.cpu().numpy()
+    tt = t.cpu().numpy()
+    keep = O.keep_mask(tm_np, lse_np, tt, np.full(N, 1.0 / N), eps=np.float32(m.FILTER_LOG_EPS))
+    # the kernel's comparison is fp32 (tile_max - lse >= eps): replay it in fp32
+    hot = (tm_np - lse_np[None, :]).astype(np.float32) >= np.float32(m.FILTER_LOG_EPS)
+    kept, total = stats.tolist()
+    assert total == keep.size
+    assert kept == int(keep.sum()), (kept, int(keep.sum()))
+    assert 0 < kept < total
+    print(f"filter: kept {kept}/{total} tiles (skip {1 - kept / total:.3f}); hot fraction {hot.mean():.4f}")
+    ee, cc = f64(e), f64(c)
+    fE, fC, _ = O.grads_filtered(ee, cc, tt, keep, 128, 128, None, d_nll=np.full(N, 1.0 / N))
+    assert O.rel_fro(f64(dE), fE) < 2e-2 and O.rel_fro(f64(dC), fC) < 2e-2
+    dense = O.grads(ee, cc, tt, None, "mean")
+    errs = [O.rel_fro(f64(x), y) for x, y in zip((dE, dC), dense[:2])]
+    ref_keep = O.reference_keep_mask(ee, cc, tt)
+    rE, rC, _ = O.grads_filtered(ee, cc, tt, ref_keep, 32, 32, None, d_nll=np.full(N, 1.0 / N))
+    print(f"filtered vs dense: dE {errs[0]:.3e} dC {errs[1]:.3e}; reference filter: "
+          f"dE {O.rel_fro(rE, dense[0]):.3e} dC {O.rel_fro(rC, dense[1]):.3e}")
+    assert errs[0] < 2e-2 and errs[1] < 2e-2
+
+
+def test_filter_disabled_is_dense(m, cuda):
+    e, c, t = _peaked(cuda, N=256, V=4096)
+    tm, _, _, lse, _ = m._ext.forward(e, c, t, None, -100)
+    d_nll = torch.full((256,), 1.0 / 256, device=cuda)
+    stats = torch.zeros(2, dtype=torch.int64, device=cuda)
+    m._ext.backward(e, c, t, lse, tm, d_nll, None, -100, None, True, True, False, tile_stats=stats)
+    kept, total = stats.tolist()
+    assert kept == total == 2 * 32
+
+
+# --------------------------------------------------- benchmark configurations
+def _cfg_check(m, name, scale, tol_grad):
+    w = workloads.make(name, device="cuda", scale=scale)
+    e, c, t, b = w["e"], w["c"], w["targets"], w["bias"]
+    red = w["reduction"]
+    loss, dE, dC, dB = run(m, e, c, t, b, red, -100, filter_eps=None)
+    ee = f64(e).reshape(-1, w["D"])
+    cc = f64(c)
+    tt = t.cpu().numpy().reshape(-1)
+    bb = f64(b)
+    ref = O.linear_cross_entropy(ee, cc, tt, bb, red)
+    np.testing.assert_allclose(f64(loss).reshape(-1), np.ravel(ref), rtol=1e-3, atol=1e-5)
+    rE, rC, rB = O.grads(ee, cc, tt, bb, red)
+    errs = {"dE": O.rel_fro(f64(dE).reshape(-1, w["D"]), rE), "dC": O.rel_fro(f64(dC), rC)}
+    if b is not None:
+        errs["dBias"] = O.rel_fro(f64(dB), rB)
+    print(name, {k: f"{v:.3e}" for k, v in errs.items()})
+    for k, v in errs.items():
+        assert v < tol_grad, (k, v)
+
+
+def test_config_c1_fp32_full(m, cuda):
+    _cfg_check(m, "c1", 1.0, 1e-3)
+
+
+def test_config_c2_slice(m, cuda):
+    _cfg_check(m, "c2", 1 / 16, 2e-2)
+
+
+def test_config_c4_slice_bias(m, cuda):
+    _cfg_check(m, "c4", 1 / 32, 2e-2)
+
+
+def test_config_c3_full_size_properties(m, cuda):
+    """c3 at full size: loss is ~0 (target logit ~40, F2 degeneracy), lse of sampled rows matches the oracle."""
+    w = workloads.make("c3", device="cuda")
+    e = w["e"].reshape(-1, w["D"])
+    c, t = w["c"], w["targets"].reshape(-1)
+    tm, ts, ntl, lse, nll = m._ext.forward(e, c, t, None, -100)
+    rows = torch.arange(0, w["N"], 997, device=cuda)
+    ref_nll, ref_lse, _ = O.per_token(f64(e[rows]), f64(c), t[rows].cpu().numpy())
+    ulp = np.spacing(np.float32(np.abs(ref_lse).max()))
+    np.testing.assert_allclose(f64(lse[rows]), ref_lse, rtol=0, atol=8 * ulp)
+    assert np.abs(f64(nll[rows]) - ref_nll).max() < 16 * ulp
+    e2 = e.detach().clone().requires_grad_(True)
+    c2 = c.detach().clone().requires_grad_(True)
+    loss = m.linear_cross_entropy(e2, c2, t)
+    loss.backward()
+    torch.cuda.synchronize()
+    kept, total = m.last_tile_stats()
+    print(f"c3: loss {loss.item():.3e} kept {kept}/{total} skip {1 - kept / total:.4f}")
+    assert 0 < kept < total and torch.isfinite(e2.grad).all() and torch.isfinite(c2.grad).all()

@@ -1,0 +1,334 @@
+"""Pin the CPU oracle (oracle/cce_oracle.py) — CPU only.
+
+Each oracle function is checked against something it was not derived from:
+brute-force loops, an independent float64 torch autograd, finite differences,
+closed-form special cases, invariants, and the committed golden fixtures.
+A final group plants mistakes in a copy of the oracle's math and asserts that
+these checks catch them.
+"""
+
+import glob
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import cce_oracle as O
+from oracle import cpu_baseline as CB
+
+GOLDEN = sorted(glob.glob(os.path.join(os.path.dirname(__file__), "golden", "*.npz")))
+
+
+def rand_case(N, D, V, seed, bias=False, n_ignored=0, c_std=1.0, boost=None):
+    rng = np.random.default_rng(seed)
+    c = rng.standard_normal((V, D)) * c_std
+    e = rng.standard_normal((N, D))
+    t = rng.integers(0, V, N)
+    if boost is not None:
+        ct = c[t]
+        e = 0.5 * e + boost * ct / (ct ** 2).sum(1, keepdims=True)
+    b = rng.standard_normal(V) if bias else None
+    if n_ignored:
+        t[rng.permutation(N)[:n_ignored]] = -100
+    return e, c, t, b
+
+
+def torch_ref(e, c, t, b, reduction, ignore_index=-100, grad_out=None):
+    """Independent float64 autograd through materialised logits."""
+    ec = torch.tensor(e, dtype=torch.float64, requires_grad=True)
+    cc = torch.tensor(c, dtype=torch.float64, requires_grad=True)
+    bc = torch.tensor(b, dtype=torch.float64, requires_grad=True) if b is not None else None
+    tt = torch.tensor(t, dtype=torch.int64)
+    logits = ec @ cc.T + (bc if bc is not None else 0.0)
+    ii = ignore_index if ignore_index is not None else -(10 ** 9)
+    nll = F.cross_entropy(logits, tt.clamp(min=0) if ignore_index is None else tt, reduction="none",
+                          ignore_index=ii)
+    valid = (tt != ii).double()
+    nll = nll * valid
+    if reduction == "none":
+        loss = nll
+        loss.backward(torch.ones_like(nll) if grad_out is None else torch.tensor(grad_out, dtype=torch.float64))
+    elif reduction == "sum":
+        loss = nll.sum()
+        loss.backward()
+    else:
+        loss = nll.sum() / valid.sum().clamp(min=1)
+        loss.backward()
+    return (loss.detach().numpy(), torch.logsumexp(logits, 1).detach().numpy(), ec.grad.numpy(), cc.grad.numpy(),
+            bc.grad.numpy() if bc is not None else None)
+
+
+# ----------------------------------------------------------------- brute force
+def brute(e, c, t, b, reduction, ignore_index=-100):
+    N, D = len(e), len(e[0])
+    V = len(c)
+    S = [[sum(e[n][k] * c[v][k] for k in range(D)) + (b[v] if b is not None else 0.0) for v in range(V)]
+         for n in range(N)]
+    lse = []
+    for n in range(N):
+        m = max(S[n])
+        lse.append(m + math.log(sum(math.exp(x - m) for x in S[n])))
+    valid = [ignore_index is None or t[n] != ignore_index for n in range(N)]
+    nll = [(lse[n] - S[n][t[n]]) if valid[n] else 0.0 for n in range(N)]
+    cnt = max(sum(valid), 1)
+    g = [(1.0 / cnt if reduction == "mean" else 1.0) if valid[n] else 0.0 for n in range(N)]
+    G = [[g[n] * (math.exp(S[n][v] - lse[n]) - (1.0 if (valid[n] and v == t[n]) else 0.0)) for v in range(V)]
+         for n in range(N)]
+    dE = [[sum(G[n][v] * c[v][k] for v in range(V)) for k in range(D)] for n in range(N)]
+    dC = [[sum(G[n][v] * e[n][k] for n in range(N)) for k in range(D)] for v in range(V)]
+    dB = [sum(G[n][v] for n in range(N)) for v in range(V)]
+    loss = nll if reduction == "none" else (sum(nll) if reduction == "sum" else sum(nll) / cnt)
+    return loss, lse, dE, dC, dB
+
+
+@pytest.mark.parametrize("reduction", ["mean", "sum", "none"])
+@pytest.mark.parametrize("bias", [False, True])
+def test_brute_force_tiny(reduction, bias):
+    e, c, t, b = rand_case(5, 3, 7, seed=1, bias=bias, n_ignored=2)
+    loss, lse, dE, dC, dB = brute(e.tolist(), c.tolist(), t.tolist(), b.tolist() if bias else None, reduction)
+    got = O.linear_cross_entropy(e, c, t, b, reduction)
+    np.testing.assert_allclose(got, loss, rtol=1e-12, atol=1e-14)
+    _, lse_o = O.linear_cross_entropy(e, c, t, b, reduction, return_lse=True)
+    np.testing.assert_allclose(lse_o, lse, rtol=1e-13)
+    gE, gC, gB = O.grads(e, c, t, b, reduction)
+    np.testing.assert_allclose(gE, dE, rtol=1e-11, atol=1e-14)
+    np.testing.assert_allclose(gC, dC, rtol=1e-11, atol=1e-14)
+    if bias:
+        np.testing.assert_allclose(gB, dB, rtol=1e-11, atol=1e-14)
+
+
+# ------------------------------------------------------- independent autograd
+@pytest.mark.parametrize("reduction", ["mean", "sum", "none"])
+@pytest.mark.parametrize("bias", [False, True])
+@pytest.mark.parametrize("n_ignored", [0, 9])
+def test_against_torch_autograd(reduction, bias, n_ignored):
+    e, c, t, b = rand_case(48, 40, 333, seed=7, bias=bias, n_ignored=n_ignored)
+    loss, lse, dE, dC, dB = torch_ref(e, c, t, b, reduction)
+    np.testing.assert_allclose(O.linear_cross_entropy(e, c, t, b, reduction), loss, rtol=1e-12, atol=1e-13)
+    gE, gC, gB = O.grads(e, c, t, b, reduction)
+    np.testing.assert_allclose(gE, dE, rtol=1e-10, atol=1e-13)
+    np.testing.assert_allclose(gC, dC, rtol=1e-10, atol=1e-13)
+    if bias:
+        np.testing.assert_allclose(gB, dB, rtol=1e-10, atol=1e-13)
+
+
+def test_ignore_index_none_means_all_valid():
+    e, c, t, b = rand_case(16, 8, 50, seed=3)
+    loss, *_ = torch_ref(e, c, t, None, "mean", ignore_index=None)
+    np.testing.assert_allclose(O.linear_cross_entropy(e, c, t, None, "mean", ignore_index=None), loss, rtol=1e-12)
+
+
+def test_shift_and_batched_shape():
+    rng = np.random.default_rng(5)
+    e = rng.standard_normal((2, 6, 4))
+    c = rng.standard_normal((11, 4))
+    t = rng.integers(0, 11, (2, 6))
+    got = O.linear_cross_entropy(e, c, t, reduction="none", shift=1)
+    assert got.shape == (2, 5)
+    exp = O.linear_cross_entropy(e[:, :-1, :], c, t[:, 1:], reduction="none")
+    np.testing.assert_array_equal(got, exp)
+
+
+def test_finite_differences():
+    e, c, t, b = rand_case(6, 5, 9, seed=11, bias=True, n_ignored=1)
+    dE, dC, dB = O.grads(e, c, t, b, "mean")
+    h = 1e-6
+
+    def f(e_, c_, b_):
+        return O.linear_cross_entropy(e_, c_, t, b_, "mean")
+
+    for (i, j) in [(0, 0), (2, 3), (5, 4)]:
+        ep, em = e.copy(), e.copy()
+        ep[i, j] += h
+        em[i, j] -= h
+        assert abs((f(ep, c, b) - f(em, c, b)) / (2 * h) - dE[i, j]) < 1e-8
+    for (i, j) in [(0, 1), (8, 4)]:
+        cp, cm = c.copy(), c.copy()
+        cp[i, j] += h
+        cm[i, j] -= h
+        assert abs((f(e, cp, b) - f(e, cm, b)) / (2 * h) - dC[i, j]) < 1e-8
+    for i in [0, 7]:
+        bp, bm = b.copy(), b.copy()
+        bp[i] += h
+        bm[i] -= h
+        assert abs((f(e, c, bp) - f(e, c, bm)) / (2 * h) - dB[i]) < 1e-8
+
+
+# --------------------------------------------------------------- closed forms
+def test_zero_weights_give_log_v():
+    N, D, V = 10, 6, 97
+    e = np.random.default_rng(0).standard_normal((N, D))
+    c = np.zeros((V, D))
+    t = np.arange(N) % V
+    nll = O.linear_cross_entropy(e, c, t, reduction="none")
+    np.testing.assert_allclose(nll, np.full(N, math.log(V)), rtol=1e-15)
+    dE, dC, _ = O.grads(e, c, t, None, "sum")
+    np.testing.assert_allclose(dE, 0.0, atol=0)  # C = 0 makes G C = 0 exactly
+
+
+def test_equal_logits_and_single_class():
+    e = np.ones((4, 3))
+    c = np.ones((5, 3)) * 0.5
+    t = np.array([0, 1, 2, 4])
+    _, lse = O.linear_cross_entropy(e, c, t, reduction="none", return_lse=True)
+    np.testing.assert_allclose(lse, 1.5 + math.log(5), rtol=1e-15)
+    c1 = np.random.default_rng(1).standard_normal((1, 3))
+    nll = O.linear_cross_entropy(np.random.default_rng(2).standard_normal((4, 3)), c1, np.zeros(4, int),
+                                 reduction="none")
+    np.testing.assert_allclose(nll, 0.0, atol=1e-15)
+
+
+def test_all_ignored_mean_is_zero():
+    e, c, t, b = rand_case(8, 4, 20, seed=4)
+    t[:] = -100
+    assert O.linear_cross_entropy(e, c, t, reduction="mean") == 0.0
+    dE, dC, _ = O.grads(e, c, t, None, "mean")
+    assert not dE.any() and not dC.any()
+
+
+# ---------------------------------------------------------------- invariants
+def test_invariants():
+    e, c, t, b = rand_case(30, 12, 77, seed=9, bias=True, n_ignored=4)
+    dE, dC, dB = O.grads(e, c, t, b, "sum")
+    assert abs(dB.sum()) < 1e-10  # rows of G sum to zero
+    dE0, dC0, _ = O.grads(e, c, t, None, "sum")
+    np.testing.assert_allclose(np.vdot(e, dE0), np.vdot(c, dC0), rtol=1e-10)  # <E, GC> = <C, G^T E>
+    g = np.random.default_rng(1).standard_normal(30)
+    a1 = O.grads(e, c, t, b, "none", grad_out=g)
+    a2 = O.grads(e, c, t, b, "none", grad_out=2.5 * g)
+    for x, y in zip(a1, a2):
+        np.testing.assert_allclose(2.5 * x, y, rtol=1e-12, atol=1e-15)
+    # ignored rows: zero loss and zero dE rows
+    nll = O.linear_cross_entropy(e, c, t, b, "none")
+    ign = t == -100
+    assert (nll[ign] == 0).all() and (dE[ign] == 0).all()
+
+
+# -------------------------------------------------------------- tile stats
+def test_tile_stats_merge_to_lse():
+    e, c, t, b = rand_case(9, 5, 300, seed=12, bias=True)
+    tm, ts = O.tile_stats(e, c, b)
+    assert tm.shape == (3, 9)
+    s = O.logits(e, c, b)
+    for k in range(3):
+        np.testing.assert_array_equal(tm[k], s[:, 128 * k:128 * (k + 1)].max(1))
+    M = tm.max(0)
+    lse = M + np.log((ts * np.exp(tm - M)).sum(0))
+    _, lse_ref = O.linear_cross_entropy(e, c, t, b, "none", return_lse=True)
+    np.testing.assert_allclose(lse, lse_ref, rtol=1e-14)
+
+
+# ------------------------------------------------------------------ filter
+def test_filter_off_is_dense():
+    e, c, t, b = rand_case(200, 16, 700, seed=13, bias=True, n_ignored=3)
+    valid = O.valid_mask(t, -100)
+    g = O.upstream(valid, "mean")
+    tm, _ = O.tile_stats(e, c, b)
+    _, lse = O.linear_cross_entropy(e, c, t, b, "none", return_lse=True)
+    keep = O.keep_mask(tm, lse, t, g, eps=-np.inf)
+    assert keep.all()
+    dense = O.grads(e, c, t, b, d_nll=g)
+    filt = O.grads_filtered(e, c, t, keep, 128, 128, b, d_nll=g)
+    for x, y in zip(filt, dense):
+        np.testing.assert_allclose(x, y, rtol=1e-12, atol=1e-15)
+
+
+def test_build_filter_is_superset_of_reference_filter():
+    rng = np.random.default_rng(14)
+    N, D, V = 256, 64, 4096
+    c = rng.standard_normal((V, D)) * 0.02
+    t = rng.integers(0, V // 4, N)  # targets confined to the first quarter of the vocabulary
+    ct = c[t]
+    e = 0.5 * rng.standard_normal((N, D)) + 30.0 * ct / (ct ** 2).sum(1, keepdims=True)
+    t[rng.permutation(N)[:10]] = -100
+    valid = O.valid_mask(t, -100)
+    g = O.upstream(valid, "mean")
+    tm, _ = O.tile_stats(e, c, None)
+    _, lse = O.linear_cross_entropy(e, c, t, None, "none", return_lse=True)
+    ours = O.keep_mask(tm, lse, t, g)
+    ref = O.reference_keep_mask(e, c, t)
+    assert 0 < ours.sum() < ours.size  # the filter is exercised
+    # every reference-kept 32x32 tile whose rows carry gradient lies in a kept 128x128 tile
+    for vt32, rb32 in zip(*np.nonzero(ref)):
+        rows = slice(rb32 * 32, rb32 * 32 + 32)
+        if (g[rows] != 0).any():
+            assert ours[vt32 // 4, rb32 // 4]
+    dense = O.grads(e, c, t, None, d_nll=g)
+    ours_g = O.grads_filtered(e, c, t, ours, 128, 128, None, d_nll=g)
+    ref_g = O.grads_filtered(e, c, t, ref, 32, 32, None, d_nll=g)
+    for k in range(2):
+        # keeping a superset of the reference's tiles can only move the result toward the dense one
+        assert O.rel_fro(ours_g[k], dense[k]) <= O.rel_fro(ref_g[k], dense[k]) + 1e-12
+
+
+# ---------------------------------------------------------------- fixtures
+@pytest.mark.parametrize("path", GOLDEN, ids=[os.path.basename(p) for p in GOLDEN])
+def test_oracle_matches_golden(path):
+    z = np.load(path)
+    e, c, t = z["e"], z["c"], z["targets"]
+    b = z["bias"] if "bias" in z else None
+    red = str(z["reduction"])
+    ii = int(z["ignore_index"])
+    loss, lse = O.linear_cross_entropy(e, c, t, b, red, ii, return_lse=True)
+    np.testing.assert_allclose(loss, z["loss"], rtol=1e-12, atol=1e-13)
+    np.testing.assert_allclose(lse, z["lse"], rtol=1e-13)
+    dE, dC, dB = O.grads(e, c, t, b, red, ii)
+    np.testing.assert_allclose(dE, z["dE"], rtol=1e-10, atol=1e-14)
+    np.testing.assert_allclose(dC, z["dC"], rtol=1e-10, atol=1e-14)
+    if b is not None:
+        np.testing.assert_allclose(dB, z["dBias"], rtol=1e-10, atol=1e-14)
+
+
+def test_cpu_baseline_matches_oracle():
+    e, c, t, b = rand_case(40, 16, 200, seed=15, bias=True, n_ignored=5)
+    te, tc, tb = (torch.tensor(x, dtype=torch.float32) for x in (e, c, b))
+    loss, dE, dC, dB = CB.loss_and_grads(te, tc, torch.tensor(t), tb, "mean")
+    e32, c32, b32 = te.double().numpy(), tc.double().numpy(), tb.double().numpy()
+    np.testing.assert_allclose(loss.item(), O.linear_cross_entropy(e32, c32, t, b32, "mean"), rtol=1e-5)
+    oE, oC, oB = O.grads(e32, c32, t, b32, "mean")
+    assert O.rel_fro(dE.numpy(), oE) < 1e-5 and O.rel_fro(dC.numpy(), oC) < 1e-5 and O.rel_fro(dB.numpy(), oB) < 1e-5
+
+
+# ---------------------------------------------------------- planted mistakes
+def _mutant_grads(e, c, t, b, kind):
+    s = O.logits(e, c, b)
+    lse = O.logsumexp_rows(s)
+    N = len(t)
+    valid = t != -100
+    p = np.exp(s - lse[:, None])
+    rows = np.nonzero(valid)[0]
+    if kind == "onehot_sign":
+        p[rows, t[rows]] += 1.0
+    elif kind == "target_off_by_one":
+        p[rows, (t[rows] + 1) % c.shape[0]] -= 1.0
+    else:
+        p[rows, t[rows]] -= 1.0
+    if kind == "count_includes_ignored":
+        g = np.full(N, 1.0 / N)
+    else:
+        g = np.full(N, 1.0 / max(valid.sum(), 1))
+    g = np.where(valid, g, 0.0)
+    G = p * g[:, None]
+    dE = G @ c
+    if kind == "transposed_operand":
+        dC = (G.T @ e)[::-1]
+    else:
+        dC = G.T @ e
+    return dE, dC
+
+
+@pytest.mark.parametrize("kind", ["onehot_sign", "target_off_by_one", "count_includes_ignored",
+                                  "transposed_operand"])
+def test_planted_mistakes_are_caught(kind):
+    e, c, t, b = rand_case(24, 10, 60, seed=21, n_ignored=4)
+    _, _, dE, dC, _ = torch_ref(e, c, t, None, "mean")
+    mE, mC = _mutant_grads(e, c, t, None, kind)
+    caught = not (np.allclose(mE, dE, rtol=1e-8, atol=1e-12) and np.allclose(mC, dC, rtol=1e-8, atol=1e-12))
+    assert caught, kind
+    # and the unmutated restatement passes the same check
+    oE, oC = _mutant_grads(e, c, t, None, "none")
+    np.testing.assert_allclose(oE, dE, rtol=1e-8, atol=1e-12)
+    np.testing.assert_allclose(oC, dC, rtol=1e-8, atol=1e-12)
