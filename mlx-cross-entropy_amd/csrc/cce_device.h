@@ -144,17 +144,18 @@ struct NTMainLoop {
     u32x4 pre[LOADS];
     const int KT = (int)((kbytes + kStageRowBytes - 1) / kStageRowBytes);
 
+    // Global -> registers for K tile kt.  Full tiles take the branch-free path;
+    // only a ragged last tile (D*sizeof(T) not a multiple of 128) predicates per lane.
     auto gload = [&](int kt) {
-      const int64_t kb = (int64_t)kt * kStageRowBytes + q * 16;
-      const bool kin = kb < kbytes;
+      const int64_t k0 = (int64_t)kt * kStageRowBytes;
+      if (k0 + kStageRowBytes <= kbytes) {
 #pragma unroll
-      for (int i = 0; i < LOADS; ++i) {
-        const char* base = (i < LA ? abase : bbase) + (int64_t)kt * kStageRowBytes;
-        if (kin) {
-          pre[i] = gld16(base + off[i]);
-        } else {
-          pre[i] = u32x4{0u, 0u, 0u, 0u};
-        }
+        for (int i = 0; i < LOADS; ++i) pre[i] = gld16((i < LA ? abase : bbase) + k0 + off[i]);
+      } else {
+        const bool kin = k0 + q * 16 < kbytes;
+#pragma unroll
+        for (int i = 0; i < LOADS; ++i)
+          pre[i] = kin ? gld16((i < LA ? abase : bbase) + k0 + off[i]) : u32x4{0u, 0u, 0u, 0u};
       }
     };
     auto sstore = [&](int stage) {
@@ -163,28 +164,34 @@ struct NTMainLoop {
       for (int i = 0; i < LOADS; ++i) lds_st16(s, swz(rr + 32 * i, q, kStageRowBytes), pre[i]);
     };
 
+    const int arow = wa * (ROWS_A / WA) + (lane & 31);
+    const int brow = ROWS_A + wb * (ROWS_B / WB) + (lane & 31);
+    const int kg = lane >> 5;
+    auto frags = [&](const char* s, int ks, u32x4 (&af)[TI], u32x4 (&bf)[TJ]) {
+#pragma unroll
+      for (int ti = 0; ti < TI; ++ti) af[ti] = lds_ld16(s, swz(arow + ti * 32, ks * 2 + kg, kStageRowBytes));
+#pragma unroll
+      for (int tj = 0; tj < TJ; ++tj) bf[tj] = lds_ld16(s, swz(brow + tj * 32, ks * 2 + kg, kStageRowBytes));
+    };
+
     gload(0);
     sstore(0);
     __syncthreads();
 
-    const int arow = wa * (ROWS_A / WA) + (lane & 31);
-    const int brow = ROWS_A + wb * (ROWS_B / WB) + (lane & 31);
-    const int kg = lane >> 5;
-
+    constexpr int KS = kStageRowBytes / 32;  // 32-byte K steps per stage
     for (int kt = 0; kt < KT; ++kt) {
       if (kt + 1 < KT) gload(kt + 1);
       const char* s = smem + (kt & 1) * STAGE_BYTES;
+      // Fragments of step ks+1 are read from LDS while the MFMAs of step ks run.
+      u32x4 af[2][TI], bf[2][TJ];
+      frags(s, 0, af[0], bf[0]);
 #pragma unroll
-      for (int ks = 0; ks < kStageRowBytes / 32; ++ks) {
-        u32x4 af[TI], bf[TJ];
-#pragma unroll
-        for (int ti = 0; ti < TI; ++ti) af[ti] = lds_ld16(s, swz(arow + ti * 32, ks * 2 + kg, kStageRowBytes));
-#pragma unroll
-        for (int tj = 0; tj < TJ; ++tj) bf[tj] = lds_ld16(s, swz(brow + tj * 32, ks * 2 + kg, kStageRowBytes));
+      for (int ks = 0; ks < KS; ++ks) {
+        if (ks + 1 < KS) frags(s, ks + 1, af[(ks + 1) & 1], bf[(ks + 1) & 1]);
 #pragma unroll
         for (int ti = 0; ti < TI; ++ti)
 #pragma unroll
-          for (int tj = 0; tj < TJ; ++tj) acc[ti][tj] = Traits<T>::mfma(af[ti], bf[tj], acc[ti][tj]);
+          for (int tj = 0; tj < TJ; ++tj) acc[ti][tj] = Traits<T>::mfma(af[ks & 1][ti], bf[ks & 1][tj], acc[ti][tj]);
       }
       if (kt + 1 < KT) sstore((kt + 1) & 1);
       __syncthreads();

@@ -286,14 +286,19 @@ def test_filtered_backward_matches_filter_emulation(m, cuda):
     print(f"filter: kept {kept}/{total} tiles (skip {1 - kept / total:.3f}); hot fraction {hot.mean():.4f}")
     ee, cc = f64(e), f64(c)
     fE, fC, _ = O.grads_filtered(ee, cc, tt, keep, 128, 128, None, d_nll=np.full(N, 1.0 / N))
-    assert O.rel_fro(f64(dE), fE) < 2e-2 and O.rel_fro(f64(dC), fC) < 2e-2
+    emu = [O.rel_fro(f64(dE), fE), O.rel_fro(f64(dC), fC)]
+    print(f"kernel vs filter emulation: dE {emu[0]:.3e} dC {emu[1]:.3e}")
+    assert emu[0] < 2e-2 and emu[1] < 2e-2  # bf16 tolerance against the same kept-tile set
+    # The 2^-12 filter itself drops softmax mass; against the dense gradient the error must be
+    # no larger than the reference's own 32x32 filter produces on the same inputs.
     dense = O.grads(ee, cc, tt, None, "mean")
     errs = [O.rel_fro(f64(x), y) for x, y in zip((dE, dC), dense[:2])]
     ref_keep = O.reference_keep_mask(ee, cc, tt)
     rE, rC, _ = O.grads_filtered(ee, cc, tt, ref_keep, 32, 32, None, d_nll=np.full(N, 1.0 / N))
+    ref_errs = [O.rel_fro(rE, dense[0]), O.rel_fro(rC, dense[1])]
     print(f"filtered vs dense: dE {errs[0]:.3e} dC {errs[1]:.3e}; reference filter: "
-          f"dE {O.rel_fro(rE, dense[0]):.3e} dC {O.rel_fro(rC, dense[1]):.3e}")
-    assert errs[0] < 2e-2 and errs[1] < 2e-2
+          f"dE {ref_errs[0]:.3e} dC {ref_errs[1]:.3e}")
+    assert errs[0] <= ref_errs[0] + 2e-3 and errs[1] <= ref_errs[1] + 2e-3
 
 
 def test_filter_disabled_is_dense(m, cuda):
