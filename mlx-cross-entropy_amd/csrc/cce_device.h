@@ -34,8 +34,32 @@ constexpr float kLn2 = 0.6931471805599453f;
 template <typename T>
 struct Traits;
 
+// Instruction scheduling hints: interleave the MF MFMA instructions of one step
+// with NR LDS reads, NV global loads and NW LDS writes, front-loading the memory
+// instructions into the first half of the MFMAs (masks: 0x008 MFMA, 0x100 DS
+// read, 0x200 DS write, 0x020 VMEM read).
+__host__ __device__ constexpr int sched_share(int i, int slots, int n) {
+  const int use = slots / 2 > 0 ? slots / 2 : 1;
+  return i < use ? (n * (i + 1) / use - n * i / use) : 0;
+}
+
+template <int I, int MF, int NR, int NV, int NW>
+__device__ __forceinline__ void sched_interleave() {
+  if constexpr (I < MF) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    constexpr int r = sched_share(I, MF, NR);
+    constexpr int v = sched_share(I, MF, NV);
+    constexpr int w = sched_share(I, MF, NW);
+    if constexpr (r > 0) __builtin_amdgcn_sched_group_barrier(0x100, r, 0);
+    if constexpr (v > 0) __builtin_amdgcn_sched_group_barrier(0x020, v, 0);
+    if constexpr (w > 0) __builtin_amdgcn_sched_group_barrier(0x200, w, 0);
+    sched_interleave<I + 1, MF, NR, NV, NW>();
+  }
+}
+
 template <>
 struct Traits<__bf16> {
+  static constexpr int kInstrPerStep = 1;
   static __device__ __forceinline__ f32x16 mfma(u32x4 a, u32x4 b, f32x16 acc) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
                                                    __builtin_bit_cast(bf16x8, b), acc, 0, 0, 0);
@@ -44,6 +68,7 @@ struct Traits<__bf16> {
 
 template <>
 struct Traits<_Float16> {
+  static constexpr int kInstrPerStep = 1;
   static __device__ __forceinline__ f32x16 mfma(u32x4 a, u32x4 b, f32x16 acc) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
                                                   __builtin_bit_cast(f16x8, b), acc, 0, 0, 0);
@@ -52,6 +77,7 @@ struct Traits<_Float16> {
 
 template <>
 struct Traits<float> {
+  static constexpr int kInstrPerStep = 4;
   static __device__ __forceinline__ f32x16 mfma(u32x4 a, u32x4 b, f32x16 acc) {
     acc = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a.x), __uint_as_float(b.x), acc, 0, 0, 0);
     acc = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a.y), __uint_as_float(b.y), acc, 0, 0, 0);
@@ -141,61 +167,95 @@ struct NTMainLoop {
       }
     }
 
-    u32x4 pre[LOADS];
     const int KT = (int)((kbytes + kStageRowBytes - 1) / kStageRowBytes);
-
-    // Global -> registers for K tile kt.  Full tiles take the branch-free path;
-    // only a ragged last tile (D*sizeof(T) not a multiple of 128) predicates per lane.
-    auto gload = [&](int kt) {
-      const int64_t k0 = (int64_t)kt * kStageRowBytes;
-      if (k0 + kStageRowBytes <= kbytes) {
-#pragma unroll
-        for (int i = 0; i < LOADS; ++i) pre[i] = gld16((i < LA ? abase : bbase) + k0 + off[i]);
-      } else {
-        const bool kin = k0 + q * 16 < kbytes;
-#pragma unroll
-        for (int i = 0; i < LOADS; ++i)
-          pre[i] = kin ? gld16((i < LA ? abase : bbase) + k0 + off[i]) : u32x4{0u, 0u, 0u, 0u};
-      }
-    };
-    auto sstore = [&](int stage) {
-      char* s = smem + stage * STAGE_BYTES;
-#pragma unroll
-      for (int i = 0; i < LOADS; ++i) lds_st16(s, swz(rr + 32 * i, q, kStageRowBytes), pre[i]);
-    };
-
     const int arow = wa * (ROWS_A / WA) + (lane & 31);
     const int brow = ROWS_A + wb * (ROWS_B / WB) + (lane & 31);
     const int kg = lane >> 5;
+    // A ragged contraction length (D*sizeof(T) not a multiple of 128) only changes
+    // the loads of the last K tile; resolve it once, outside the pipelined loop.
+    if (kbytes % kStageRowBytes == 0) {
+      loop<false>(abase, bbase, off, kbytes, KT, smem, arow, brow, kg, q, rr, acc);
+    } else {
+      loop<true>(abase, bbase, off, kbytes, KT, smem, arow, brow, kg, q, rr, acc);
+    }
+  }
+
+  // One K tile = 4 MFMA steps of 32 bytes.  Software pipeline (one barrier per tile):
+  //   step 0: issue the global loads of tile kt+1, read fragments of step 1
+  //   step 1: read fragments of step 2
+  //   step 2: read fragments of step 3, write tile kt+1 (registers -> other stage)
+  //   barrier
+  //   step 3: read fragments of step 0 of tile kt+1
+  // and every step's MFMAs are interleaved with those memory instructions so that
+  // LDS and global latency hide behind the matrix cores.  The last iteration
+  // reloads the last tile into the idle stage, which keeps the body branch-free.
+  template <bool RAGGED>
+  static __device__ __forceinline__ void loop(const char* abase, const char* bbase, const uint32_t (&off)[LOADS],
+                                              int64_t kbytes, int KT, char* smem, int arow, int brow, int kg,
+                                              int q, int rr, f32x16 (&acc)[TI][TJ]) {
+    u32x4 pre[LOADS];
+    auto gload = [&](int kt) {
+      const int64_t k0 = (int64_t)kt * kStageRowBytes;
+      if constexpr (RAGGED) {
+        const bool kin = k0 + q * 16 < kbytes;
+        const int64_t kk = kin ? k0 : 0;  // out-of-range chunks re-read column 0 and are zeroed
+#pragma unroll
+        for (int i = 0; i < LOADS; ++i) {
+          const u32x4 v = gld16((i < LA ? abase : bbase) + kk + off[i]);
+          pre[i] = kin ? v : u32x4{0u, 0u, 0u, 0u};
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < LOADS; ++i) pre[i] = gld16((i < LA ? abase : bbase) + k0 + off[i]);
+      }
+    };
+    auto sstore = [&](char* s) {
+#pragma unroll
+      for (int i = 0; i < LOADS; ++i) lds_st16(s, swz(rr + 32 * i, q, kStageRowBytes), pre[i]);
+    };
     auto frags = [&](const char* s, int ks, u32x4 (&af)[TI], u32x4 (&bf)[TJ]) {
 #pragma unroll
       for (int ti = 0; ti < TI; ++ti) af[ti] = lds_ld16(s, swz(arow + ti * 32, ks * 2 + kg, kStageRowBytes));
 #pragma unroll
       for (int tj = 0; tj < TJ; ++tj) bf[tj] = lds_ld16(s, swz(brow + tj * 32, ks * 2 + kg, kStageRowBytes));
     };
+    auto mma = [&](const u32x4 (&af)[TI], const u32x4 (&bf)[TJ]) {
+#pragma unroll
+      for (int ti = 0; ti < TI; ++ti)
+#pragma unroll
+        for (int tj = 0; tj < TJ; ++tj) acc[ti][tj] = Traits<T>::mfma(af[ti], bf[tj], acc[ti][tj]);
+    };
+    static_assert(kStageRowBytes / 32 == 4, "the pipeline below is written for 4 steps per K tile");
+    constexpr int MF = TI * TJ * Traits<T>::kInstrPerStep;  // MFMA instructions per step
+    constexpr int NR = TI + TJ;                             // fragment reads per step
 
     gload(0);
-    sstore(0);
+    sstore(smem);
     __syncthreads();
-
-    constexpr int KS = kStageRowBytes / 32;  // 32-byte K steps per stage
+    u32x4 fa0[TI], fb0[TJ], fa1[TI], fb1[TJ];
+    frags(smem, 0, fa0, fb0);
     for (int kt = 0; kt < KT; ++kt) {
-      if (kt + 1 < KT) gload(kt + 1);
       const char* s = smem + (kt & 1) * STAGE_BYTES;
-      // Fragments of step ks+1 are read from LDS while the MFMAs of step ks run.
-      u32x4 af[2][TI], bf[2][TJ];
-      frags(s, 0, af[0], bf[0]);
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        if (ks + 1 < KS) frags(s, ks + 1, af[(ks + 1) & 1], bf[(ks + 1) & 1]);
-#pragma unroll
-        for (int ti = 0; ti < TI; ++ti)
-#pragma unroll
-          for (int tj = 0; tj < TJ; ++tj) acc[ti][tj] = Traits<T>::mfma(af[ks & 1][ti], bf[ks & 1][tj], acc[ti][tj]);
-      }
-      if (kt + 1 < KT) sstore((kt + 1) & 1);
+      char* sn = smem + ((kt + 1) & 1) * STAGE_BYTES;
+      gload(kt + 1 < KT ? kt + 1 : KT - 1);
+      frags(s, 1, fa1, fb1);
+      mma(fa0, fb0);
+      sched_interleave<0, MF, NR, LOADS, 0>();
+      frags(s, 2, fa0, fb0);
+      mma(fa1, fb1);
+      sched_interleave<0, MF, NR, 0, 0>();
+      frags(s, 3, fa1, fb1);
+      mma(fa0, fb0);
+      sstore(sn);
+      sched_interleave<0, MF, NR, 0, LOADS>();
+      __builtin_amdgcn_sched_barrier(0);  // keep every step-2 MFMA ahead of the barrier
       __syncthreads();
+      __builtin_amdgcn_sched_barrier(0);
+      frags(sn, 0, fa0, fb0);
+      mma(fa1, fb1);
+      sched_interleave<0, MF, NR, 0, 0>();
     }
+    __syncthreads();
   }
 };
 
