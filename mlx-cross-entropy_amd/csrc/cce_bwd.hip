@@ -255,7 +255,7 @@ __device__ __forceinline__ void store_w_vocab_major(char* wsm, const f32x16 (&w)
 template <typename T, bool HAS_BIAS, bool WANT_DE, bool WANT_DC, bool WANT_DB>
 __global__ __launch_bounds__(kThreads, 1) void bwd_tile_kernel(BwdArgs a, int nrb) {
   using Loop = NTMainLoop<T, kBwdVocab, kBwdTokens, 2, 2>;  // A = C rows (vocab), B = E rows (tokens)
-  constexpr uint32_t STAGE = 2 * Loop::STAGE_BYTES;          // 64 KiB, reused by pass 2
+  constexpr uint32_t STAGE = Loop::SMEM_BYTES;               // 64 KiB, reused by pass 2
   constexpr uint32_t W_BYTES = 128 * 128 * sizeof(T);
   static_assert(2 * Pass2<T>::CHUNK_BYTES <= STAGE, "pass-2 chunks alias the pass-1 stages");
   __shared__ __attribute__((aligned(16))) char smem[STAGE + W_BYTES];

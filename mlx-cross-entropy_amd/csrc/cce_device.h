@@ -26,7 +26,6 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
 constexpr int kThreads = 256;      // 4 waves of 64
-constexpr int kStageRowBytes = 128; // bytes of the contraction dim staged per row per K tile
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 
@@ -120,104 +119,134 @@ __device__ __forceinline__ f32x16 zero16() {
 }
 
 // --------------------------------------------------------------- main loop
-// acc[TI][TJ] = A_blk . B_blk^T over the full contraction length Kbytes, where
+// Stage geometry: every stage holds one 64-byte slice of the contraction dim for
+// all ROWS_A + ROWS_B rows; a row slice is four 16-byte chunks stored in the order
+// chunk ^ f(row), f(row) = ((row >> 1) ^ (row >> 3)) & 3.  With that order the
+// 8 (or 16) consecutive rows an MFMA fragment read touches fall on distinct LDS
+// bank groups, and each global_load_lds_dwordx4 (64 lanes x 16 bytes written
+// contiguously) fills 16 whole rows.
+constexpr int kSliceBytes = 64;
+constexpr int kStages = 4;
+
+__device__ __forceinline__ uint32_t slice_off(uint32_t row, uint32_t chunk) {
+  return row * kSliceBytes + ((chunk ^ (((row >> 1) ^ (row >> 3)) & 3u)) << 4);
+}
+
+// Source of the zeros that pad a ragged last slice (contraction length not a
+// multiple of 64 bytes): lanes whose chunk lies past the row end read these 16 bytes.
+__device__ __attribute__((aligned(16))) static const uint32_t g_zero16[4] = {0u, 0u, 0u, 0u};
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  // gfx9 s_waitcnt: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14]
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// Workgroup barrier for the LDS pipeline: waits until at most N of this wave's
+// LDS-DMA loads are in flight and all its LDS reads have returned, then
+// s_barrier.  Unlike __syncthreads() it does not drain every outstanding load
+// (the workgroup release fence would wait for vmcnt(0)), so later stages keep
+// streaming in across the barrier.  The empty asm statements stop the compiler
+// from moving memory operations across it.
+template <int N>
+__device__ __forceinline__ void stage_barrier() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (0 << 8) | ((N >> 4) << 14));
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// acc[TI][TJ] = A_blk . B_blk^T over the full contraction length kbytes, where
 // A_blk = rows [a_row0, a_row0 + ROWS_A) of A (row pitch `pitch` bytes, rows past
 // a_rows-1 clamped to the last row) and B_blk likewise.  Waves are arranged
 // WA x WB; wave (wa, wb) owns A rows [wa*ROWS_A/WA, ...) and B rows
-// [wb*ROWS_B/WB, ...).  smem holds two stages of (ROWS_A + ROWS_B) x 128 bytes.
+// [wb*ROWS_B/WB, ...).  smem holds kStages stages of (ROWS_A + ROWS_B) x 64 bytes.
 // Ends with a barrier, so the caller may reuse smem immediately.
 template <typename T, int ROWS_A, int ROWS_B, int WA, int WB>
 struct NTMainLoop {
   static constexpr int TI = ROWS_A / WA / 32;
   static constexpr int TJ = ROWS_B / WB / 32;
   static constexpr int ROWS = ROWS_A + ROWS_B;
-  static constexpr int LOADS = ROWS * (kStageRowBytes / 16) / kThreads;  // 16-byte loads per thread
-  static constexpr int LA = ROWS_A / 32;
-  static constexpr uint32_t STAGE_BYTES = ROWS * kStageRowBytes;
-  static_assert(LOADS * kThreads == ROWS * 8, "stage must split evenly over the workgroup");
-  static_assert(LA * 32 == ROWS_A && (ROWS_B % 32) == 0, "rows must be multiples of 32");
+  static constexpr int LPW = ROWS / 16 / (kThreads / 64);  // 16-row LDS loads per wave per stage
+  static constexpr uint32_t STAGE_BYTES = ROWS * kSliceBytes;
+  static constexpr uint32_t SMEM_BYTES = kStages * STAGE_BYTES;
+  static_assert(LPW * 16 * (kThreads / 64) == ROWS, "stage must split evenly over the waves");
+  static_assert(ROWS_A % 32 == 0 && ROWS_B % 32 == 0, "rows must be multiples of 32");
 
   static __device__ __forceinline__ void run(const char* __restrict__ A, int64_t a_rows, int64_t a_row0,
                                              const char* __restrict__ B, int64_t b_rows, int64_t b_row0,
                                              int64_t pitch, int64_t kbytes, char* smem,
                                              f32x16 (&acc)[TI][TJ]) {
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
     const int wa = wave % WA;
     const int wb = wave / WA;
-    const int q = tid & 7;    // 16-byte chunk within the 128-byte row slice
-    const int rr = tid >> 3;  // 0..31
 
-    // Per-load row byte offsets relative to the block base (rows clamped).
-    const char* abase = A + a_row0 * pitch;
-    const char* bbase = B + b_row0 * pitch;
-    uint32_t off[LOADS];
+    // Load j of this wave fills rows [r0, r0 + 16) of a stage, r0 = (wave*LPW + j)*16;
+    // lane l writes row r0 + l/4, stored chunk l%4, i.e. logical chunk (l%4) ^ f(row).
+    const char* base[LPW];
+    uint32_t off[LPW];
+    uint32_t lds_row0[LPW];
 #pragma unroll
-    for (int i = 0; i < LOADS; ++i) {
-      const int row = rr + 32 * i;
-      if (i < LA) {
+    for (int j = 0; j < LPW; ++j) {
+      const int r0 = (wave * LPW + j) * 16;
+      const int row = r0 + (lane >> 2);
+      const uint32_t q = (uint32_t)(lane & 3) ^ ((((uint32_t)row >> 1) ^ ((uint32_t)row >> 3)) & 3u);
+      lds_row0[j] = (uint32_t)r0 * kSliceBytes;
+      if (row < ROWS_A) {
         int64_t g = a_row0 + row;
         g = g < a_rows ? g : a_rows - 1;
-        off[i] = (uint32_t)((g - a_row0) * pitch) + q * 16;
+        base[j] = A + g * pitch;
       } else {
         int64_t g = b_row0 + (row - ROWS_A);
         g = g < b_rows ? g : b_rows - 1;
-        off[i] = (uint32_t)((g - b_row0) * pitch) + q * 16;
+        base[j] = B + g * pitch;
       }
+      off[j] = q * 16;
     }
-
-    const int KT = (int)((kbytes + kStageRowBytes - 1) / kStageRowBytes);
+    const int KT = (int)((kbytes + kSliceBytes - 1) / kSliceBytes);
     const int arow = wa * (ROWS_A / WA) + (lane & 31);
     const int brow = ROWS_A + wb * (ROWS_B / WB) + (lane & 31);
     const int kg = lane >> 5;
-    // A ragged contraction length (D*sizeof(T) not a multiple of 128) only changes
-    // the loads of the last K tile; resolve it once, outside the pipelined loop.
-    if (kbytes % kStageRowBytes == 0) {
-      loop<false>(abase, bbase, off, kbytes, KT, smem, arow, brow, kg, q, rr, acc);
+    if (kbytes % kSliceBytes == 0) {
+      loop<false>(base, off, lds_row0, kbytes, KT, smem, arow, brow, kg, acc);
     } else {
-      loop<true>(abase, bbase, off, kbytes, KT, smem, arow, brow, kg, q, rr, acc);
+      loop<true>(base, off, lds_row0, kbytes, KT, smem, arow, brow, kg, acc);
     }
   }
 
-  // One K tile = 4 MFMA steps of 32 bytes.  Software pipeline (one barrier per tile):
-  //   step 0: issue the global loads of tile kt+1, read fragments of step 1
-  //   step 1: read fragments of step 2
-  //   step 2: read fragments of step 3, write tile kt+1 (registers -> other stage)
-  //   barrier
-  //   step 3: read fragments of step 0 of tile kt+1
-  // and every step's MFMAs are interleaved with those memory instructions so that
-  // LDS and global latency hide behind the matrix cores.  The last iteration
-  // reloads the last tile into the idle stage, which keeps the body branch-free.
+  // Iteration it consumes slice it (stage it % 4, two 32-byte MFMA steps):
+  //   issue the LDS loads of slice it+3 | read fragments of step 1 | MFMAs of step 0
+  //   wait for slice it+1 (vmcnt), barrier
+  //   read fragments of step 0 of slice it+1 | MFMAs of step 1
+  // Slices past the end are clamped to the last one (harmless reloads into idle stages).
   template <bool RAGGED>
-  static __device__ __forceinline__ void loop(const char* abase, const char* bbase, const uint32_t (&off)[LOADS],
+  static __device__ __forceinline__ void loop(const char* const (&base)[LPW], const uint32_t (&off)[LPW],
+                                              const uint32_t (&lds_row0)[LPW],
                                               int64_t kbytes, int KT, char* smem, int arow, int brow, int kg,
-                                              int q, int rr, f32x16 (&acc)[TI][TJ]) {
-    u32x4 pre[LOADS];
-    auto gload = [&](int kt) {
-      const int64_t k0 = (int64_t)kt * kStageRowBytes;
-      if constexpr (RAGGED) {
-        const bool kin = k0 + q * 16 < kbytes;
-        const int64_t kk = kin ? k0 : 0;  // out-of-range chunks re-read column 0 and are zeroed
+                                              f32x16 (&acc)[TI][TJ]) {
+    auto issue = [&](int kt) {
+      kt = kt < KT ? kt : KT - 1;
+      char* st = smem + (kt % kStages) * STAGE_BYTES;
+      const int64_t k0 = (int64_t)kt * kSliceBytes;
 #pragma unroll
-        for (int i = 0; i < LOADS; ++i) {
-          const u32x4 v = gld16((i < LA ? abase : bbase) + kk + off[i]);
-          pre[i] = kin ? v : u32x4{0u, 0u, 0u, 0u};
+      for (int j = 0; j < LPW; ++j) {
+        const char* g = base[j] + k0 + off[j];
+        if constexpr (RAGGED) {
+          if (k0 + (int64_t)off[j] >= kbytes) g = reinterpret_cast<const char*>(g_zero16);
         }
-      } else {
-#pragma unroll
-        for (int i = 0; i < LOADS; ++i) pre[i] = gld16((i < LA ? abase : bbase) + k0 + off[i]);
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(g),
+                                         (__attribute__((address_space(3))) void*)(st + lds_row0[j]),
+                                         16, 0, 0);
       }
-    };
-    auto sstore = [&](char* s) {
-#pragma unroll
-      for (int i = 0; i < LOADS; ++i) lds_st16(s, swz(rr + 32 * i, q, kStageRowBytes), pre[i]);
     };
     auto frags = [&](const char* s, int ks, u32x4 (&af)[TI], u32x4 (&bf)[TJ]) {
 #pragma unroll
-      for (int ti = 0; ti < TI; ++ti) af[ti] = lds_ld16(s, swz(arow + ti * 32, ks * 2 + kg, kStageRowBytes));
+      for (int ti = 0; ti < TI; ++ti) af[ti] = lds_ld16(s, slice_off(arow + ti * 32, ks * 2 + kg));
 #pragma unroll
-      for (int tj = 0; tj < TJ; ++tj) bf[tj] = lds_ld16(s, swz(brow + tj * 32, ks * 2 + kg, kStageRowBytes));
+      for (int tj = 0; tj < TJ; ++tj) bf[tj] = lds_ld16(s, slice_off(brow + tj * 32, ks * 2 + kg));
     };
     auto mma = [&](const u32x4 (&af)[TI], const u32x4 (&bf)[TJ]) {
 #pragma unroll
@@ -225,36 +254,31 @@ struct NTMainLoop {
 #pragma unroll
         for (int tj = 0; tj < TJ; ++tj) acc[ti][tj] = Traits<T>::mfma(af[ti], bf[tj], acc[ti][tj]);
     };
-    static_assert(kStageRowBytes / 32 == 4, "the pipeline below is written for 4 steps per K tile");
-    constexpr int MF = TI * TJ * Traits<T>::kInstrPerStep;  // MFMA instructions per step
-    constexpr int NR = TI + TJ;                             // fragment reads per step
+    static_assert(kSliceBytes / 32 == 2, "two MFMA steps per slice");
+    constexpr int MF = TI * TJ * Traits<T>::kInstrPerStep;
+    constexpr int NR = TI + TJ;
 
-    gload(0);
-    sstore(smem);
-    __syncthreads();
+    issue(0);
+    issue(1);
+    issue(2);
+    stage_barrier<2 * LPW>();
     u32x4 fa0[TI], fb0[TJ], fa1[TI], fb1[TJ];
     frags(smem, 0, fa0, fb0);
-    for (int kt = 0; kt < KT; ++kt) {
-      const char* s = smem + (kt & 1) * STAGE_BYTES;
-      char* sn = smem + ((kt + 1) & 1) * STAGE_BYTES;
-      gload(kt + 1 < KT ? kt + 1 : KT - 1);
+    for (int it = 0; it < KT; ++it) {
+      const char* s = smem + (it % kStages) * STAGE_BYTES;
+      const char* sn = smem + ((it + 1) % kStages) * STAGE_BYTES;
+      issue(it + 3);
       frags(s, 1, fa1, fb1);
       mma(fa0, fb0);
-      sched_interleave<0, MF, NR, LOADS, 0>();
-      frags(s, 2, fa0, fb0);
-      mma(fa1, fb1);
-      sched_interleave<0, MF, NR, 0, 0>();
-      frags(s, 3, fa1, fb1);
-      mma(fa0, fb0);
-      sstore(sn);
-      sched_interleave<0, MF, NR, 0, LOADS>();
-      __builtin_amdgcn_sched_barrier(0);  // keep every step-2 MFMA ahead of the barrier
-      __syncthreads();
+      sched_interleave<0, MF, NR, LPW, 0>();
+      __builtin_amdgcn_sched_barrier(0);
+      stage_barrier<2 * LPW>();  // slice it+1 has landed in every wave's share of the stage
       __builtin_amdgcn_sched_barrier(0);
       frags(sn, 0, fa0, fb0);
       mma(fa1, fb1);
       sched_interleave<0, MF, NR, 0, 0>();
     }
+    wait_vmcnt<0>();
     __syncthreads();
   }
 };

@@ -24,7 +24,7 @@ template <typename T, bool HAS_BIAS>
 __global__ __launch_bounds__(kThreads, 1) void fwd_tile_kernel(FwdArgs a, int n_tok_blocks, int n_voc_blocks,
                                                                int grid_padded, int nvt) {
   using Loop = NTMainLoop<T, kFwdVocab, kFwdTokens, 2, 2>;  // A = C rows (vocab), B = E rows (tokens)
-  __shared__ __attribute__((aligned(16))) char smem[2 * Loop::STAGE_BYTES];
+  __shared__ __attribute__((aligned(16))) char smem[Loop::SMEM_BYTES];
 
   // Tile order: workgroups are dealt round-robin to the 8 XCDs, so first make
   // each XCD walk a contiguous range of logical tiles, then walk that range in
