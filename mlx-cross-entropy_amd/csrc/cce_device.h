@@ -119,21 +119,34 @@ __device__ __forceinline__ f32x16 zero16() {
 }
 
 // --------------------------------------------------------------- main loop
-// Stage geometry: every stage holds one 64-byte slice of the contraction dim for
-// all ROWS_A + ROWS_B rows; a row slice is four 16-byte chunks stored in the order
-// chunk ^ f(row), f(row) = ((row >> 1) ^ (row >> 3)) & 3.  With that order the
-// 8 (or 16) consecutive rows an MFMA fragment read touches fall on distinct LDS
-// bank groups, and each global_load_lds_dwordx4 (64 lanes x 16 bytes written
-// contiguously) fills 16 whole rows.
-constexpr int kSliceBytes = 64;
-constexpr int kStages = 4;
+// Stage geometry: every stage holds one kSliceBytes slice of the contraction
+// dim for all ROWS_A + ROWS_B rows, as 16-byte chunks stored in the order
+// chunk ^ f(row).  Measured on gfx950 with the MFMA fragment pattern (lane l
+// reads row l%32, chunk 2s + l/32), both orders below are free of LDS bank
+// conflicts (unswizzled 64-byte rows conflict 75% of the time).  One
+// global_load_lds_dwordx4 (64 lanes x 16 bytes, written contiguously) fills
+// 1024 / kSliceBytes whole rows, each lane group covering one row's slice with
+// a single kSliceBytes-wide request.
+#ifndef CCE_SLICE_BYTES
+#define CCE_SLICE_BYTES 128
+#endif
+#ifndef CCE_STAGES
+#define CCE_STAGES 2
+#endif
+constexpr int kSliceBytes = CCE_SLICE_BYTES;
+constexpr int kStages = CCE_STAGES;
+constexpr int kChunks = kSliceBytes / 16;
+static_assert(kSliceBytes == 64 || kSliceBytes == 128, "slice of 64 or 128 bytes");
 
+__device__ __forceinline__ uint32_t slice_swz(uint32_t row) {
+  return kSliceBytes == 128 ? ((row ^ (row >> 3)) & 7u) : ((row >> 2) & 3u);
+}
 __device__ __forceinline__ uint32_t slice_off(uint32_t row, uint32_t chunk) {
-  return row * kSliceBytes + ((chunk ^ (((row >> 1) ^ (row >> 3)) & 3u)) << 4);
+  return row * kSliceBytes + ((chunk ^ slice_swz(row)) << 4);
 }
 
 // Source of the zeros that pad a ragged last slice (contraction length not a
-// multiple of 64 bytes): lanes whose chunk lies past the row end read these 16 bytes.
+// multiple of the slice): lanes whose chunk lies past the row end read these 16 bytes.
 __device__ __attribute__((aligned(16))) static const uint32_t g_zero16[4] = {0u, 0u, 0u, 0u};
 
 template <int N>
@@ -162,18 +175,21 @@ __device__ __forceinline__ void stage_barrier() {
 // A_blk = rows [a_row0, a_row0 + ROWS_A) of A (row pitch `pitch` bytes, rows past
 // a_rows-1 clamped to the last row) and B_blk likewise.  Waves are arranged
 // WA x WB; wave (wa, wb) owns A rows [wa*ROWS_A/WA, ...) and B rows
-// [wb*ROWS_B/WB, ...).  smem holds kStages stages of (ROWS_A + ROWS_B) x 64 bytes.
+// [wb*ROWS_B/WB, ...).  smem holds kStages stages of (ROWS_A + ROWS_B) x kSliceBytes.
 // Ends with a barrier, so the caller may reuse smem immediately.
 template <typename T, int ROWS_A, int ROWS_B, int WA, int WB>
 struct NTMainLoop {
   static constexpr int TI = ROWS_A / WA / 32;
   static constexpr int TJ = ROWS_B / WB / 32;
   static constexpr int ROWS = ROWS_A + ROWS_B;
-  static constexpr int LPW = ROWS / 16 / (kThreads / 64);  // 16-row LDS loads per wave per stage
+  static constexpr int RPL = 1024 / kSliceBytes;                 // rows filled by one LDS-DMA load
+  static constexpr int LPW = ROWS / RPL / (kThreads / 64);       // LDS-DMA loads per wave per stage
+  static constexpr int KSTEPS = kSliceBytes / 32;                // 32-byte MFMA steps per slice
   static constexpr uint32_t STAGE_BYTES = ROWS * kSliceBytes;
   static constexpr uint32_t SMEM_BYTES = kStages * STAGE_BYTES;
-  static_assert(LPW * 16 * (kThreads / 64) == ROWS, "stage must split evenly over the waves");
+  static_assert(LPW * RPL * (kThreads / 64) == ROWS, "stage must split evenly over the waves");
   static_assert(ROWS_A % 32 == 0 && ROWS_B % 32 == 0, "rows must be multiples of 32");
+  static_assert((kStages - 1) * LPW < 64, "in-flight loads must fit vmcnt");
 
   static __device__ __forceinline__ void run(const char* __restrict__ A, int64_t a_rows, int64_t a_row0,
                                              const char* __restrict__ B, int64_t b_rows, int64_t b_row0,
@@ -184,16 +200,17 @@ struct NTMainLoop {
     const int wa = wave % WA;
     const int wb = wave / WA;
 
-    // Load j of this wave fills rows [r0, r0 + 16) of a stage, r0 = (wave*LPW + j)*16;
-    // lane l writes row r0 + l/4, stored chunk l%4, i.e. logical chunk (l%4) ^ f(row).
+    // Load j of this wave fills rows [r0, r0 + RPL) of a stage, r0 = (wave*LPW + j)*RPL;
+    // lane l writes row r0 + l/kChunks, stored chunk l%kChunks, i.e. logical chunk
+    // (l%kChunks) ^ f(row).
     const char* base[LPW];
     uint32_t off[LPW];
     uint32_t lds_row0[LPW];
 #pragma unroll
     for (int j = 0; j < LPW; ++j) {
-      const int r0 = (wave * LPW + j) * 16;
-      const int row = r0 + (lane >> 2);
-      const uint32_t q = (uint32_t)(lane & 3) ^ ((((uint32_t)row >> 1) ^ ((uint32_t)row >> 3)) & 3u);
+      const int r0 = (wave * LPW + j) * RPL;
+      const int row = r0 + lane / kChunks;
+      const uint32_t q = (uint32_t)(lane % kChunks) ^ slice_swz((uint32_t)row);
       lds_row0[j] = (uint32_t)r0 * kSliceBytes;
       if (row < ROWS_A) {
         int64_t g = a_row0 + row;
@@ -217,16 +234,16 @@ struct NTMainLoop {
     }
   }
 
-  // Iteration it consumes slice it (stage it % 4, two 32-byte MFMA steps):
-  //   issue the LDS loads of slice it+3 | read fragments of step 1 | MFMAs of step 0
+  // Iteration it consumes slice it (stage it % kStages, KSTEPS MFMA steps):
+  //   issue the LDS-DMA loads of slice it + kStages - 1 (into the stage freed by
+  //   the previous iteration) | step s: read fragments of step s+1, MFMAs of step s
   //   wait for slice it+1 (vmcnt), barrier
-  //   read fragments of step 0 of slice it+1 | MFMAs of step 1
+  //   read fragments of step 0 of slice it+1 | MFMAs of the last step
   // Slices past the end are clamped to the last one (harmless reloads into idle stages).
   template <bool RAGGED>
   static __device__ __forceinline__ void loop(const char* const (&base)[LPW], const uint32_t (&off)[LPW],
-                                              const uint32_t (&lds_row0)[LPW],
-                                              int64_t kbytes, int KT, char* smem, int arow, int brow, int kg,
-                                              f32x16 (&acc)[TI][TJ]) {
+                                              const uint32_t (&lds_row0)[LPW], int64_t kbytes, int KT, char* smem,
+                                              int arow, int brow, int kg, f32x16 (&acc)[TI][TJ]) {
     auto issue = [&](int kt) {
       kt = kt < KT ? kt : KT - 1;
       char* st = smem + (kt % kStages) * STAGE_BYTES;
@@ -238,8 +255,7 @@ struct NTMainLoop {
           if (k0 + (int64_t)off[j] >= kbytes) g = reinterpret_cast<const char*>(g_zero16);
         }
         __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(g),
-                                         (__attribute__((address_space(3))) void*)(st + lds_row0[j]),
-                                         16, 0, 0);
+                                         (__attribute__((address_space(3))) void*)(st + lds_row0[j]), 16, 0, 0);
       }
     };
     auto frags = [&](const char* s, int ks, u32x4 (&af)[TI], u32x4 (&bf)[TJ]) {
@@ -254,25 +270,37 @@ struct NTMainLoop {
 #pragma unroll
         for (int tj = 0; tj < TJ; ++tj) acc[ti][tj] = Traits<T>::mfma(af[ti], bf[tj], acc[ti][tj]);
     };
-    static_assert(kSliceBytes / 32 == 2, "two MFMA steps per slice");
+    static_assert(KSTEPS % 2 == 0, "fragments alternate between two register sets");
     constexpr int MF = TI * TJ * Traits<T>::kInstrPerStep;
     constexpr int NR = TI + TJ;
+    constexpr int INFLIGHT = (kStages - 2) * LPW;  // loads allowed in flight at the barrier
 
-    issue(0);
-    issue(1);
-    issue(2);
-    stage_barrier<2 * LPW>();
+#pragma unroll
+    for (int p = 0; p < kStages - 1; ++p) issue(p);
+    stage_barrier<INFLIGHT>();
     u32x4 fa0[TI], fb0[TJ], fa1[TI], fb1[TJ];
     frags(smem, 0, fa0, fb0);
     for (int it = 0; it < KT; ++it) {
       const char* s = smem + (it % kStages) * STAGE_BYTES;
       const char* sn = smem + ((it + 1) % kStages) * STAGE_BYTES;
-      issue(it + 3);
-      frags(s, 1, fa1, fb1);
-      mma(fa0, fb0);
-      sched_interleave<0, MF, NR, LPW, 0>();
+      issue(it + kStages - 1);
+#pragma unroll
+      for (int ks = 0; ks + 1 < KSTEPS; ks += 2) {
+        frags(s, ks + 1, fa1, fb1);
+        mma(fa0, fb0);
+        if (ks == 0) {
+          sched_interleave<0, MF, NR, LPW, 0>();
+        } else {
+          sched_interleave<0, MF, NR, 0, 0>();
+        }
+        if (ks + 2 < KSTEPS) {
+          frags(s, ks + 2, fa0, fb0);
+          mma(fa1, fb1);
+          sched_interleave<0, MF, NR, 0, 0>();
+        }
+      }
       __builtin_amdgcn_sched_barrier(0);
-      stage_barrier<2 * LPW>();  // slice it+1 has landed in every wave's share of the stage
+      stage_barrier<INFLIGHT>();  // slice it+1 has landed in every wave's share of its stage
       __builtin_amdgcn_sched_barrier(0);
       frags(sn, 0, fa0, fb0);
       mma(fa1, fb1);
