@@ -83,32 +83,6 @@ int check_common(const char* fn, int dtype, const void* e, const void* c, const 
   return CCE_OK;
 }
 
-struct WsLayout {
-  size_t de, dc, db, acc_end, flags, list, count, total;
-};
-
-WsLayout ws_layout(int64_t N, int64_t D, int64_t V, bool want_de, bool want_dc, bool want_db) {
-  WsLayout L{};
-  const size_t nvt = (size_t)((V + cce::kBwdVocab - 1) / cce::kBwdVocab);
-  const size_t nrb = (size_t)((N + cce::kBwdTokens - 1) / cce::kBwdTokens);
-  size_t off = 0;
-  L.de = off;
-  if (want_de) off += align256((size_t)N * (size_t)D * 4);
-  L.dc = off;
-  if (want_dc) off += align256((size_t)V * (size_t)D * 4);
-  L.db = off;
-  if (want_db) off += align256((size_t)V * 4);
-  L.acc_end = off;
-  L.flags = off;
-  off += align256(nvt * nrb);
-  L.list = off;
-  off += align256(nvt * nrb * 4);
-  L.count = off;
-  off += 256;
-  L.total = off;
-  return L;
-}
-
 }  // namespace
 
 extern "C" {
@@ -163,9 +137,9 @@ int cce_forward(int dtype, const void* e, const void* c, const void* bias, const
 
 size_t cce_backward_workspace_size(int dtype, int64_t N, int64_t D, int64_t V, int want_dE, int want_dC,
                                    int want_dBias) {
-  (void)dtype;
   if (N <= 0 || D <= 0 || V <= 0) return 0;
-  return ws_layout(N, D, V, want_dE != 0, want_dC != 0, want_dBias != 0).total;
+  if (dtype != CCE_DTYPE_F32 && dtype != CCE_DTYPE_F16 && dtype != CCE_DTYPE_BF16) return 0;
+  return cce::make_bwd_plan(elem_size(dtype), N, D, V, want_dE != 0, want_dC != 0, want_dBias != 0).total_bytes;
 }
 
 int cce_backward(int dtype, const void* e, const void* c, const void* bias, const int64_t* targets,
@@ -185,9 +159,9 @@ int cce_backward(int dtype, const void* e, const void* c, const void* bias, cons
     return fail(CCE_ERR_INVALID_ARGUMENT, "[cce_backward] gradient outputs must be 16-byte aligned");
   if (std::isnan(filter_log_eps))
     return fail(CCE_ERR_INVALID_ARGUMENT, "[cce_backward] filter_log_eps must not be NaN");
-  const WsLayout L = ws_layout(N, D, V, dE != nullptr, dC != nullptr, dBias != nullptr);
-  if (!workspace || workspace_bytes < L.total)
-    return fail(CCE_ERR_WORKSPACE, "[cce_backward] workspace of %zu bytes required, %zu given", L.total,
+  const cce::BwdPlan P = cce::make_bwd_plan(elem_size(dtype), N, D, V, dE != nullptr, dC != nullptr, dBias != nullptr);
+  if (!workspace || workspace_bytes < P.total_bytes)
+    return fail(CCE_ERR_WORKSPACE, "[cce_backward] workspace of %zu bytes required, %zu given", P.total_bytes,
                 workspace ? workspace_bytes : (size_t)0);
   if (!aligned(workspace, 256))
     return fail(CCE_ERR_WORKSPACE, "[cce_backward] workspace must be 256-byte aligned");
@@ -210,20 +184,26 @@ int cce_backward(int dtype, const void* e, const void* c, const void* bias, cons
   a.tile_max = tile_max;
   a.d_nll = d_nll;
   a.filter_log_eps = filter_log_eps;
-  a.dE_acc = dE ? reinterpret_cast<float*>(ws + L.de) : nullptr;
-  a.dC_acc = dC ? reinterpret_cast<float*>(ws + L.dc) : nullptr;
-  a.dBias_acc = dBias ? reinterpret_cast<float*>(ws + L.db) : nullptr;
-  a.flags = reinterpret_cast<uint8_t*>(ws + L.flags);
-  a.list = reinterpret_cast<int*>(ws + L.list);
-  a.count = reinterpret_cast<int*>(ws + L.count);
+  a.dE = dE;
+  a.dC = dC;
+  a.dBias = dBias;
+  a.flags = reinterpret_cast<uint8_t*>(ws + P.flags);
+  a.slot_map = reinterpret_cast<int*>(ws + P.slot_map);
+  a.list = reinterpret_cast<int*>(ws + P.list);
+  a.vt_start = reinterpret_cast<int*>(ws + P.vt_start);
+  a.rb_list = reinterpret_cast<int*>(ws + P.rb_list);
+  a.rb_start = reinterpret_cast<int*>(ws + P.rb_start);
+  a.chunk_vt = reinterpret_cast<int*>(ws + P.chunk_vt);
+  a.chunk_slot = reinterpret_cast<int*>(ws + P.chunk_slot);
+  a.w_tok = dE ? ws + P.w_tok : nullptr;
+  a.w_voc = dC ? ws + P.w_voc : nullptr;
+  a.colsum = dBias ? reinterpret_cast<float*>(ws + P.colsum) : nullptr;
+  a.de_acc = (dE && P.max_chunks > 1) ? reinterpret_cast<float*>(ws + P.de_acc) : nullptr;
   a.tile_stats = tile_stats;
+  a.plan = P;
   a.num_cus = cus;
 
-  hipError_t err = cce::launch_fill_zero(ws, L.acc_end, s);
-  if (err == hipSuccess) err = cce::launch_backward(dtype, a, s);
-  if (err == hipSuccess && dE) err = cce::launch_cast(dtype, a.dE_acc, dE, N * D, s);
-  if (err == hipSuccess && dC) err = cce::launch_cast(dtype, a.dC_acc, dC, V * D, s);
-  if (err == hipSuccess && dBias) err = cce::launch_cast(dtype, a.dBias_acc, dBias, V, s);
+  const hipError_t err = cce::launch_backward(dtype, a, s);
   if (err != hipSuccess)
     return fail(CCE_ERR_LAUNCH, "[cce_backward] kernel launch failed: %s", hipGetErrorString(err));
   return CCE_OK;

@@ -3,30 +3,42 @@
 //   G[r, v] = d_nll[r] * (softmax_v(E_r . C^T + b) - [v == t_r])
 //   dE = G . C      dC = G^T . E      dBias = sum_r G[r, :]
 //
-// Pipeline (all on the caller's stream):
-//   1. bwd_filter_kernel  — one wave per (vocab tile, token block): keep the
-//      128x128 tile iff some row with d_nll != 0 has its target in the tile or
-//      tile_max - lse >= filter_log_eps.
-//      Reference predicate: csrc/cce/cce.metal:191-204 (32x32 granularity there).
-//   2. bwd_compact_kernel — ordered compaction of the kept tiles (vocab-tile
-//      major, so consecutive work items share C rows).
-//   3. bwd_tile_kernel    — persistent; per kept tile: recompute the logits on
-//      MFMA, form W = G tile in fp32 registers, then stream D in 256-byte chunks
-//      through LDS (transposed on the way in) for dE_tile = W . C_blk and
-//      dC_tile = W^T . E_blk on MFMA, each flushed with fp32 atomics.  dBias is a
-//      column sum of W.  No [N, tiles, D] scratch exists.
-//      Reference: cce.metal:146-326 (cce_backward) and the full-gradient spec
-//      reference/_fused_backward.py:1406-1587 (dC :1535-1545, dBias :1546-1553).
-//   4. cast_kernel        — fp32 accumulators -> output dtype
-//      (reference: astype in cce.cpp:178,442-446 / _fused_backward.py:1652-1654).
+// Reference: csrc/cce/cce.metal:146-326 (cce_backward: filter :191-204, weight
+// w = d_nll exp(S + b - lse) - d_nll [v == t] :279-280) and the full-gradient
+// research kernel reference/_fused_backward.py:1406-1587 (dC :1535-1545,
+// dBias :1546-1553), which accumulate per-tile partials with fp32 atomics.
+//
+// On MI355X fp32 global atomics retire at ~2.9e11 per second (one per memory
+// channel per clock) — 2.5e9 of them (the per-tile partial flushes at the
+// Llama-3.1-8B head) cost ~8 ms — so this backward gives every output element
+// exactly one writer instead, and never materialises a [N, tiles, D] scratch:
+//
+//   1. bwd_filter_kernel     one wave per (vocab tile, token block): keep the
+//                            128 x 128 tile iff a row with d_nll != 0 has its
+//                            target in it or tile_max - lse >= filter_log_eps.
+//   2. bwd_compact_vt_kernel kept pairs -> slots in vocab-major order; chunk plan.
+//   3. bwd_compact_rb_kernel the same slots ordered by token block.
+//   per chunk of at most `cap` slots (chunk boundaries between vocab tiles):
+//   4. bwd_g_kernel          recompute the logit tile on MFMA, form G, store it in
+//                            the chunk's scratch (bf16/fp16/fp32, token-major and
+//                            vocab-major) plus its fp32 column sums.
+//   5. bwd_de_kernel         one workgroup per (token block, 256-byte D slice):
+//                            dE = sum over the block's kept tiles of G_j . C_j.
+//   6. bwd_dc_kernel         one workgroup per (vocab tile, D slice):
+//                            dC = sum over the tile's kept blocks of G_j^T . E_j,
+//                            dBias from the column sums; written in the output dtype.
+//   7. dE_cast_kernel        only when there is more than one chunk (fp32 -> dtype).
 #include "cce_device.h"
 #include "cce_launch.h"
 
 namespace cce {
 
 static_assert(kStatTile == kBwdVocab, "filter statistics are kept per backward vocabulary tile");
+static_assert(kBwdTokens == 128 && kBwdVocab == 128, "the G-tile kernels assume 128 x 128 tiles");
 
-__global__ __launch_bounds__(256) void bwd_filter_kernel(BwdArgs a, int nvt, int nrb) {
+// ---------------------------------------------------------------- 1. filter
+__global__ __launch_bounds__(256) void bwd_filter_kernel(BwdArgs a) {
+  const int nvt = (int)a.plan.nvt, nrb = (int)a.plan.nrb;
   const int lane = threadIdx.x & 63;
   const int pair = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (pair >= nvt * nrb) return;  // uniform per wave
@@ -52,160 +64,106 @@ __global__ __launch_bounds__(256) void bwd_filter_kernel(BwdArgs a, int nvt, int
   if (lane == 0) a.flags[pair] = any ? 1 : 0;
 }
 
-__global__ __launch_bounds__(1024) void bwd_compact_kernel(BwdArgs a, int total) {
+// Inclusive prefix sum over 1024 threads (one value each), in LDS.
+__device__ __forceinline__ int block_scan_1024(int v, int* scan) {
+  const int tid = threadIdx.x;
+  scan[tid] = v;
+  __syncthreads();
+  for (int o = 1; o < 1024; o <<= 1) {
+    const int add = tid >= o ? scan[tid - o] : 0;
+    __syncthreads();
+    scan[tid] += add;
+    __syncthreads();
+  }
+  return scan[tid];
+}
+
+// ---------------------------------------------------------------- 2. compaction, vocab-major
+// Thread t owns a contiguous range of pair indices (vt * nrb + rb).  Writes
+// list / slot_map / vt_start, the tile statistics, and the chunk plan: vocab
+// tile vt belongs to chunk vt_start[vt] / step, step = cap - nrb + 1.
+__global__ __launch_bounds__(1024) void bwd_compact_vt_kernel(BwdArgs a) {
   __shared__ int scan[1024];
+  const int total = (int)a.plan.total, nrb = (int)a.plan.nrb, nvt = (int)a.plan.nvt;
   const int tid = threadIdx.x;
   const int per = (total + 1023) / 1024;
   const int beg = min(tid * per, total);
   const int end = min(beg + per, total);
   int cnt = 0;
   for (int i = beg; i < end; ++i) cnt += a.flags[i];
-  scan[tid] = cnt;
-  __syncthreads();
-  for (int o = 1; o < 1024; o <<= 1) {
-    const int v = tid >= o ? scan[tid - o] : 0;
-    __syncthreads();
-    scan[tid] += v;
-    __syncthreads();
+  int pos = block_scan_1024(cnt, scan) - cnt;
+  for (int i = beg; i < end; ++i) {
+    if (i % nrb == 0) a.vt_start[i / nrb] = pos;
+    if (a.flags[i]) {
+      a.list[pos] = i;
+      a.slot_map[i] = pos;
+      ++pos;
+    } else {
+      a.slot_map[i] = -1;
+    }
   }
-  int pos = scan[tid] - cnt;
-  for (int i = beg; i < end; ++i)
-    if (a.flags[i]) a.list[pos++] = i;
+  const int kept = scan[1023];
   if (tid == 1023) {
-    *a.count = scan[1023];
+    a.vt_start[nvt] = kept;
     if (a.tile_stats) {
-      a.tile_stats[0] = scan[1023];
+      a.tile_stats[0] = kept;
       a.tile_stats[1] = total;
+    }
+  }
+  __threadfence_block();
+  __syncthreads();
+  const int step = (int)(a.plan.cap - a.plan.nrb + 1);
+  const int maxc = (int)a.plan.max_chunks;
+  for (int vt = tid; vt <= nvt; vt += 1024) {
+    // chunk c starts at the first vocab tile whose first slot reaches c * step
+    const int c = vt < nvt ? min(a.vt_start[vt] / step, maxc - 1) : maxc;
+    const int prev = vt == 0 ? -1 : min(a.vt_start[vt - 1] / step, maxc - 1);
+    const int first_slot = vt < nvt ? a.vt_start[vt] : kept;
+    for (int cc = prev + 1; cc <= c; ++cc) {
+      a.chunk_vt[cc] = vt;
+      a.chunk_slot[cc] = first_slot;
     }
   }
 }
 
-// ------------------------------------------------------------------ pass 2
-// out[out_row0 + m, d] += sum_k W[m, k] * SRC[src_row0 + k, d]   for m, k in [0, 128)
-// W sits in LDS (wsm) as 128 rows of 128 elements (row-major, k contiguous).
-// SRC rows are streamed in chunks of 256 bytes of D, transposed into LDS
-// ([d][k], k contiguous) so both MFMA operands are k-contiguous fragments.
+// ---------------------------------------------------------------- 3. compaction, block-major
+__global__ __launch_bounds__(1024) void bwd_compact_rb_kernel(BwdArgs a) {
+  __shared__ int scan[1024];
+  const int total = (int)a.plan.total, nrb = (int)a.plan.nrb, nvt = (int)a.plan.nvt;
+  const int tid = threadIdx.x;
+  const int per = (total + 1023) / 1024;
+  const int beg = min(tid * per, total);
+  const int end = min(beg + per, total);
+  int cnt = 0;
+  for (int j = beg; j < end; ++j) {
+    const int rb = j / nvt, vt = j - rb * nvt;
+    cnt += a.flags[vt * nrb + rb];
+  }
+  int pos = block_scan_1024(cnt, scan) - cnt;
+  for (int j = beg; j < end; ++j) {
+    const int rb = j / nvt, vt = j - rb * nvt;
+    if (vt == 0) a.rb_start[rb] = pos;
+    if (a.flags[vt * nrb + rb]) a.rb_list[pos++] = a.slot_map[vt * nrb + rb];
+  }
+  if (tid == 1023) a.rb_start[nrb] = scan[1023];
+}
+
+// ---------------------------------------------------------------- LDS tiles of G
+// A G tile in LDS: 128 rows x 128 elements, row-major, 16-byte chunks swizzled by swz().
 template <typename T>
-struct Pass2 {
-  static constexpr int EPC = 16 / sizeof(T);           // elements per 16-byte fragment
-  static constexpr int DK = 256 / sizeof(T);           // D elements per chunk
-  static constexpr uint32_t ROW_BYTES = 128 * sizeof(T);  // one row of W or of the transposed chunk
-  static constexpr uint32_t CHUNK_BYTES = DK * ROW_BYTES;  // 32 KiB for every dtype
-  static constexpr int NB = (128 / EPC) * 16 / kThreads;   // EPC x EPC transpose blocks per thread
-  static constexpr int TJ = DK / 2 / 32;                   // 32-col MFMA tiles per wave along D
-  static constexpr int KS = (int)(ROW_BYTES / 32);         // 32-byte K steps over 128 elements
-  static_assert(NB >= 1 && NB * kThreads == (128 / EPC) * 16, "transpose blocks must split evenly");
-
-  static __device__ __forceinline__ void load(u32x4 (&reg)[NB][EPC], const char* src, int64_t src_rows,
-                                              int64_t src_row0, int64_t pitch, int64_t kbytes, int c) {
-#pragma unroll
-    for (int s = 0; s < NB; ++s) {
-      const int b = threadIdx.x + kThreads * s;
-      const int dblk = b & 15;
-      const int vblk = b >> 4;
-      const int64_t col = (int64_t)c * 256 + dblk * 16;
-      const bool in = col < kbytes;
-#pragma unroll
-      for (int x = 0; x < EPC; ++x) {
-        int64_t g = src_row0 + vblk * EPC + x;
-        g = g < src_rows ? g : src_rows - 1;
-        reg[s][x] = in ? gld16(src + g * pitch + col) : u32x4{0u, 0u, 0u, 0u};
-      }
-    }
-  }
-
-  static __device__ __forceinline__ void store_transposed(const u32x4 (&reg)[NB][EPC], char* buf) {
-#pragma unroll
-    for (int s = 0; s < NB; ++s) {
-      const int b = threadIdx.x + kThreads * s;
-      const int dblk = b & 15;
-      const int vblk = b >> 4;
-#pragma unroll
-      for (int y = 0; y < EPC; ++y) {
-        u32x4 o;
-        if constexpr (sizeof(T) == 4) {
-          o = u32x4{reg[s][0][y], reg[s][1][y], reg[s][2][y], reg[s][3][y]};
-        } else {
-          const int wd = y >> 1;
-          const bool hi = y & 1;
-#pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            const uint32_t lo_src = reg[s][2 * k][wd];
-            const uint32_t hi_src = reg[s][2 * k + 1][wd];
-            o[k] = hi ? ((lo_src >> 16) | (hi_src & 0xffff0000u)) : ((lo_src & 0xffffu) | (hi_src << 16));
-          }
-        }
-        lds_st16(buf, swz(dblk * EPC + y, vblk, ROW_BYTES), o);
-      }
-    }
-  }
-
-  static __device__ __forceinline__ void run(const char* wsm, const char* src, int64_t src_rows, int64_t src_row0,
-                                             int64_t pitch, int64_t D, float* out, int64_t out_rows,
-                                             int64_t out_row0, char* smem) {
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int wm = wave & 1;
-    const int wn = wave >> 1;
-    const int n = lane & 31;
-    const int h = lane >> 5;
-    const int kg = lane >> 5;
-    const int64_t kbytes = D * (int64_t)sizeof(T);
-    const int NC = (int)((kbytes + 255) / 256);
-
-    u32x4 reg[NB][EPC];
-    load(reg, src, src_rows, src_row0, pitch, kbytes, 0);
-    store_transposed(reg, smem);
-    __syncthreads();
-
-    for (int c = 0; c < NC; ++c) {
-      if (c + 1 < NC) load(reg, src, src_rows, src_row0, pitch, kbytes, c + 1);
-      const char* buf = smem + (c & 1) * CHUNK_BYTES;
-      f32x16 acc[2][TJ];
-#pragma unroll
-      for (int ti = 0; ti < 2; ++ti)
-#pragma unroll
-        for (int tj = 0; tj < TJ; ++tj) acc[ti][tj] = zero16();
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        u32x4 af[2], bf[TJ];
-#pragma unroll
-        for (int ti = 0; ti < 2; ++ti) af[ti] = lds_ld16(wsm, swz(wm * 64 + ti * 32 + n, ks * 2 + kg, ROW_BYTES));
-#pragma unroll
-        for (int tj = 0; tj < TJ; ++tj)
-          bf[tj] = lds_ld16(buf, swz(wn * (DK / 2) + tj * 32 + n, ks * 2 + kg, ROW_BYTES));
-#pragma unroll
-        for (int ti = 0; ti < 2; ++ti)
-#pragma unroll
-          for (int tj = 0; tj < TJ; ++tj) acc[ti][tj] = Traits<T>::mfma(af[ti], bf[tj], acc[ti][tj]);
-      }
-      if (c + 1 < NC) store_transposed(reg, smem + ((c + 1) & 1) * CHUNK_BYTES);
-      // flush: lane holds column d = c*DK + wn*DK/2 + 32 tj + n, rows 8(r/4) + 4h + r%4
-#pragma unroll
-      for (int tj = 0; tj < TJ; ++tj) {
-        const int64_t d = (int64_t)c * DK + wn * (DK / 2) + tj * 32 + n;
-        if (d < D) {
-#pragma unroll
-          for (int ti = 0; ti < 2; ++ti) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-              const int64_t row = out_row0 + wm * 64 + ti * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
-              if (row < out_rows) atomicAdd(out + row * D + d, acc[ti][tj][r]);
-            }
-          }
-        }
-      }
-      __syncthreads();
-    }
-  }
+struct GTile {
+  static constexpr uint32_t ROW_BYTES = 128 * sizeof(T);
+  static constexpr uint32_t BYTES = 128 * ROW_BYTES;
+  static constexpr int CPR = ROW_BYTES / 16;           // chunks per row
+  static constexpr int PER_THREAD = 128 * CPR / kThreads;  // 16-byte chunks per thread
 };
 
-// W (fp32, in the pass-1 accumulator layout) -> LDS as [token][vocab].
+// G (fp32 registers, pass-1 accumulator layout) -> LDS as [token][vocab].
 // acc[i][j][r]: vocab 64 wv + 32 i + 8 (r/4) + 4 h + r%4, token 64 wt + 32 j + n.
 template <typename T>
-__device__ __forceinline__ void store_w_token_major(char* wsm, const f32x16 (&w)[2][2], int wv, int wt, int n,
+__device__ __forceinline__ void store_g_token_major(char* gsm, const f32x16 (&w)[2][2], int wv, int wt, int n,
                                                     int h) {
-  constexpr uint32_t ROW_BYTES = 128 * sizeof(T);
+  constexpr uint32_t ROW_BYTES = GTile<T>::ROW_BYTES;
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int row = wt * 64 + j * 32 + n;
@@ -217,7 +175,7 @@ __device__ __forceinline__ void store_w_token_major(char* wsm, const f32x16 (&w)
         if constexpr (sizeof(T) == 4) {
           u32x4 o{__float_as_uint(w[i][j][rq * 4 + 0]), __float_as_uint(w[i][j][rq * 4 + 1]),
                   __float_as_uint(w[i][j][rq * 4 + 2]), __float_as_uint(w[i][j][rq * 4 + 3])};
-          lds_st16(wsm, swz(row, col >> 2, ROW_BYTES), o);
+          lds_st16(gsm, swz(row, col >> 2, ROW_BYTES), o);
         } else {
           T v0 = (T)w[i][j][rq * 4 + 0], v1 = (T)w[i][j][rq * 4 + 1];
           T v2 = (T)w[i][j][rq * 4 + 2], v3 = (T)w[i][j][rq * 4 + 3];
@@ -225,18 +183,18 @@ __device__ __forceinline__ void store_w_token_major(char* wsm, const f32x16 (&w)
                               ((uint32_t)__builtin_bit_cast(uint16_t, v1) << 16);
           const uint32_t p1 = (uint32_t)__builtin_bit_cast(uint16_t, v2) |
                               ((uint32_t)__builtin_bit_cast(uint16_t, v3) << 16);
-          *reinterpret_cast<u32x2*>(wsm + swz(row, col >> 3, ROW_BYTES) + (col & 7) * 2) = u32x2{p0, p1};
+          *reinterpret_cast<u32x2*>(gsm + swz(row, col >> 3, ROW_BYTES) + (col & 7) * 2) = u32x2{p0, p1};
         }
       }
     }
   }
 }
 
-// W -> LDS as [vocab][token].
+// G -> LDS as [vocab][token].
 template <typename T>
-__device__ __forceinline__ void store_w_vocab_major(char* wsm, const f32x16 (&w)[2][2], int wv, int wt, int n,
+__device__ __forceinline__ void store_g_vocab_major(char* gsm, const f32x16 (&w)[2][2], int wv, int wt, int n,
                                                     int h) {
-  constexpr uint32_t ROW_BYTES = 128 * sizeof(T);
+  constexpr uint32_t ROW_BYTES = GTile<T>::ROW_BYTES;
   constexpr int EPC = 16 / sizeof(T);
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
@@ -246,21 +204,32 @@ __device__ __forceinline__ void store_w_vocab_major(char* wsm, const f32x16 (&w)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int row = wv * 64 + i * 32 + (r >> 2) * 8 + h * 4 + (r & 3);  // vocab
-        *reinterpret_cast<T*>(wsm + swz(row, col / EPC, ROW_BYTES) + (col % EPC) * sizeof(T)) = (T)w[i][j][r];
+        *reinterpret_cast<T*>(gsm + swz(row, col / EPC, ROW_BYTES) + (col % EPC) * sizeof(T)) = (T)w[i][j][r];
       }
     }
   }
 }
 
-template <typename T, bool HAS_BIAS, bool WANT_DE, bool WANT_DC, bool WANT_DB>
-__global__ __launch_bounds__(kThreads, 1) void bwd_tile_kernel(BwdArgs a, int nrb) {
-  using Loop = NTMainLoop<T, kBwdVocab, kBwdTokens, 2, 2>;  // A = C rows (vocab), B = E rows (tokens)
-  constexpr uint32_t STAGE = Loop::SMEM_BYTES;               // 64 KiB, reused by pass 2
-  constexpr uint32_t W_BYTES = 128 * 128 * sizeof(T);
-  static_assert(2 * Pass2<T>::CHUNK_BYTES <= STAGE, "pass-2 chunks alias the pass-1 stages");
-  __shared__ __attribute__((aligned(16))) char smem[STAGE + W_BYTES];
-  char* wsm = smem + STAGE;
+// Swizzled LDS tile <-> plain row-major tile in global memory (coalesced 16-byte accesses).
+template <typename T>
+__device__ __forceinline__ void copy_lds_to_global(const char* gsm, char* dst) {
+#pragma unroll
+  for (int k = 0; k < GTile<T>::PER_THREAD; ++k) {
+    const int i = threadIdx.x + kThreads * k;
+    const int row = i / GTile<T>::CPR, ch = i % GTile<T>::CPR;
+    *reinterpret_cast<u32x4*>(dst + (size_t)i * 16) = lds_ld16(gsm, swz(row, ch, GTile<T>::ROW_BYTES));
+  }
+}
 
+// ---------------------------------------------------------------- 4. G tiles
+template <typename T, bool HAS_BIAS, bool WANT_TOK, bool WANT_VOC, bool WANT_DB>
+__global__ __launch_bounds__(kThreads, 1) void bwd_g_kernel(BwdArgs a, int chunk) {
+  using Loop = NTMainLoop<T, kBwdVocab, kBwdTokens, 2, 2>;  // A = C rows (vocab), B = E rows (tokens)
+  __shared__ __attribute__((aligned(16))) char smem[Loop::SMEM_BYTES + GTile<T>::BYTES];
+  char* gsm = smem + Loop::SMEM_BYTES;
+
+  const int nrb = (int)a.plan.nrb;
+  const int lo = a.chunk_slot[chunk], hi = a.chunk_slot[chunk + 1];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int wv = wave & 1;
@@ -271,10 +240,9 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_tile_kernel(BwdArgs a, int nr
   const T* bias = reinterpret_cast<const T*>(a.bias);
   const char* E = reinterpret_cast<const char*>(a.e);
   const char* C = reinterpret_cast<const char*>(a.c);
-  const int count = *a.count;
 
-  for (int idx = blockIdx.x; idx < count; idx += gridDim.x) {
-    const int pair = a.list[idx];
+  for (int slot = lo + (int)blockIdx.x; slot < hi; slot += (int)gridDim.x) {
+    const int pair = a.list[slot];
     const int vt = pair / nrb;
     const int rb = pair - vt * nrb;
     const int64_t v0 = (int64_t)vt * kBwdVocab;
@@ -287,7 +255,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_tile_kernel(BwdArgs a, int nr
       for (int j = 0; j < 2; ++j) w[i][j] = zero16();
     Loop::run(C, a.V, v0, E, a.N, t0, pitch, pitch, smem, w);
 
-    // W = g (softmax - onehot), zero outside [0,N) x [0,V) and for rows with g == 0.
+    // G = g (softmax - onehot), zero outside [0,N) x [0,V) and for rows with g == 0.
     float g[2], lz[2];
     int64_t tg[2];
 #pragma unroll
@@ -318,8 +286,11 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_tile_kernel(BwdArgs a, int nr
         }
       }
     }
+    const size_t s_local = (size_t)(slot - lo);
 
     if constexpr (WANT_DB) {
+      // column sums over this wave's 64 tokens; lanes n == 0 of each half hold them
+      float* cs = a.colsum + s_local * 2 * kBwdVocab + wt * kBwdVocab;
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
 #pragma unroll
@@ -330,114 +301,352 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_tile_kernel(BwdArgs a, int nr
           s += __shfl_xor(s, 4);
           s += __shfl_xor(s, 8);
           s += __shfl_xor(s, 16);
-          const int64_t v = v0 + wv * 64 + i * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
-          if (n == 0 && v < a.V) atomicAdd(a.dBias_acc + v, s);
+          if (n == 0) cs[wv * 64 + i * 32 + (r >> 2) * 8 + h * 4 + (r & 3)] = s;
         }
       }
     }
-
-    if constexpr (WANT_DE) {
-      store_w_token_major<T>(wsm, w, wv, wt, n, h);
-      Pass2<T>::run(wsm, C, a.V, v0, pitch, a.D, a.dE_acc, a.N, t0, smem);
+    if constexpr (WANT_TOK) {
+      store_g_token_major<T>(gsm, w, wv, wt, n, h);
+      __syncthreads();
+      copy_lds_to_global<T>(gsm, a.w_tok + s_local * a.plan.w_bytes);
+      __syncthreads();
     }
-    if constexpr (WANT_DC) {
-      store_w_vocab_major<T>(wsm, w, wv, wt, n, h);
-      Pass2<T>::run(wsm, E, a.N, t0, pitch, a.D, a.dC_acc, a.V, v0, smem);
+    if constexpr (WANT_VOC) {
+      store_g_vocab_major<T>(gsm, w, wv, wt, n, h);
+      __syncthreads();
+      copy_lds_to_global<T>(gsm, a.w_voc + s_local * a.plan.w_bytes);
+      __syncthreads();
     }
   }
 }
 
-__global__ __launch_bounds__(256) void fill_zero_kernel(u32x4* p, int64_t n16) {
-  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride) p[i] = u32x4{0u, 0u, 0u, 0u};
+// ---------------------------------------------------------------- 5/6. sums of G_j . X_j
+// acc[128 x DK] += G_j[128 x 128] . X_j[128 x DK] over a list of tiles j, where
+// G_j is a stored G tile (rows = output rows, columns = contraction) and X_j is
+// a 128-row block of E or C restricted to one 256-byte slice of D.  X_j is
+// transposed into LDS ([d][k], k contiguous) on the way in so both MFMA operands
+// are k-contiguous 16-byte fragments.
+template <typename T>
+struct GSum {
+  static constexpr int EPC = 16 / sizeof(T);               // elements per 16-byte fragment
+  static constexpr int DK = 256 / sizeof(T);               // D elements per slice
+  static constexpr uint32_t XROW_BYTES = 128 * sizeof(T);  // transposed slice row (128 k)
+  static constexpr uint32_t X_BYTES = DK * XROW_BYTES;     // 32 KiB for every dtype
+  static constexpr uint32_t G_BYTES = GTile<T>::BYTES;
+  static constexpr uint32_t BUF_BYTES = G_BYTES + X_BYTES;
+  static constexpr int NBUF = (2 * BUF_BYTES <= 160 * 1024) ? 2 : 1;
+  static constexpr int NB = (128 / EPC) * 16 / kThreads;  // EPC x EPC transpose blocks per thread
+  static constexpr int GP = GTile<T>::PER_THREAD;          // G-tile chunks per thread
+  static constexpr int TJ = DK / 2 / 32;                   // 32-col MFMA tiles per wave along D
+  static constexpr int KS = (int)(XROW_BYTES / 32);        // 32-byte K steps over 128 elements
+  static_assert(NB >= 1 && NB * kThreads == (128 / EPC) * 16, "transpose blocks must split evenly");
+
+  struct Regs {
+    u32x4 x[NB][EPC];
+    u32x4 g[GP];
+  };
+
+  static __device__ __forceinline__ void load(Regs& R, const char* gtile, const char* src, int64_t src_rows,
+                                              int64_t src_row0, int64_t pitch, int64_t kbytes, int ds) {
+#pragma unroll
+    for (int k = 0; k < GP; ++k) R.g[k] = gld16(gtile + (size_t)(threadIdx.x + kThreads * k) * 16);
+#pragma unroll
+    for (int s = 0; s < NB; ++s) {
+      const int b = threadIdx.x + kThreads * s;
+      const int dblk = b & 15;
+      const int vblk = b >> 4;
+      const int64_t col = (int64_t)ds * 256 + dblk * 16;
+      const bool in = col < kbytes;
+#pragma unroll
+      for (int x = 0; x < EPC; ++x) {
+        int64_t g = src_row0 + vblk * EPC + x;
+        g = g < src_rows ? g : src_rows - 1;
+        R.x[s][x] = in ? gld16(src + g * pitch + col) : u32x4{0u, 0u, 0u, 0u};
+      }
+    }
+  }
+
+  static __device__ __forceinline__ void store(const Regs& R, char* buf) {
+    char* gsm = buf;
+    char* xsm = buf + G_BYTES;
+#pragma unroll
+    for (int k = 0; k < GP; ++k) {
+      const int i = threadIdx.x + kThreads * k;
+      lds_st16(gsm, swz(i / GTile<T>::CPR, i % GTile<T>::CPR, GTile<T>::ROW_BYTES), R.g[k]);
+    }
+#pragma unroll
+    for (int s = 0; s < NB; ++s) {
+      const int b = threadIdx.x + kThreads * s;
+      const int dblk = b & 15;
+      const int vblk = b >> 4;
+#pragma unroll
+      for (int y = 0; y < EPC; ++y) {
+        u32x4 o;
+        if constexpr (sizeof(T) == 4) {
+          o = u32x4{R.x[s][0][y], R.x[s][1][y], R.x[s][2][y], R.x[s][3][y]};
+        } else {
+          const int wd = y >> 1;
+          const bool hi = y & 1;
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            const uint32_t lo_src = R.x[s][2 * k][wd];
+            const uint32_t hi_src = R.x[s][2 * k + 1][wd];
+            o[k] = hi ? ((lo_src >> 16) | (hi_src & 0xffff0000u)) : ((lo_src & 0xffffu) | (hi_src << 16));
+          }
+        }
+        lds_st16(xsm, swz(dblk * EPC + y, vblk, XROW_BYTES), o);
+      }
+    }
+  }
+
+  static __device__ __forceinline__ void mma(const char* buf, f32x16 (&acc)[2][TJ]) {
+    const char* gsm = buf;
+    const char* xsm = buf + G_BYTES;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int wm = wave & 1, wn = wave >> 1;
+    const int n = lane & 31, kg = lane >> 5;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      u32x4 af[2], bf[TJ];
+#pragma unroll
+      for (int ti = 0; ti < 2; ++ti)
+        af[ti] = lds_ld16(gsm, swz(wm * 64 + ti * 32 + n, ks * 2 + kg, GTile<T>::ROW_BYTES));
+#pragma unroll
+      for (int tj = 0; tj < TJ; ++tj) bf[tj] = lds_ld16(xsm, swz(wn * (DK / 2) + tj * 32 + n, ks * 2 + kg, XROW_BYTES));
+#pragma unroll
+      for (int ti = 0; ti < 2; ++ti)
+#pragma unroll
+        for (int tj = 0; tj < TJ; ++tj) acc[ti][tj] = Traits<T>::mfma(af[ti], bf[tj], acc[ti][tj]);
+    }
+  }
+
+  // Sum over `count` tiles; tile j's G tile and source row block come from get(j).
+  template <typename Get>
+  static __device__ __forceinline__ void run(int count, Get get, const char* src, int64_t src_rows, int64_t pitch,
+                                             int64_t kbytes, int ds, char* smem, f32x16 (&acc)[2][TJ]) {
+#pragma unroll
+    for (int ti = 0; ti < 2; ++ti)
+#pragma unroll
+      for (int tj = 0; tj < TJ; ++tj) acc[ti][tj] = zero16();
+    if (count == 0) return;
+    Regs R;
+    const char* gt;
+    int64_t row0;
+    get(0, gt, row0);
+    load(R, gt, src, src_rows, row0, pitch, kbytes, ds);
+    if constexpr (NBUF == 2) {
+      store(R, smem);
+      __syncthreads();
+      for (int j = 0; j < count; ++j) {
+        if (j + 1 < count) {
+          get(j + 1, gt, row0);
+          load(R, gt, src, src_rows, row0, pitch, kbytes, ds);
+        }
+        mma(smem + (j & 1) * BUF_BYTES, acc);
+        if (j + 1 < count) store(R, smem + ((j + 1) & 1) * BUF_BYTES);
+        __syncthreads();
+      }
+    } else {
+      for (int j = 0; j < count; ++j) {
+        if (j > 0) __syncthreads();  // previous tile's MFMA reads are done
+        store(R, smem);
+        __syncthreads();
+        if (j + 1 < count) {
+          get(j + 1, gt, row0);
+          load(R, gt, src, src_rows, row0, pitch, kbytes, ds);
+        }
+        mma(smem, acc);
+      }
+      __syncthreads();
+    }
+  }
+};
+
+// XCD-aware block order: the 8 XCDs each take a contiguous range of logical
+// blocks, so the D slices of one row block (which share its G tiles) run on the
+// same XCD and meet in its L2.
+__device__ __forceinline__ int xcd_block(int nblocks) {
+  const int per = (nblocks + 7) / 8;
+  return (int)(blockIdx.x & 7) * per + (int)(blockIdx.x >> 3);
 }
 
 template <typename T>
-__global__ __launch_bounds__(256) void cast_kernel(const float* __restrict__ src, T* __restrict__ dst, int64_t n) {
+__device__ __forceinline__ void write_out_tile(void* out_t, float* out_f32, int mode, const f32x16 (&acc)[2][GSum<T>::TJ],
+                                               int64_t row0, int64_t rows, int64_t D, int ds, bool has_tiles) {
+  // mode 0: write dtype; 1: store fp32 accumulator; 2: add into fp32 accumulator (only if has_tiles)
+  constexpr int TJ = GSum<T>::TJ, DK = GSum<T>::DK;
+  if (mode == 2 && !has_tiles) return;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int wm = wave & 1, wn = wave >> 1;
+  const int n = lane & 31, h = lane >> 5;
+#pragma unroll
+  for (int tj = 0; tj < TJ; ++tj) {
+    const int64_t d = (int64_t)ds * DK + wn * (DK / 2) + tj * 32 + n;
+    if (d >= D) continue;
+#pragma unroll
+    for (int ti = 0; ti < 2; ++ti) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t row = row0 + wm * 64 + ti * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
+        if (row >= rows) continue;
+        const size_t idx = (size_t)row * D + d;
+        const float v = acc[ti][tj][r];
+        if (mode == 0) {
+          reinterpret_cast<T*>(out_t)[idx] = (T)v;
+        } else if (mode == 1) {
+          out_f32[idx] = v;
+        } else {
+          out_f32[idx] += v;
+        }
+      }
+    }
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kThreads, 1) void bwd_de_kernel(BwdArgs a, int chunk, int mode) {
+  __shared__ __attribute__((aligned(16))) char smem[GSum<T>::NBUF * GSum<T>::BUF_BYTES];
+  const int nrb = (int)a.plan.nrb, nds = (int)a.plan.n_dslices;
+  const int pid = xcd_block(nrb * nds);
+  if (pid >= nrb * nds) return;
+  const int rb = pid / nds, ds = pid - rb * nds;
+  const int vt_lo = a.chunk_vt[chunk], vt_hi = a.chunk_vt[chunk + 1];
+  const int slot_lo = a.chunk_slot[chunk];
+  // this block's slots are sorted by vocab tile; keep those of this chunk
+  int b = a.rb_start[rb], e = a.rb_start[rb + 1];
+  while (b < e && a.list[a.rb_list[b]] / nrb < vt_lo) ++b;
+  int cnt = 0;
+  while (b + cnt < e && a.list[a.rb_list[b + cnt]] / nrb < vt_hi) ++cnt;
+  const int64_t pitch = a.D * (int64_t)sizeof(T);
+  auto get = [&](int j, const char*& gt, int64_t& row0) {
+    const int slot = a.rb_list[b + j];
+    gt = a.w_tok + (size_t)(slot - slot_lo) * a.plan.w_bytes;
+    row0 = (int64_t)(a.list[slot] / nrb) * kBwdVocab;
+  };
+  f32x16 acc[2][GSum<T>::TJ];
+  GSum<T>::run(cnt, get, reinterpret_cast<const char*>(a.c), a.V, pitch, pitch, ds, smem, acc);
+  write_out_tile<T>(a.dE, a.de_acc, mode, acc, (int64_t)rb * kBwdTokens, a.N, a.D, ds, cnt > 0);
+}
+
+template <typename T, bool WANT_DC, bool WANT_DB>
+__global__ __launch_bounds__(kThreads, 1) void bwd_dc_kernel(BwdArgs a, int chunk) {
+  __shared__ __attribute__((aligned(16))) char smem[GSum<T>::NBUF * GSum<T>::BUF_BYTES];
+  const int nvt = (int)a.plan.nvt, nrb = (int)a.plan.nrb, nds = (int)a.plan.n_dslices;
+  const int pid = xcd_block(nvt * nds);
+  if (pid >= nvt * nds) return;
+  const int vt = pid / nds, ds = pid - vt * nds;
+  if (vt < a.chunk_vt[chunk] || vt >= a.chunk_vt[chunk + 1]) return;  // another chunk owns it
+  const int slot_lo = a.chunk_slot[chunk];
+  const int b = a.vt_start[vt], cnt = a.vt_start[vt + 1] - b;
+  if constexpr (WANT_DC) {
+    const int64_t pitch = a.D * (int64_t)sizeof(T);
+    auto get = [&](int j, const char*& gt, int64_t& row0) {
+      const int slot = b + j;
+      gt = a.w_voc + (size_t)(slot - slot_lo) * a.plan.w_bytes;
+      row0 = (int64_t)(a.list[slot] % nrb) * kBwdTokens;
+    };
+    f32x16 acc[2][GSum<T>::TJ];
+    GSum<T>::run(cnt, get, reinterpret_cast<const char*>(a.e), a.N, pitch, pitch, ds, smem, acc);
+    write_out_tile<T>(a.dC, nullptr, 0, acc, (int64_t)vt * kBwdVocab, a.V, a.D, ds, cnt > 0);
+  }
+  if constexpr (WANT_DB) {
+    if (ds == 0 && threadIdx.x < kBwdVocab) {
+      const int64_t v = (int64_t)vt * kBwdVocab + threadIdx.x;
+      float s = 0.f;
+      for (int j = 0; j < cnt; ++j) {
+        const float* cs = a.colsum + (size_t)(b + j - slot_lo) * 2 * kBwdVocab;
+        s += cs[threadIdx.x] + cs[kBwdVocab + threadIdx.x];
+      }
+      if (v < a.V) reinterpret_cast<T*>(a.dBias)[v] = (T)s;
+    }
+  }
+}
+
+// ---------------------------------------------------------------- 7. dE cast (multi-chunk only)
+template <typename T>
+__global__ __launch_bounds__(256) void de_cast_kernel(const float* __restrict__ src, T* __restrict__ dst, int64_t n) {
   const int64_t stride = (int64_t)gridDim.x * blockDim.x * 4;
   for (int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4; i < n; i += stride) {
     if (i + 4 <= n) {
       const f32x4 v = *reinterpret_cast<const f32x4*>(src + i);
-      if constexpr (sizeof(T) == 4) {
-        *reinterpret_cast<f32x4*>(dst + i) = v;
-      } else {
-        T o0 = (T)v.x, o1 = (T)v.y, o2 = (T)v.z, o3 = (T)v.w;
-        const uint32_t p0 = (uint32_t)__builtin_bit_cast(uint16_t, o0) | ((uint32_t)__builtin_bit_cast(uint16_t, o1) << 16);
-        const uint32_t p1 = (uint32_t)__builtin_bit_cast(uint16_t, o2) | ((uint32_t)__builtin_bit_cast(uint16_t, o3) << 16);
-        *reinterpret_cast<u32x2*>(dst + i) = u32x2{p0, p1};
-      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k) dst[i + k] = (T)v[k];
     } else {
       for (int64_t k = i; k < n; ++k) dst[k] = (T)src[k];
     }
   }
 }
 
-static unsigned grid_for(int64_t items, int per_block) {
-  int64_t g = (items + per_block - 1) / per_block;
-  if (g < 1) g = 1;
-  if (g > 65536) g = 65536;
-  return (unsigned)g;
-}
-
-hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t s) {
-  const int64_t n16 = (int64_t)(bytes / 16);
-  if (n16 == 0) return hipSuccess;
-  hipLaunchKernelGGL(fill_zero_kernel, dim3(grid_for(n16, 256)), dim3(256), 0, s, reinterpret_cast<u32x4*>(p), n16);
-  return hipGetLastError();
-}
-
-hipError_t launch_cast(int dtype, const float* src, void* dst, int64_t n, hipStream_t s) {
-  if (n <= 0) return hipSuccess;
-  const dim3 grid(grid_for(n, 1024)), block(256);
-  switch (dtype) {
-    case 0:
-      hipLaunchKernelGGL((cast_kernel<float>), grid, block, 0, s, src, reinterpret_cast<float*>(dst), n);
-      break;
-    case 1:
-      hipLaunchKernelGGL((cast_kernel<_Float16>), grid, block, 0, s, src, reinterpret_cast<_Float16*>(dst), n);
-      break;
-    default:
-      hipLaunchKernelGGL((cast_kernel<__bf16>), grid, block, 0, s, src, reinterpret_cast<__bf16*>(dst), n);
-      break;
-  }
-  return hipGetLastError();
-}
-
+// ---------------------------------------------------------------- launch
 template <typename T, bool HB>
-static void launch_tile(const BwdArgs& a, int nrb, dim3 grid, hipStream_t s) {
-  const bool de = a.dE_acc != nullptr, dc = a.dC_acc != nullptr, db = a.dBias_acc != nullptr;
-#define CCE_TILE(DE, DC, DB)                                                                              \
-  if (de == DE && dc == DC && db == DB) {                                                               \
-    hipLaunchKernelGGL((bwd_tile_kernel<T, HB, DE, DC, DB>), grid, dim3(kThreads), 0, s, a, nrb);        \
+static void launch_g(const BwdArgs& a, int chunk, dim3 grid, hipStream_t s) {
+  const bool tok = a.dE != nullptr, voc = a.dC != nullptr, db = a.dBias != nullptr;
+#define CCE_G(TOK, VOC, DB)                                                                               \
+  if (tok == TOK && voc == VOC && db == DB) {                                                           \
+    hipLaunchKernelGGL((bwd_g_kernel<T, HB, TOK, VOC, DB>), grid, dim3(kThreads), 0, s, a, chunk);       \
     return;                                                                                             \
   }
-  CCE_TILE(true, true, true)
-  CCE_TILE(true, true, false)
-  CCE_TILE(true, false, true)
-  CCE_TILE(true, false, false)
-  CCE_TILE(false, true, true)
-  CCE_TILE(false, true, false)
-  CCE_TILE(false, false, true)
-#undef CCE_TILE
+  CCE_G(true, true, true)
+  CCE_G(true, true, false)
+  CCE_G(true, false, true)
+  CCE_G(true, false, false)
+  CCE_G(false, true, true)
+  CCE_G(false, true, false)
+  CCE_G(false, false, true)
+#undef CCE_G
 }
 
 template <typename T>
 static hipError_t backward_typed(const BwdArgs& a, hipStream_t s) {
-  const int nvt = (int)((a.V + kBwdVocab - 1) / kBwdVocab);
-  const int nrb = (int)((a.N + kBwdTokens - 1) / kBwdTokens);
-  const int total = nvt * nrb;
-  hipLaunchKernelGGL(bwd_filter_kernel, dim3((unsigned)((total + 3) / 4)), dim3(256), 0, s, a, nvt, nrb);
+  const BwdPlan& P = a.plan;
+  const int total = (int)P.total;
+  hipLaunchKernelGGL(bwd_filter_kernel, dim3((unsigned)((total + 3) / 4)), dim3(256), 0, s, a);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
-  hipLaunchKernelGGL(bwd_compact_kernel, dim3(1), dim3(1024), 0, s, a, total);
+  hipLaunchKernelGGL(bwd_compact_vt_kernel, dim3(1), dim3(1024), 0, s, a);
   if ((err = hipGetLastError()) != hipSuccess) return err;
-  if (a.dE_acc || a.dC_acc || a.dBias_acc) {
-    int g = a.num_cus > 0 ? a.num_cus : 256;
-    if (g > total) g = total;
+  const bool want_de = a.dE != nullptr, want_dc = a.dC != nullptr, want_db = a.dBias != nullptr;
+  if (!(want_de || want_dc || want_db)) return hipSuccess;
+  if (want_de) {
+    hipLaunchKernelGGL(bwd_compact_rb_kernel, dim3(1), dim3(1024), 0, s, a);
+    if ((err = hipGetLastError()) != hipSuccess) return err;
+  }
+  int g = a.num_cus > 0 ? a.num_cus : 256;
+  if (g > P.cap) g = (int)P.cap;
+  const bool multi = P.max_chunks > 1;
+  for (int chunk = 0; chunk < (int)P.max_chunks; ++chunk) {
     if (a.bias)
-      launch_tile<T, true>(a, nrb, dim3(g), s);
+      launch_g<T, true>(a, chunk, dim3(g), s);
     else
-      launch_tile<T, false>(a, nrb, dim3(g), s);
+      launch_g<T, false>(a, chunk, dim3(g), s);
+    if ((err = hipGetLastError()) != hipSuccess) return err;
+    if (want_de) {
+      const int mode = !multi ? 0 : (chunk == 0 ? 1 : 2);
+      const int nb = (int)(P.nrb * P.n_dslices);
+      hipLaunchKernelGGL((bwd_de_kernel<T>), dim3((unsigned)((nb + 7) / 8 * 8)), dim3(kThreads), 0, s, a, chunk, mode);
+      if ((err = hipGetLastError()) != hipSuccess) return err;
+    }
+    if (want_dc || want_db) {
+      const int nb = (int)(P.nvt * P.n_dslices);
+      const dim3 grid((unsigned)((nb + 7) / 8 * 8));
+      if (want_dc && want_db)
+        hipLaunchKernelGGL((bwd_dc_kernel<T, true, true>), grid, dim3(kThreads), 0, s, a, chunk);
+      else if (want_dc)
+        hipLaunchKernelGGL((bwd_dc_kernel<T, true, false>), grid, dim3(kThreads), 0, s, a, chunk);
+      else
+        hipLaunchKernelGGL((bwd_dc_kernel<T, false, true>), grid, dim3(kThreads), 0, s, a, chunk);
+      if ((err = hipGetLastError()) != hipSuccess) return err;
+    }
+  }
+  if (want_de && multi) {
+    const int64_t n = a.N * a.D;
+    int64_t blocks = (n / 4 + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    if (blocks < 1) blocks = 1;
+    hipLaunchKernelGGL((de_cast_kernel<T>), dim3((unsigned)blocks), dim3(256), 0, s, a.de_acc,
+                       reinterpret_cast<T*>(a.dE), n);
   }
   return hipGetLastError();
 }
