@@ -192,6 +192,7 @@ int cce_backward(int dtype, const void* e, const void* c, const void* bias, cons
   a.list = reinterpret_cast<int*>(ws + P.list);
   a.vt_start = reinterpret_cast<int*>(ws + P.vt_start);
   a.rb_list = reinterpret_cast<int*>(ws + P.rb_list);
+  a.rb_vt = reinterpret_cast<int*>(ws + P.rb_vt);
   a.rb_start = reinterpret_cast<int*>(ws + P.rb_start);
   a.chunk_vt = reinterpret_cast<int*>(ws + P.chunk_vt);
   a.chunk_slot = reinterpret_cast<int*>(ws + P.chunk_slot);

@@ -22,12 +22,14 @@
 //   4. bwd_g_kernel          recompute the logit tile on MFMA, form G, store it in
 //                            the chunk's scratch (bf16/fp16/fp32, token-major and
 //                            vocab-major) plus its fp32 column sums.
-//   5. bwd_de_kernel         one workgroup per (token block, 256-byte D slice):
+//   5. bwd_sum_kernel<0>     dE: owner = (token block, 256-byte D slice);
 //                            dE = sum over the block's kept tiles of G_j . C_j.
-//   6. bwd_dc_kernel         one workgroup per (vocab tile, D slice):
+//   6. bwd_sum_kernel<1>     dC: owner = (vocab tile, D slice);
 //                            dC = sum over the tile's kept blocks of G_j^T . E_j,
 //                            dBias from the column sums; written in the output dtype.
-//   7. dE_cast_kernel        only when there is more than one chunk (fp32 -> dtype).
+//   Both are persistent workgroups walking (owner, tile) steps as one pipeline.
+//   With more than one chunk, dE is carried between chunks in an fp32 buffer by
+//   the owner itself (store / add / finish), still without atomics.
 #include "cce_device.h"
 #include "cce_launch.h"
 
@@ -143,7 +145,11 @@ __global__ __launch_bounds__(1024) void bwd_compact_rb_kernel(BwdArgs a) {
   for (int j = beg; j < end; ++j) {
     const int rb = j / nvt, vt = j - rb * nvt;
     if (vt == 0) a.rb_start[rb] = pos;
-    if (a.flags[vt * nrb + rb]) a.rb_list[pos++] = a.slot_map[vt * nrb + rb];
+    if (a.flags[vt * nrb + rb]) {
+      a.rb_list[pos] = a.slot_map[vt * nrb + rb];
+      a.rb_vt[pos] = vt;
+      ++pos;
+    }
   }
   if (tid == 1023) a.rb_start[nrb] = scan[1023];
 }
@@ -421,62 +427,19 @@ struct GSum {
     }
   }
 
-  // Sum over `count` tiles; tile j's G tile and source row block come from get(j).
-  template <typename Get>
-  static __device__ __forceinline__ void run(int count, Get get, const char* src, int64_t src_rows, int64_t pitch,
-                                             int64_t kbytes, int ds, char* smem, f32x16 (&acc)[2][TJ]) {
-#pragma unroll
-    for (int ti = 0; ti < 2; ++ti)
-#pragma unroll
-      for (int tj = 0; tj < TJ; ++tj) acc[ti][tj] = zero16();
-    if (count == 0) return;
-    Regs R;
-    const char* gt;
-    int64_t row0;
-    get(0, gt, row0);
-    load(R, gt, src, src_rows, row0, pitch, kbytes, ds);
-    if constexpr (NBUF == 2) {
-      store(R, smem);
-      __syncthreads();
-      for (int j = 0; j < count; ++j) {
-        if (j + 1 < count) {
-          get(j + 1, gt, row0);
-          load(R, gt, src, src_rows, row0, pitch, kbytes, ds);
-        }
-        mma(smem + (j & 1) * BUF_BYTES, acc);
-        if (j + 1 < count) store(R, smem + ((j + 1) & 1) * BUF_BYTES);
-        __syncthreads();
-      }
-    } else {
-      for (int j = 0; j < count; ++j) {
-        if (j > 0) __syncthreads();  // previous tile's MFMA reads are done
-        store(R, smem);
-        __syncthreads();
-        if (j + 1 < count) {
-          get(j + 1, gt, row0);
-          load(R, gt, src, src_rows, row0, pitch, kbytes, ds);
-        }
-        mma(smem, acc);
-      }
-      __syncthreads();
-    }
-  }
 };
 
-// XCD-aware block order: the 8 XCDs each take a contiguous range of logical
-// blocks, so the D slices of one row block (which share its G tiles) run on the
-// same XCD and meet in its L2.
-__device__ __forceinline__ int xcd_block(int nblocks) {
-  const int per = (nblocks + 7) / 8;
-  return (int)(blockIdx.x & 7) * per + (int)(blockIdx.x >> 3);
-}
+// Output write of one owner tile (128 rows x one D slice).
+//   kWriteT: write the output dtype; kStoreF32 / kAddF32: fp32 accumulator;
+//   kFinishT: write dtype of (fp32 accumulator + acc); kSkip: nothing.
+enum WriteMode { kWriteT = 0, kStoreF32 = 1, kAddF32 = 2, kFinishT = 3, kSkip = 4 };
 
 template <typename T>
-__device__ __forceinline__ void write_out_tile(void* out_t, float* out_f32, int mode, const f32x16 (&acc)[2][GSum<T>::TJ],
-                                               int64_t row0, int64_t rows, int64_t D, int ds, bool has_tiles) {
-  // mode 0: write dtype; 1: store fp32 accumulator; 2: add into fp32 accumulator (only if has_tiles)
+__device__ __forceinline__ void write_owner_tile(void* out_t, float* out_f32, int mode,
+                                                 const f32x16 (&acc)[2][GSum<T>::TJ], int64_t row0, int64_t rows,
+                                                 int64_t D, int ds) {
   constexpr int TJ = GSum<T>::TJ, DK = GSum<T>::DK;
-  if (mode == 2 && !has_tiles) return;
+  if (mode == kSkip) return;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int wm = wave & 1, wn = wave >> 1;
@@ -493,90 +456,187 @@ __device__ __forceinline__ void write_out_tile(void* out_t, float* out_f32, int 
         if (row >= rows) continue;
         const size_t idx = (size_t)row * D + d;
         const float v = acc[ti][tj][r];
-        if (mode == 0) {
+        if (mode == kWriteT) {
           reinterpret_cast<T*>(out_t)[idx] = (T)v;
-        } else if (mode == 1) {
+        } else if (mode == kStoreF32) {
           out_f32[idx] = v;
-        } else {
+        } else if (mode == kAddF32) {
           out_f32[idx] += v;
+        } else {
+          reinterpret_cast<T*>(out_t)[idx] = (T)(out_f32[idx] + v);
         }
       }
     }
   }
 }
 
-template <typename T>
-__global__ __launch_bounds__(kThreads, 1) void bwd_de_kernel(BwdArgs a, int chunk, int mode) {
-  __shared__ __attribute__((aligned(16))) char smem[GSum<T>::NBUF * GSum<T>::BUF_BYTES];
+// Persistent owner-computes sums.  PHASE 0 (dE): owner = token block rb; group
+// (rb, D slice) sums G_j . C_j over rb's kept tiles j of this chunk (G from the
+// token-major scratch, C rows of tile j's vocab tile).  PHASE 1 (dC): owner =
+// vocab tile vt of this chunk; group (vt, slice) sums G_j^T . E_j over vt's kept
+// token blocks (G from the vocab-major scratch); the slice-0 group also writes
+// dBias from the column sums.
+//
+// Owners are dealt to the 8 XCDs round-robin; the workgroups of an XCD take its
+// groups in order, so all D slices of one owner run at the same time on one XCD
+// and share its G tiles in L2.  Each workgroup walks its
+// (group, tile) steps as one software pipeline: the next step's G tile and
+// source slice are fetched while the current step's MFMAs run and while a
+// finished group's output is written, so short groups cost no extra latency.
+template <typename T, int PHASE, bool WANT_DB>
+__global__ __launch_bounds__(kThreads, 1) void bwd_sum_kernel(BwdArgs a, int chunk) {
+  using S = GSum<T>;
+  __shared__ __attribute__((aligned(16))) char smem[S::NBUF * S::BUF_BYTES];
   const int nrb = (int)a.plan.nrb, nds = (int)a.plan.n_dslices;
-  const int pid = xcd_block(nrb * nds);
-  if (pid >= nrb * nds) return;
-  const int rb = pid / nds, ds = pid - rb * nds;
+  const bool single = a.plan.max_chunks == 1;
   const int vt_lo = a.chunk_vt[chunk], vt_hi = a.chunk_vt[chunk + 1];
   const int slot_lo = a.chunk_slot[chunk];
-  // this block's slots are sorted by vocab tile; keep those of this chunk
-  int b = a.rb_start[rb], e = a.rb_start[rb + 1];
-  while (b < e && a.list[a.rb_list[b]] / nrb < vt_lo) ++b;
-  int cnt = 0;
-  while (b + cnt < e && a.list[a.rb_list[b + cnt]] / nrb < vt_hi) ++cnt;
+  const int own_lo = PHASE == 0 ? 0 : vt_lo;
+  const int own_hi = PHASE == 0 ? nrb : vt_hi;
+  const int n_own = own_hi - own_lo;
+  if (n_own <= 0) return;
+  if (PHASE == 0 && !single && slot_lo == a.chunk_slot[chunk + 1] && chunk > 0) return;  // nothing to add
+  // Owners are dealt to the XCDs round-robin (owner own_lo + xcd + 8k), which spreads
+  // the heavy owners of skewed target distributions over all XCDs.
+  const int xcd = (int)(blockIdx.x & 7), lidx = (int)(blockIdx.x >> 3), nper = (int)(gridDim.x >> 3);
+  const int n_mine = n_own > xcd ? (n_own - xcd + 7) / 8 : 0;
+  const int ngroups = n_mine * nds;
   const int64_t pitch = a.D * (int64_t)sizeof(T);
-  auto get = [&](int j, const char*& gt, int64_t& row0) {
-    const int slot = a.rb_list[b + j];
-    gt = a.w_tok + (size_t)(slot - slot_lo) * a.plan.w_bytes;
-    row0 = (int64_t)(a.list[slot] / nrb) * kBwdVocab;
-  };
-  f32x16 acc[2][GSum<T>::TJ];
-  GSum<T>::run(cnt, get, reinterpret_cast<const char*>(a.c), a.V, pitch, pitch, ds, smem, acc);
-  write_out_tile<T>(a.dE, a.de_acc, mode, acc, (int64_t)rb * kBwdTokens, a.N, a.D, ds, cnt > 0);
-}
+  const char* src = reinterpret_cast<const char*>(PHASE == 0 ? a.c : a.e);
+  const int64_t src_rows = PHASE == 0 ? a.V : a.N;
 
-template <typename T, bool WANT_DC, bool WANT_DB>
-__global__ __launch_bounds__(kThreads, 1) void bwd_dc_kernel(BwdArgs a, int chunk) {
-  __shared__ __attribute__((aligned(16))) char smem[GSum<T>::NBUF * GSum<T>::BUF_BYTES];
-  const int nvt = (int)a.plan.nvt, nrb = (int)a.plan.nrb, nds = (int)a.plan.n_dslices;
-  const int pid = xcd_block(nvt * nds);
-  if (pid >= nvt * nds) return;
-  const int vt = pid / nds, ds = pid - vt * nds;
-  if (vt < a.chunk_vt[chunk] || vt >= a.chunk_vt[chunk + 1]) return;  // another chunk owns it
-  const int slot_lo = a.chunk_slot[chunk];
-  const int b = a.vt_start[vt], cnt = a.vt_start[vt + 1] - b;
-  if constexpr (WANT_DC) {
-    const int64_t pitch = a.D * (int64_t)sizeof(T);
-    auto get = [&](int j, const char*& gt, int64_t& row0) {
-      const int slot = b + j;
+  struct Step {
+    int q, owner, ds, b, cnt, j, mode;
+  };
+  auto group = [&](int q, Step& st) -> bool {
+    if (q >= ngroups) return false;
+    st.q = q;
+    st.owner = own_lo + xcd + 8 * (q / nds);
+    st.ds = q - (q / nds) * nds;
+    st.j = 0;
+    if (PHASE == 0) {
+      const int rs = a.rb_start[st.owner], re = a.rb_start[st.owner + 1];
+      if (single) {
+        st.b = rs;
+        st.cnt = re - rs;
+        st.mode = kWriteT;
+      } else {
+        int b = rs;
+        while (b < re && a.rb_vt[b] < vt_lo) ++b;
+        int cnt = 0;
+        while (b + cnt < re && a.rb_vt[b + cnt] < vt_hi) ++cnt;
+        st.b = b;
+        st.cnt = cnt;
+        const bool prev = b > rs, next = b + cnt < re;
+        if (cnt == 0) st.mode = (rs == re && chunk == 0) ? kWriteT : kSkip;
+        else st.mode = prev ? (next ? kAddF32 : kFinishT) : (next ? kStoreF32 : kWriteT);
+      }
+    } else {
+      st.b = a.vt_start[st.owner];
+      st.cnt = a.vt_start[st.owner + 1] - st.b;
+      st.mode = kWriteT;
+    }
+    return true;
+  };
+  auto next = [&](const Step& cur, Step& nx) -> bool {
+    if (cur.j + 1 < cur.cnt) {
+      nx = cur;
+      ++nx.j;
+      return true;
+    }
+    return group(cur.q + nper, nx);
+  };
+  auto source = [&](const Step& st, const char*& gt, int64_t& row0) {
+    if (PHASE == 0) {
+      const int pos = st.b + st.j;
+      gt = a.w_tok + (size_t)(a.rb_list[pos] - slot_lo) * a.plan.w_bytes;
+      row0 = (int64_t)a.rb_vt[pos] * kBwdVocab;
+    } else {
+      const int slot = st.b + st.j;
       gt = a.w_voc + (size_t)(slot - slot_lo) * a.plan.w_bytes;
       row0 = (int64_t)(a.list[slot] % nrb) * kBwdTokens;
-    };
-    f32x16 acc[2][GSum<T>::TJ];
-    GSum<T>::run(cnt, get, reinterpret_cast<const char*>(a.e), a.N, pitch, pitch, ds, smem, acc);
-    write_out_tile<T>(a.dC, nullptr, 0, acc, (int64_t)vt * kBwdVocab, a.V, a.D, ds, cnt > 0);
-  }
-  if constexpr (WANT_DB) {
-    if (ds == 0 && threadIdx.x < kBwdVocab) {
-      const int64_t v = (int64_t)vt * kBwdVocab + threadIdx.x;
-      float s = 0.f;
-      for (int j = 0; j < cnt; ++j) {
-        const float* cs = a.colsum + (size_t)(b + j - slot_lo) * 2 * kBwdVocab;
-        s += cs[threadIdx.x] + cs[kBwdVocab + threadIdx.x];
-      }
-      if (v < a.V) reinterpret_cast<T*>(a.dBias)[v] = (T)s;
     }
+  };
+  auto finish = [&](const Step& st, const f32x16 (&acc)[2][S::TJ]) {
+    if (PHASE == 0) {
+      write_owner_tile<T>(a.dE, a.de_acc, st.mode, acc, (int64_t)st.owner * kBwdTokens, a.N, a.D, st.ds);
+    } else {
+      write_owner_tile<T>(a.dC, nullptr, kWriteT, acc, (int64_t)st.owner * kBwdVocab, a.V, a.D, st.ds);
+      if constexpr (WANT_DB) {
+        if (st.ds == 0 && threadIdx.x < kBwdVocab) {
+          const int64_t v = (int64_t)st.owner * kBwdVocab + threadIdx.x;
+          float sum = 0.f;
+          for (int j = 0; j < st.cnt; ++j) {
+            const float* cs = a.colsum + (size_t)(st.b + j - slot_lo) * 2 * kBwdVocab;
+            sum += cs[threadIdx.x] + cs[kBwdVocab + threadIdx.x];
+          }
+          if (v < a.V) reinterpret_cast<T*>(a.dBias)[v] = (T)sum;
+        }
+      }
+    }
+  };
+
+  Step cur;
+  if (!group(lidx, cur)) return;
+  f32x16 acc[2][S::TJ];
+#pragma unroll
+  for (int ti = 0; ti < 2; ++ti)
+#pragma unroll
+    for (int tj = 0; tj < S::TJ; ++tj) acc[ti][tj] = zero16();
+  typename S::Regs R;
+  const char* gt;
+  int64_t row0;
+  if (cur.cnt > 0) {
+    source(cur, gt, row0);
+    S::load(R, gt, src, src_rows, row0, pitch, pitch, cur.ds);
+    S::store(R, smem);
+  }
+  __syncthreads();
+  int bi = 0;
+  for (;;) {
+    Step nx;
+    const bool has_next = next(cur, nx);
+    const bool next_loads = has_next && nx.cnt > 0;
+    if (next_loads) {
+      source(nx, gt, row0);
+      S::load(R, gt, src, src_rows, row0, pitch, pitch, nx.ds);
+    }
+    if (cur.cnt > 0) S::mma(smem + bi * S::BUF_BYTES, acc);
+    if (cur.j + 1 >= (cur.cnt > 0 ? cur.cnt : 1)) {
+      finish(cur, acc);
+#pragma unroll
+      for (int ti = 0; ti < 2; ++ti)
+#pragma unroll
+        for (int tj = 0; tj < S::TJ; ++tj) acc[ti][tj] = zero16();
+    }
+    if (!has_next) break;
+    if constexpr (S::NBUF == 2) {
+      if (next_loads) S::store(R, smem + (bi ^ 1) * S::BUF_BYTES);
+      __syncthreads();
+      bi ^= 1;
+    } else {
+      __syncthreads();  // every wave is done reading the single buffer
+      if (next_loads) S::store(R, smem);
+      __syncthreads();
+    }
+    cur = nx;
   }
 }
 
-// ---------------------------------------------------------------- 7. dE cast (multi-chunk only)
+// dBias only (c does not require a gradient): sum of the column sums per vocab tile.
 template <typename T>
-__global__ __launch_bounds__(256) void de_cast_kernel(const float* __restrict__ src, T* __restrict__ dst, int64_t n) {
-  const int64_t stride = (int64_t)gridDim.x * blockDim.x * 4;
-  for (int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4; i < n; i += stride) {
-    if (i + 4 <= n) {
-      const f32x4 v = *reinterpret_cast<const f32x4*>(src + i);
-#pragma unroll
-      for (int k = 0; k < 4; ++k) dst[i + k] = (T)v[k];
-    } else {
-      for (int64_t k = i; k < n; ++k) dst[k] = (T)src[k];
-    }
+__global__ __launch_bounds__(kBwdVocab) void bwd_dbias_kernel(BwdArgs a, int chunk) {
+  const int vt = a.chunk_vt[chunk] + (int)blockIdx.x;
+  if (vt >= a.chunk_vt[chunk + 1]) return;
+  const int slot_lo = a.chunk_slot[chunk];
+  const int b = a.vt_start[vt], cnt = a.vt_start[vt + 1] - b;
+  const int64_t v = (int64_t)vt * kBwdVocab + threadIdx.x;
+  float sum = 0.f;
+  for (int j = 0; j < cnt; ++j) {
+    const float* cs = a.colsum + (size_t)(b + j - slot_lo) * 2 * kBwdVocab;
+    sum += cs[threadIdx.x] + cs[kBwdVocab + threadIdx.x];
   }
+  if (v < a.V) reinterpret_cast<T*>(a.dBias)[v] = (T)sum;
 }
 
 // ---------------------------------------------------------------- launch
@@ -615,6 +675,7 @@ static hipError_t backward_typed(const BwdArgs& a, hipStream_t s) {
   }
   int g = a.num_cus > 0 ? a.num_cus : 256;
   if (g > P.cap) g = (int)P.cap;
+  const int gp = ((a.num_cus > 0 ? a.num_cus : 256) + 7) / 8 * 8;  // persistent sum kernels
   const bool multi = P.max_chunks > 1;
   for (int chunk = 0; chunk < (int)P.max_chunks; ++chunk) {
     if (a.bias)
@@ -623,31 +684,21 @@ static hipError_t backward_typed(const BwdArgs& a, hipStream_t s) {
       launch_g<T, false>(a, chunk, dim3(g), s);
     if ((err = hipGetLastError()) != hipSuccess) return err;
     if (want_de) {
-      const int mode = !multi ? 0 : (chunk == 0 ? 1 : 2);
-      const int nb = (int)(P.nrb * P.n_dslices);
-      hipLaunchKernelGGL((bwd_de_kernel<T>), dim3((unsigned)((nb + 7) / 8 * 8)), dim3(kThreads), 0, s, a, chunk, mode);
+      hipLaunchKernelGGL((bwd_sum_kernel<T, 0, false>), dim3(gp), dim3(kThreads), 0, s, a, chunk);
       if ((err = hipGetLastError()) != hipSuccess) return err;
     }
-    if (want_dc || want_db) {
-      const int nb = (int)(P.nvt * P.n_dslices);
-      const dim3 grid((unsigned)((nb + 7) / 8 * 8));
-      if (want_dc && want_db)
-        hipLaunchKernelGGL((bwd_dc_kernel<T, true, true>), grid, dim3(kThreads), 0, s, a, chunk);
-      else if (want_dc)
-        hipLaunchKernelGGL((bwd_dc_kernel<T, true, false>), grid, dim3(kThreads), 0, s, a, chunk);
+    if (want_dc) {
+      if (want_db)
+        hipLaunchKernelGGL((bwd_sum_kernel<T, 1, true>), dim3(gp), dim3(kThreads), 0, s, a, chunk);
       else
-        hipLaunchKernelGGL((bwd_dc_kernel<T, false, true>), grid, dim3(kThreads), 0, s, a, chunk);
+        hipLaunchKernelGGL((bwd_sum_kernel<T, 1, false>), dim3(gp), dim3(kThreads), 0, s, a, chunk);
+      if ((err = hipGetLastError()) != hipSuccess) return err;
+    } else if (want_db) {
+      hipLaunchKernelGGL((bwd_dbias_kernel<T>), dim3((unsigned)P.nvt), dim3(kBwdVocab), 0, s, a, chunk);
       if ((err = hipGetLastError()) != hipSuccess) return err;
     }
   }
-  if (want_de && multi) {
-    const int64_t n = a.N * a.D;
-    int64_t blocks = (n / 4 + 255) / 256;
-    if (blocks > 65536) blocks = 65536;
-    if (blocks < 1) blocks = 1;
-    hipLaunchKernelGGL((de_cast_kernel<T>), dim3((unsigned)blocks), dim3(256), 0, s, a.de_acc,
-                       reinterpret_cast<T*>(a.dE), n);
-  }
+  (void)multi;
   return hipGetLastError();
 }
 

@@ -45,7 +45,7 @@ struct BwdPlan {
   int64_t n_dslices;        // 256-byte slices of a row of E / C
   size_t w_bytes;           // bytes of one G tile in one layout (128 x 128 x sizeof(T))
   // workspace byte offsets
-  size_t flags, slot_map, list, vt_start, rb_list, rb_start, chunk_vt, chunk_slot, w_tok, w_voc, colsum, de_acc;
+  size_t flags, slot_map, list, vt_start, rb_list, rb_vt, rb_start, chunk_vt, chunk_slot, w_tok, w_voc, colsum, de_acc;
   size_t total_bytes;
 };
 
@@ -81,6 +81,7 @@ inline BwdPlan make_bwd_plan(size_t esize, int64_t N, int64_t D, int64_t V, bool
   P.list = take((size_t)P.total * 4);
   P.vt_start = take((size_t)(P.nvt + 1) * 4);
   P.rb_list = take((size_t)P.total * 4);
+  P.rb_vt = take((size_t)P.total * 4);
   P.rb_start = take((size_t)(P.nrb + 1) * 4);
   P.chunk_vt = take((size_t)(P.max_chunks + 1) * 4);
   P.chunk_slot = take((size_t)(P.max_chunks + 1) * 4);
@@ -113,6 +114,7 @@ struct BwdArgs {
   int* list;          // [nvt * nrb] slot -> pair, vocab-major
   int* vt_start;      // [nvt + 1] first slot of each vocab tile
   int* rb_list;       // [nvt * nrb] slots ordered by token block, then vocab tile
+  int* rb_vt;         // [nvt * nrb] vocab tile of each rb_list entry
   int* rb_start;      // [nrb + 1]
   int* chunk_vt;      // [max_chunks + 1] first vocab tile of each chunk
   int* chunk_slot;    // [max_chunks + 1] first slot of each chunk
