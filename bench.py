@@ -160,7 +160,7 @@ def main():
         "step": {"fwd_ms": fwd_ms, "bwd_ms": bwd_ms, "tile_skip": skip, "kept_tiles": kept, "total_tiles": total,
                  "algorithmic_flops": step_flops, "tflops": step_flops / (ms * 1e-3) / 1e12,
                  "mfma_frac": step_flops / (ms * 1e-3) / 1e12 / peak,
-                 "dense_equiv_mfma_frac": dense_flops / (ms * 1e-3) / 1e12 / peak,
+                 "dense_flops": dense_flops,
                  "peak_mem_gb": peak_mem / 2 ** 30, "logits_bytes_if_materialised": 4.0 * N * V},
         "cpu_baseline": None,
     }

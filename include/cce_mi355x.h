@@ -97,7 +97,11 @@ size_t cce_backward_workspace_size(int dtype, int64_t N, int64_t D, int64_t V,
  * target inside the tile and every row's tile_max - lse < filter_log_eps
  * (reference predicate: cce.metal:191-204).  filter_log_eps = -INFINITY keeps all tiles.
  * dE/dC/dBias are written in `dtype`; pass NULL for any gradient not wanted.
- * Accumulation is fp32 atomics into the workspace, then one cast pass.
+ * No atomics: kept tiles' G blocks are staged (bf16/fp16/fp32, the input dtype) in
+ * the workspace, then every output row block is summed in fp32 registers by the one
+ * workgroup that owns it and written once.  Every output element is written, so the
+ * outputs need no zero-fill.  Rows of dE/dC/dBias that no kept tile touches are 0.
+ * The workspace must stay untouched until the backward's work on the stream ends.
  * tile_stats (nullable, device int64[2]) receives {kept tiles, total tiles}.
  */
 int cce_backward(int dtype, const void* e, const void* c, const void* bias,

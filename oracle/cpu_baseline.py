@@ -47,7 +47,13 @@ def time_tokens_per_s(e, c, targets, bias=None, reduction="mean", ignore_index=-
     The full vocabulary and hidden size are kept, so per-token cost matches the
     workload; only the number of tokens is bounded.
     """
-    threads = threads or os.cpu_count() or 1
+    if not threads:
+        # The CPUs this process may run on, capped by OMP_NUM_THREADS when the host sets it
+        # (a GPU box shares its host's cores; os.cpu_count() reports all of them).
+        threads = len(os.sched_getaffinity(0)) or 1
+        omp = os.environ.get("OMP_NUM_THREADS", "")
+        if omp.isdigit() and int(omp) > 0:
+            threads = min(threads, int(omp))
     torch.set_num_threads(threads)
     e = e.reshape(-1, e.shape[-1])
     t = targets.reshape(-1)

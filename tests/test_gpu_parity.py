@@ -363,3 +363,74 @@ def test_config_c3_full_size_properties(m, cuda):
     kept, total = m.last_tile_stats()
     print(f"c3: loss {loss.item():.3e} kept {kept}/{total} skip {1 - kept / total:.4f}")
     assert 0 < kept < total and torch.isfinite(e2.grad).all() and torch.isfinite(c2.grad).all()
+
+
+def test_config_c3_full_size_moderate_peak_sampled_grads(m, cuda):
+    """c3 at full size (N=8192, D=4096, V=128256, bf16, filter on) with the target boost
+    lowered from 40 to 12 so the softmax is peaked but the gradients are not ~0.
+
+    Checks, with the filter on:
+      * the kept-tile count equals the filter predicate evaluated on the CPU from the
+        kernel's own fp32 tile_max / lse (exact);
+      * dE on sampled rows against float64 G_r . C restricted to the kept tiles
+        (2e-2 relative Frobenius, bf16);
+      * dC on sampled vocabulary rows (hot Zipf targets, untargeted and untouched rows)
+        against float64 G[:, v]^T . E restricted to the kept tiles, normalised by the
+        kernel's lse (itself checked against float64 on sampled rows, 8 ulp);
+      * <E, dE> = <C, dC> (both equal sum G * S; no bias) to 5e-3 relative.
+    """
+    w = workloads.make("c3", device="cuda", target_boost=12.0)
+    N, D, V = w["N"], w["D"], w["V"]
+    e = w["e"].reshape(N, D)
+    c, t = w["c"], w["targets"].reshape(N)
+    tm, ts, ntl, lse, nll = m._ext.forward(e, c, t, None, -100)
+    e2 = e.detach().clone().requires_grad_(True)
+    c2 = c.detach().clone().requires_grad_(True)
+    loss = m.linear_cross_entropy(e2, c2, t)
+    loss.backward()
+    torch.cuda.synchronize()
+    kept, total = m.last_tile_stats()
+    dE, dC = e2.grad, c2.grad
+
+    # kept-tile set, from the kernel's fp32 statistics (float32 comparison, as on the GPU)
+    tn = t.cpu().numpy()
+    d_nll = np.full(N, np.float32(1.0 / N), dtype=np.float32)
+    keep = O.keep_mask(tm.cpu().numpy(), lse.cpu().numpy(), tn, d_nll)
+    print(f"c3 boost 12: loss {loss.item():.4f} kept {kept}/{total} (cpu predicate {int(keep.sum())})")
+    assert int(keep.sum()) == kept and total == keep.size
+
+    cc = f64(c)
+    lse64 = f64(lse)
+    g = 1.0 / N
+
+    # dE rows
+    rows = np.array([0, 1, 127, 128, 4095, 5000, 8191])
+    S = O.logits(f64(e[rows]), cc)
+    ref_lse = O.logsumexp_rows(S)
+    ulp = np.spacing(np.float32(np.abs(ref_lse).max()))
+    np.testing.assert_allclose(lse64[rows], ref_lse, rtol=0, atol=8 * ulp)
+    G = g * np.exp(S - ref_lse[:, None])
+    G[np.arange(len(rows)), tn[rows]] -= g
+    mask = np.repeat(keep[:, rows // 128], 128, axis=0)[:V].T  # [rows, V]
+    refE = np.where(mask, G, 0.0) @ cc
+    errE = O.rel_fro(f64(dE[rows]), refE)
+
+    # dC vocabulary rows: the hottest targets, a mid-frequency one, an untargeted one, the last
+    ee = f64(e)
+    counts = np.bincount(tn, minlength=V)
+    untargeted = int(np.nonzero(counts == 0)[0][len(np.nonzero(counts == 0)[0]) // 2])
+    vs = np.array(sorted({0, 1, 2, 7, 63, 128, 1000, untargeted, V - 1}))
+    Sc = ee @ cc[vs].T  # [N, len(vs)]
+    Gc = g * np.exp(Sc - lse64[:, None])
+    Gc -= g * (tn[:, None] == vs[None, :])
+    maskc = np.repeat(keep[vs // 128, :], 128, axis=1)[:, :N].T  # [N, len(vs)]
+    refC = np.where(maskc, Gc, 0.0).T @ ee
+    errC = O.rel_fro(f64(dC[vs]), refC)
+
+    ip_e = float((e.double() * dE.double()).sum())
+    ip_c = float((c.double() * dC.double()).sum())
+    rel_ip = abs(ip_e - ip_c) / max(abs(ip_e), abs(ip_c))
+    print(f"c3 boost 12: dE rows {errE:.3e}  dC rows {errC:.3e}  <E,dE> {ip_e:.6e} <C,dC> {ip_c:.6e} ({rel_ip:.2e})")
+    assert errE < 2e-2 and errC < 2e-2
+    assert rel_ip < 5e-3
+    assert torch.isfinite(dE).all() and torch.isfinite(dC).all()
