@@ -66,46 +66,100 @@ __global__ __launch_bounds__(256) void bwd_filter_kernel(BwdArgs a) {
   if (lane == 0) a.flags[pair] = any ? 1 : 0;
 }
 
-// Inclusive prefix sum over 1024 threads (one value each), in LDS.
-__device__ __forceinline__ int block_scan_1024(int v, int* scan) {
-  const int tid = threadIdx.x;
-  scan[tid] = v;
-  __syncthreads();
-  for (int o = 1; o < 1024; o <<= 1) {
-    const int add = tid >= o ? scan[tid - o] : 0;
-    __syncthreads();
-    scan[tid] += add;
-    __syncthreads();
+// Inclusive prefix sum across the 64 lanes of a wave.
+__device__ __forceinline__ int wave_incl_scan(int v) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int u = __shfl_up(v, o);
+    if (lane >= o) v += u;
   }
-  return scan[tid];
+  return v;
 }
 
 // ---------------------------------------------------------------- 2. compaction, vocab-major
-// Thread t owns a contiguous range of pair indices (vt * nrb + rb).  Writes
-// list / slot_map / vt_start, the tile statistics, and the chunk plan: vocab
-// tile vt belongs to chunk vt_start[vt] / step, step = cap - nrb + 1.
+// One workgroup of 16 waves.  Pair indices (vt * nrb + rb) are taken in rounds of
+// 65536; thread t of a round owns the 64 consecutive pairs [64 t, 64 t + 64),
+// loaded as four 16-byte vectors.  Writes list / slot_map / vt_start, the tile
+// statistics, and the chunk plan: vocab tile vt belongs to chunk
+// vt_start[vt] / step, step = cap - nrb + 1.
 __global__ __launch_bounds__(1024) void bwd_compact_vt_kernel(BwdArgs a) {
-  __shared__ int scan[1024];
+  __shared__ int wsum[16];
   const int total = (int)a.plan.total, nrb = (int)a.plan.nrb, nvt = (int)a.plan.nvt;
-  const int tid = threadIdx.x;
-  const int per = (total + 1023) / 1024;
-  const int beg = min(tid * per, total);
-  const int end = min(beg + per, total);
-  int cnt = 0;
-  for (int i = beg; i < end; ++i) cnt += a.flags[i];
-  int pos = block_scan_1024(cnt, scan) - cnt;
-  for (int i = beg; i < end; ++i) {
-    if (i % nrb == 0) a.vt_start[i / nrb] = pos;
-    if (a.flags[i]) {
-      a.list[pos] = i;
-      a.slot_map[i] = pos;
-      ++pos;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  int carry = 0;
+  for (int base = 0; base < total; base += 65536) {
+    const int i0 = base + tid * 64;
+    uint32_t f[16];
+    if (i0 + 64 <= total) {
+      const u32x4* src = reinterpret_cast<const u32x4*>(a.flags + i0);  // i0 % 64 == 0: 16-byte aligned
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const u32x4 v = src[q];
+        f[4 * q] = v.x;
+        f[4 * q + 1] = v.y;
+        f[4 * q + 2] = v.z;
+        f[4 * q + 3] = v.w;
+      }
     } else {
-      a.slot_map[i] = -1;
+#pragma unroll
+      for (int w = 0; w < 16; ++w) {
+        uint32_t x = 0;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          const int i = i0 + 4 * w + b;
+          if (i < total) x |= (uint32_t)a.flags[i] << (8 * b);
+        }
+        f[w] = x;
+      }
     }
+    int cnt = 0;
+#pragma unroll
+    for (int w = 0; w < 16; ++w) cnt += __builtin_popcount(f[w]);  // flags are 0 / 1 bytes
+    const int incl = wave_incl_scan(cnt);
+    if (lane == 63) wsum[wave] = incl;
+    __syncthreads();
+    int wbase = 0, round_total = 0;
+#pragma unroll
+    for (int w = 0; w < 16; ++w) {
+      const int x = wsum[w];
+      wbase += w < wave ? x : 0;
+      round_total += x;
+    }
+    int pos = carry + wbase + incl - cnt;
+    if (i0 < total) {
+      int vt = i0 / nrb;
+      int rb = i0 - vt * nrb;
+      int sm[64];
+#pragma unroll
+      for (int k = 0; k < 64; ++k) {
+        const bool in = i0 + k < total;
+        const bool kept = in && ((f[k >> 2] >> (8 * (k & 3))) & 1u);
+        if (in && rb == 0) a.vt_start[vt] = pos;
+        sm[k] = kept ? pos : -1;
+        if (kept) a.list[pos++] = i0 + k;
+        if (++rb == nrb) {
+          rb = 0;
+          ++vt;
+        }
+      }
+      if (i0 + 64 <= total) {
+        int* dst = a.slot_map + i0;
+#pragma unroll
+        for (int q = 0; q < 16; ++q)
+          *reinterpret_cast<u32x4*>(dst + 4 * q) =
+              u32x4{(uint32_t)sm[4 * q], (uint32_t)sm[4 * q + 1], (uint32_t)sm[4 * q + 2], (uint32_t)sm[4 * q + 3]};
+      } else {
+#pragma unroll
+        for (int k = 0; k < 64; ++k)
+          if (i0 + k < total) a.slot_map[i0 + k] = sm[k];
+      }
+    }
+    carry += round_total;
+    __syncthreads();  // wsum is rewritten by the next round
   }
-  const int kept = scan[1023];
-  if (tid == 1023) {
+  const int kept = carry;
+  if (tid == 0) {
     a.vt_start[nvt] = kept;
     if (a.tile_stats) {
       a.tile_stats[0] = kept;
@@ -129,29 +183,55 @@ __global__ __launch_bounds__(1024) void bwd_compact_vt_kernel(BwdArgs a) {
 }
 
 // ---------------------------------------------------------------- 3. compaction, block-major
+// One workgroup of 16 waves.  Token blocks are taken 64 at a time, one per lane;
+// wave w walks the vocab tiles [w R, w R + R), R = ceil(nvt / 16), in order, so
+// each load reads 64 consecutive flags of one vocab tile.  A first pass counts
+// per (wave, block), a second writes rb_list / rb_vt in (block, vocab tile) order.
 __global__ __launch_bounds__(1024) void bwd_compact_rb_kernel(BwdArgs a) {
-  __shared__ int scan[1024];
-  const int total = (int)a.plan.total, nrb = (int)a.plan.nrb, nvt = (int)a.plan.nvt;
-  const int tid = threadIdx.x;
-  const int per = (total + 1023) / 1024;
-  const int beg = min(tid * per, total);
-  const int end = min(beg + per, total);
-  int cnt = 0;
-  for (int j = beg; j < end; ++j) {
-    const int rb = j / nvt, vt = j - rb * nvt;
-    cnt += a.flags[vt * nrb + rb];
-  }
-  int pos = block_scan_1024(cnt, scan) - cnt;
-  for (int j = beg; j < end; ++j) {
-    const int rb = j / nvt, vt = j - rb * nvt;
-    if (vt == 0) a.rb_start[rb] = pos;
-    if (a.flags[vt * nrb + rb]) {
-      a.rb_list[pos] = a.slot_map[vt * nrb + rb];
-      a.rb_vt[pos] = vt;
-      ++pos;
+  __shared__ int cnt_s[16][64];
+  __shared__ int colbase[65];
+  const int nrb = (int)a.plan.nrb, nvt = (int)a.plan.nvt;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int R = (nvt + 15) / 16;
+  const int vt_lo = min(wave * R, nvt), vt_hi = min(vt_lo + R, nvt);
+  int carry = 0;
+  for (int rb0 = 0; rb0 < nrb; rb0 += 64) {
+    const int rb = rb0 + lane;
+    const bool ok = rb < nrb;
+    int c = 0;
+    if (ok) {
+#pragma unroll 8
+      for (int vt = vt_lo; vt < vt_hi; ++vt) c += a.flags[(size_t)vt * nrb + rb];
     }
+    cnt_s[wave][lane] = c;
+    __syncthreads();
+    if (wave == 0) {
+      int tot = 0;
+#pragma unroll
+      for (int w = 0; w < 16; ++w) tot += cnt_s[w][lane];
+      const int incl = wave_incl_scan(tot);
+      const int st = carry + incl - tot;
+      if (ok) a.rb_start[rb] = st;
+      colbase[lane] = st;
+      if (lane == 63) colbase[64] = carry + incl;
+    }
+    __syncthreads();
+    if (ok) {
+      int pos = colbase[lane];
+      for (int w = 0; w < wave; ++w) pos += cnt_s[w][lane];
+      for (int vt = vt_lo; vt < vt_hi; ++vt) {
+        const size_t pr = (size_t)vt * nrb + rb;
+        if (a.flags[pr]) {
+          a.rb_list[pos] = a.slot_map[pr];
+          a.rb_vt[pos] = vt;
+          ++pos;
+        }
+      }
+    }
+    carry = colbase[64];
+    __syncthreads();  // cnt_s / colbase are rewritten by the next group
   }
-  if (tid == 1023) a.rb_start[nrb] = scan[1023];
+  if (tid == 0) a.rb_start[nrb] = carry;
 }
 
 // ---------------------------------------------------------------- LDS tiles of G

@@ -51,7 +51,7 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_tile_kernel(FwdArgs a, int n_
 
   const int64_t pitch = a.D * (int64_t)sizeof(T);
   Loop::run(reinterpret_cast<const char*>(a.c), a.V, (int64_t)vb * kFwdVocab, reinterpret_cast<const char*>(a.e),
-            a.N, (int64_t)tb * kFwdTokens, pitch, pitch, smem, acc);
+            a.N, (int64_t)tb * kFwdTokens, pitch, pitch, smem, acc, b & 7);
 
   // ---------------------------------------------------------------- epilogue
   // acc[i][j][r] holds logit(vocab = vbase + 32i + 8(r/4) + 4h + r%4,
@@ -133,27 +133,38 @@ __device__ __forceinline__ void lse_merge(float& M, float& S, float m, float s) 
   }
 }
 
-// 64 tokens per workgroup; the 4 waves split the vocabulary tiles 4 ways.
-__global__ __launch_bounds__(256) void lse_kernel(FwdArgs a, int nvt) {
-  __shared__ float sm[4][64];
-  __shared__ float ss[4][64];
+// 64 tokens per workgroup (one per lane, coalesced 256-byte rows); the 16 waves
+// split the vocabulary tiles 16 ways and each lane keeps 8 loads in flight.
+constexpr int kLseSplits = 16;
+__global__ __launch_bounds__(64 * kLseSplits) void lse_kernel(FwdArgs a, int nvt) {
+  __shared__ float sm[kLseSplits][64];
+  __shared__ float ss[kLseSplits][64];
   const int lane = threadIdx.x & 63;
   const int split = threadIdx.x >> 6;
   const int64_t tok = (int64_t)blockIdx.x * 64 + lane;
   float M = -INFINITY, S = 0.f;
   if (tok < a.N) {
-    for (int t = split; t < nvt; t += 4) {
-      const float m = a.tile_max[(size_t)t * a.N + tok];
-      const float s = a.tile_sum_exp[(size_t)t * a.N + tok];
-      lse_merge(M, S, m, s);
+    const float* tm = a.tile_max + tok;
+    const float* ts = a.tile_sum_exp + tok;
+    int t = split;
+    for (; t + 7 * kLseSplits < nvt; t += 8 * kLseSplits) {
+      float m[8], x[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        m[u] = tm[(size_t)(t + u * kLseSplits) * a.N];
+        x[u] = ts[(size_t)(t + u * kLseSplits) * a.N];
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) lse_merge(M, S, m[u], x[u]);
     }
+    for (; t < nvt; t += kLseSplits) lse_merge(M, S, tm[(size_t)t * a.N], ts[(size_t)t * a.N]);
   }
   sm[split][lane] = M;
   ss[split][lane] = S;
   __syncthreads();
   if (split == 0 && tok < a.N) {
 #pragma unroll
-    for (int k = 1; k < 4; ++k) lse_merge(M, S, sm[k][lane], ss[k][lane]);
+    for (int k = 1; k < kLseSplits; ++k) lse_merge(M, S, sm[k][lane], ss[k][lane]);
     const float l = M + __logf(S);
     a.lse[tok] = l;
     const int64_t tg = a.targets[tok];
@@ -183,7 +194,7 @@ static hipError_t forward_typed(const FwdArgs& a, hipStream_t s) {
   }
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
-  hipLaunchKernelGGL(lse_kernel, dim3((unsigned)((a.N + 63) / 64)), dim3(256), 0, s, a, nvt);
+  hipLaunchKernelGGL(lse_kernel, dim3((unsigned)((a.N + 63) / 64)), dim3(64 * kLseSplits), 0, s, a, nvt);
   return hipGetLastError();
 }
 
