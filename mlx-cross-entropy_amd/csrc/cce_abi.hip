@@ -71,8 +71,10 @@ int check_common(const char* fn, int dtype, const void* e, const void* c, const 
   if ((int64_t)elem_size(dtype) * D >= (int64_t)1 << 23)
     return fail(CCE_ERR_INVALID_ARGUMENT, "[%s] row of %lld bytes exceeds the 8 MiB limit", fn,
                 (long long)(elem_size(dtype) * D));
-  if (N >= ((int64_t)1 << 31) - 256 || V >= ((int64_t)1 << 31) - 256)
-    return fail(CCE_ERR_INVALID_ARGUMENT, "[%s] N and V must be below 2^31", fn);
+  if (N > ((int64_t)cce::kCompactMaxWords * cce::kBwdTokens))
+    return fail(CCE_ERR_INVALID_ARGUMENT, "[%s] N must be at most %lld tokens per call, got N=%lld", fn,
+                (long long)cce::kCompactMaxWords * cce::kBwdTokens, (long long)N);
+  if (V >= ((int64_t)1 << 31) - 256) return fail(CCE_ERR_INVALID_ARGUMENT, "[%s] V must be below 2^31", fn);
   const int64_t tiles = ((N + cce::kBwdTokens - 1) / cce::kBwdTokens) * ((V + cce::kBwdVocab - 1) / cce::kBwdVocab);
   if (tiles >= ((int64_t)1 << 31))
     return fail(CCE_ERR_INVALID_ARGUMENT, "[%s] N*V/16384 must be below 2^31", fn);
@@ -187,19 +189,18 @@ int cce_backward(int dtype, const void* e, const void* c, const void* bias, cons
   a.dE = dE;
   a.dC = dC;
   a.dBias = dBias;
-  a.flags = reinterpret_cast<uint8_t*>(ws + P.flags);
-  a.slot_map = reinterpret_cast<int*>(ws + P.slot_map);
-  a.list = reinterpret_cast<int*>(ws + P.list);
-  a.vt_start = reinterpret_cast<int*>(ws + P.vt_start);
-  a.rb_list = reinterpret_cast<int*>(ws + P.rb_list);
-  a.rb_vt = reinterpret_cast<int*>(ws + P.rb_vt);
+  a.bits = reinterpret_cast<uint32_t*>(ws + P.bits);
+  a.counts = reinterpret_cast<int*>(ws + P.counts);
   a.rb_start = reinterpret_cast<int*>(ws + P.rb_start);
-  a.chunk_vt = reinterpret_cast<int*>(ws + P.chunk_vt);
-  a.chunk_slot = reinterpret_cast<int*>(ws + P.chunk_slot);
-  a.w_tok = dE ? ws + P.w_tok : nullptr;
-  a.w_voc = dC ? ws + P.w_voc : nullptr;
+  a.slot_vt = reinterpret_cast<int*>(ws + P.slot_vt);
+  a.slot_rb = reinterpret_cast<int*>(ws + P.slot_rb);
+  a.vt_start = reinterpret_cast<int*>(ws + P.vt_start);
+  a.vt_slot = reinterpret_cast<int*>(ws + P.vt_slot);
+  a.g_task = reinterpret_cast<int*>(ws + P.g_task);
+  a.g_task_rb = reinterpret_cast<int*>(ws + P.g_task_rb);
+  a.gtile = (dE || dC) ? ws + P.gtile : nullptr;
   a.colsum = dBias ? reinterpret_cast<float*>(ws + P.colsum) : nullptr;
-  a.de_acc = (dE && P.max_chunks > 1) ? reinterpret_cast<float*>(ws + P.de_acc) : nullptr;
+  a.de_acc = (dE && P.n_chunks > 1) ? reinterpret_cast<float*>(ws + P.de_acc) : nullptr;
   a.tile_stats = tile_stats;
   a.plan = P;
   a.num_cus = cus;

@@ -111,6 +111,28 @@ __device__ __forceinline__ u32x4 gld16(const char* p) {
   return *reinterpret_cast<const u32x4*>(p);
 }
 
+// 16 bytes per lane from global memory into LDS (global_load_lds_dwordx4; the
+// wave's 64 lanes fill 1 KiB at LDS byte address `lds`, lane l at lds + 16 l).
+// Issued as inline assembly: the compiler then does not track the LDS write, so
+// it adds no conservative vmcnt wait in front of later LDS reads it cannot prove
+// disjoint (it would for the transposing reads).  The caller orders the DMA and
+// the reads of its LDS bytes with explicit vmcnt waits and barriers.
+__device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
+}
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)(p);
+}
+
+// Wave-uniform read of an int list written by an earlier kernel: through the
+// constant address space with a readfirstlane'd index the compiler emits a scalar
+// load (counted by lgkmcnt), so it never waits on the vector-memory counter that
+// tracks the LDS-DMA pipeline.
+__device__ __forceinline__ int ldu(const int* p, int i) {
+  return reinterpret_cast<const __attribute__((address_space(4))) int*>(reinterpret_cast<uintptr_t>(p))
+      [__builtin_amdgcn_readfirstlane(i)];
+}
+
 __device__ __forceinline__ f32x16 zero16() {
   f32x16 z;
 #pragma unroll
@@ -200,43 +222,66 @@ struct NTMainLoop {
                                              const char* __restrict__ B, int64_t b_rows, int64_t b_row0,
                                              int64_t pitch, int64_t kbytes, char* smem,
                                              f32x16 (&acc)[TI][TJ], int phase8 = 0) {
+    const int64_t seg[1] = {a_row0};
+    run_gather<ROWS_A>(A, a_rows, seg, B, b_rows, b_row0, pitch, kbytes, smem, acc, phase8);
+  }
+
+  // As run(), but A_blk is gathered from ROWS_A / A_SEG segments: rows
+  // [s * A_SEG, (s + 1) * A_SEG) of A_blk are rows [a_seg0[s], a_seg0[s] + A_SEG) of A.
+  template <int A_SEG>
+  static __device__ __forceinline__ void run_gather(const char* __restrict__ A, int64_t a_rows,
+                                                    const int64_t (&a_seg0)[ROWS_A / A_SEG],
+                                                    const char* __restrict__ B, int64_t b_rows, int64_t b_row0,
+                                                    int64_t pitch, int64_t kbytes, char* smem,
+                                                    f32x16 (&acc)[TI][TJ], int phase8 = 0) {
+    constexpr int NW = kThreads / 64;
+    constexpr int NSEG = ROWS_A / A_SEG;
+    static_assert(ROWS_A % A_SEG == 0 && A_SEG % (NW * RPL) == 0, "a load round must not straddle two segments");
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wa = wave % WA;
     const int wb = wave / WA;
 
-    // Load j of this wave fills rows [r0, r0 + RPL) of a stage, r0 = (wave*LPW + j)*RPL;
-    // lane l writes row r0 + l/kChunks, stored chunk l%kChunks, i.e. logical chunk
-    // (l%kChunks) ^ f(row).
-    const char* base[LPW];
+    // Load j of wave w fills rows [r0, r0 + RPL) of a stage, r0 = (j * NW + w) * RPL:
+    // which operand (and which segment of A) a load reads is then known at compile
+    // time.  Lane l writes row r0 + l/kChunks, stored chunk l%kChunks, i.e. logical
+    // chunk (l%kChunks) ^ f(row).  The source is the segment's wave-uniform base plus
+    // a per-lane 32-bit offset; rows past the operand's end are clamped to its last
+    // row (a segment always starts inside the operand).
+    const char* segb[NSEG + 1];
+#pragma unroll
+    for (int k = 0; k < NSEG; ++k) segb[k] = A + a_seg0[k] * pitch;
+    segb[NSEG] = B + b_row0 * pitch;
     uint32_t off[LPW];
-    uint32_t lds_row0[LPW];
+    uint32_t qb[LPW];
 #pragma unroll
     for (int j = 0; j < LPW; ++j) {
-      const int r0 = (wave * LPW + j) * RPL;
+      const int r0 = (j * NW + wave) * RPL;
       const int row = r0 + lane / kChunks;
       const uint32_t q = (uint32_t)(lane % kChunks) ^ slice_swz((uint32_t)row);
-      lds_row0[j] = (uint32_t)r0 * kSliceBytes;
-      if (row < ROWS_A) {
-        int64_t g = a_row0 + row;
+      qb[j] = q * 16;
+      int64_t g;
+      if (j * NW * RPL < ROWS_A) {
+        const int sg = (j * NW * RPL) / A_SEG;
+        g = a_seg0[sg] + (row - sg * A_SEG);
         g = g < a_rows ? g : a_rows - 1;
-        base[j] = A + g * pitch;
+        off[j] = (uint32_t)((g - a_seg0[sg]) * pitch) + q * 16;
       } else {
-        int64_t g = b_row0 + (row - ROWS_A);
+        g = b_row0 + (row - ROWS_A);
         g = g < b_rows ? g : b_rows - 1;
-        base[j] = B + g * pitch;
+        off[j] = (uint32_t)((g - b_row0) * pitch) + q * 16;
       }
-      off[j] = q * 16;
     }
+    const uint32_t lds_w = (uint32_t)(wave * RPL * kSliceBytes);
     const int KT = (int)((kbytes + kSliceBytes - 1) / kSliceBytes);
     const int arow = wa * (ROWS_A / WA) + (lane & 31);
     const int brow = ROWS_A + wb * (ROWS_B / WB) + (lane & 31);
     const int kg = lane >> 5;
     const int kskew = (int)(((int64_t)(phase8 & 7) * KT) >> 3);
     if (kbytes % kSliceBytes == 0) {
-      loop<false>(base, off, lds_row0, kbytes, KT, kskew, smem, arow, brow, kg, acc);
+      loop<false, NSEG>(segb, off, qb, lds_w, kbytes, KT, kskew, smem, arow, brow, kg, acc);
     } else {
-      loop<true>(base, off, lds_row0, kbytes, KT, kskew, smem, arow, brow, kg, acc);
+      loop<true, NSEG>(segb, off, qb, lds_w, kbytes, KT, kskew, smem, arow, brow, kg, acc);
     }
   }
 
@@ -251,9 +296,10 @@ struct NTMainLoop {
   // follow the DMA in program order are held behind all of it, and the MFMAs of
   // step 1 would then wait on their own operands.
   // Slices past the end are clamped to the last one (harmless reloads into idle stages).
-  template <bool RAGGED>
-  static __device__ __forceinline__ void loop(const char* const (&base)[LPW], const uint32_t (&off)[LPW],
-                                              const uint32_t (&lds_row0)[LPW], int64_t kbytes, int KT, int kskew,
+  template <bool RAGGED, int NSEG>
+  static __device__ __forceinline__ void loop(const char* const (&segb)[NSEG + 1], const uint32_t (&off)[LPW],
+                                              const uint32_t (&qb)[LPW], uint32_t lds_w,
+                                              int64_t kbytes, int KT, int kskew,
                                               char* smem, int arow, int brow, int kg, f32x16 (&acc)[TI][TJ]) {
     auto issue = [&](int kt) {
       kt = kt < KT ? kt : KT - 1;
@@ -263,12 +309,15 @@ struct NTMainLoop {
       const int64_t k0 = (int64_t)kr * kSliceBytes;
 #pragma unroll
       for (int j = 0; j < LPW; ++j) {
-        const char* g = base[j] + k0 + off[j];
+        constexpr int NW = kThreads / 64;
+        const int sg = j * NW * RPL < ROWS_A ? (j * NW * RPL) / (ROWS_A / NSEG) : NSEG;
+        const char* g = (segb[sg] + k0) + off[j];
         if constexpr (RAGGED) {
-          if (k0 + (int64_t)off[j] >= kbytes) g = reinterpret_cast<const char*>(g_zero16);
+          if (k0 + (int64_t)qb[j] >= kbytes) g = reinterpret_cast<const char*>(g_zero16);
         }
-        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(g),
-                                         (__attribute__((address_space(3))) void*)(st + lds_row0[j]), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(
+            reinterpret_cast<const void*>(g),
+            (__attribute__((address_space(3))) void*)(st + lds_w + j * NW * RPL * kSliceBytes), 16, 0, 0);
       }
     };
     auto frags = [&](const char* s, int ks, u32x4 (&af)[TI], u32x4 (&bf)[TJ]) {

@@ -4,6 +4,9 @@
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <stdlib.h>
+
+#include <cstdlib>
 
 namespace cce {
 
@@ -31,21 +34,28 @@ struct FwdArgs {
   float* nll;
 };
 
-// Backward work plan: kept (vocab tile, token block) pairs get consecutive
-// "slots" in vocab-major order; the slots are processed in chunks of at most
-// `cap` whose boundaries fall between vocabulary tiles, so that every vocab tile
-// (and its dC rows) belongs to exactly one chunk.  Each chunk's G tiles live in
-// a bounded scratch of `cap` slots.
+// Backward work plan.  Kept (token block, vocabulary tile) pairs are found by the
+// filter as a bitmap, one bit per pair, rows by token block.  The vocabulary is
+// cut into chunks of `chunk_nvt` tiles (one chunk unless the problem is large);
+// per chunk the kept pairs get consecutive "slots" in (token block, vocab tile)
+// order, and every slot's 128 x 128 G tile lives in a scratch of `cap` slots.
+// A chunk holds every token block of its vocabulary tiles, so dC and dBias of a
+// chunk are final when its sums end; dE is carried between chunks in fp32.
 constexpr size_t kWScratchBudget = size_t(2) << 30;  // bytes of G-tile scratch per chunk
+constexpr int kCompactMaxWords = 8192;                 // bitmap words one compaction holds in LDS
+constexpr int kCompactMaxVt = 4096;                    // vocabulary tiles per chunk (LDS counts)
+constexpr int kSumDN = 256;                            // output columns (D) per sum task
 
 struct BwdPlan {
   int64_t nvt, nrb, total;  // vocab tiles, token blocks, pairs
-  int64_t cap;              // slots per chunk
-  int64_t max_chunks;       // upper bound on chunks (host launches this many)
-  int64_t n_dslices;        // 256-byte slices of a row of E / C
-  size_t w_bytes;           // bytes of one G tile in one layout (128 x 128 x sizeof(T))
+  int64_t nwords;           // 32-bit bitmap words per token block: ceil(nvt / 32)
+  int64_t chunk_nvt;        // vocab tiles per chunk (a multiple of 32 unless it is nvt)
+  int64_t n_chunks;
+  int64_t cap;              // slots per chunk: nrb * chunk_nvt
+  int64_t n_dslices;        // kSumDN-wide column slices of a row of E / C
+  size_t g_bytes;           // bytes of one G tile (128 x 128 x sizeof(T))
   // workspace byte offsets
-  size_t flags, slot_map, list, vt_start, rb_list, rb_vt, rb_start, chunk_vt, chunk_slot, w_tok, w_voc, colsum, de_acc;
+  size_t bits, counts, rb_start, slot_vt, slot_rb, vt_start, vt_slot, g_task, g_task_rb, gtile, colsum, de_acc;
   size_t total_bytes;
 };
 
@@ -57,38 +67,49 @@ inline BwdPlan make_bwd_plan(size_t esize, int64_t N, int64_t D, int64_t V, bool
   P.nvt = (V + kBwdVocab - 1) / kBwdVocab;
   P.nrb = (N + kBwdTokens - 1) / kBwdTokens;
   P.total = P.nvt * P.nrb;
-  P.w_bytes = (size_t)kBwdTokens * kBwdVocab * esize;
-  const size_t per_slot = (want_de ? P.w_bytes : 0) + (want_dc ? P.w_bytes : 0) +
-                          (want_db ? 2 * kBwdVocab * sizeof(float) : 0);
-  int64_t cap = per_slot ? (int64_t)(kWScratchBudget / per_slot) : P.total;
-  if (cap < 2 * P.nrb) cap = 2 * P.nrb;  // a chunk must hold any one vocab tile's token blocks
-  if (cap > P.total) cap = P.total;
-  P.cap = cap;
-  // Vocab tile vt goes to chunk vt_start[vt] / step (computed on the device); a chunk then
-  // spans fewer than step + nrb slots, i.e. at most cap, and there are at most
-  // total / step + 1 chunks.  With cap == total everything fits one chunk.
-  const int64_t step = cap - P.nrb + 1;
-  P.max_chunks = (cap == P.total) ? 1 : P.total / step + 1;
-  P.n_dslices = (D * (int64_t)esize + 255) / 256;
+  P.nwords = (P.nvt + 31) / 32;
+  P.g_bytes = (size_t)kBwdTokens * kBwdVocab * esize;
+  const bool want_g = want_de || want_dc;
+  // Chunk width: bounded by the G scratch budget (a chunk may keep every pair),
+  // the compaction's LDS bitmap, and its per-tile counts; at least 32 tiles.
+  int64_t cw = P.nvt;
+  if (want_g) {
+    const int64_t by_budget = (int64_t)(kWScratchBudget / P.g_bytes) / P.nrb;
+    cw = cw < by_budget ? cw : by_budget;
+  }
+  const int64_t by_lds = 32 * (kCompactMaxWords / P.nrb);
+  cw = cw < by_lds ? cw : by_lds;
+  cw = cw < kCompactMaxVt ? cw : kCompactMaxVt;
+  // Test hook: CCE_TEST_CHUNK_VT narrows the chunks (rounded down to a multiple of 32)
+  // so that the multi-chunk path runs at small sizes.
+  if (const char* env = std::getenv("CCE_TEST_CHUNK_VT")) {
+    const long long t = std::atoll(env);
+    if (t > 0 && t < cw) cw = t;
+  }
+  if (cw < P.nvt) cw = cw / 32 * 32;
+  if (cw < 32) cw = P.nvt < 32 ? P.nvt : 32;
+  P.chunk_nvt = cw;
+  P.n_chunks = (P.nvt + cw - 1) / cw;
+  P.cap = P.nrb * cw;
+  P.n_dslices = (D + kSumDN - 1) / kSumDN;
   size_t off = 0;
   auto take = [&](size_t bytes) {
     const size_t o = off;
     off += plan_align(bytes);
     return o;
   };
-  P.flags = take((size_t)P.total);
-  P.slot_map = take((size_t)P.total * 4);
-  P.list = take((size_t)P.total * 4);
-  P.vt_start = take((size_t)(P.nvt + 1) * 4);
-  P.rb_list = take((size_t)P.total * 4);
-  P.rb_vt = take((size_t)P.total * 4);
+  P.bits = take((size_t)P.nrb * P.nwords * 4);
+  P.counts = take(16 * 4);
   P.rb_start = take((size_t)(P.nrb + 1) * 4);
-  P.chunk_vt = take((size_t)(P.max_chunks + 1) * 4);
-  P.chunk_slot = take((size_t)(P.max_chunks + 1) * 4);
-  P.w_tok = want_de ? take((size_t)cap * P.w_bytes) : 0;
-  P.w_voc = want_dc ? take((size_t)cap * P.w_bytes) : 0;
-  P.colsum = want_db ? take((size_t)cap * 2 * kBwdVocab * sizeof(float)) : 0;
-  P.de_acc = (want_de && P.max_chunks > 1) ? take((size_t)N * (size_t)D * sizeof(float)) : 0;
+  P.slot_vt = take((size_t)P.cap * 4);
+  P.slot_rb = take((size_t)P.cap * 4);
+  P.vt_start = take((size_t)(cw + 1) * 4);
+  P.vt_slot = take((size_t)P.cap * 4);
+  P.g_task = take((size_t)P.cap * 4);
+  P.g_task_rb = take((size_t)P.cap * 4);
+  P.gtile = want_g ? take((size_t)P.cap * P.g_bytes) : 0;
+  P.colsum = want_db ? take((size_t)P.cap * kBwdVocab * sizeof(float)) : 0;
+  P.de_acc = (want_de && P.n_chunks > 1) ? take((size_t)N * (size_t)D * sizeof(float)) : 0;
   P.total_bytes = off;
   return P;
 }
@@ -108,20 +129,19 @@ struct BwdArgs {
   void* dE;     // output, dtype, or null
   void* dC;     // output, dtype, or null
   void* dBias;  // output, dtype, or null
-  // workspace (see BwdPlan)
-  uint8_t* flags;     // [nvt * nrb], index vt * nrb + rb
-  int* slot_map;      // [nvt * nrb] slot of a kept pair, -1 otherwise
-  int* list;          // [nvt * nrb] slot -> pair, vocab-major
-  int* vt_start;      // [nvt + 1] first slot of each vocab tile
-  int* rb_list;       // [nvt * nrb] slots ordered by token block, then vocab tile
-  int* rb_vt;         // [nvt * nrb] vocab tile of each rb_list entry
-  int* rb_start;      // [nrb + 1]
-  int* chunk_vt;      // [max_chunks + 1] first vocab tile of each chunk
-  int* chunk_slot;    // [max_chunks + 1] first slot of each chunk
-  char* w_tok;        // [cap][128 tokens][128 vocab] G tiles, token-major
-  char* w_voc;        // [cap][128 vocab][128 tokens] G tiles, vocab-major
-  float* colsum;      // [cap][2][128] per-tile column sums of G (two token halves)
-  float* de_acc;      // [N, D] fp32, only when max_chunks > 1
+  // workspace (see BwdPlan); the lists are rebuilt for every chunk
+  uint32_t* bits;     // [nrb][nwords] keep bitmap, bit b of word w = vocab tile 32 w + b
+  int* counts;        // [0] kept pairs of the chunk, [1] G tasks of the chunk
+  int* rb_start;      // [nrb + 1] first slot of each token block
+  int* slot_vt;       // [cap] chunk-local vocab tile of each slot
+  int* slot_rb;       // [cap] token block of each slot
+  int* vt_start;      // [chunk_nvt + 1] first entry of each vocab tile in vt_slot
+  int* vt_slot;       // [cap] slots grouped by vocab tile, token blocks ascending
+  int* g_task;        // [cap] first slot of each G task (up to 4 slots of one token block)
+  int* g_task_rb;     // [cap] token block of each G task
+  char* gtile;        // [cap][128 tokens][128 vocab] G tiles, token-major, dtype
+  float* colsum;      // [cap][128] per-slot column sums of G (dBias)
+  float* de_acc;      // [N, D] fp32, only when n_chunks > 1
   int64_t* tile_stats;  // [2] or null
   BwdPlan plan;
   int num_cus;

@@ -311,6 +311,41 @@ def test_filter_disabled_is_dense(m, cuda):
     assert kept == total == 2 * 32
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("filtered", [False, True])
+def test_vocabulary_chunks(m, cuda, dtype, filtered, monkeypatch):
+    """Several vocabulary chunks (forced narrow through CCE_TEST_CHUNK_VT): dE carried in fp32
+    between chunks, dC / dBias final per chunk; equal to the single-chunk result and the oracle.
+    D = 264 also leaves a ragged second column slice."""
+    N, D, V = 300, 264, 9000
+    if filtered:
+        e, c, t = _peaked(cuda, N=N, D=D, V=V, dtype=dtype, seed=11)
+    else:
+        e, c, t = normal_case(N, D, V, dtype, cuda, seed=11, std=0.05)
+    t[7] = -100
+    b = (torch.randn(V, device=cuda) * 0.1).to(dtype)
+    feps = m.FILTER_LOG_EPS if filtered else None
+    one = run(m, e, c, t, b, reduction="sum", filter_eps=feps)
+    monkeypatch.setenv("CCE_TEST_CHUNK_VT", "32")
+    assert m._ext.workspace_size(e, c, True, True, True) != 0
+    many = run(m, e, c, t, b, reduction="sum", filter_eps=feps)
+    monkeypatch.delenv("CCE_TEST_CHUNK_VT")
+    np.testing.assert_allclose(f64(many[0]), f64(one[0]), rtol=1e-6)
+    tol_same = 1e-5 if dtype == torch.float32 else 1e-2  # fp32 partial sums per chunk reassociate
+    for x, y, name in zip(many[1:], one[1:], ("dE", "dC", "dBias")):
+        err = O.rel_fro(f64(x), f64(y))
+        print(f"chunked vs single {name}: {err:.2e}")
+        assert err < tol_same, (name, err)
+    if filtered:
+        return
+    rE, rC, rB = O.grads(f64(e), f64(c), t.cpu().numpy(), f64(b), "sum")
+    tol = 1e-4 if dtype == torch.float32 else 2e-2
+    for got, r, name in zip(many[1:], (rE, rC, rB), ("dE", "dC", "dBias")):
+        err = O.rel_fro(f64(got), r)
+        print(f"chunked vs oracle {name}: {err:.2e}")
+        assert err < tol, (name, err)
+
+
 # --------------------------------------------------- benchmark configurations
 def _cfg_check(m, name, scale, tol_grad):
     w = workloads.make(name, device="cuda", scale=scale)
