@@ -453,32 +453,57 @@ __device__ __forceinline__ uint32_t tr_off(uint32_t row, uint32_t byte) {
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 
-// MFMA fragment of column col0 + lane%32 of a [k][col] tile with rows of P bytes:
-// the contraction elements k0 + 8 (lane/32) + 0..7 (16-bit; two transposing reads)
-// or k0 + 4 (lane/32) + 0..3 (fp32; four 32-bit reads).
-template <typename T, int P>
-__device__ __forceinline__ u32x4 frag_tr(const char* region, int k0, int col0) {
+// Transposing fragment reads of a [k][col] tile with rows of P bytes (16-bit types).
+// The MFMA fragment of column col0 + lane%32 holds the contraction elements
+// k0 + 8 (lane/32) + 0..7: two ds_read_b64_tr_b16, where source lane s of each
+// 16-lane group g addresses row k0 + 8 (g/2) + 4 t + s/4 and columns
+// col0 + 16 (g%2) + 4 (s%4) .. +3.  For k0 a multiple of 16 the row's swizzle term
+// does not depend on k0 or t, so the address is a per-lane constant (tr_lane_off)
+// plus (k0 + 4 t) P.
+template <int P>
+__device__ __forceinline__ uint32_t tr_lane_off(int col0) {
   const int lane = threadIdx.x & 63;
+  const int g = lane >> 4, s = lane & 15;
+  const uint32_t row0 = (uint32_t)(8 * (g >> 1) + (s >> 2));
+  const uint32_t byte = (uint32_t)(col0 * 2 + 32 * (g & 1) + 8 * (s & 3));
+  return tr_off<P>(row0, byte);
+}
+
+__device__ __forceinline__ u32x4 frag_tr16(const char* p, uint32_t step_bytes) {
   u32x4 out;
-  if constexpr (sizeof(T) == 2) {
-    const int g = lane >> 4, s = lane & 15;
-    const uint32_t byte = (uint32_t)(col0 + 16 * (g & 1) + 4 * (s & 3)) * 2u;
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const uint32_t row = (uint32_t)(k0 + 8 * (g >> 1) + 4 * t + (s >> 2));
-      const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          (__attribute__((address_space(3))) s16x4*)(region + tr_off<P>(row, byte)));
-      const u32x2 w = __builtin_bit_cast(u32x2, v);
-      out[2 * t] = w.x;
-      out[2 * t + 1] = w.y;
-    }
-  } else {
-    const uint32_t byte = (uint32_t)(col0 + (lane & 31)) * 4u;
-    const uint32_t row = (uint32_t)(k0 + 4 * (lane >> 5));
-#pragma unroll
-    for (int q = 0; q < 4; ++q) out[q] = *reinterpret_cast<const uint32_t*>(region + tr_off<P>(row + q, byte));
+  for (int t = 0; t < 2; ++t) {
+    const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) s16x4*)(p + t * step_bytes));
+    const u32x2 w = __builtin_bit_cast(u32x2, v);
+    out[2 * t] = w.x;
+    out[2 * t + 1] = w.y;
   }
   return out;
+}
+
+// fp32: the fragment of column col0 + lane%32 holds k0 + 4 (lane/32) + 0..3, four
+// 32-bit reads.
+template <int P>
+__device__ __forceinline__ u32x4 frag_tr32(const char* region, int k0, int col0) {
+  const int lane = threadIdx.x & 63;
+  const uint32_t byte = (uint32_t)(col0 + (lane & 31)) * 4u;
+  const uint32_t row = (uint32_t)(k0 + 4 * (lane >> 5));
+  u32x4 out;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) out[q] = *reinterpret_cast<const uint32_t*>(region + tr_off<P>(row + q, byte));
+  return out;
+}
+
+// As dma16, with a wave-uniform 64-bit base and a per-lane 32-bit offset (saddr form).
+// The base is passed through readfirstlane so it is held in scalar registers.
+__device__ __forceinline__ void dma16_s(const char* sbase, uint32_t voff, uint32_t lds) {
+  const uint64_t v = reinterpret_cast<uint64_t>(sbase);
+  const uint64_t u = (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)v) |
+                     ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(v >> 32)) << 32);
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(u),
+               "s"(__builtin_amdgcn_readfirstlane(lds))
+               : "memory", "m0");
 }
 
 // Output of a finished dE / dC task: kWriteT stores the output dtype (single chunk,
@@ -497,6 +522,8 @@ enum WriteMode { kWriteT = 0, kStoreF32 = 1, kAddF32 = 2, kFinishT = 3 };
 // consumed, across task boundaries.  The vmcnt waits count the epilogue's stores:
 // buffer stores, issued unconditionally (out-of-range lanes are dropped by the
 // buffer's range check), so every epilogue issues exactly NSTORE of them per wave.
+// Every per-step address is a wave-uniform base plus a per-lane constant computed
+// once: DMA sources in the saddr form, fragment reads as constant LDS offsets.
 template <typename T, int PHASE>
 __global__ __launch_bounds__(kThreads, 1) void bwd_sum_kernel(BwdArgs a, int chunk) {
   using S = SumGeo<T>;
@@ -525,26 +552,37 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_kernel(BwdArgs a, int chu
 
   // This wave's DMA loads: XLW into the X region, GLW into the G region.  Per lane:
   // the region row it fills and the byte of the source row that belongs there.
-  uint32_t xrow[S::XLW], xcol[S::XLW], grow[S::GLW], gcol[S::GLW];
+  uint32_t xrow[S::XLW], xcol[S::XLW], xoff[S::XLW], goff[S::GLW];
 #pragma unroll
   for (int j = 0; j < S::XLW; ++j) {
     const uint32_t o = (uint32_t)(wave * S::XLW + j) * 1024u + lane * 16u;
     const uint32_t row = o / S::XP, pb = o % S::XP;
     xrow[j] = row;
     xcol[j] = tr_off<S::XP>(row, pb) - row * S::XP;  // the swizzle is an involution on the segment index
+    xoff[j] = (uint32_t)(row * pitch) + xcol[j];
   }
 #pragma unroll
   for (int j = 0; j < S::GLW; ++j) {
     const uint32_t o = (uint32_t)(wave * S::GLW + j) * 1024u + lane * 16u;
     if (PHASE == 0) {
       const uint32_t row = o / 128u, ch = (o % 128u) / 16u;
-      grow[j] = row;
-      gcol[j] = (ch ^ ((row ^ (row >> 3)) & 7u)) * 16u;
+      goff[j] = row * S::GTP + (ch ^ ((row ^ (row >> 3)) & 7u)) * 16u;
     } else {
       const uint32_t row = o / S::GTP, pb = o % S::GTP;
-      grow[j] = row;
-      gcol[j] = tr_off<S::GTP>(row, pb) - row * S::GTP;
+      goff[j] = tr_off<S::GTP>(row, pb);
     }
+  }
+  // Fragment read offsets within a stage (16-bit types).
+  uint32_t xo[4], go_t[2], go_n[2][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) xo[i] = tr_lane_off<S::XP>(wd * 128 + 32 * i);
+#pragma unroll
+  for (int jj = 0; jj < 2; ++jj) {
+    go_t[jj] = S::X_BYTES + tr_lane_off<S::GTP>(wm * 64 + 32 * jj);
+    const uint32_t row = (uint32_t)(wm * 64 + 32 * jj + n);
+    const uint32_t c = (row ^ (row >> 3)) & 7u;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) go_n[jj][ks] = S::X_BYTES + row * 128u + ((((uint32_t)(2 * ks + kg)) ^ c) << 4);
   }
 
   struct Cur {
@@ -575,8 +613,9 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_kernel(BwdArgs a, int chu
     return seek(c.q + nper, c);
   };
 
+  const uint32_t smem_lds = lds_addr(smem);
   auto issue = [&](const Cur& c, int st) {
-    char* sb = smem + st * S::STAGE;
+    const uint32_t sb = smem_lds + (uint32_t)(st * S::STAGE);
     int slot;
     int64_t xr0;
     if (PHASE == 0) {
@@ -586,40 +625,51 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_kernel(BwdArgs a, int chu
       slot = ldu(a.vt_slot, c.b + c.j);
       xr0 = (int64_t)ldu(a.slot_rb, slot) * kBwdTokens + c.h * S::KS;
     }
-    const char* gsrc = a.gtile + (size_t)slot * a.plan.g_bytes;
     const int64_t dcol = (int64_t)c.ds * S::DN * ES;
+    const char* xbase = X + xr0 * pitch + dcol;
+    if (xr0 + S::KS <= xrows && dcol + S::DN * ES <= pitch) {
 #pragma unroll
-    for (int j = 0; j < S::XLW; ++j) {
-      int64_t r = xr0 + xrow[j];
-      r = r < xrows ? r : xrows - 1;
-      const int64_t cb = dcol + xcol[j];
-      const char* src = cb < pitch ? X + r * pitch + cb : reinterpret_cast<const char*>(g_zero16);
-      dma16(src, lds_addr(sb + (wave * S::XLW + j) * 1024));
-    }
+      for (int j = 0; j < S::XLW; ++j) dma16_s(xbase, xoff[j], sb + (wave * S::XLW + j) * 1024);
+    } else {  // last row block or ragged D slice: clamp rows, zeros past the row end
 #pragma unroll
-    for (int j = 0; j < S::GLW; ++j) {
-      const char* src = PHASE == 0 ? gsrc + grow[j] * S::GTP + c.h * 128 + gcol[j]
-                                   : gsrc + (c.h * S::KS + grow[j]) * S::GTP + gcol[j];
-      dma16(src, lds_addr(sb + S::X_BYTES + (wave * S::GLW + j) * 1024));
+      for (int j = 0; j < S::XLW; ++j) {
+        int64_t r = xr0 + xrow[j];
+        r = r < xrows ? r : xrows - 1;
+        const int64_t cb = dcol + xcol[j];
+        const char* src = cb < pitch ? X + r * pitch + cb : reinterpret_cast<const char*>(g_zero16);
+        dma16(src, sb + (wave * S::XLW + j) * 1024);
+      }
     }
+    const char* gbase = a.gtile + (size_t)slot * a.plan.g_bytes + (PHASE == 0 ? c.h * 128 : c.h * S::KS * S::GTP);
+#pragma unroll
+    for (int j = 0; j < S::GLW; ++j) dma16_s(gbase, goff[j], sb + S::X_BYTES + (wave * S::GLW + j) * 1024);
   };
 
   f32x16 acc[4][2];
   auto mma = [&](int st) {
-    const char* xr = smem + st * S::STAGE;
-    const char* gr = xr + S::X_BYTES;
+    const char* sp = smem + st * S::STAGE;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       u32x4 xf[4], gf[2];
+      if constexpr (ES == 2) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) xf[i] = frag_tr<T, S::XP>(xr, ks * S::KE, wd * 128 + 32 * i);
+        for (int i = 0; i < 4; ++i) xf[i] = frag_tr16(sp + xo[i] + 16 * ks * S::XP, 4 * S::XP);
 #pragma unroll
-      for (int jj = 0; jj < 2; ++jj) {
-        if (PHASE == 0) {
-          const uint32_t row = (uint32_t)(wm * 64 + 32 * jj + n);
-          gf[jj] = lds_ld16(gr, row * 128u + ((((uint32_t)(ks * 2 + kg)) ^ ((row ^ (row >> 3)) & 7u)) << 4));
-        } else {
-          gf[jj] = frag_tr<T, S::GTP>(gr, ks * S::KE, wm * 64 + 32 * jj);
+        for (int jj = 0; jj < 2; ++jj) {
+          if (PHASE == 0)
+            gf[jj] = lds_ld16(sp, go_n[jj][ks]);
+          else
+            gf[jj] = frag_tr16(sp + go_t[jj] + 16 * ks * S::GTP, 4 * S::GTP);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) xf[i] = frag_tr32<S::XP>(sp, ks * S::KE, wd * 128 + 32 * i);
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) {
+          if (PHASE == 0)
+            gf[jj] = lds_ld16(sp, go_n[jj][ks]);
+          else
+            gf[jj] = frag_tr32<S::GTP>(sp + S::X_BYTES, ks * S::KE, wm * 64 + 32 * jj);
         }
       }
 #pragma unroll
@@ -707,31 +757,33 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_kernel(BwdArgs a, int chu
   };
 #pragma unroll
   for (int p = 0; p < S::STAGES - 1; ++p) issue_next(p);
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int jj = 0; jj < 2; ++jj) acc[i][jj] = zero16();
 
+  // Tasks outside, their steps inside: the accumulators are zeroed once per task,
+  // so the step loop carries them only through MFMAs (no register copies), while
+  // issue_next keeps STAGES - 1 slices in flight across the task boundary.
   int st = 0;
   int since_store = S::STAGES;  // steps since the last epilogue that left stores in flight
   for (;;) {
-    if (since_store < S::STAGES)
-      stage_barrier<(S::STAGES - 2) * S::LPW + S::NSTORE>();
-    else
-      stage_barrier<(S::STAGES - 2) * S::LPW>();
-    issue_next((st + S::STAGES - 1) % S::STAGES);
-    mma(st);
-    ++since_store;
-    if (cs.h == S::SPT - 1 && cs.j == cs.cnt - 1) {
-      epilogue(cs);
-      if (mode == kWriteT) since_store = 1;
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int jj = 0; jj < 2; ++jj) acc[i][jj] = zero16();
+      for (int jj = 0; jj < 2; ++jj) acc[i][jj] = zero16();
+    for (;;) {
+      if (since_store < S::STAGES)
+        stage_barrier<(S::STAGES - 2) * S::LPW + S::NSTORE>();
+      else
+        stage_barrier<(S::STAGES - 2) * S::LPW>();
+      issue_next((st + S::STAGES - 1) % S::STAGES);
+      mma(st);
+      ++since_store;
+      st = st + 1 == S::STAGES ? 0 : st + 1;
+      if (++cs.h < S::SPT) continue;
+      cs.h = 0;
+      if (++cs.j == cs.cnt) break;
     }
-    if (!advance(cs)) break;
-    st = st + 1 == S::STAGES ? 0 : st + 1;
+    epilogue(cs);
+    if (mode == kWriteT) since_store = 1;
+    if (!seek(cs.q + nper, cs)) break;
   }
   wait_vmcnt<0>();
 }
