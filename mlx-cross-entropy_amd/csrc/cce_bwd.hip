@@ -182,19 +182,26 @@ __global__ __launch_bounds__(1024) void bwd_compact_kernel(BwdArgs a, int chunk)
     }
   }
 
-  // G tasks: each token block's slots in runs of at most 4
-  const int pr = (nrb + 1023) >> 10;
-  const int r0 = min(nrb, tid * pr), r1 = min(nrb, r0 + pr);
-  int nt = 0;
-  for (int rb = r0; rb < r1; ++rb) nt += (pre[(rb + 1) * cwd] - pre[rb * cwd] + 3) >> 2;
+  // G tasks: runs of at most 4 consecutive slots of one token block, ordered by run
+  // index first and token block second.  Tasks that run at the same time then read
+  // the same vocabulary tiles when the lists are dense, and every block's first run
+  // (its lowest, most shared tiles) is taken early.  Thread k (one per run index,
+  // kb <= 1024 of them) counts the blocks with more than k runs, the counts are
+  // scanned, and thread k writes its column.
+  const int kb = (nv + 3) >> 2;
+  int colc = 0;
+  if (tid < kb)
+    for (int rb = 0; rb < nrb; ++rb) colc += ((pre[(rb + 1) * cwd] - pre[rb * cwd] + 3) >> 2) > tid;
   int ntask;
-  int tb = block_excl_scan(nt, wsum, ntask);
-  for (int rb = r0; rb < r1; ++rb) {
-    const int end = pre[(rb + 1) * cwd];
-    for (int f = pre[rb * cwd]; f < end; f += 4) {
-      a.g_task[tb] = f;
-      a.g_task_rb[tb] = rb;
-      ++tb;
+  int tb = block_excl_scan(colc, wsum, ntask);
+  if (tid < kb) {
+    for (int rb = 0; rb < nrb; ++rb) {
+      const int first = pre[rb * cwd];
+      if (((pre[(rb + 1) * cwd] - first + 3) >> 2) > tid) {
+        a.g_task[tb] = first + 4 * tid;
+        a.g_task_rb[tb] = rb;
+        ++tb;
+      }
     }
   }
 
@@ -328,81 +335,88 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_g_kernel(BwdArgs a, int chunk
     if (wave >= cnt) continue;  // uniform per wave; the loop above ended with a barrier
 
     // w[i][j][r]: vocab v0 + 32 i + 8 (r/4) + 4 h + r%4, token t0 + 32 j + n.
+    // Per token: g (0 for masked / out-of-range rows), lz = lse log2(e), or +inf
+    // when g == 0 so that p = 0 and G = 0 without a select, and the target's place
+    // in the tile as tl - 4 h, which register (i, r) holds iff it equals
+    // 32 i + 8 (r/4) + r%4 (a compile-time constant).
     const int slot = s0 + wave;
     int64_t v0 = seg[0];
 #pragma unroll
     for (int k = 1; k < 4; ++k) v0 = wave == k ? seg[k] : v0;
     float g[4], lz[4];
-    int64_t tg[4];
+    int tl[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int64_t tok = t0 + j * 32 + n;
       g[j] = 0.f;
-      lz[j] = 0.f;
-      tg[j] = -1;
+      lz[j] = INFINITY;
+      tl[j] = -4096;
       if (tok < a.N) {
-        tg[j] = a.targets[tok];
-        g[j] = (a.has_ignore && tg[j] == a.ignore_index) ? 0.f : a.d_nll[tok];
-        lz[j] = a.lse[tok] * kLog2e;
+        const int64_t tg = a.targets[tok];
+        g[j] = (a.has_ignore && tg == a.ignore_index) ? 0.f : a.d_nll[tok];
+        if (g[j] != 0.f) lz[j] = a.lse[tok] * kLog2e;
+        const int64_t loc = tg - v0;
+        if (loc >= 0 && loc < kBwdVocab) tl[j] = (int)loc - 4 * h;
       }
     }
+    // Columns past V (last vocabulary tile) keep finite values: the dE sums read
+    // zeros for C rows past V, and dC / dBias are never written there.  One
+    // 32-column block i at a time: form its 64 G values per lane, store them
+    // token-major (4 consecutive vocab columns per store), add their column sums;
+    // only one block's values are live, which keeps the epilogue out of scratch.
+    char* gt = a.gtile + (size_t)slot * a.plan.g_bytes;
+    float* cs = WANT_DB ? a.colsum + (size_t)slot * kBwdVocab : nullptr;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
+      float gv[4][16];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int64_t v = v0 + i * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
-        const bool vok = v < a.V;
+        const int c = i * 32 + (r >> 2) * 8 + (r & 3);
         float add = 0.f;
-        if (HAS_BIAS) add = vok ? to_f32(bias[v]) : 0.f;
+        if (HAS_BIAS) {
+          const int64_t v = v0 + c + 4 * h;
+          add = v < a.V ? to_f32(bias[v]) * kLog2e : 0.f;
+        }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const float p = __builtin_amdgcn_exp2f(fmaf(w[i][j][r] + add, kLog2e, -lz[j]));
-          const float val = g[j] * (p - (v == tg[j] ? 1.f : 0.f));
-          w[i][j][r] = (vok && g[j] != 0.f) ? val : 0.f;
+          const float p = __builtin_amdgcn_exp2f(fmaf(w[i][j][r], kLog2e, add - lz[j]));
+          gv[j][r] = g[j] * p - (tl[j] == c ? g[j] : 0.f);
         }
       }
-    }
-    if constexpr (WANT_G) {
-      // token-major: row = token (32 j + n), 4 consecutive vocab columns per store
-      char* gt = a.gtile + (size_t)slot * a.plan.g_bytes;
+      if constexpr (WANT_G) {
+        // byte offsets within the 128 x 128 tile stay 32-bit: (32 j + n) rows of
+        // 128 ES bytes, plus (32 i + 8 q + 4 h) columns
+        const uint32_t lane_off = (uint32_t)(n * kBwdVocab * ES + h * 4 * ES);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        char* rowp = gt + (size_t)(j * 32 + n) * (kBwdVocab * ES);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int j = 0; j < 4; ++j) {
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
-            const int col = i * 32 + q * 8 + h * 4;
+            char* dst = gt + (lane_off + (uint32_t)((j * 32 * kBwdVocab + i * 32 + q * 8) * ES));
             if constexpr (ES == 4) {
-              *reinterpret_cast<f32x4*>(rowp + col * 4) =
-                  f32x4{w[i][j][q * 4], w[i][j][q * 4 + 1], w[i][j][q * 4 + 2], w[i][j][q * 4 + 3]};
+              *reinterpret_cast<f32x4*>(dst) = f32x4{gv[j][q * 4], gv[j][q * 4 + 1], gv[j][q * 4 + 2], gv[j][q * 4 + 3]};
             } else {
-              const T v0_ = (T)w[i][j][q * 4], v1_ = (T)w[i][j][q * 4 + 1];
-              const T v2_ = (T)w[i][j][q * 4 + 2], v3_ = (T)w[i][j][q * 4 + 3];
+              const T v0_ = (T)gv[j][q * 4], v1_ = (T)gv[j][q * 4 + 1];
+              const T v2_ = (T)gv[j][q * 4 + 2], v3_ = (T)gv[j][q * 4 + 3];
               const uint32_t p0 = (uint32_t)__builtin_bit_cast(uint16_t, v0_) |
                                   ((uint32_t)__builtin_bit_cast(uint16_t, v1_) << 16);
               const uint32_t p1 = (uint32_t)__builtin_bit_cast(uint16_t, v2_) |
                                   ((uint32_t)__builtin_bit_cast(uint16_t, v3_) << 16);
-              *reinterpret_cast<u32x2*>(rowp + col * 2) = u32x2{p0, p1};
+              *reinterpret_cast<u32x2*>(dst) = u32x2{p0, p1};
             }
           }
         }
       }
-    }
-    if constexpr (WANT_DB) {
-      // column sums over the block's 128 tokens; lanes n == 0 of each half hold them
-      float* cs = a.colsum + (size_t)slot * kBwdVocab;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      if constexpr (WANT_DB) {
+        // column sums over the block's 128 tokens; lanes n == 0 of each half hold them
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          float s = w[i][0][r] + w[i][1][r] + w[i][2][r] + w[i][3][r];
-          s += __shfl_xor(s, 1);
-          s += __shfl_xor(s, 2);
-          s += __shfl_xor(s, 4);
-          s += __shfl_xor(s, 8);
-          s += __shfl_xor(s, 16);
-          if (n == 0) cs[i * 32 + (r >> 2) * 8 + h * 4 + (r & 3)] = s;
+          float sm = gv[0][r] + gv[1][r] + gv[2][r] + gv[3][r];
+          sm += __shfl_xor(sm, 1);
+          sm += __shfl_xor(sm, 2);
+          sm += __shfl_xor(sm, 4);
+          sm += __shfl_xor(sm, 8);
+          sm += __shfl_xor(sm, 16);
+          if (n == 0) cs[i * 32 + (r >> 2) * 8 + h * 4 + (r & 3)] = sm;
         }
       }
     }
@@ -630,13 +644,12 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_kernel(BwdArgs a, int chu
     if (xr0 + S::KS <= xrows && dcol + S::DN * ES <= pitch) {
 #pragma unroll
       for (int j = 0; j < S::XLW; ++j) dma16_s(xbase, xoff[j], sb + (wave * S::XLW + j) * 1024);
-    } else {  // last row block or ragged D slice: clamp rows, zeros past the row end
+    } else {  // last row block or ragged D slice: zeros past the last row and the row end
 #pragma unroll
       for (int j = 0; j < S::XLW; ++j) {
-        int64_t r = xr0 + xrow[j];
-        r = r < xrows ? r : xrows - 1;
+        const int64_t r = xr0 + xrow[j];
         const int64_t cb = dcol + xcol[j];
-        const char* src = cb < pitch ? X + r * pitch + cb : reinterpret_cast<const char*>(g_zero16);
+        const char* src = (r < xrows && cb < pitch) ? X + r * pitch + cb : reinterpret_cast<const char*>(g_zero16);
         dma16(src, sb + (wave * S::XLW + j) * 1024);
       }
     }

@@ -210,11 +210,13 @@ struct NTMainLoop {
   static constexpr int TJ = ROWS_B / WB / 32;
   static constexpr int ROWS = ROWS_A + ROWS_B;
   static constexpr int RPL = 1024 / kSliceBytes;                 // rows filled by one LDS-DMA load
-  static constexpr int LPW = ROWS / RPL / (kThreads / 64);       // LDS-DMA loads per wave per stage
+  static constexpr int NW = WA * WB;                             // waves (64 NW threads)
+  static constexpr int NTHREADS = 64 * NW;
+  static constexpr int LPW = ROWS / RPL / NW;                    // LDS-DMA loads per wave per stage
   static constexpr int KSTEPS = kSliceBytes / 32;                // 32-byte MFMA steps per slice
   static constexpr uint32_t STAGE_BYTES = ROWS * kSliceBytes;
   static constexpr uint32_t SMEM_BYTES = kStages * STAGE_BYTES;
-  static_assert(LPW * RPL * (kThreads / 64) == ROWS, "stage must split evenly over the waves");
+  static_assert(LPW * RPL * NW == ROWS, "stage must split evenly over the waves");
   static_assert(ROWS_A % 32 == 0 && ROWS_B % 32 == 0, "rows must be multiples of 32");
   static_assert((kStages - 1) * LPW < 64, "in-flight loads must fit vmcnt");
 
@@ -234,7 +236,6 @@ struct NTMainLoop {
                                                     const char* __restrict__ B, int64_t b_rows, int64_t b_row0,
                                                     int64_t pitch, int64_t kbytes, char* smem,
                                                     f32x16 (&acc)[TI][TJ], int phase8 = 0) {
-    constexpr int NW = kThreads / 64;
     constexpr int NSEG = ROWS_A / A_SEG;
     static_assert(ROWS_A % A_SEG == 0 && A_SEG % (NW * RPL) == 0, "a load round must not straddle two segments");
     const int lane = threadIdx.x & 63;
@@ -309,7 +310,6 @@ struct NTMainLoop {
       const int64_t k0 = (int64_t)kr * kSliceBytes;
 #pragma unroll
       for (int j = 0; j < LPW; ++j) {
-        constexpr int NW = kThreads / 64;
         const int sg = j * NW * RPL < ROWS_A ? (j * NW * RPL) / (ROWS_A / NSEG) : NSEG;
         const char* g = (segb[sg] + k0) + off[j];
         if constexpr (RAGGED) {

@@ -20,10 +20,22 @@ namespace cce {
 
 static_assert(kStatTile == 128, "one wave covers one statistic tile");
 
+// Waves of the forward tile: 2 along the vocabulary (128 rows each, one statistic
+// tile) x kFwdWB along the tokens.  With kFwdWB = 4 two waves share each SIMD, so
+// one wave's LDS / barrier / epilogue stalls are covered by the other's MFMAs.
+#ifndef CCE_FWD_WB
+#define CCE_FWD_WB 4
+#endif
+constexpr int kFwdWB = CCE_FWD_WB;
+template <typename T>
+using FwdLoop = NTMainLoop<T, kFwdVocab, kFwdTokens, 2, kFwdWB>;  // A = C rows (vocab), B = E rows (tokens)
+
 template <typename T, bool HAS_BIAS>
-__global__ __launch_bounds__(kThreads, 1) void fwd_tile_kernel(FwdArgs a, int n_tok_blocks, int n_voc_blocks,
-                                                               int grid_padded, int nvt) {
-  using Loop = NTMainLoop<T, kFwdVocab, kFwdTokens, 2, 2>;  // A = C rows (vocab), B = E rows (tokens)
+__global__ __launch_bounds__(FwdLoop<T>::NTHREADS, 1) void fwd_tile_kernel(FwdArgs a, int n_tok_blocks,
+                                                                           int n_voc_blocks, int grid_padded,
+                                                                           int nvt) {
+  using Loop = FwdLoop<T>;
+  constexpr int TI = Loop::TI, TJ = Loop::TJ;
   __shared__ __attribute__((aligned(16))) char smem[Loop::SMEM_BYTES];
 
   // Tile order: workgroups are dealt round-robin to the 8 XCDs, so first make
@@ -43,11 +55,11 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_tile_kernel(FwdArgs a, int n_
   const int tb = first + local % gsize;
   const int vb = local / gsize;
 
-  f32x16 acc[4][4];
+  f32x16 acc[TI][TJ];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < TI; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = zero16();
+    for (int j = 0; j < TJ; ++j) acc[i][j] = zero16();
 
   const int64_t pitch = a.D * (int64_t)sizeof(T);
   Loop::run(reinterpret_cast<const char*>(a.c), a.V, (int64_t)vb * kFwdVocab, reinterpret_cast<const char*>(a.e),
@@ -59,11 +71,11 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_tile_kernel(FwdArgs a, int n_
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int wv = wave & 1;   // vocab half (NTMainLoop: wa = wave % 2)
-  const int wt = wave >> 1;  // token half
+  const int wt = wave >> 1;  // token part of kFwdTokens / kFwdWB rows
   const int n = lane & 31;
   const int h = lane >> 5;
   const int64_t vbase = (int64_t)vb * kFwdVocab + wv * 128;
-  const int64_t tbase = (int64_t)tb * kFwdTokens + wt * 128;
+  const int64_t tbase = (int64_t)tb * kFwdTokens + wt * (kFwdTokens / kFwdWB);
   const T* bias = reinterpret_cast<const T*>(a.bias);
 
 #pragma unroll
@@ -75,13 +87,13 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_tile_kernel(FwdArgs a, int n_
       float add = 0.f;
       if (HAS_BIAS) add = ok ? to_f32(bias[v]) : 0.f;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) acc[i][j][r] = ok ? acc[i][j][r] + add : -INFINITY;
+      for (int j = 0; j < TJ; ++j) acc[i][j][r] = ok ? acc[i][j][r] + add : -INFINITY;
     }
   }
 
   const int tile = (int)(vbase / kStatTile);
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < TJ; ++j) {
     const int64_t tok = tbase + j * 32 + n;
 
     float m = -INFINITY;
@@ -188,9 +200,9 @@ static hipError_t forward_typed(const FwdArgs& a, hipStream_t s) {
   const int total = ntb * nvb;
   const int grid = (total + 7) / 8 * 8;
   if (a.bias) {
-    hipLaunchKernelGGL((fwd_tile_kernel<T, true>), dim3(grid), dim3(kThreads), 0, s, a, ntb, nvb, grid, nvt);
+    hipLaunchKernelGGL((fwd_tile_kernel<T, true>), dim3(grid), dim3(FwdLoop<T>::NTHREADS), 0, s, a, ntb, nvb, grid, nvt);
   } else {
-    hipLaunchKernelGGL((fwd_tile_kernel<T, false>), dim3(grid), dim3(kThreads), 0, s, a, ntb, nvb, grid, nvt);
+    hipLaunchKernelGGL((fwd_tile_kernel<T, false>), dim3(grid), dim3(FwdLoop<T>::NTHREADS), 0, s, a, ntb, nvb, grid, nvt);
   }
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
