@@ -67,8 +67,11 @@ def main():
     ap.add_argument("--workload", default="c3", choices=["c1", "c2", "c3", "c4", "c5"])
     ap.add_argument("--filter", default="on", choices=["on", "off"])
     ap.add_argument("--cpu-baseline", default="on", choices=["on", "off"])
-    ap.add_argument("--cpu-rows", type=int, default=256)
-    ap.add_argument("--cpu-budget", type=float, default=20.0)
+    ap.add_argument("--cpu-rows", type=int, default=1024)
+    ap.add_argument("--cpu-budget", type=float, default=12.0)
+    ap.add_argument("--calib-copy-mib", type=int, default=0,
+                    help="after the timed steps, run one device-to-device copy of this many MiB: the known-size "
+                         "kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -127,6 +130,13 @@ def main():
     _ext.set_timing(False)
     peak_mem = torch.cuda.max_memory_allocated(dev)
     log(f"bench: {args.steps} steps in {elapsed:.3f} s")
+    if args.calib_copy_mib > 0:
+        src = torch.empty(args.calib_copy_mib << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"bench: calibration copy of {args.calib_copy_mib} MiB done")
+        del src, dst
 
     ms = elapsed * 1e3 / args.steps
     fwd_ms = statistics.mean(tm["forward"])
