@@ -114,7 +114,8 @@ int cce_forward(int dtype, const void* e, const void* c, const void* bias, const
                 "[cce_forward] tile_max, tile_sum_exp, neg_target_logit, lse and nll must be non-null");
   if (bias && !aligned(bias, elem_size(dtype)))
     return fail(CCE_ERR_INVALID_ARGUMENT, "[cce_forward] bias is not aligned to its element size");
-  if (num_cus_current() <= 0) return fail(CCE_ERR_NO_DEVICE, "[cce_forward] no HIP device is available");
+  const int cus = num_cus_current();
+  if (cus <= 0) return fail(CCE_ERR_NO_DEVICE, "[cce_forward] no HIP device is available");
 
   cce::FwdArgs a{};
   a.e = e;
@@ -131,6 +132,7 @@ int cce_forward(int dtype, const void* e, const void* c, const void* bias, const
   a.neg_target_logit = neg_target_logit;
   a.lse = lse;
   a.nll = nll;
+  a.num_cus = cus;
   hipError_t err = cce::launch_forward(dtype, a, reinterpret_cast<hipStream_t>(hip_stream));
   if (err != hipSuccess)
     return fail(CCE_ERR_LAUNCH, "[cce_forward] kernel launch failed: %s", hipGetErrorString(err));

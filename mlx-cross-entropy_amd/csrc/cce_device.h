@@ -193,17 +193,13 @@ __device__ __forceinline__ void stage_barrier() {
   asm volatile("" ::: "memory");
 }
 
-// acc[TI][TJ] = A_blk . B_blk^T over the full contraction length kbytes, where
-// A_blk = rows [a_row0, a_row0 + ROWS_A) of A (row pitch `pitch` bytes, rows past
-// a_rows-1 clamped to the last row) and B_blk likewise.  Waves are arranged
-// WA x WB; wave (wa, wb) owns A rows [wa*ROWS_A/WA, ...) and B rows
-// [wb*ROWS_B/WB, ...).  smem holds kStages stages of (ROWS_A + ROWS_B) x kSliceBytes.
-// The slices are visited starting at slice phase8 * KT / 8 and wrapping around
-// (phase8 in [0, 8)): workgroups on different XCDs then stream different columns
-// of the same rows at any moment, which spreads their L2 misses over more memory
-// channels (measured 5% faster forward than all XCDs in phase); workgroups on one
-// XCD share a phase so that they keep sharing slices in that XCD's L2.
-// Ends with a barrier, so the caller may reuse smem immediately.
+// The "NT" main loop: acc[TI][TJ] = A_blk . B_blk^T for a ROWS_A x ROWS_B block,
+// both operands row-major with the contraction contiguous, staged through LDS in
+// kStages stages of (ROWS_A + ROWS_B) x kSliceBytes by direct-to-LDS loads.
+// make_src() computes one block pair's per-lane sources, prefetch() issues the
+// pipeline fill and consume() runs the contraction; run() / run_gather() do all
+// three.  The phase rotation of the slices (make_src) measured 5% faster in the
+// forward than all XCDs streaming the same slice.
 template <typename T, int ROWS_A, int ROWS_B, int WA, int WB>
 struct NTMainLoop {
   static constexpr int TI = ROWS_A / WA / 32;
@@ -220,72 +216,106 @@ struct NTMainLoop {
   static_assert(ROWS_A % 32 == 0 && ROWS_B % 32 == 0, "rows must be multiples of 32");
   static_assert((kStages - 1) * LPW < 64, "in-flight loads must fit vmcnt");
 
-  static __device__ __forceinline__ void run(const char* __restrict__ A, int64_t a_rows, int64_t a_row0,
-                                             const char* __restrict__ B, int64_t b_rows, int64_t b_row0,
-                                             int64_t pitch, int64_t kbytes, char* smem,
-                                             f32x16 (&acc)[TI][TJ], int phase8 = 0) {
-    const int64_t seg[1] = {a_row0};
-    run_gather<ROWS_A>(A, a_rows, seg, B, b_rows, b_row0, pitch, kbytes, smem, acc, phase8);
-  }
+  // Per-lane sources of one operand block pair.  Load j of wave w fills rows
+  // [r0, r0 + RPL) of a stage, r0 = (j * NW + w) * RPL, so which operand (and which
+  // segment of A) a load reads is known at compile time.  Lane l writes row
+  // r0 + l/kChunks, stored chunk l%kChunks, i.e. logical chunk (l%kChunks) ^ f(row).
+  // The source is the segment's wave-uniform base plus a per-lane 32-bit offset;
+  // rows past the operand's end are clamped to its last row (a segment always
+  // starts inside the operand).
+  template <int NSEG>
+  struct Src {
+    const char* segb[NSEG + 1];
+    uint32_t off[LPW];
+    uint32_t qb[LPW];
+    int64_t kbytes;
+    int KT, kskew;
+  };
 
-  // As run(), but A_blk is gathered from ROWS_A / A_SEG segments: rows
-  // [s * A_SEG, (s + 1) * A_SEG) of A_blk are rows [a_seg0[s], a_seg0[s] + A_SEG) of A.
+  // Sources for A_blk gathered from ROWS_A / A_SEG segments (rows [s * A_SEG,
+  // (s + 1) * A_SEG) of A_blk are rows [a_seg0[s], a_seg0[s] + A_SEG) of A) and
+  // B_blk = rows [b_row0, b_row0 + ROWS_B) of B.  The slices are visited starting
+  // at slice phase8 * KT / 8 and wrapping around (phase8 in [0, 8)): workgroups on
+  // different XCDs then stream different columns of the same rows at any moment,
+  // which spreads their L2 misses over more memory channels; workgroups on one XCD
+  // share a phase so that they keep sharing slices in that XCD's L2.
   template <int A_SEG>
-  static __device__ __forceinline__ void run_gather(const char* __restrict__ A, int64_t a_rows,
-                                                    const int64_t (&a_seg0)[ROWS_A / A_SEG],
-                                                    const char* __restrict__ B, int64_t b_rows, int64_t b_row0,
-                                                    int64_t pitch, int64_t kbytes, char* smem,
-                                                    f32x16 (&acc)[TI][TJ], int phase8 = 0) {
+  static __device__ __forceinline__ Src<ROWS_A / A_SEG> make_src(const char* __restrict__ A, int64_t a_rows,
+                                                                 const int64_t (&a_seg0)[ROWS_A / A_SEG],
+                                                                 const char* __restrict__ B, int64_t b_rows,
+                                                                 int64_t b_row0, int64_t pitch, int64_t kbytes,
+                                                                 int phase8) {
     constexpr int NSEG = ROWS_A / A_SEG;
     static_assert(ROWS_A % A_SEG == 0 && A_SEG % (NW * RPL) == 0, "a load round must not straddle two segments");
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int wa = wave % WA;
-    const int wb = wave / WA;
-
-    // Load j of wave w fills rows [r0, r0 + RPL) of a stage, r0 = (j * NW + w) * RPL:
-    // which operand (and which segment of A) a load reads is then known at compile
-    // time.  Lane l writes row r0 + l/kChunks, stored chunk l%kChunks, i.e. logical
-    // chunk (l%kChunks) ^ f(row).  The source is the segment's wave-uniform base plus
-    // a per-lane 32-bit offset; rows past the operand's end are clamped to its last
-    // row (a segment always starts inside the operand).
-    const char* segb[NSEG + 1];
+    Src<NSEG> src;
 #pragma unroll
-    for (int k = 0; k < NSEG; ++k) segb[k] = A + a_seg0[k] * pitch;
-    segb[NSEG] = B + b_row0 * pitch;
-    uint32_t off[LPW];
-    uint32_t qb[LPW];
+    for (int k = 0; k < NSEG; ++k) src.segb[k] = A + a_seg0[k] * pitch;
+    src.segb[NSEG] = B + b_row0 * pitch;
 #pragma unroll
     for (int j = 0; j < LPW; ++j) {
       const int r0 = (j * NW + wave) * RPL;
       const int row = r0 + lane / kChunks;
       const uint32_t q = (uint32_t)(lane % kChunks) ^ slice_swz((uint32_t)row);
-      qb[j] = q * 16;
+      src.qb[j] = q * 16;
       int64_t g;
       if (j * NW * RPL < ROWS_A) {
         const int sg = (j * NW * RPL) / A_SEG;
         g = a_seg0[sg] + (row - sg * A_SEG);
         g = g < a_rows ? g : a_rows - 1;
-        off[j] = (uint32_t)((g - a_seg0[sg]) * pitch) + q * 16;
+        src.off[j] = (uint32_t)((g - a_seg0[sg]) * pitch) + q * 16;
       } else {
         g = b_row0 + (row - ROWS_A);
         g = g < b_rows ? g : b_rows - 1;
-        off[j] = (uint32_t)((g - b_row0) * pitch) + q * 16;
+        src.off[j] = (uint32_t)((g - b_row0) * pitch) + q * 16;
       }
     }
+    src.kbytes = kbytes;
+    src.KT = (int)((kbytes + kSliceBytes - 1) / kSliceBytes);
+    src.kskew = (int)(((int64_t)(phase8 & 7) * src.KT) >> 3);
+    return src;
+  }
+
+  // LDS-DMA loads of slice kt (clamped to the last slice: harmless reloads into
+  // idle stages) into stage kt % kStages.
+  template <bool RAGGED, int NSEG>
+  static __device__ __forceinline__ void issue(const Src<NSEG>& src, int kt, char* smem) {
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t lds_w = (uint32_t)(wave * RPL * kSliceBytes);
-    const int KT = (int)((kbytes + kSliceBytes - 1) / kSliceBytes);
-    const int arow = wa * (ROWS_A / WA) + (lane & 31);
-    const int brow = ROWS_A + wb * (ROWS_B / WB) + (lane & 31);
-    const int kg = lane >> 5;
-    const int kskew = (int)(((int64_t)(phase8 & 7) * KT) >> 3);
-    if (kbytes % kSliceBytes == 0) {
-      loop<false, NSEG>(segb, off, qb, lds_w, kbytes, KT, kskew, smem, arow, brow, kg, acc);
-    } else {
-      loop<true, NSEG>(segb, off, qb, lds_w, kbytes, KT, kskew, smem, arow, brow, kg, acc);
+    kt = kt < src.KT ? kt : src.KT - 1;
+    char* st = smem + (kt % kStages) * STAGE_BYTES;
+    int kr = kt + src.kskew;  // slice actually loaded: rotated by the phase
+    kr = kr < src.KT ? kr : kr - src.KT;
+    const int64_t k0 = (int64_t)kr * kSliceBytes;
+#pragma unroll
+    for (int j = 0; j < LPW; ++j) {
+      const int sg = j * NW * RPL < ROWS_A ? (j * NW * RPL) / (ROWS_A / NSEG) : NSEG;
+      const char* g = (src.segb[sg] + k0) + src.off[j];
+      if constexpr (RAGGED) {
+        if (k0 + (int64_t)src.qb[j] >= src.kbytes) g = reinterpret_cast<const char*>(g_zero16);
+      }
+      __builtin_amdgcn_global_load_lds(
+          reinterpret_cast<const void*>(g),
+          (__attribute__((address_space(3))) void*)(st + lds_w + j * NW * RPL * kSliceBytes), 16, 0, 0);
     }
   }
 
+  // Pipeline fill: the loads of the first kStages - 1 slices.  smem must be free
+  // (no wave still reads it); consume() then runs the contraction.  Issuing the
+  // fill early lets its latency overlap other work (a persistent kernel's
+  // epilogue of the previous tile).
+  template <bool RAGGED, int NSEG>
+  static __device__ __forceinline__ void prefetch(const Src<NSEG>& src, char* smem) {
+#pragma unroll
+    for (int p = 0; p < kStages - 1; ++p) issue<RAGGED>(src, p, smem);
+  }
+
+  // acc[TI][TJ] += A_blk . B_blk^T over the full contraction, after prefetch() of
+  // the same sources.  Waves are arranged WA x WB; wave (wa, wb) owns A rows
+  // [wa*ROWS_A/WA, ...) and B rows [wb*ROWS_B/WB, ...).  Ends with a barrier, so
+  // the caller may reuse smem immediately.
+  //
   // Iteration it consumes slice it (stage it % kStages, KSTEPS MFMA steps):
   //   read fragments of step 1 | issue the LDS-DMA loads of slice it + kStages - 1
   //   (into the stage freed by the previous iteration) | MFMAs of step 0
@@ -296,30 +326,16 @@ struct NTMainLoop {
   // compiler cannot tell the DMA's LDS writes from the reads, so reads that
   // follow the DMA in program order are held behind all of it, and the MFMAs of
   // step 1 would then wait on their own operands.
-  // Slices past the end are clamped to the last one (harmless reloads into idle stages).
   template <bool RAGGED, int NSEG>
-  static __device__ __forceinline__ void loop(const char* const (&segb)[NSEG + 1], const uint32_t (&off)[LPW],
-                                              const uint32_t (&qb)[LPW], uint32_t lds_w,
-                                              int64_t kbytes, int KT, int kskew,
-                                              char* smem, int arow, int brow, int kg, f32x16 (&acc)[TI][TJ]) {
-    auto issue = [&](int kt) {
-      kt = kt < KT ? kt : KT - 1;
-      char* st = smem + (kt % kStages) * STAGE_BYTES;
-      int kr = kt + kskew;  // slice actually loaded: rotated by the phase
-      kr = kr < KT ? kr : kr - KT;
-      const int64_t k0 = (int64_t)kr * kSliceBytes;
-#pragma unroll
-      for (int j = 0; j < LPW; ++j) {
-        const int sg = j * NW * RPL < ROWS_A ? (j * NW * RPL) / (ROWS_A / NSEG) : NSEG;
-        const char* g = (segb[sg] + k0) + off[j];
-        if constexpr (RAGGED) {
-          if (k0 + (int64_t)qb[j] >= kbytes) g = reinterpret_cast<const char*>(g_zero16);
-        }
-        __builtin_amdgcn_global_load_lds(
-            reinterpret_cast<const void*>(g),
-            (__attribute__((address_space(3))) void*)(st + lds_w + j * NW * RPL * kSliceBytes), 16, 0, 0);
-      }
-    };
+  static __device__ __forceinline__ void consume(const Src<NSEG>& src, char* smem, f32x16 (&acc)[TI][TJ]) {
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wa = wave % WA;
+    const int wb = wave / WA;
+    const int arow = wa * (ROWS_A / WA) + (lane & 31);
+    const int brow = ROWS_A + wb * (ROWS_B / WB) + (lane & 31);
+    const int kg = lane >> 5;
+    const int KT = src.KT;
     auto frags = [&](const char* s, int ks, u32x4 (&af)[TI], u32x4 (&bf)[TJ]) {
 #pragma unroll
       for (int ti = 0; ti < TI; ++ti) af[ti] = lds_ld16(s, slice_off(arow + ti * 32, ks * 2 + kg));
@@ -337,8 +353,6 @@ struct NTMainLoop {
     constexpr int NR = TI + TJ;
     constexpr int INFLIGHT = (kStages - 2) * LPW;  // loads allowed in flight at the barrier
 
-#pragma unroll
-    for (int p = 0; p < kStages - 1; ++p) issue(p);
     stage_barrier<INFLIGHT>();
     u32x4 fa0[TI], fb0[TJ], fa1[TI], fb1[TJ];
     frags(smem, 0, fa0, fb0);
@@ -346,7 +360,7 @@ struct NTMainLoop {
       const char* s = smem + (it % kStages) * STAGE_BYTES;
       const char* sn = smem + ((it + 1) % kStages) * STAGE_BYTES;
       frags(s, 1, fa1, fb1);
-      issue(it + kStages - 1);
+      issue<RAGGED>(src, it + kStages - 1, smem);
 #pragma unroll
       for (int ks = 0; ks + 1 < KSTEPS; ks += 2) {
         if (ks > 0) frags(s, ks + 1, fa1, fb1);
@@ -372,6 +386,35 @@ struct NTMainLoop {
     }
     wait_vmcnt<0>();
     __syncthreads();
+  }
+
+  // acc[TI][TJ] = A_blk . B_blk^T over the full contraction length kbytes, where
+  // A_blk = rows [a_row0, a_row0 + ROWS_A) of A (row pitch `pitch` bytes, rows past
+  // a_rows-1 clamped to the last row) and B_blk likewise.  smem holds kStages
+  // stages of (ROWS_A + ROWS_B) x kSliceBytes.
+  static __device__ __forceinline__ void run(const char* __restrict__ A, int64_t a_rows, int64_t a_row0,
+                                             const char* __restrict__ B, int64_t b_rows, int64_t b_row0,
+                                             int64_t pitch, int64_t kbytes, char* smem,
+                                             f32x16 (&acc)[TI][TJ], int phase8 = 0) {
+    const int64_t seg[1] = {a_row0};
+    run_gather<ROWS_A>(A, a_rows, seg, B, b_rows, b_row0, pitch, kbytes, smem, acc, phase8);
+  }
+
+  // As run(), with A_blk gathered from segments (see make_src).
+  template <int A_SEG>
+  static __device__ __forceinline__ void run_gather(const char* __restrict__ A, int64_t a_rows,
+                                                    const int64_t (&a_seg0)[ROWS_A / A_SEG],
+                                                    const char* __restrict__ B, int64_t b_rows, int64_t b_row0,
+                                                    int64_t pitch, int64_t kbytes, char* smem,
+                                                    f32x16 (&acc)[TI][TJ], int phase8 = 0) {
+    const auto src = make_src<A_SEG>(A, a_rows, a_seg0, B, b_rows, b_row0, pitch, kbytes, phase8);
+    if (kbytes % kSliceBytes == 0) {
+      prefetch<false>(src, smem);
+      consume<false>(src, smem, acc);
+    } else {
+      prefetch<true>(src, smem);
+      consume<true>(src, smem, acc);
+    }
   }
 };
 

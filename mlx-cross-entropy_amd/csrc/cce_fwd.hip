@@ -30,44 +30,31 @@ constexpr int kFwdWB = CCE_FWD_WB;
 template <typename T>
 using FwdLoop = NTMainLoop<T, kFwdVocab, kFwdTokens, 2, kFwdWB>;  // A = C rows (vocab), B = E rows (tokens)
 
-template <typename T, bool HAS_BIAS>
-__global__ __launch_bounds__(FwdLoop<T>::NTHREADS, 1) void fwd_tile_kernel(FwdArgs a, int n_tok_blocks,
-                                                                           int n_voc_blocks, int grid_padded,
-                                                                           int nvt) {
-  using Loop = FwdLoop<T>;
-  constexpr int TI = Loop::TI, TJ = Loop::TJ;
-  __shared__ __attribute__((aligned(16))) char smem[Loop::SMEM_BYTES];
+// Persistent schedule of the forward tiles.  The grid is 8 * cpx workgroups, one
+// per CU: the hardware deals workgroups to the 8 XCDs round-robin, so workgroup b
+// runs on XCD b % 8 as that XCD's member s = b / 8.  Tiles are grouped in rounds of
+// gt token blocks x gv vocabulary blocks (gt * gv = cpx), numbered token-group
+// major; XCD x takes rounds [x R / 8, (x + 1) R / 8).  In a round, member s
+// computes tile (token block tg gt + s % gt, vocabulary block vg gv + s / gt).
+// All members of an XCD do equal work per round, so they move through the rounds
+// together and stream the same gt E blocks and gv C blocks through that XCD's L2
+// at the same time; the XCDs sweep the vocabulary in step, so they share C blocks
+// in the infinity cache.
+struct FwdSched {
+  int ntb, nvb;     // token / vocabulary blocks
+  int gt, gv, ngv;  // round shape, vocabulary groups
+  int rounds;       // R
+  int nvt;          // statistic tiles
+};
 
-  // Tile order: workgroups are dealt round-robin to the 8 XCDs, so first make
-  // each XCD walk a contiguous range of logical tiles, then walk that range in
-  // groups of 4 token blocks so the 32 workgroups an XCD runs at once share
-  // 4 E blocks and 8 C blocks in its L2.
-  const int b = blockIdx.x;
-  const int pid = (b & 7) * (grid_padded >> 3) + (b >> 3);
-  const int total = n_tok_blocks * n_voc_blocks;
-  if (pid >= total) return;
-  constexpr int GROUP = 4;
-  const int per_group = GROUP * n_voc_blocks;
-  const int grp = pid / per_group;
-  const int first = grp * GROUP;
-  const int gsize = min(n_tok_blocks - first, GROUP);
-  const int local = pid - grp * per_group;
-  const int tb = first + local % gsize;
-  const int vb = local / gsize;
-
-  f32x16 acc[TI][TJ];
-#pragma unroll
-  for (int i = 0; i < TI; ++i)
-#pragma unroll
-    for (int j = 0; j < TJ; ++j) acc[i][j] = zero16();
-
-  const int64_t pitch = a.D * (int64_t)sizeof(T);
-  Loop::run(reinterpret_cast<const char*>(a.c), a.V, (int64_t)vb * kFwdVocab, reinterpret_cast<const char*>(a.e),
-            a.N, (int64_t)tb * kFwdTokens, pitch, pitch, smem, acc, b & 7);
-
-  // ---------------------------------------------------------------- epilogue
-  // acc[i][j][r] holds logit(vocab = vbase + 32i + 8(r/4) + 4h + r%4,
-  //                           token = tbase + 32j + n)   with n = lane%32, h = lane/32.
+// Epilogue of one tile, registers only: bias, ragged-vocabulary mask, per token
+// and 128-column tile the max and sum of exp(logit - max), and the target gather.
+// acc[i][j][r] holds logit(vocab = vbase + 32i + 8(r/4) + 4h + r%4,
+//                          token = tbase + 32j + n)   with n = lane%32, h = lane/32.
+template <typename T, bool HAS_BIAS, int TI, int TJ>
+__device__ __forceinline__ void fwd_epilogue(const FwdArgs& a, int nvt, f32x16 (&acc)[TI][TJ], int tb, int vb,
+                                             const int64_t (&tg)[TJ]) {
+  static_assert(TI == 4, "a wave covers one 128-column statistic tile");
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int wv = wave & 1;   // vocab half (NTMainLoop: wa = wave % 2)
@@ -76,19 +63,30 @@ __global__ __launch_bounds__(FwdLoop<T>::NTHREADS, 1) void fwd_tile_kernel(FwdAr
   const int h = lane >> 5;
   const int64_t vbase = (int64_t)vb * kFwdVocab + wv * 128;
   const int64_t tbase = (int64_t)tb * kFwdTokens + wt * (kFwdTokens / kFwdWB);
-  const T* bias = reinterpret_cast<const T*>(a.bias);
 
+  if constexpr (HAS_BIAS) {
+    const T* bias = reinterpret_cast<const T*>(a.bias);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < 4; ++i) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int64_t v = vbase + i * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
-      const bool ok = v < a.V;
-      float add = 0.f;
-      if (HAS_BIAS) add = ok ? to_f32(bias[v]) : 0.f;
+      for (int r = 0; r < 16; ++r) {
+        const int64_t v = vbase + i * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
+        const float add = v < a.V ? to_f32(bias[v]) : 0.f;
 #pragma unroll
-      for (int j = 0; j < TJ; ++j) acc[i][j][r] = ok ? acc[i][j][r] + add : -INFINITY;
+        for (int j = 0; j < TJ; ++j) acc[i][j][r] += add;
+      }
     }
+  }
+  if (vbase + 128 > a.V) {  // last vocabulary block only (uniform per wave)
+    const int lim = (int)(a.V - vbase) - 4 * h;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const bool ok = i * 32 + (r >> 2) * 8 + (r & 3) < lim;
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) acc[i][j][r] = ok ? acc[i][j][r] : -INFINITY;
+      }
   }
 
   const int tile = (int)(vbase / kStatTile);
@@ -116,9 +114,8 @@ __global__ __launch_bounds__(FwdLoop<T>::NTHREADS, 1) void fwd_tile_kernel(FwdAr
     }
 
     // Target gather: the lane holding (target, token) writes -(logit + bias).
-    const int64_t tg = tok < a.N ? a.targets[tok] : -1;
-    const int64_t loc = tg - vbase;
-    const bool hit = loc >= 0 && loc < 128 && tg < a.V;
+    const int64_t loc = tg[j] - vbase;
+    const bool hit = tok < a.N && loc >= 0 && loc < 128 && tg[j] < a.V;
     if (__any(hit)) {
       const int li = hit ? (int)loc : 0;
       const int ti = li >> 5;
@@ -132,6 +129,78 @@ __global__ __launch_bounds__(FwdLoop<T>::NTHREADS, 1) void fwd_tile_kernel(FwdAr
         for (int r = 0; r < 16; ++r) val = (i == ti && r == rt) ? acc[i][j][r] : val;
       if (hit && h == ht) a.neg_target_logit[tok] = -val;
     }
+  }
+}
+
+template <typename T, bool HAS_BIAS, bool RAGGED>
+__global__ __launch_bounds__(FwdLoop<T>::NTHREADS, 1) void fwd_tile_kernel(FwdArgs a, FwdSched sc) {
+  using Loop = FwdLoop<T>;
+  constexpr int TI = Loop::TI, TJ = Loop::TJ;
+  __shared__ __attribute__((aligned(16))) char smem[Loop::SMEM_BYTES];
+
+  const int xcd = blockIdx.x & 7;
+  const int member = blockIdx.x >> 3;
+  const int st = member % sc.gt, sv = member / sc.gt;
+  const int r_end = (int)((int64_t)(xcd + 1) * sc.rounds / 8);
+  // first round at or after r that holds a tile for this member (r_end if none)
+  auto next_round = [&](int r, int& tb, int& vb) {
+    for (; r < r_end; ++r) {
+      tb = (r / sc.ngv) * sc.gt + st;
+      vb = (r % sc.ngv) * sc.gv + sv;
+      if (tb < sc.ntb && vb < sc.nvb) break;
+    }
+    return r;
+  };
+  const int64_t pitch = a.D * (int64_t)sizeof(T);
+  const char* C = reinterpret_cast<const char*>(a.c);
+  const char* E = reinterpret_cast<const char*>(a.e);
+  auto sources = [&](int tb, int vb) {
+    const int64_t seg[1] = {(int64_t)vb * kFwdVocab};
+    return Loop::template make_src<kFwdVocab>(C, a.V, seg, E, a.N, (int64_t)tb * kFwdTokens, pitch, pitch, xcd);
+  };
+  // targets of this lane's tokens (clamped reads past N; the epilogue ignores them)
+  auto targets = [&](int tb, int64_t (&tg)[TJ]) {
+    const int64_t tbase = (int64_t)tb * kFwdTokens + (threadIdx.x >> 7) * (kFwdTokens / kFwdWB) + (threadIdx.x & 31);
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) {
+      const int64_t tok = tbase + j * 32;
+      tg[j] = a.targets[tok < a.N ? tok : a.N - 1];
+    }
+  };
+
+  int tb = 0, vb = 0;
+  int r = next_round((int)((int64_t)xcd * sc.rounds / 8), tb, vb);
+  if (r >= r_end) return;
+  auto src = sources(tb, vb);
+  Loop::template prefetch<RAGGED>(src, smem);
+  int64_t tg[TJ];
+  targets(tb, tg);
+
+  for (;;) {
+    f32x16 acc[TI][TJ];
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+      for (int j = 0; j < TJ; ++j) acc[i][j] = zero16();
+    Loop::template consume<RAGGED>(src, smem, acc);
+
+    // Start the next tile's pipeline fill and target reads, then reduce this
+    // tile from registers while they are in flight.
+    int tbn = tb, vbn = vb;
+    const int rn = next_round(r + 1, tbn, vbn);
+    int64_t tgn[TJ];
+    if (rn < r_end) {
+      src = sources(tbn, vbn);
+      Loop::template prefetch<RAGGED>(src, smem);
+      targets(tbn, tgn);
+    }
+    fwd_epilogue<T, HAS_BIAS>(a, sc.nvt, acc, tb, vb, tg);
+    if (rn >= r_end) break;
+    r = rn;
+    tb = tbn;
+    vb = vbn;
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) tg[j] = tgn[j];
   }
 }
 
@@ -194,19 +263,35 @@ __global__ __launch_bounds__(64 * kLseSplits) void lse_kernel(FwdArgs a, int nvt
 
 template <typename T>
 static hipError_t forward_typed(const FwdArgs& a, hipStream_t s) {
-  const int ntb = (int)((a.N + kFwdTokens - 1) / kFwdTokens);
-  const int nvb = (int)((a.V + kFwdVocab - 1) / kFwdVocab);
-  const int nvt = (int)((a.V + kStatTile - 1) / kStatTile);
-  const int total = ntb * nvb;
-  const int grid = (total + 7) / 8 * 8;
+  FwdSched sc{};
+  sc.ntb = (int)((a.N + kFwdTokens - 1) / kFwdTokens);
+  sc.nvb = (int)((a.V + kFwdVocab - 1) / kFwdVocab);
+  sc.nvt = (int)((a.V + kStatTile - 1) / kStatTile);
+  // members per XCD; a round is gt token blocks x gv vocabulary blocks
+  const int cpx = a.num_cus / 8 > 0 ? a.num_cus / 8 : 1;
+  sc.gt = (sc.ntb >= 4 && cpx % 4 == 0) ? 4 : (sc.ntb >= 2 && cpx % 2 == 0) ? 2 : 1;
+  sc.gv = cpx / sc.gt;
+  sc.ngv = (sc.nvb + sc.gv - 1) / sc.gv;
+  const int64_t ngt = (sc.ntb + sc.gt - 1) / sc.gt;
+  const int64_t rounds = ngt * sc.ngv;
+  if (rounds > INT32_MAX / 8) return hipErrorInvalidValue;
+  sc.rounds = (int)rounds;
+  const dim3 grid(8 * cpx), block(FwdLoop<T>::NTHREADS);
+  const bool ragged = (a.D * (int64_t)sizeof(T)) % kSliceBytes != 0;
   if (a.bias) {
-    hipLaunchKernelGGL((fwd_tile_kernel<T, true>), dim3(grid), dim3(FwdLoop<T>::NTHREADS), 0, s, a, ntb, nvb, grid, nvt);
+    if (ragged)
+      hipLaunchKernelGGL((fwd_tile_kernel<T, true, true>), grid, block, 0, s, a, sc);
+    else
+      hipLaunchKernelGGL((fwd_tile_kernel<T, true, false>), grid, block, 0, s, a, sc);
   } else {
-    hipLaunchKernelGGL((fwd_tile_kernel<T, false>), dim3(grid), dim3(FwdLoop<T>::NTHREADS), 0, s, a, ntb, nvb, grid, nvt);
+    if (ragged)
+      hipLaunchKernelGGL((fwd_tile_kernel<T, false, true>), grid, block, 0, s, a, sc);
+    else
+      hipLaunchKernelGGL((fwd_tile_kernel<T, false, false>), grid, block, 0, s, a, sc);
   }
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
-  hipLaunchKernelGGL(lse_kernel, dim3((unsigned)((a.N + 63) / 64)), dim3(64 * kLseSplits), 0, s, a, nvt);
+  hipLaunchKernelGGL(lse_kernel, dim3((unsigned)((a.N + 63) / 64)), dim3(64 * kLseSplits), 0, s, a, sc.nvt);
   return hipGetLastError();
 }
 

@@ -10,7 +10,7 @@
 
 namespace cce {
 
-// Forward workgroup tile: 256 tokens x 256 vocabulary rows (4 waves, each 128 x 128).
+// Forward workgroup tile: 256 tokens x 256 vocabulary rows.
 constexpr int kFwdTokens = 256;
 constexpr int kFwdVocab = 256;
 // Statistic / filter tile: 128 vocabulary columns (one wave's share of a forward tile).
@@ -32,6 +32,7 @@ struct FwdArgs {
   float* neg_target_logit;
   float* lse;
   float* nll;
+  int num_cus;  // compute units of the device (the persistent forward runs one workgroup per CU)
 };
 
 // Backward work plan.  Kept (token block, vocabulary tile) pairs are found by the

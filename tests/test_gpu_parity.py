@@ -77,7 +77,9 @@ def test_golden(m, cuda, path, dtype):
     loss, dE, dC, dB = run(m, e, c, t, b, red, int(z["ignore_index"]))
     tol_loss = 1e-5 if dtype == torch.float32 else 1e-3
     np.testing.assert_allclose(f64(loss), z["loss"], rtol=tol_loss, atol=1e-6)
-    tol = 1e-4 if dtype == torch.float32 else 2e-2
+    # fp32: the north-star bound with the filter off (1e-3).  The peaked fixture's target
+    # gradient p_t - 1 is ~0.02, so one ulp of lse moves dE by ~5e-5 relative.
+    tol = 1e-3 if dtype == torch.float32 else 2e-2
     for name, got, ref in (("dE", dE, z["dE"]), ("dC", dC, z["dC"])) + ((("dBias", dB, z["dBias"]),) if b is not None else ()):
         err = O.rel_fro(f64(got), ref)
         print(f"{os.path.basename(path)} {dtype} {name} rel_fro={err:.3e}")
