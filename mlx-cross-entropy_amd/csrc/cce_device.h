@@ -291,7 +291,12 @@ struct NTMainLoop {
 #pragma unroll
     for (int j = 0; j < LPW; ++j) {
       const int sg = j * NW * RPL < ROWS_A ? (j * NW * RPL) / (ROWS_A / NSEG) : NSEG;
-      const char* g = (src.segb[sg] + k0) + src.off[j];
+      // The per-lane offset passes through an empty asm so its zero extension stays
+      // next to the load: the address is then a scalar base plus a 32-bit VGPR (the
+      // saddr form), not a 64-bit VGPR pair kept live per load across the loop.
+      uint32_t o = src.off[j];
+      asm("" : "+v"(o));
+      const char* g = (src.segb[sg] + k0) + o;
       if constexpr (RAGGED) {
         if (k0 + (int64_t)src.qb[j] >= src.kbytes) g = reinterpret_cast<const char*>(g_zero16);
       }
