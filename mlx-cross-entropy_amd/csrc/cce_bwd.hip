@@ -294,132 +294,189 @@ __global__ __launch_bounds__(256) void bwd_empty_kernel(BwdArgs a, int chunk) {
 
 // ---------------------------------------------------------------- 4. G tiles
 // Task = up to 4 consecutive slots of one token block (its kept vocab tiles in this
-// chunk).  Wave w owns vocab tile w of the task: its 128 x 128 logits, recomputed
+// chunk).  The 128 x 128 logit tiles of the task's 4 vocab tiles are recomputed
 // with the forward's main loop over the gathered 512 C rows and the block's 128 E
-// rows.  Waves beyond the task's tile count compute a duplicate and store nothing.
-// Tasks are taken XCD-major (consecutive tasks, i.e. the same token block, on one
-// XCD) so the block's E rows are shared in that XCD's L2.
+// rows; 8 waves, wave (wa, wb) = (w % 4, w / 4) owns vocab tile wa and tokens
+// [64 wb, 64 wb + 64).  Waves whose vocab tile is beyond the task's count compute a
+// duplicate and store nothing.  The kernel is persistent: a workgroup issues the
+// next task's pipeline fill before it forms G of the current one.  Tasks are taken
+// XCD-major (consecutive tasks on one XCD) so tasks that run together share C rows
+// in that XCD's L2.
+using GLoopShape = NTMainLoop<__bf16, 4 * kBwdVocab, kBwdTokens, 4, 2>;
+constexpr int kGThreads = GLoopShape::NTHREADS;
+
 template <typename T, bool HAS_BIAS, bool WANT_G, bool WANT_DB>
-__global__ __launch_bounds__(kThreads, 1) void bwd_g_kernel(BwdArgs a, int chunk) {
-  using Loop = NTMainLoop<T, 4 * kBwdVocab, kBwdTokens, 4, 1>;  // A = 4 x 128 C rows, B = 128 E rows
+__global__ __launch_bounds__(kGThreads, 1) void bwd_g_kernel(BwdArgs a, int chunk) {
+  using Loop = NTMainLoop<T, 4 * kBwdVocab, kBwdTokens, 4, 2>;  // A = 4 x 128 C rows, B = 128 E rows
+  static_assert(Loop::NTHREADS == kGThreads, "one launch shape for every dtype");
+  constexpr int TI = Loop::TI, TJ = Loop::TJ;
+  static_assert(TI == 4 && TJ == 2, "wave tile: one vocab tile x 64 tokens");
   __shared__ __attribute__((aligned(16))) char smem[Loop::SMEM_BYTES];
   constexpr int ES = sizeof(T);
   const int ntask = ldu(a.counts, 1);
   const int vlo = chunk * (int)a.plan.chunk_nvt;
   const int xcd = (int)(blockIdx.x & 7), lidx = (int)(blockIdx.x >> 3), nper = (int)(gridDim.x >> 3);
-  const int lw = xcd * nper + lidx;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wa = wave & 3, wb = wave >> 2;
   const int n = lane & 31;
   const int h = lane >> 5;
   const int64_t pitch = a.D * (int64_t)ES;
   const T* bias = reinterpret_cast<const T*>(a.bias);
   const char* E = reinterpret_cast<const char*>(a.e);
   const char* C = reinterpret_cast<const char*>(a.c);
+  const bool ragged = pitch % kSliceBytes != 0;
 
-  for (int t = lw; t < ntask; t += (int)gridDim.x) {
-    const int s0 = ldu(a.g_task, t);
-    const int rb = ldu(a.g_task_rb, t);
-    const int cnt = min(4, ldu(a.rb_start, rb + 1) - s0);
+  struct Task {
+    int s0, rb, cnt;
     int64_t seg[4];
+  };
+  auto load_task = [&](int t, Task& k) {
+    k.s0 = ldu(a.g_task, t);
+    k.rb = ldu(a.g_task_rb, t);
+    k.cnt = min(4, ldu(a.rb_start, k.rb + 1) - k.s0);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) seg[i] = (int64_t)(vlo + ldu(a.slot_vt, s0 + (i < cnt ? i : cnt - 1))) * kBwdVocab;
-    const int64_t t0 = (int64_t)rb * kBwdTokens;
+    for (int i = 0; i < 4; ++i) k.seg[i] = (int64_t)(vlo + ldu(a.slot_vt, k.s0 + (i < k.cnt ? i : k.cnt - 1))) * kBwdVocab;
+  };
+  auto sources = [&](const Task& k) {
+    return Loop::template make_src<kBwdVocab>(C, a.V, k.seg, E, a.N, (int64_t)k.rb * kBwdTokens, pitch, pitch, xcd);
+  };
+  auto prefetch = [&](const typename Loop::template Src<4>& src) {
+    if (ragged)
+      Loop::template prefetch<true>(src, smem);
+    else
+      Loop::template prefetch<false>(src, smem);
+  };
 
-    f32x16 w[4][4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) w[i][j] = zero16();
-    Loop::template run_gather<kBwdVocab>(C, a.V, seg, E, a.N, t0, pitch, pitch, smem, w, (int)(blockIdx.x & 7));
-    if (wave >= cnt) continue;  // uniform per wave; the loop above ended with a barrier
+  int t = xcd * nper + lidx;  // logical task of this workgroup; advances by the grid size
+  if (t >= ntask) return;
+  Task cur;
+  load_task(t, cur);
+  auto src = sources(cur);
+  prefetch(src);
 
-    // w[i][j][r]: vocab v0 + 32 i + 8 (r/4) + 4 h + r%4, token t0 + 32 j + n.
+  for (;;) {
+    f32x16 w[TI][TJ];
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+      for (int j = 0; j < TJ; ++j) w[i][j] = zero16();
+    if (ragged)
+      Loop::template consume<true>(src, smem, w);
+    else
+      Loop::template consume<false>(src, smem, w);
+
+    const int tn = t + (int)gridDim.x;
+    Task nxt;
+    if (tn < ntask) {
+      load_task(tn, nxt);
+      src = sources(nxt);
+      prefetch(src);  // stage 0 only; the epilogue below uses stage 1's bytes
+    }
+
+    // w[i][j][r]: vocab v0 + 32 i + 8 (r/4) + 4 h + r%4, token t0 + 64 wb + 32 j + n.
     // Per token: g (0 for masked / out-of-range rows), lz = lse log2(e), or +inf
     // when g == 0 so that p = 0 and G = 0 without a select, and the target's place
     // in the tile as tl - 4 h, which register (i, r) holds iff it equals
     // 32 i + 8 (r/4) + r%4 (a compile-time constant).
-    const int slot = s0 + wave;
-    int64_t v0 = seg[0];
+    const bool active = wa < cur.cnt;  // uniform per wave
+    const int slot = cur.s0 + wa;
+    int64_t v0 = cur.seg[0];
 #pragma unroll
-    for (int k = 1; k < 4; ++k) v0 = wave == k ? seg[k] : v0;
-    float g[4], lz[4];
-    int tl[4];
+    for (int k = 1; k < 4; ++k) v0 = wa == k ? cur.seg[k] : v0;
+    const int64_t t0 = (int64_t)cur.rb * kBwdTokens;
+    float* red = reinterpret_cast<float*>(smem + Loop::STAGE_BYTES);  // [2 wb][4 wa][128] column sums
+    if (active) {
+      float g[TJ], lz[TJ];
+      int tl[TJ];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int64_t tok = t0 + j * 32 + n;
-      g[j] = 0.f;
-      lz[j] = INFINITY;
-      tl[j] = -4096;
-      if (tok < a.N) {
-        const int64_t tg = a.targets[tok];
-        g[j] = (a.has_ignore && tg == a.ignore_index) ? 0.f : a.d_nll[tok];
-        if (g[j] != 0.f) lz[j] = a.lse[tok] * kLog2e;
-        const int64_t loc = tg - v0;
-        if (loc >= 0 && loc < kBwdVocab) tl[j] = (int)loc - 4 * h;
-      }
-    }
-    // Columns past V (last vocabulary tile) keep finite values: the dE sums read
-    // zeros for C rows past V, and dC / dBias are never written there.  One
-    // 32-column block i at a time: form its 64 G values per lane, store them
-    // token-major (4 consecutive vocab columns per store), add their column sums;
-    // only one block's values are live, which keeps the epilogue out of scratch.
-    char* gt = a.gtile + (size_t)slot * a.plan.g_bytes;
-    float* cs = WANT_DB ? a.colsum + (size_t)slot * kBwdVocab : nullptr;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float gv[4][16];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int c = i * 32 + (r >> 2) * 8 + (r & 3);
-        float add = 0.f;
-        if (HAS_BIAS) {
-          const int64_t v = v0 + c + 4 * h;
-          add = v < a.V ? to_f32(bias[v]) * kLog2e : 0.f;
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float p = __builtin_amdgcn_exp2f(fmaf(w[i][j][r], kLog2e, add - lz[j]));
-          gv[j][r] = g[j] * p - (tl[j] == c ? g[j] : 0.f);
+      for (int j = 0; j < TJ; ++j) {
+        const int64_t tok = t0 + wb * 64 + j * 32 + n;
+        g[j] = 0.f;
+        lz[j] = INFINITY;
+        tl[j] = -4096;
+        if (tok < a.N) {
+          const int64_t tg = a.targets[tok];
+          g[j] = (a.has_ignore && tg == a.ignore_index) ? 0.f : a.d_nll[tok];
+          if (g[j] != 0.f) lz[j] = a.lse[tok] * kLog2e;
+          const int64_t loc = tg - v0;
+          if (loc >= 0 && loc < kBwdVocab) tl[j] = (int)loc - 4 * h;
         }
       }
-      if constexpr (WANT_G) {
-        // byte offsets within the 128 x 128 tile stay 32-bit: (32 j + n) rows of
-        // 128 ES bytes, plus (32 i + 8 q + 4 h) columns
-        const uint32_t lane_off = (uint32_t)(n * kBwdVocab * ES + h * 4 * ES);
+      // Columns past V (last vocabulary tile) keep finite values: the dE sums read
+      // zeros for C rows past V, and dC / dBias are never written there.  One
+      // 32-column block i at a time: form its 32 G values per lane, store them
+      // token-major (4 consecutive vocab columns per store), add their column sums.
+      char* gt = a.gtile + (size_t)slot * a.plan.g_bytes;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+      for (int i = 0; i < TI; ++i) {
+        float gv[TJ][16];
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            char* dst = gt + (lane_off + (uint32_t)((j * 32 * kBwdVocab + i * 32 + q * 8) * ES));
-            if constexpr (ES == 4) {
-              *reinterpret_cast<f32x4*>(dst) = f32x4{gv[j][q * 4], gv[j][q * 4 + 1], gv[j][q * 4 + 2], gv[j][q * 4 + 3]};
-            } else {
-              const T v0_ = (T)gv[j][q * 4], v1_ = (T)gv[j][q * 4 + 1];
-              const T v2_ = (T)gv[j][q * 4 + 2], v3_ = (T)gv[j][q * 4 + 3];
-              const uint32_t p0 = (uint32_t)__builtin_bit_cast(uint16_t, v0_) |
-                                  ((uint32_t)__builtin_bit_cast(uint16_t, v1_) << 16);
-              const uint32_t p1 = (uint32_t)__builtin_bit_cast(uint16_t, v2_) |
-                                  ((uint32_t)__builtin_bit_cast(uint16_t, v3_) << 16);
-              *reinterpret_cast<u32x2*>(dst) = u32x2{p0, p1};
+        for (int r = 0; r < 16; ++r) {
+          const int c = i * 32 + (r >> 2) * 8 + (r & 3);
+          float add = 0.f;
+          if (HAS_BIAS) {
+            const int64_t v = v0 + c + 4 * h;
+            add = v < a.V ? to_f32(bias[v]) * kLog2e : 0.f;
+          }
+#pragma unroll
+          for (int j = 0; j < TJ; ++j) {
+            const float p = __builtin_amdgcn_exp2f(fmaf(w[i][j][r], kLog2e, add - lz[j]));
+            gv[j][r] = g[j] * p - (tl[j] == c ? g[j] : 0.f);
+          }
+        }
+        if constexpr (WANT_G) {
+          // byte offsets within the 128 x 128 tile stay 32-bit: (64 wb + 32 j + n) rows
+          // of 128 ES bytes, plus (32 i + 8 q + 4 h) columns
+          const uint32_t lane_off = (uint32_t)((wb * 64 + n) * kBwdVocab * ES + h * 4 * ES);
+#pragma unroll
+          for (int j = 0; j < TJ; ++j) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              char* dst = gt + (lane_off + (uint32_t)((j * 32 * kBwdVocab + i * 32 + q * 8) * ES));
+              if constexpr (ES == 4) {
+                *reinterpret_cast<f32x4*>(dst) =
+                    f32x4{gv[j][q * 4], gv[j][q * 4 + 1], gv[j][q * 4 + 2], gv[j][q * 4 + 3]};
+              } else {
+                const T v0_ = (T)gv[j][q * 4], v1_ = (T)gv[j][q * 4 + 1];
+                const T v2_ = (T)gv[j][q * 4 + 2], v3_ = (T)gv[j][q * 4 + 3];
+                const uint32_t p0 = (uint32_t)__builtin_bit_cast(uint16_t, v0_) |
+                                    ((uint32_t)__builtin_bit_cast(uint16_t, v1_) << 16);
+                const uint32_t p1 = (uint32_t)__builtin_bit_cast(uint16_t, v2_) |
+                                    ((uint32_t)__builtin_bit_cast(uint16_t, v3_) << 16);
+                *reinterpret_cast<u32x2*>(dst) = u32x2{p0, p1};
+              }
             }
           }
         }
-      }
-      if constexpr (WANT_DB) {
-        // column sums over the block's 128 tokens; lanes n == 0 of each half hold them
+        if constexpr (WANT_DB) {
+          // column sums over this wave's 64 tokens; lanes n == 0 of each half hold them
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          float sm = gv[0][r] + gv[1][r] + gv[2][r] + gv[3][r];
-          sm += __shfl_xor(sm, 1);
-          sm += __shfl_xor(sm, 2);
-          sm += __shfl_xor(sm, 4);
-          sm += __shfl_xor(sm, 8);
-          sm += __shfl_xor(sm, 16);
-          if (n == 0) cs[i * 32 + (r >> 2) * 8 + h * 4 + (r & 3)] = sm;
+          for (int r = 0; r < 16; ++r) {
+            float sm = gv[0][r] + gv[1][r];
+            sm += __shfl_xor(sm, 1);
+            sm += __shfl_xor(sm, 2);
+            sm += __shfl_xor(sm, 4);
+            sm += __shfl_xor(sm, 8);
+            sm += __shfl_xor(sm, 16);
+            if (n == 0) red[(wb * 4 + wa) * kBwdVocab + i * 32 + (r >> 2) * 8 + h * 4 + (r & 3)] = sm;
+          }
         }
       }
     }
+    if constexpr (WANT_DB) {
+      // the two token halves' column sums meet in LDS (stage 1, which no DMA fills
+      // until the next task's main loop has passed its first barrier)
+      __syncthreads();
+      if (active && wb == 0) {
+        float* cs = a.colsum + (size_t)slot * kBwdVocab;
+        for (int c = lane; c < kBwdVocab; c += 64) cs[c] = red[wa * kBwdVocab + c] + red[(4 + wa) * kBwdVocab + c];
+      }
+      __syncthreads();
+    }
+    if (tn >= ntask) break;
+    t = tn;
+    cur = nxt;
   }
 }
 
@@ -599,8 +656,12 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_kernel(BwdArgs a, int chu
     for (int ks = 0; ks < 4; ++ks) go_n[jj][ks] = S::X_BYTES + row * 128u + ((((uint32_t)(2 * ks + kg)) ^ c) << 4);
   }
 
+  // slot / xrow: the G slot and first X row of tile j, resolved by prep() from the
+  // scalar lists; the loads are issued at the end of a step and land at the next
+  // step's barrier, so no fragment read waits behind them.
   struct Cur {
-    int q, owner, ds, b, cnt, j, h;
+    int q, owner, ds, b, cnt, j, h, slot;
+    int64_t xrow;
   };
   auto seek = [&](int q, Cur& c) -> bool {
     for (; q < ngroups; q += nper) {
@@ -620,25 +681,34 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_kernel(BwdArgs a, int chu
     }
     return false;
   };
+  auto prep = [&](Cur& c) {
+    if (PHASE == 0) {
+      c.slot = c.b + c.j;
+      c.xrow = (int64_t)(vlo + ldu(a.slot_vt, c.slot)) * kBwdVocab;
+    } else {
+      c.slot = ldu(a.vt_slot, c.b + c.j);
+      c.xrow = (int64_t)ldu(a.slot_rb, c.slot) * kBwdTokens;
+    }
+  };
   auto advance = [&](Cur& c) -> bool {
     if (++c.h < S::SPT) return true;
     c.h = 0;
-    if (++c.j < c.cnt) return true;
-    return seek(c.q + nper, c);
+    if (++c.j < c.cnt) {
+      prep(c);
+      return true;
+    }
+    if (!seek(c.q + nper, c)) return false;
+    prep(c);
+    return true;
   };
 
+  // LDS-DMA of tile c's slice into stage st.  The loads are inline assembly: the
+  // compiler then adds no vmcnt wait for them in front of the fragment reads of
+  // other stages (the stage barriers order them).
   const uint32_t smem_lds = lds_addr(smem);
   auto issue = [&](const Cur& c, int st) {
     const uint32_t sb = smem_lds + (uint32_t)(st * S::STAGE);
-    int slot;
-    int64_t xr0;
-    if (PHASE == 0) {
-      slot = c.b + c.j;
-      xr0 = (int64_t)(vlo + ldu(a.slot_vt, slot)) * kBwdVocab + c.h * S::KS;
-    } else {
-      slot = ldu(a.vt_slot, c.b + c.j);
-      xr0 = (int64_t)ldu(a.slot_rb, slot) * kBwdTokens + c.h * S::KS;
-    }
+    const int64_t xr0 = c.xrow + c.h * S::KS;
     const int64_t dcol = (int64_t)c.ds * S::DN * ES;
     const char* xbase = X + xr0 * pitch + dcol;
     if (xr0 + S::KS <= xrows && dcol + S::DN * ES <= pitch) {
@@ -653,43 +723,54 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_kernel(BwdArgs a, int chu
         dma16(src, sb + (wave * S::XLW + j) * 1024);
       }
     }
-    const char* gbase = a.gtile + (size_t)slot * a.plan.g_bytes + (PHASE == 0 ? c.h * 128 : c.h * S::KS * S::GTP);
+    const char* gbase = a.gtile + (size_t)c.slot * a.plan.g_bytes + (PHASE == 0 ? c.h * 128 : c.h * S::KS * S::GTP);
 #pragma unroll
     for (int j = 0; j < S::GLW; ++j) dma16_s(gbase, goff[j], sb + S::X_BYTES + (wave * S::GLW + j) * 1024);
   };
 
   f32x16 acc[4][2];
-  auto mma = [&](int st) {
+  // A step's fragments for its four 32-byte contraction steps (ks): the reads of
+  // ks 0 and 1 go first, those of ks 2 and 3 among the MFMAs of ks 0 and 1.
+  u32x4 xf[4][4], gf[4][2];
+  auto frags = [&](int st) {
     const char* sp = smem + st * S::STAGE;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-      u32x4 xf[4], gf[2];
-      if constexpr (ES == 2) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) xf[i] = frag_tr16(sp + xo[i] + 16 * ks * S::XP, 4 * S::XP);
-#pragma unroll
-        for (int jj = 0; jj < 2; ++jj) {
-          if (PHASE == 0)
-            gf[jj] = lds_ld16(sp, go_n[jj][ks]);
-          else
-            gf[jj] = frag_tr16(sp + go_t[jj] + 16 * ks * S::GTP, 4 * S::GTP);
-        }
-      } else {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) xf[i] = frag_tr32<S::XP>(sp, ks * S::KE, wd * 128 + 32 * i);
-#pragma unroll
-        for (int jj = 0; jj < 2; ++jj) {
-          if (PHASE == 0)
-            gf[jj] = lds_ld16(sp, go_n[jj][ks]);
-          else
-            gf[jj] = frag_tr32<S::GTP>(sp + S::X_BYTES, ks * S::KE, wm * 64 + 32 * jj);
-        }
+      for (int jj = 0; jj < 2; ++jj) {
+        if constexpr (PHASE == 0)
+          gf[ks][jj] = lds_ld16(sp, go_n[jj][ks]);
+        else if constexpr (ES == 2)
+          gf[ks][jj] = frag_tr16(sp + go_t[jj] + 16 * ks * S::GTP, 4 * S::GTP);
+        else
+          gf[ks][jj] = frag_tr32<S::GTP>(sp + S::X_BYTES, ks * S::KE, wm * 64 + 32 * jj);
       }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if constexpr (ES == 2)
+          xf[ks][i] = frag_tr16(sp + xo[i] + 16 * ks * S::XP, 4 * S::XP);
+        else
+          xf[ks][i] = frag_tr32<S::XP>(sp, ks * S::KE, wd * 128 + 32 * i);
+      }
+    }
+  };
+  auto mma = [&]() {
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int jj = 0; jj < 2; ++jj) acc[i][jj] = Traits<T>::mfma(xf[i], gf[jj], acc[i][jj]);
-    }
+        for (int jj = 0; jj < 2; ++jj) acc[i][jj] = Traits<T>::mfma(xf[ks][i], gf[ks][jj], acc[i][jj]);
+  };
+  // RK = LDS read instructions per contraction step, MK = MFMAs per contraction step.
+  constexpr int RK = (ES == 2 ? 8 : 16) + (PHASE == 0 ? 2 : (ES == 2 ? 4 : 8));
+  constexpr int MK = 8 * Traits<T>::kInstrPerStep;
+  auto schedule = [&]() {
+    __builtin_amdgcn_sched_group_barrier(0x100, 2 * RK, 0);
+    sched_interleave<0, MK, RK, 0, 0>();
+    sched_interleave<0, MK, RK, 0, 0>();
+    sched_interleave<0, MK, 0, 0, 0>();
+    sched_interleave<0, MK, 0, 0, 0>();
   };
 
   // acc[i][jj][r]: output column ds DN + 128 wd + 32 i + 8 (r/4) + 4 h + r%4 of row 64 wm + 32 jj + n.
@@ -757,19 +838,24 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_kernel(BwdArgs a, int chu
 
   Cur cs;
   if (!seek(lidx, cs)) return;
+  prep(cs);
   Cur nx = cs, last = cs;
   bool have = true;
-  auto issue_next = [&](int st) {
+  // issue_next: the loads of nx (or, past the end, a repeat of the last one, which
+  // keeps the per-stage load count uniform and is never consumed); advance_next:
+  // step nx on, issuing the scalar list loads of its next tile.
+  auto issue_next = [&](int st) { issue(have ? nx : last, st); };
+  auto advance_next = [&]() {
     if (have) {
-      issue(nx, st);
       last = nx;
       have = advance(nx);
-    } else {
-      issue(last, st);  // keeps the per-stage load count uniform; never consumed
     }
   };
 #pragma unroll
-  for (int p = 0; p < S::STAGES - 1; ++p) issue_next(p);
+  for (int p = 0; p < S::STAGES - 1; ++p) {
+    issue_next(p);
+    advance_next();
+  }
 
   // Tasks outside, their steps inside: the accumulators are zeroed once per task,
   // so the step loop carries them only through MFMAs (no register copies), while
@@ -787,7 +873,10 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_kernel(BwdArgs a, int chu
       else
         stage_barrier<(S::STAGES - 2) * S::LPW>();
       issue_next((st + S::STAGES - 1) % S::STAGES);
-      mma(st);
+      frags(st);
+      mma();
+      schedule();
+      advance_next();
       ++since_store;
       st = st + 1 == S::STAGES ? 0 : st + 1;
       if (++cs.h < S::SPT) continue;
@@ -822,7 +911,7 @@ static void launch_g(const BwdArgs& a, int chunk, dim3 grid, hipStream_t s) {
   const bool g = a.dE != nullptr || a.dC != nullptr, db = a.dBias != nullptr;
 #define CCE_G(G, DB)                                                                                   \
   if (g == G && db == DB) {                                                                            \
-    hipLaunchKernelGGL((bwd_g_kernel<T, HB, G, DB>), grid, dim3(kThreads), 0, s, a, chunk);            \
+    hipLaunchKernelGGL((bwd_g_kernel<T, HB, G, DB>), grid, dim3(kGThreads), 0, s, a, chunk);           \
     return;                                                                                            \
   }
   CCE_G(true, true)
