@@ -113,6 +113,29 @@ int cce_backward(int dtype, const void* e, const void* c, const void* bias,
                  void* workspace, size_t workspace_bytes,
                  int64_t* tile_stats, void* hip_stream);
 
+/* Reduction modes of cce_reduce_loss. */
+#define CCE_REDUCE_SUM 1
+#define CCE_REDUCE_MEAN 2
+
+/*
+ * Reduced loss of cce_loss (reference mlx_cce/__init__.py:72-76, where MLX ops do
+ * it; no native counterpart there).  One workgroup sums nll[0..N) in a fixed order
+ * (deterministic) and counts the rows kept by the ignore mask (all N when
+ * has_ignore == 0):
+ *   CCE_REDUCE_SUM:  loss_out[0] = sum
+ *   CCE_REDUCE_MEAN: loss_out[0] = sum / max(count, 1)
+ * scale_out (nullable, fp32[1]) receives max(count, 1).  nll is cce_forward's.
+ */
+int cce_reduce_loss(const float* nll, const int64_t* targets, int64_t ignore_index, int has_ignore,
+                    int64_t N, int mode, float* loss_out, float* scale_out, void* hip_stream);
+
+/*
+ * Cotangent of every per-token loss under a reduced loss (the VJP of
+ * mlx_cce/__init__.py:72-76): d_nll[r] = grad[0] / scale[0], or grad[0] when scale
+ * is NULL.  grad and scale are device fp32[1]; d_nll is device fp32[N].
+ */
+int cce_broadcast_grad(const float* grad, const float* scale, int64_t N, float* d_nll, void* hip_stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -213,4 +213,32 @@ int cce_backward(int dtype, const void* e, const void* c, const void* bias, cons
   return CCE_OK;
 }
 
+int cce_reduce_loss(const float* nll, const int64_t* targets, int64_t ignore_index, int has_ignore, int64_t N,
+                    int mode, float* loss_out, float* scale_out, void* hip_stream) {
+  g_err[0] = 0;
+  if (N <= 0) return fail(CCE_ERR_INVALID_ARGUMENT, "[cce_reduce_loss] N must be positive, got %lld", (long long)N);
+  if (mode != CCE_REDUCE_SUM && mode != CCE_REDUCE_MEAN)
+    return fail(CCE_ERR_INVALID_ARGUMENT, "[cce_reduce_loss] mode must be CCE_REDUCE_SUM or CCE_REDUCE_MEAN, got %d",
+                mode);
+  if (!nll || !loss_out || (has_ignore && !targets))
+    return fail(CCE_ERR_INVALID_ARGUMENT, "[cce_reduce_loss] nll, loss_out (and targets with has_ignore) must be non-null");
+  if (num_cus_current() <= 0) return fail(CCE_ERR_NO_DEVICE, "[cce_reduce_loss] no HIP device is available");
+  const hipError_t err = cce::launch_reduce_loss(nll, targets, ignore_index, has_ignore, N, mode, loss_out, scale_out,
+                                                 reinterpret_cast<hipStream_t>(hip_stream));
+  if (err != hipSuccess)
+    return fail(CCE_ERR_LAUNCH, "[cce_reduce_loss] kernel launch failed: %s", hipGetErrorString(err));
+  return CCE_OK;
+}
+
+int cce_broadcast_grad(const float* grad, const float* scale, int64_t N, float* d_nll, void* hip_stream) {
+  g_err[0] = 0;
+  if (N <= 0) return fail(CCE_ERR_INVALID_ARGUMENT, "[cce_broadcast_grad] N must be positive, got %lld", (long long)N);
+  if (!grad || !d_nll) return fail(CCE_ERR_INVALID_ARGUMENT, "[cce_broadcast_grad] grad and d_nll must be non-null");
+  if (num_cus_current() <= 0) return fail(CCE_ERR_NO_DEVICE, "[cce_broadcast_grad] no HIP device is available");
+  const hipError_t err = cce::launch_broadcast_grad(grad, scale, N, d_nll, reinterpret_cast<hipStream_t>(hip_stream));
+  if (err != hipSuccess)
+    return fail(CCE_ERR_LAUNCH, "[cce_broadcast_grad] kernel launch failed: %s", hipGetErrorString(err));
+  return CCE_OK;
+}
+
 }  // extern "C"

@@ -20,8 +20,9 @@
 //   2. bwd_compact_kernel  one workgroup turns the chunk's bitmap (held in LDS)
 //                          into slots in (token block, vocab tile) order, the same
 //                          slots grouped by vocab tile, and the G task list.
-//   3. bwd_empty_kernel    owners (row blocks of dE / dC) without kept tiles get
-//                          zeros (and the fp32 dE carry is started / finished).
+//   3. empty_owner         owners (row blocks of dE / dC) without kept tiles get
+//                          zeros (and the fp32 dE carry is started / finished);
+//                          done by the G kernel's workgroups once out of tasks.
 //   4. bwd_g_kernel        per task (one token block, up to 4 of its kept vocab
 //                          tiles): recompute the 512 x 128 logits on MFMA, form G,
 //                          store each 128 x 128 G tile token-major in the input
@@ -233,6 +234,7 @@ __global__ __launch_bounds__(1024) void bwd_compact_kernel(BwdArgs a, int chunk)
     a.vt_start[nv] = vtot;
     a.counts[0] = kept;
     a.counts[1] = ntask;
+    a.counts[2] = 0;  // next owner-without-kept-tiles item (taken by the G kernel's tail)
     if (a.tile_stats) {
       if (chunk == 0) {
         a.tile_stats[0] = kept;
@@ -245,17 +247,17 @@ __global__ __launch_bounds__(1024) void bwd_compact_kernel(BwdArgs a, int chunk)
 }
 
 // ---------------------------------------------------------------- 3. owners without kept tiles
-// One workgroup per owner: token block rb < nrb (dE rows), then the chunk's vocab
-// tiles (dC rows).  With one chunk, an empty owner's rows are zero.  With several,
-// dE goes through the fp32 carry: the first chunk zeroes an empty block's carry
-// rows, the last converts them to the output dtype (blocks with kept tiles are
-// stored / added / finished by the dE sums themselves).
-template <typename T>
-__global__ __launch_bounds__(256) void bwd_empty_kernel(BwdArgs a, int chunk) {
+// Item o: token block rb = o < nrb (dE rows), then the chunk's vocab tiles (dC
+// rows).  With one chunk, an empty owner's rows are zero.  With several, dE goes
+// through the fp32 carry: the first chunk zeroes an empty block's carry rows, the
+// last converts them to the output dtype (blocks with kept tiles are stored / added
+// / finished by the dE sums themselves).  NT threads work on one item.  The G
+// kernel's workgroups take these items once they run out of G tasks.
+template <typename T, int NT>
+__device__ __forceinline__ void empty_owner(const BwdArgs& a, int chunk, int o) {
   const int nrb = (int)a.plan.nrb, nvt = (int)a.plan.nvt;
   const int vlo = chunk * (int)a.plan.chunk_nvt;
   const int nv = min(nvt, vlo + (int)a.plan.chunk_nvt) - vlo;
-  const int o = (int)blockIdx.x;
   const int64_t D = a.D;
   if (o < nrb) {
     if (!a.dE || ldu(a.rb_start, o + 1) != ldu(a.rb_start, o)) return;
@@ -266,16 +268,16 @@ __global__ __launch_bounds__(256) void bwd_empty_kernel(BwdArgs a, int chunk) {
     const int64_t n = (a.N - row0 < kBwdTokens ? a.N - row0 : kBwdTokens) * D;  // elements
     if (!multi) {
       T* out = reinterpret_cast<T*>(a.dE) + row0 * D;
-      for (int64_t i = (int64_t)threadIdx.x * (16 / sizeof(T)); i < n; i += 256 * (16 / sizeof(T)))
+      for (int64_t i = (int64_t)threadIdx.x * (16 / sizeof(T)); i < n; i += NT * (16 / sizeof(T)))
         *reinterpret_cast<u32x4*>(out + i) = u32x4{0u, 0u, 0u, 0u};
     } else if (first) {
       float* acc = a.de_acc + row0 * D;
-      for (int64_t i = (int64_t)threadIdx.x * 4; i < n; i += 1024)
+      for (int64_t i = (int64_t)threadIdx.x * 4; i < n; i += NT * 4)
         *reinterpret_cast<f32x4*>(acc + i) = f32x4{0.f, 0.f, 0.f, 0.f};
     } else {
       const float* acc = a.de_acc + row0 * D;
       T* out = reinterpret_cast<T*>(a.dE) + row0 * D;
-      for (int64_t i = (int64_t)threadIdx.x * 4; i < n; i += 1024) {
+      for (int64_t i = (int64_t)threadIdx.x * 4; i < n; i += NT * 4) {
         const f32x4 x = *reinterpret_cast<const f32x4*>(acc + i);
 #pragma unroll
         for (int k = 0; k < 4; ++k) out[i + k] = (T)x[k];
@@ -288,7 +290,7 @@ __global__ __launch_bounds__(256) void bwd_empty_kernel(BwdArgs a, int chunk) {
   const int64_t row0 = (int64_t)(vlo + v) * kBwdVocab;
   const int64_t n = (a.V - row0 < kBwdVocab ? a.V - row0 : kBwdVocab) * D;
   T* out = reinterpret_cast<T*>(a.dC) + row0 * D;
-  for (int64_t i = (int64_t)threadIdx.x * (16 / sizeof(T)); i < n; i += 256 * (16 / sizeof(T)))
+  for (int64_t i = (int64_t)threadIdx.x * (16 / sizeof(T)); i < n; i += NT * (16 / sizeof(T)))
     *reinterpret_cast<u32x4*>(out + i) = u32x4{0u, 0u, 0u, 0u};
 }
 
@@ -348,8 +350,28 @@ __global__ __launch_bounds__(kGThreads, 1) void bwd_g_kernel(BwdArgs a, int chun
       Loop::template prefetch<false>(src, smem);
   };
 
+  // Once out of tasks, the workgroup zeroes owners without kept tiles, taking items
+  // from a counter the compaction kernel reset (only when dE or dC is wanted).
+  auto tail = [&]() {
+    if constexpr (WANT_G) {
+      const int nitems = (int)a.plan.nrb + (min((int)a.plan.nvt, vlo + (int)a.plan.chunk_nvt) - vlo);
+      int* box = reinterpret_cast<int*>(smem);
+      for (;;) {
+        __syncthreads();  // box (and smem) free
+        if (threadIdx.x == 0) box[0] = atomicAdd(&a.counts[2], 1);
+        __syncthreads();
+        const int o = box[0];
+        if (o >= nitems) break;
+        empty_owner<T, kGThreads>(a, chunk, o);
+      }
+    }
+  };
+
   int t = xcd * nper + lidx;  // logical task of this workgroup; advances by the grid size
-  if (t >= ntask) return;
+  if (t >= ntask) {
+    tail();
+    return;
+  }
   Task cur;
   load_task(t, cur);
   auto src = sources(cur);
@@ -478,6 +500,7 @@ __global__ __launch_bounds__(kGThreads, 1) void bwd_g_kernel(BwdArgs a, int chun
     t = tn;
     cur = nxt;
   }
+  tail();
 }
 
 // ---------------------------------------------------------------- 5. sums of G_j . X_j
@@ -936,10 +959,6 @@ static hipError_t backward_typed(const BwdArgs& a, hipStream_t s) {
     hipLaunchKernelGGL(bwd_compact_kernel, dim3(1), dim3(1024), 0, s, a, chunk);
     if ((err = hipGetLastError()) != hipSuccess) return err;
     if (!(want_de || want_dc || want_db)) continue;
-    if (want_de || want_dc) {
-      hipLaunchKernelGGL((bwd_empty_kernel<T>), dim3((unsigned)(P.nrb + nv)), dim3(256), 0, s, a, chunk);
-      if ((err = hipGetLastError()) != hipSuccess) return err;
-    }
     if (a.bias)
       launch_g<T, true>(a, chunk, dim3(gp), s);
     else

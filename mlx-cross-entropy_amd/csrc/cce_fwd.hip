@@ -295,6 +295,63 @@ static hipError_t forward_typed(const FwdArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
+// Reduced loss of cce_loss (mlx_cce/__init__.py:72-76): one workgroup sums nll in a
+// fixed order (fp64 per thread, then a tree over the threads) and counts the rows
+// the ignore mask keeps.  mode 1: loss = sum; mode 2: loss = sum / max(count, 1),
+// scale = max(count, 1).  Masked rows already hold nll = 0.
+constexpr int kReduceThreads = 1024;
+__global__ __launch_bounds__(kReduceThreads) void reduce_loss_kernel(const float* __restrict__ nll,
+                                                                     const int64_t* __restrict__ targets,
+                                                                     int64_t ignore_index, int has_ignore, int64_t N,
+                                                                     int mode, float* loss, float* scale) {
+  __shared__ double ssum[kReduceThreads];
+  __shared__ long long scnt[kReduceThreads];
+  double acc = 0.0;
+  long long cnt = 0;
+  for (int64_t i = threadIdx.x; i < N; i += kReduceThreads) {
+    acc += (double)nll[i];
+    cnt += (has_ignore && targets[i] == ignore_index) ? 0 : 1;
+  }
+  ssum[threadIdx.x] = acc;
+  scnt[threadIdx.x] = cnt;
+  __syncthreads();
+  for (int w = kReduceThreads / 2; w > 0; w >>= 1) {
+    if ((int)threadIdx.x < w) {
+      ssum[threadIdx.x] += ssum[threadIdx.x + w];
+      scnt[threadIdx.x] += scnt[threadIdx.x + w];
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    const double c = scnt[0] > 0 ? (double)scnt[0] : 1.0;
+    loss[0] = mode == 2 ? (float)(ssum[0] / c) : (float)ssum[0];
+    if (scale) scale[0] = (float)c;
+  }
+}
+
+hipError_t launch_reduce_loss(const float* nll, const int64_t* targets, int64_t ignore_index, int has_ignore,
+                              int64_t N, int mode, float* loss, float* scale, hipStream_t s) {
+  hipLaunchKernelGGL(reduce_loss_kernel, dim3(1), dim3(kReduceThreads), 0, s, nll, targets, ignore_index,
+                     has_ignore, N, mode, loss, scale);
+  return hipGetLastError();
+}
+
+// d_nll[r] = grad[0] / scale[0] (scale null: grad[0]) — the cotangent of every
+// per-token loss under a summed or averaged reduction.
+__global__ __launch_bounds__(256) void broadcast_grad_kernel(const float* __restrict__ grad,
+                                                             const float* __restrict__ scale, int64_t N,
+                                                             float* __restrict__ d_nll) {
+  const float g = scale ? grad[0] / scale[0] : grad[0];
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < N; i += (int64_t)gridDim.x * 256) d_nll[i] = g;
+}
+
+hipError_t launch_broadcast_grad(const float* grad, const float* scale, int64_t N, float* d_nll, hipStream_t s) {
+  const int64_t blocks = (N + 255) / 256;
+  hipLaunchKernelGGL(broadcast_grad_kernel, dim3((unsigned)(blocks < 1024 ? blocks : 1024)), dim3(256), 0, s, grad,
+                     scale, N, d_nll);
+  return hipGetLastError();
+}
+
 hipError_t launch_forward(int dtype, const FwdArgs& a, hipStream_t s) {
   switch (dtype) {
     case 0:

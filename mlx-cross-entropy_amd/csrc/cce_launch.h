@@ -151,5 +151,8 @@ struct BwdArgs {
 // dtype: 0 f32, 1 f16, 2 bf16.  Return hipError_t of the launches.
 hipError_t launch_forward(int dtype, const FwdArgs& a, hipStream_t s);
 hipError_t launch_backward(int dtype, const BwdArgs& a, hipStream_t s);
+hipError_t launch_reduce_loss(const float* nll, const int64_t* targets, int64_t ignore_index, int has_ignore,
+                              int64_t N, int mode, float* loss, float* scale, hipStream_t s);
+hipError_t launch_broadcast_grad(const float* grad, const float* scale, int64_t N, float* d_nll, hipStream_t s);
 
 }  // namespace cce

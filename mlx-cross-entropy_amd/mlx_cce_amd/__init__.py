@@ -59,20 +59,11 @@ class _CCEFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, e, c, bias, targets, ignore_index, reduction, filter_eps, grad_c, grad_bias):
         tile_max, _tse, _ntl, lse, nll = _ext.forward(e, c, targets, bias, ignore_index)
-        N = e.shape[0]
         if reduction == "none":
             loss = nll
             scale = None
-        elif reduction == "sum":
-            loss = nll.sum()
-            scale = None
-        else:  # mean over valid rows, divided by max(count, 1) (mlx_cce/__init__.py:73-75)
-            if ignore_index is None:
-                count = torch.full((), float(N), dtype=torch.float32, device=e.device)
-            else:
-                count = (targets != ignore_index).sum().clamp_(min=1).to(torch.float32)
-            loss = nll.sum() / count
-            scale = count
+        else:  # sum, or mean over the kept rows divided by max(count, 1) (mlx_cce/__init__.py:73-75)
+            loss, scale = _ext.reduce_loss(nll, targets, ignore_index, reduction)
         ctx.save_for_backward(e, c, bias, targets, lse, tile_max, scale)
         ctx.cce = (ignore_index, reduction, filter_eps, grad_c, grad_bias)
         ctx.mark_non_differentiable(lse)
@@ -83,13 +74,10 @@ class _CCEFunction(torch.autograd.Function):
         e, c, bias, targets, lse, tile_max, scale = ctx.saved_tensors
         ignore_index, reduction, filter_eps, grad_c, grad_bias = ctx.cce
         N = e.shape[0]
-        g = grad_loss.to(torch.float32)
         if reduction == "none":
-            d_nll = g.reshape(N)
-        elif reduction == "sum":
-            d_nll = g.reshape(1).expand(N)
+            d_nll = grad_loss.to(torch.float32).reshape(N)
         else:
-            d_nll = (g / scale).reshape(1).expand(N)
+            d_nll = _ext.broadcast_grad(grad_loss, scale, N)
         want_de = ctx.needs_input_grad[0]
         want_dc = ctx.needs_input_grad[1] and grad_c
         want_db = bias is not None and ctx.needs_input_grad[2] and grad_bias

@@ -40,7 +40,12 @@ SIGNATURES = {
     "cce_backward_workspace_size": (ctypes.c_size_t, [_INT, _I64, _I64, _I64, _INT, _INT, _INT]),
     "cce_backward": (_INT, [_INT, _P, _P, _P, _P, _I64, _INT, _I64, _I64, _I64, _P, _P, _P, ctypes.c_float,
                             _P, _P, _P, _P, ctypes.c_size_t, _P, _P]),
+    "cce_reduce_loss": (_INT, [_P, _P, _I64, _INT, _I64, _INT, _P, _P, _P]),
+    "cce_broadcast_grad": (_INT, [_P, _P, _I64, _P, _P]),
 }
+
+CCE_REDUCE_SUM = 1
+CCE_REDUCE_MEAN = 2
 
 _lib = None
 
@@ -274,3 +279,36 @@ class _nullctx:
 
     def __exit__(self, *a):
         return False
+
+
+def reduce_loss(nll, targets, ignore_index, reduction):
+    """Reduced loss of the per-token nll ('sum' or 'mean'); returns (loss, scale).
+
+    scale is max(count of rows kept by the ignore mask, 1) for 'mean', else None.
+    Both are fp32 device tensors of shape () (one deterministic workgroup reduction).
+    """
+    N = nll.shape[0]
+    mode = CCE_REDUCE_MEAN if reduction == "mean" else CCE_REDUCE_SUM
+    loss = torch.empty((), dtype=torch.float32, device=nll.device)
+    scale = torch.empty((), dtype=torch.float32, device=nll.device) if mode == CCE_REDUCE_MEAN else None
+    has_ignore = ignore_index is not None
+    t = targets.to(torch.int64).contiguous()
+    with torch.cuda.device(nll.device):
+        stream = torch.cuda.current_stream(nll.device).cuda_stream
+        rc = lib().cce_reduce_loss(_ptr(nll), _ptr(t), int(ignore_index) if has_ignore else 0, 1 if has_ignore else 0,
+                                   N, mode, _ptr(loss), _ptr(scale), ctypes.c_void_p(stream))
+    if rc != CCE_OK:
+        _raise(rc, "cce_reduce_loss")
+    return loss, scale
+
+
+def broadcast_grad(grad, scale, N):
+    """d_nll [N] fp32 = grad / scale (scale None: grad) for a scalar upstream gradient."""
+    g = grad.to(torch.float32).reshape(1).contiguous()
+    d_nll = torch.empty((N,), dtype=torch.float32, device=g.device)
+    with torch.cuda.device(g.device):
+        stream = torch.cuda.current_stream(g.device).cuda_stream
+        rc = lib().cce_broadcast_grad(_ptr(g), _ptr(scale), N, _ptr(d_nll), ctypes.c_void_p(stream))
+    if rc != CCE_OK:
+        _raise(rc, "cce_broadcast_grad")
+    return d_nll

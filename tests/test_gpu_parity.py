@@ -236,6 +236,37 @@ def test_out_of_range_target_is_nan(m, cuda):
     assert math.isnan(float(loss[3])) and np.isfinite(f64(loss)[[0, 1, 2, 4]]).all()
 
 
+def test_reduce_loss_and_broadcast_grad(m, cuda):
+    """cce_reduce_loss / cce_broadcast_grad against fp64 numpy: sum, mean / max(count, 1), ignore_index
+    (and None), all rows ignored, NaN propagation; d_nll = grad / scale."""
+    from mlx_cce_amd import _ext
+    g = torch.Generator(device=cuda).manual_seed(5)
+    N = 5000
+    nll = torch.rand(N, generator=g, device=cuda) * 10
+    t = torch.randint(0, 50, (N,), generator=g, device=cuda)
+    t[::7] = -100
+    nll[t == -100] = 0.0  # the forward writes 0 for masked rows
+    x = nll.double().cpu().numpy()
+    kept = int((t != -100).sum())
+    loss, scale = _ext.reduce_loss(nll, t, -100, "mean")
+    assert abs(float(loss) - x.sum() / kept) <= 1e-6 * abs(x.sum() / kept) and float(scale) == kept
+    loss, scale = _ext.reduce_loss(nll, t, -100, "sum")
+    assert abs(float(loss) - x.sum()) <= 1e-6 * x.sum() and scale is None
+    loss, scale = _ext.reduce_loss(nll, t, None, "mean")
+    assert abs(float(loss) - x.sum() / N) <= 1e-6 * x.sum() / N and float(scale) == N
+    t_all = torch.full_like(t, -100)
+    loss, scale = _ext.reduce_loss(torch.zeros_like(nll), t_all, -100, "mean")
+    assert float(loss) == 0.0 and float(scale) == 1.0
+    nll[11] = float("nan")
+    loss, _ = _ext.reduce_loss(nll, t, -100, "sum")
+    assert math.isnan(float(loss))
+    up = torch.tensor(3.0, device=cuda)
+    d = _ext.broadcast_grad(up, torch.tensor(8.0, device=cuda), N)
+    assert d.shape == (N,) and bool((d == 0.375).all())
+    d = _ext.broadcast_grad(up, None, 7)
+    assert bool((d == 3.0).all())
+
+
 def test_only_dE_requested(m, cuda):
     e, c, t = normal_case(64, 64, 1000, torch.bfloat16, cuda)
     e.requires_grad_(True)

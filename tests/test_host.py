@@ -102,6 +102,17 @@ def test_backward_validation_errors(ext):
     assert _bwd(lib, ext, dtype=3) == ext.CCE_ERR_UNSUPPORTED_DTYPE
 
 
+def test_reduction_helpers_validation_errors(ext):
+    lib = ext.lib()
+    assert lib.cce_reduce_loss(FAKE, FAKE, -100, 1, 0, ext.CCE_REDUCE_MEAN, FAKE, None, None) == ext.CCE_ERR_INVALID_ARGUMENT
+    assert b"positive" in lib.cce_last_error()
+    assert lib.cce_reduce_loss(FAKE, FAKE, -100, 1, 8, 3, FAKE, None, None) == ext.CCE_ERR_INVALID_ARGUMENT
+    assert b"mode" in lib.cce_last_error()
+    assert lib.cce_reduce_loss(FAKE, None, -100, 1, 8, ext.CCE_REDUCE_SUM, FAKE, None, None) == ext.CCE_ERR_INVALID_ARGUMENT
+    assert lib.cce_broadcast_grad(FAKE, None, 0, FAKE, None) == ext.CCE_ERR_INVALID_ARGUMENT
+    assert lib.cce_broadcast_grad(None, None, 8, FAKE, None) == ext.CCE_ERR_INVALID_ARGUMENT
+
+
 @pytest.mark.skipif(gpu_available(), reason="would launch on fake pointers when a GPU is present")
 def test_no_device_is_reported(ext):
     lib = ext.lib()
