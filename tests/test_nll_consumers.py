@@ -110,6 +110,6 @@ def test_dpo_gradient_through_cce_backward(cuda):
     ep, er, cc = (x.detach().double().cpu().requires_grad_(True) for x in (e_p, e_r, c))
     rl = NLL.dpo_loss(ref_nll(ep, cc, t_p.cpu()), ref_nll(er, cc, t_r.cpu()), beta=0.5)
     rl.backward()
-    assert abs(float(loss) - float(rl)) < 1e-5 * max(1.0, abs(float(rl)))
+    assert abs(float(loss.detach()) - float(rl.detach())) < 1e-5 * max(1.0, abs(float(rl.detach())))
     for got, ref in ((e_p.grad, ep.grad), (e_r.grad, er.grad), (c.grad, cc.grad)):
         assert O.rel_fro(got.double().cpu().numpy(), ref.numpy()) < 1e-4
