@@ -505,9 +505,12 @@ __global__ __launch_bounds__(kGThreads, 1) void bwd_g_kernel(BwdArgs a, int chun
 
 // ---------------------------------------------------------------- 5. sums of G_j . X_j
 // Geometry of one sum task: output rows = the owner's 128 rows (tokens for dE,
-// vocabulary for dC), output columns = one kSumDN slice of D; contraction over the
-// owner's kept tiles, 128 deep each, in slices of 128 bytes of a G row.
-//   X region of a stage: KS contraction rows x kSumDN columns of E / C, natural
+// vocabulary for dC), output columns = one DN (512) slice of D; contraction over
+// the owner's kept tiles, 128 deep each, in slices of 128 bytes of a G row.  Eight
+// waves (two per SIMD): wave (wm, wd) = (w % 2, w / 2) owns rows [64 wm, +64) and
+// columns [128 wd, +128) of the slice.  A wide slice loads each G slice once for
+// 512 output columns: the stage's DMA (80 KiB) per 2048 MFMA cycles of a SIMD.
+//   X region of a stage: KS contraction rows x DN columns of E / C, natural
 //     [k][d] layout, 64-byte segments XOR-swizzled by tr_swz(row) so the
 //     transposing fragment reads are free of bank conflicts.
 //   G region: dE — 128 G rows (tokens) x 128 bytes of contraction (vocab), the
@@ -516,7 +519,33 @@ __global__ __launch_bounds__(kGThreads, 1) void bwd_g_kernel(BwdArgs a, int chun
 template <typename T>
 struct SumGeo {
   static constexpr int ES = sizeof(T);
-  static constexpr int DN = kSumDN;
+  static constexpr int NW = 8;                     // waves: 2 (rows) x 4 (column quarters)
+  static constexpr int NT = 64 * NW;
+  static constexpr int DN = 512;
+  static constexpr int KS = 128 / ES;              // contraction elements per slice
+  static constexpr int SPT = kBwdVocab / KS;       // slices per 128-deep tile
+  static constexpr int XP = DN * ES;               // bytes of one X row in LDS
+  static constexpr int X_BYTES = KS * XP;          // 64 KiB
+  static constexpr int GTP = kBwdVocab * ES;       // bytes of one G row
+  static constexpr int G_BYTES = 16384;            // 128 x 128 B (dE) = KS x GTP (dC)
+  static constexpr int STAGE = X_BYTES + G_BYTES;  // 80 KiB
+  static constexpr int STAGES = 2;
+  static constexpr int XLW = X_BYTES / 1024 / NW;  // X loads per wave per stage (8)
+  static constexpr int GLW = G_BYTES / 1024 / NW;  // G loads per wave per stage (2)
+  static constexpr int LPW = XLW + GLW;
+  static constexpr int KE = 32 / ES;               // contraction elements per MFMA step
+  static_assert(X_BYTES == 65536 && KS * GTP == G_BYTES, "stage geometry");
+  static_assert(STAGES * STAGE <= 163840, "two stages fill the 160 KiB of LDS");
+};
+
+// The narrow geometry: 4 waves, 256 output columns, 3 stages of 48 KiB (the dC sums:
+// many owners with one or two kept tiles, where a deeper pipeline and shorter
+// epilogues pay more than the wide slice's halved G traffic).
+template <typename T>
+struct SumGeoNarrow {
+  static constexpr int NT = 256;
+  static constexpr int ES = sizeof(T);
+  static constexpr int DN = 256;
   static constexpr int KS = 128 / ES;              // contraction elements per slice
   static constexpr int SPT = kBwdVocab / KS;       // slices per 128-deep tile
   static constexpr int XP = DN * ES;               // bytes of one X row in LDS
@@ -612,18 +641,318 @@ enum WriteMode { kWriteT = 0, kStoreF32 = 1, kAddF32 = 2, kFinishT = 3 };
 // Owners are dealt to the 8 XCDs round-robin; the 32 workgroups of an XCD take its
 // (owner, D slice) tasks in order, so all D slices of one owner run at once on one
 // XCD and share its G tiles in L2.  A workgroup walks the (task, tile, slice) steps
-// of its tasks as one pipeline: STAGES - 1 slices are in flight while one is
-// consumed, across task boundaries.  The vmcnt waits count the epilogue's stores:
-// buffer stores, issued unconditionally (out-of-range lanes are dropped by the
-// buffer's range check), so every epilogue issues exactly NSTORE of them per wave.
-// Every per-step address is a wave-uniform base plus a per-lane constant computed
-// once: DMA sources in the saddr form, fragment reads as constant LDS offsets.
+// of its tasks as one pipeline: the next slice is in flight while one is consumed,
+// across task boundaries.  The epilogue's stores are buffer stores (out-of-range
+// lanes are dropped by the buffer's range check).  Every per-step address is a
+// wave-uniform base plus a per-lane constant computed once: DMA sources in the
+// saddr form, fragment reads as constant LDS offsets.
 template <typename T, int PHASE>
-__global__ __launch_bounds__(kThreads, 1) void bwd_sum_kernel(BwdArgs a, int chunk) {
+__global__ __launch_bounds__(SumGeo<T>::NT, 1) void bwd_sum_kernel(BwdArgs a, int chunk) {
   using S = SumGeo<T>;
   __shared__ __attribute__((aligned(16))) char smem[S::STAGES * S::STAGE];
   constexpr int ES = S::ES;
-  const int nrb = (int)a.plan.nrb, nds = (int)a.plan.n_dslices;
+  const int nrb = (int)a.plan.nrb, nds = (int)((a.D + S::DN - 1) / S::DN);
+  const int vlo = chunk * (int)a.plan.chunk_nvt;
+  const int nv = min((int)a.plan.nvt, vlo + (int)a.plan.chunk_nvt) - vlo;
+  const int n_own = PHASE == 0 ? nrb : nv;
+  const int xcd = (int)(blockIdx.x & 7), lidx = (int)(blockIdx.x >> 3), nper = (int)(gridDim.x >> 3);
+  const int n_mine = n_own > xcd ? (n_own - xcd + 7) / 8 : 0;
+  const int ngroups = n_mine * nds;
+  const int64_t D = a.D;
+  const int64_t pitch = D * ES;
+  const char* X = reinterpret_cast<const char*>(PHASE == 0 ? a.c : a.e);
+  const int64_t xrows = PHASE == 0 ? a.V : a.N;
+  const int mode = (PHASE == 0 && a.plan.n_chunks > 1)
+                       ? (chunk == 0 ? kStoreF32 : (chunk == (int)a.plan.n_chunks - 1 ? kFinishT : kAddF32))
+                       : kWriteT;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int n = lane & 31, h = lane >> 5, kg = lane >> 5;
+  const int wm = wave & 1;   // output rows [64 wm, 64 wm + 64)
+  const int wd = wave >> 1;  // output columns [128 wd, 128 wd + 128) of the slice (4 quarters)
+
+  // This wave's DMA loads: XLW into the X region, GLW into the G region.  Per lane:
+  // the region row it fills and the byte of the source row that belongs there.
+  uint32_t xrow[S::XLW], xcol[S::XLW], xoff[S::XLW], goff[S::GLW];
+#pragma unroll
+  for (int j = 0; j < S::XLW; ++j) {
+    const uint32_t o = (uint32_t)(wave * S::XLW + j) * 1024u + lane * 16u;
+    const uint32_t row = o / S::XP, pb = o % S::XP;
+    xrow[j] = row;
+    xcol[j] = tr_off<S::XP>(row, pb) - row * S::XP;  // the swizzle is an involution on the segment index
+    xoff[j] = (uint32_t)(row * pitch) + xcol[j];
+  }
+#pragma unroll
+  for (int j = 0; j < S::GLW; ++j) {
+    const uint32_t o = (uint32_t)(wave * S::GLW + j) * 1024u + lane * 16u;
+    if (PHASE == 0) {
+      const uint32_t row = o / 128u, ch = (o % 128u) / 16u;
+      goff[j] = row * S::GTP + (ch ^ ((row ^ (row >> 3)) & 7u)) * 16u;
+    } else {
+      const uint32_t row = o / S::GTP, pb = o % S::GTP;
+      goff[j] = tr_off<S::GTP>(row, pb);
+    }
+  }
+  // Fragment read offsets within a stage (16-bit types).
+  uint32_t xo[4], go_t[2], go_n[2][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) xo[i] = tr_lane_off<S::XP>(wd * 128 + 32 * i);
+#pragma unroll
+  for (int jj = 0; jj < 2; ++jj) {
+    go_t[jj] = S::X_BYTES + tr_lane_off<S::GTP>(wm * 64 + 32 * jj);
+    const uint32_t row = (uint32_t)(wm * 64 + 32 * jj + n);
+    const uint32_t c = (row ^ (row >> 3)) & 7u;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) go_n[jj][ks] = S::X_BYTES + row * 128u + ((((uint32_t)(2 * ks + kg)) ^ c) << 4);
+  }
+
+  // slot / xrow: the G slot and first X row of tile j, resolved by prep() from the
+  // scalar lists; the loads are issued at the end of a step and land at the next
+  // step's barrier, so no fragment read waits behind them.
+  struct Cur {
+    int q, owner, ds, b, cnt, j, h, slot;
+    int64_t xrow;
+  };
+  auto seek = [&](int q, Cur& c) -> bool {
+    for (; q < ngroups; q += nper) {
+      const int owner = xcd + 8 * (q / nds);
+      const int b = ldu(PHASE == 0 ? a.rb_start : a.vt_start, owner);
+      const int e = ldu(PHASE == 0 ? a.rb_start : a.vt_start, owner + 1);
+      if (e > b) {
+        c.q = q;
+        c.owner = owner;
+        c.ds = q - (q / nds) * nds;
+        c.b = b;
+        c.cnt = e - b;
+        c.j = 0;
+        c.h = 0;
+        return true;
+      }
+    }
+    return false;
+  };
+  auto prep = [&](Cur& c) {
+    if (PHASE == 0) {
+      c.slot = c.b + c.j;
+      c.xrow = (int64_t)(vlo + ldu(a.slot_vt, c.slot)) * kBwdVocab;
+    } else {
+      c.slot = ldu(a.vt_slot, c.b + c.j);
+      c.xrow = (int64_t)ldu(a.slot_rb, c.slot) * kBwdTokens;
+    }
+  };
+  auto advance = [&](Cur& c) -> bool {
+    if (++c.h < S::SPT) return true;
+    c.h = 0;
+    if (++c.j < c.cnt) {
+      prep(c);
+      return true;
+    }
+    if (!seek(c.q + nper, c)) return false;
+    prep(c);
+    return true;
+  };
+
+  // LDS-DMA of tile c's slice into stage st.  The loads are inline assembly: the
+  // compiler then adds no vmcnt wait for them in front of the fragment reads of
+  // other stages (the stage barriers order them).
+  const uint32_t smem_lds = lds_addr(smem);
+  auto issue = [&](const Cur& c, int st) {
+    const uint32_t sb = smem_lds + (uint32_t)(st * S::STAGE);
+    const int64_t xr0 = c.xrow + c.h * S::KS;
+    const int64_t dcol = (int64_t)c.ds * S::DN * ES;
+    const char* xbase = X + xr0 * pitch + dcol;
+    if (xr0 + S::KS <= xrows && dcol + S::DN * ES <= pitch) {
+#pragma unroll
+      for (int j = 0; j < S::XLW; ++j) dma16_s(xbase, xoff[j], sb + (wave * S::XLW + j) * 1024);
+    } else {  // last row block or ragged D slice: zeros past the last row and the row end
+#pragma unroll
+      for (int j = 0; j < S::XLW; ++j) {
+        const int64_t r = xr0 + xrow[j];
+        const int64_t cb = dcol + xcol[j];
+        const char* src = (r < xrows && cb < pitch) ? X + r * pitch + cb : reinterpret_cast<const char*>(g_zero16);
+        dma16(src, sb + (wave * S::XLW + j) * 1024);
+      }
+    }
+    const char* gbase = a.gtile + (size_t)c.slot * a.plan.g_bytes + (PHASE == 0 ? c.h * 128 : c.h * S::KS * S::GTP);
+#pragma unroll
+    for (int j = 0; j < S::GLW; ++j) dma16_s(gbase, goff[j], sb + S::X_BYTES + (wave * S::GLW + j) * 1024);
+  };
+
+  f32x16 acc[4][2];
+  // Fragments of one 32-byte contraction step ks of stage st, and its 8 MFMAs.
+  auto frags = [&](int st, int ks, u32x4 (&xf)[4], u32x4 (&gf)[2]) {
+    const char* sp = smem + st * S::STAGE;
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      if constexpr (PHASE == 0)
+        gf[jj] = lds_ld16(sp, go_n[jj][ks]);
+      else if constexpr (ES == 2)
+        gf[jj] = frag_tr16(sp + go_t[jj] + 16 * ks * S::GTP, 4 * S::GTP);
+      else
+        gf[jj] = frag_tr32<S::GTP>(sp + S::X_BYTES, ks * S::KE, wm * 64 + 32 * jj);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if constexpr (ES == 2)
+        xf[i] = frag_tr16(sp + xo[i] + 16 * ks * S::XP, 4 * S::XP);
+      else
+        xf[i] = frag_tr32<S::XP>(sp, ks * S::KE, wd * 128 + 32 * i);
+    }
+  };
+  auto mma = [&](const u32x4 (&xf)[4], const u32x4 (&gf)[2]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) acc[i][jj] = Traits<T>::mfma(xf[i], gf[jj], acc[i][jj]);
+  };
+  // RK = LDS read instructions per contraction step, MK = MFMAs per contraction step.
+  constexpr int RK = (ES == 2 ? 8 : 16) + (PHASE == 0 ? 2 : (ES == 2 ? 4 : 8));
+  constexpr int MK = 8 * Traits<T>::kInstrPerStep;
+
+  // acc[i][jj][r]: output column ds DN + 128 wd + 32 i + 8 (r/4) + 4 h + r%4 of row 64 wm + 32 jj + n.
+  auto epilogue = [&](const Cur& c) {
+    const int64_t orow0 = (int64_t)(PHASE == 0 ? c.owner : vlo + c.owner) * 128;
+    const int64_t orows = PHASE == 0 ? a.N : a.V;
+    const int64_t nrows = orows - orow0 < 128 ? orows - orow0 : 128;
+    T* out = reinterpret_cast<T*>(PHASE == 0 ? a.dE : a.dC) + orow0 * D;
+    const int64_t d00 = (int64_t)c.ds * S::DN + wd * 128 + h * 4;
+    if (mode == kWriteT) {
+      const __amdgpu_buffer_rsrc_t rs =
+          __builtin_amdgcn_make_buffer_rsrc(out, (short)0, (int)(nrows * D * ES), 0x00020000);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) {
+          const int64_t m = wm * 64 + 32 * jj + n;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int64_t d = d00 + 32 * i + 8 * q;
+            const uint32_t off = d < D ? (uint32_t)((m * D + d) * ES) : 0x80000000u;
+            if constexpr (ES == 4) {
+              const u32x4 v{__float_as_uint(acc[i][jj][4 * q]), __float_as_uint(acc[i][jj][4 * q + 1]),
+                            __float_as_uint(acc[i][jj][4 * q + 2]), __float_as_uint(acc[i][jj][4 * q + 3])};
+              __builtin_amdgcn_raw_buffer_store_b128(v, rs, off, 0, 0);
+            } else {
+              const T v0 = (T)acc[i][jj][4 * q], v1 = (T)acc[i][jj][4 * q + 1];
+              const T v2 = (T)acc[i][jj][4 * q + 2], v3 = (T)acc[i][jj][4 * q + 3];
+              const u32x2 v{(uint32_t)__builtin_bit_cast(uint16_t, v0) | ((uint32_t)__builtin_bit_cast(uint16_t, v1) << 16),
+                            (uint32_t)__builtin_bit_cast(uint16_t, v2) | ((uint32_t)__builtin_bit_cast(uint16_t, v3) << 16)};
+              __builtin_amdgcn_raw_buffer_store_b64(v, rs, off, 0, 0);
+            }
+          }
+        }
+      }
+    } else {
+      float* carry = a.de_acc + orow0 * D;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) {
+          const int64_t m = wm * 64 + 32 * jj + n;
+          if (m >= nrows) continue;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int64_t d = d00 + 32 * i + 8 * q;
+            if (d >= D) continue;
+            f32x4 v{acc[i][jj][4 * q], acc[i][jj][4 * q + 1], acc[i][jj][4 * q + 2], acc[i][jj][4 * q + 3]};
+            f32x4* cp = reinterpret_cast<f32x4*>(carry + m * D + d);
+            if (mode == kStoreF32) {
+              *cp = v;
+            } else if (mode == kAddF32) {
+              *cp = *cp + v;
+            } else {
+              v = *cp + v;
+#pragma unroll
+              for (int k = 0; k < 4; ++k) out[m * D + d + k] = (T)v[k];
+            }
+          }
+        }
+      }
+      wait_vmcnt<0>();  // the fp32 modes leave nothing in flight for the stage waits
+    }
+  };
+
+  Cur cs;
+  if (!seek(lidx, cs)) return;
+  prep(cs);
+  Cur nx = cs, last = cs;
+  bool have = true;
+  // issue_next: the loads of nx (or, past the end, a repeat of the last one, which
+  // keeps the per-stage load count uniform and is never consumed); advance_next:
+  // step nx on, issuing the scalar list loads of its next tile.
+  auto issue_next = [&](int st) { issue(have ? nx : last, st); };
+  auto advance_next = [&]() {
+    if (have) {
+      last = nx;
+      have = advance(nx);
+    }
+  };
+  // Software pipeline over the (task, tile, slice) steps, two stages: step s reads
+  // stage s % 2 while slice s + 1 streams into the other one.
+  //   read ks 1 | MFMAs ks 0;  read ks 2 | MFMAs ks 1;  read ks 3 | MFMAs ks 2
+  //   barrier: slice s + 1 has landed and every wave is done with stage s % 2
+  //   DMA of slice s + 2 into stage s % 2 | read ks 0 of slice s + 1 | MFMAs ks 3
+  //   (task end: epilogue)
+  // The epilogue's stores are the newest vector memory operations at the next
+  // barrier, so it waits with vmcnt(NSTORE) and lets them drain in the background.
+  constexpr int NSTORE = 4 * 2 * 4;  // buffer stores per wave per kWriteT epilogue
+  static_assert(NSTORE < 64, "vmcnt is 6 bits");
+  issue_next(0);
+  advance_next();
+  stage_barrier<0>();
+  issue_next(1);
+  advance_next();
+  u32x4 xa[4], ga[2], xb[4], gb[2];
+  frags(0, 0, xa, ga);
+  int st = 0;
+  bool stores = false;  // the last epilogue's stores may still be in flight
+  for (;;) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) acc[i][jj] = zero16();
+    for (;;) {
+      frags(st, 1, xb, gb);
+      mma(xa, ga);
+      sched_interleave<0, MK, RK, 0, 0>();
+      frags(st, 2, xa, ga);
+      mma(xb, gb);
+      sched_interleave<0, MK, RK, 0, 0>();
+      frags(st, 3, xb, gb);
+      mma(xa, ga);
+      sched_interleave<0, MK, RK, 0, 0>();
+      __builtin_amdgcn_sched_barrier(0);
+      if (stores)
+        stage_barrier<NSTORE>();
+      else
+        stage_barrier<0>();
+      stores = false;
+      issue_next(st);
+      advance_next();
+      __builtin_amdgcn_sched_barrier(0);
+      st ^= 1;
+      frags(st, 0, xa, ga);
+      mma(xb, gb);
+      sched_interleave<0, MK, RK, 0, 0>();
+      if (++cs.h < S::SPT) continue;
+      cs.h = 0;
+      if (++cs.j == cs.cnt) break;
+    }
+    epilogue(cs);
+    stores = mode == kWriteT;
+    if (!seek(cs.q + nper, cs)) break;
+  }
+  wait_vmcnt<0>();
+}
+
+// As bwd_sum_kernel, in the narrow geometry (one 4-wave pipeline of 48 KiB stages).
+template <typename T, int PHASE>
+__global__ __launch_bounds__(kThreads, 1) void bwd_sum_narrow_kernel(BwdArgs a, int chunk) {
+  using S = SumGeoNarrow<T>;
+  __shared__ __attribute__((aligned(16))) char smem[S::STAGES * S::STAGE];
+  constexpr int ES = S::ES;
+  const int nrb = (int)a.plan.nrb, nds = (int)((a.D + S::DN - 1) / S::DN);
   const int vlo = chunk * (int)a.plan.chunk_nvt;
   const int nv = min((int)a.plan.nvt, vlo + (int)a.plan.chunk_nvt) - vlo;
   const int n_own = PHASE == 0 ? nrb : nv;
@@ -943,6 +1272,15 @@ static void launch_g(const BwdArgs& a, int chunk, dim3 grid, hipStream_t s) {
 #undef CCE_G
 }
 
+// dE sums: the wide geometry (512 columns per task, measured 0.85x the time of two
+// narrow tasks) unless it leaves so few tasks that the narrow one finishes in fewer
+// rounds of equal tasks over the persistent grid.
+static bool use_wide_de_sums(const BwdPlan& P, int64_t D, int grid) {
+  const int64_t tw = P.nrb * ((D + 511) / 512), tn = P.nrb * ((D + 255) / 256);
+  const int64_t rw = (tw + grid - 1) / grid, rn = (tn + grid - 1) / grid;
+  return rw * 512 * 85 < rn * 256 * 100;
+}
+
 template <typename T>
 static hipError_t backward_typed(const BwdArgs& a, hipStream_t s) {
   const BwdPlan& P = a.plan;
@@ -965,11 +1303,14 @@ static hipError_t backward_typed(const BwdArgs& a, hipStream_t s) {
       launch_g<T, false>(a, chunk, dim3(gp), s);
     if ((err = hipGetLastError()) != hipSuccess) return err;
     if (want_de) {
-      hipLaunchKernelGGL((bwd_sum_kernel<T, 0>), dim3(gp), dim3(kThreads), 0, s, a, chunk);
+      if (use_wide_de_sums(P, a.D, gp))
+        hipLaunchKernelGGL((bwd_sum_kernel<T, 0>), dim3(gp), dim3(SumGeo<T>::NT), 0, s, a, chunk);
+      else
+        hipLaunchKernelGGL((bwd_sum_narrow_kernel<T, 0>), dim3(gp), dim3(SumGeoNarrow<T>::NT), 0, s, a, chunk);
       if ((err = hipGetLastError()) != hipSuccess) return err;
     }
     if (want_dc) {
-      hipLaunchKernelGGL((bwd_sum_kernel<T, 1>), dim3(gp), dim3(kThreads), 0, s, a, chunk);
+      hipLaunchKernelGGL((bwd_sum_narrow_kernel<T, 1>), dim3(gp), dim3(SumGeoNarrow<T>::NT), 0, s, a, chunk);
       if ((err = hipGetLastError()) != hipSuccess) return err;
     }
     if (want_db) {

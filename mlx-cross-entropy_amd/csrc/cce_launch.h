@@ -45,7 +45,6 @@ struct FwdArgs {
 constexpr size_t kWScratchBudget = size_t(2) << 30;  // bytes of G-tile scratch per chunk
 constexpr int kCompactMaxWords = 8192;                 // bitmap words one compaction holds in LDS
 constexpr int kCompactMaxVt = 4096;                    // vocabulary tiles per chunk (LDS counts)
-constexpr int kSumDN = 256;                            // output columns (D) per sum task
 
 struct BwdPlan {
   int64_t nvt, nrb, total;  // vocab tiles, token blocks, pairs
@@ -53,7 +52,6 @@ struct BwdPlan {
   int64_t chunk_nvt;        // vocab tiles per chunk (a multiple of 32 unless it is nvt)
   int64_t n_chunks;
   int64_t cap;              // slots per chunk: nrb * chunk_nvt
-  int64_t n_dslices;        // kSumDN-wide column slices of a row of E / C
   size_t g_bytes;           // bytes of one G tile (128 x 128 x sizeof(T))
   // workspace byte offsets
   size_t bits, counts, rb_start, slot_vt, slot_rb, vt_start, vt_slot, g_task, g_task_rb, gtile, colsum, de_acc;
@@ -92,7 +90,6 @@ inline BwdPlan make_bwd_plan(size_t esize, int64_t N, int64_t D, int64_t V, bool
   P.chunk_nvt = cw;
   P.n_chunks = (P.nvt + cw - 1) / cw;
   P.cap = P.nrb * cw;
-  P.n_dslices = (D + kSumDN - 1) / kSumDN;
   size_t off = 0;
   auto take = [&](size_t bytes) {
     const size_t o = off;
