@@ -35,6 +35,8 @@
 //                          with ds_read_b64_tr_b16 (dC reads G transposed the same
 //                          way), output rows written once in the output dtype.
 //   6. bwd_dbias_kernel    dBias = sum of the column sums of a vocab tile's slots.
+#include <cstdlib>
+
 #include "cce_device.h"
 #include "cce_launch.h"
 
@@ -1276,6 +1278,11 @@ static void launch_g(const BwdArgs& a, int chunk, dim3 grid, hipStream_t s) {
 // narrow tasks) unless it leaves so few tasks that the narrow one finishes in fewer
 // rounds of equal tasks over the persistent grid.
 static bool use_wide_de_sums(const BwdPlan& P, int64_t D, int grid) {
+  // Test hook: CCE_TEST_DE_SUMS=wide|narrow forces a geometry.
+  if (const char* env = std::getenv("CCE_TEST_DE_SUMS")) {
+    if (env[0] == 'w') return true;
+    if (env[0] == 'n') return false;
+  }
   const int64_t tw = P.nrb * ((D + 511) / 512), tn = P.nrb * ((D + 255) / 256);
   const int64_t rw = (tw + grid - 1) / grid, rn = (tn + grid - 1) / grid;
   return rw * 512 * 85 < rn * 256 * 100;

@@ -346,10 +346,12 @@ def test_filter_disabled_is_dense(m, cuda):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("filtered", [False, True])
-def test_vocabulary_chunks(m, cuda, dtype, filtered, monkeypatch):
+@pytest.mark.parametrize("de_sums", ["narrow", "wide"])
+def test_vocabulary_chunks(m, cuda, dtype, filtered, de_sums, monkeypatch):
     """Several vocabulary chunks (forced narrow through CCE_TEST_CHUNK_VT): dE carried in fp32
     between chunks, dC / dBias final per chunk; equal to the single-chunk result and the oracle.
-    D = 264 also leaves a ragged second column slice."""
+    Both dE-sum geometries (CCE_TEST_DE_SUMS); D = 264 leaves a ragged column slice in each."""
+    monkeypatch.setenv("CCE_TEST_DE_SUMS", de_sums)
     N, D, V = 300, 264, 9000
     if filtered:
         e, c, t = _peaked(cuda, N=N, D=D, V=V, dtype=dtype, seed=11)
