@@ -200,6 +200,8 @@ int cce_backward(int dtype, const void* e, const void* c, const void* bias, cons
   a.vt_slot = reinterpret_cast<int*>(ws + P.vt_slot);
   a.g_task = reinterpret_cast<int*>(ws + P.g_task);
   a.g_task_rb = reinterpret_cast<int*>(ws + P.g_task_rb);
+  a.own_rb = reinterpret_cast<int*>(ws + P.own_rb);
+  a.own_vt = reinterpret_cast<int*>(ws + P.own_vt);
   a.gtile = (dE || dC) ? ws + P.gtile : nullptr;
   a.colsum = dBias ? reinterpret_cast<float*>(ws + P.colsum) : nullptr;
   a.de_acc = (dE && P.n_chunks > 1) ? reinterpret_cast<float*>(ws + P.de_acc) : nullptr;

@@ -126,17 +126,57 @@ __device__ __forceinline__ int block_excl_scan(int v, int* wsum, int& total) {
   return wbase + incl - v;
 }
 
+// Writes to out[] the owners o < n with size(o) > 0, largest size first (a counting
+// sort over LDS buckets; sizes past the last bucket share it, and the order among
+// equal sizes is not fixed), and returns how many there are.  All 1024 threads call it.
+constexpr int kOrderBuckets = 4096;
+template <typename F>
+__device__ __forceinline__ int order_by_size(int n, F size, int* out, int* hist, int* wsum) {
+  const int tid = threadIdx.x;
+  auto bucket = [](int sz) { return kOrderBuckets - 1 - min(sz, kOrderBuckets - 1); };
+  for (int i = tid; i < kOrderBuckets; i += 1024) hist[i] = 0;
+  __syncthreads();
+  for (int o = tid; o < n; o += 1024) {
+    const int sz = size(o);
+    if (sz > 0) atomicAdd(&hist[bucket(sz)], 1);
+  }
+  __syncthreads();
+  constexpr int PER = kOrderBuckets / 1024;
+  int loc[PER], sum = 0;
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    loc[k] = hist[tid * PER + k];
+    sum += loc[k];
+  }
+  int total;
+  int pos = block_excl_scan(sum, wsum, total);  // its barriers order the reads above before the writes below
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    hist[tid * PER + k] = pos;
+    pos += loc[k];
+  }
+  __syncthreads();
+  for (int o = tid; o < n; o += 1024) {
+    const int sz = size(o);
+    if (sz > 0) out[atomicAdd(&hist[bucket(sz)], 1)] = o;
+  }
+  __syncthreads();  // hist free for the next call
+  return total;
+}
+
 // ---------------------------------------------------------------- 2. compaction
 // One workgroup of 1024 threads per chunk.  The chunk's bitmap (token block rb,
 // word wl) sits in LDS as bm[rb * cwd + wl]; an exclusive scan of the word
 // popcounts in that (row-major) order gives every kept pair its slot, so slots run
 // by token block, then vocab tile.  Per vocab tile the kept token blocks are listed
 // in vt_slot (ascending), and the G tasks cut every token block's slots into runs
-// of at most 4.
+// of at most 4.  Last, the owners of the dE and dC sums (token blocks, vocab tiles)
+// that hold kept tiles are listed by descending tile count.
 __global__ __launch_bounds__(1024) void bwd_compact_kernel(BwdArgs a, int chunk) {
   __shared__ uint32_t bm[kCompactMaxWords];
   __shared__ int pre[kCompactMaxWords + 1];
   __shared__ int vcnt[kCompactMaxVt];
+  __shared__ int hist[kOrderBuckets];
   __shared__ int wsum[16];
   const int tid = threadIdx.x;
   const int nrb = (int)a.plan.nrb, nw = (int)a.plan.nwords, nvt = (int)a.plan.nvt;
@@ -232,7 +272,12 @@ __global__ __launch_bounds__(1024) void bwd_compact_kernel(BwdArgs a, int chunk)
     }
     vp += vcnt[v];
   }
+  // (the barriers of the scan above made every vcnt entry visible)
+  const int n_own_rb = order_by_size(nrb, [&](int rb) { return pre[(rb + 1) * cwd] - pre[rb * cwd]; }, a.own_rb, hist, wsum);
+  const int n_own_vt = order_by_size(nv, [&](int v) { return vcnt[v]; }, a.own_vt, hist, wsum);
   if (tid == 0) {
+    a.counts[4] = n_own_rb;
+    a.counts[5] = n_own_vt;
     a.vt_start[nv] = vtot;
     a.counts[0] = kept;
     a.counts[1] = ntask;
@@ -640,9 +685,13 @@ enum WriteMode { kWriteT = 0, kStoreF32 = 1, kAddF32 = 2, kFinishT = 3 };
 // vocab tile.  PHASE 1 (dC): owner = vocab tile v of the chunk, tiles = vt_slot
 // entries; A-side rows = E rows of each slot's token block.
 //
-// Owners are dealt to the 8 XCDs round-robin; the 32 workgroups of an XCD take its
-// (owner, D slice) tasks in order, so all D slices of one owner run at once on one
-// XCD and share its G tiles in L2.  A workgroup walks the (task, tile, slice) steps
+// Tasks are the (owner, D slice) pairs of the owners that hold kept tiles, listed
+// largest owner first (own_rb / own_vt) with an owner's D slices consecutive, and
+// dealt out in rounds of one task per workgroup, the workgroups numbered XCD-major
+// and the direction reversed every round ("snake" order): every workgroup then gets
+// a large and a small task in turn, so their totals stay close, and the tasks of
+// one round that sit next to each other in the list -- the D slices of one owner,
+// which share its G tiles -- run at the same time on one XCD.  A workgroup walks the (task, tile, slice) steps
 // of its tasks as one pipeline: the next slice is in flight while one is consumed,
 // across task boundaries.  The epilogue's stores are buffer stores (out-of-range
 // lanes are dropped by the buffer's range check).  Every per-step address is a
@@ -656,10 +705,10 @@ __global__ __launch_bounds__(SumGeo<T>::NT, 1) void bwd_sum_kernel(BwdArgs a, in
   const int nrb = (int)a.plan.nrb, nds = (int)((a.D + S::DN - 1) / S::DN);
   const int vlo = chunk * (int)a.plan.chunk_nvt;
   const int nv = min((int)a.plan.nvt, vlo + (int)a.plan.chunk_nvt) - vlo;
-  const int n_own = PHASE == 0 ? nrb : nv;
   const int xcd = (int)(blockIdx.x & 7), lidx = (int)(blockIdx.x >> 3), nper = (int)(gridDim.x >> 3);
-  const int n_mine = n_own > xcd ? (n_own - xcd + 7) / 8 : 0;
-  const int ngroups = n_mine * nds;
+  const int ntasks = ldu(a.counts, PHASE == 0 ? 4 : 5) * nds;
+  const int* own = PHASE == 0 ? a.own_rb : a.own_vt;
+  const int vwg = xcd * nper + lidx, nwg = (int)gridDim.x;  // workgroups numbered XCD-major
   const int64_t D = a.D;
   const int64_t pitch = D * ES;
   const char* X = reinterpret_cast<const char*>(PHASE == 0 ? a.c : a.e);
@@ -717,22 +766,18 @@ __global__ __launch_bounds__(SumGeo<T>::NT, 1) void bwd_sum_kernel(BwdArgs a, in
     int64_t xrow;
   };
   auto seek = [&](int q, Cur& c) -> bool {
-    for (; q < ngroups; q += nper) {
-      const int owner = xcd + 8 * (q / nds);
-      const int b = ldu(PHASE == 0 ? a.rb_start : a.vt_start, owner);
-      const int e = ldu(PHASE == 0 ? a.rb_start : a.vt_start, owner + 1);
-      if (e > b) {
-        c.q = q;
-        c.owner = owner;
-        c.ds = q - (q / nds) * nds;
-        c.b = b;
-        c.cnt = e - b;
-        c.j = 0;
-        c.h = 0;
-        return true;
-      }
-    }
-    return false;
+    const int p = q * nwg + ((q & 1) ? nwg - 1 - vwg : vwg);
+    if (p >= ntasks) return false;
+    const int owner = ldu(own, p / nds);
+    const int b = ldu(PHASE == 0 ? a.rb_start : a.vt_start, owner);
+    c.q = q;
+    c.owner = owner;
+    c.ds = p - (p / nds) * nds;
+    c.b = b;
+    c.cnt = ldu(PHASE == 0 ? a.rb_start : a.vt_start, owner + 1) - b;
+    c.j = 0;
+    c.h = 0;
+    return true;
   };
   auto prep = [&](Cur& c) {
     if (PHASE == 0) {
@@ -750,7 +795,7 @@ __global__ __launch_bounds__(SumGeo<T>::NT, 1) void bwd_sum_kernel(BwdArgs a, in
       prep(c);
       return true;
     }
-    if (!seek(c.q + nper, c)) return false;
+    if (!seek(c.q + 1, c)) return false;
     prep(c);
     return true;
   };
@@ -876,7 +921,7 @@ __global__ __launch_bounds__(SumGeo<T>::NT, 1) void bwd_sum_kernel(BwdArgs a, in
   };
 
   Cur cs;
-  if (!seek(lidx, cs)) return;
+  if (!seek(0, cs)) return;
   prep(cs);
   Cur nx = cs, last = cs;
   bool have = true;
@@ -943,7 +988,7 @@ __global__ __launch_bounds__(SumGeo<T>::NT, 1) void bwd_sum_kernel(BwdArgs a, in
     }
     epilogue(cs);
     stores = mode == kWriteT;
-    if (!seek(cs.q + nper, cs)) break;
+    if (!seek(cs.q + 1, cs)) break;
   }
   wait_vmcnt<0>();
 }
@@ -957,10 +1002,10 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_narrow_kernel(BwdArgs a, 
   const int nrb = (int)a.plan.nrb, nds = (int)((a.D + S::DN - 1) / S::DN);
   const int vlo = chunk * (int)a.plan.chunk_nvt;
   const int nv = min((int)a.plan.nvt, vlo + (int)a.plan.chunk_nvt) - vlo;
-  const int n_own = PHASE == 0 ? nrb : nv;
   const int xcd = (int)(blockIdx.x & 7), lidx = (int)(blockIdx.x >> 3), nper = (int)(gridDim.x >> 3);
-  const int n_mine = n_own > xcd ? (n_own - xcd + 7) / 8 : 0;
-  const int ngroups = n_mine * nds;
+  const int ntasks = ldu(a.counts, PHASE == 0 ? 4 : 5) * nds;
+  const int* own = PHASE == 0 ? a.own_rb : a.own_vt;
+  const int vwg = xcd * nper + lidx, nwg = (int)gridDim.x;  // workgroups numbered XCD-major
   const int64_t D = a.D;
   const int64_t pitch = D * ES;
   const char* X = reinterpret_cast<const char*>(PHASE == 0 ? a.c : a.e);
@@ -1018,22 +1063,18 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_narrow_kernel(BwdArgs a, 
     int64_t xrow;
   };
   auto seek = [&](int q, Cur& c) -> bool {
-    for (; q < ngroups; q += nper) {
-      const int owner = xcd + 8 * (q / nds);
-      const int b = ldu(PHASE == 0 ? a.rb_start : a.vt_start, owner);
-      const int e = ldu(PHASE == 0 ? a.rb_start : a.vt_start, owner + 1);
-      if (e > b) {
-        c.q = q;
-        c.owner = owner;
-        c.ds = q - (q / nds) * nds;
-        c.b = b;
-        c.cnt = e - b;
-        c.j = 0;
-        c.h = 0;
-        return true;
-      }
-    }
-    return false;
+    const int p = q * nwg + ((q & 1) ? nwg - 1 - vwg : vwg);
+    if (p >= ntasks) return false;
+    const int owner = ldu(own, p / nds);
+    const int b = ldu(PHASE == 0 ? a.rb_start : a.vt_start, owner);
+    c.q = q;
+    c.owner = owner;
+    c.ds = p - (p / nds) * nds;
+    c.b = b;
+    c.cnt = ldu(PHASE == 0 ? a.rb_start : a.vt_start, owner + 1) - b;
+    c.j = 0;
+    c.h = 0;
+    return true;
   };
   auto prep = [&](Cur& c) {
     if (PHASE == 0) {
@@ -1051,7 +1092,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_narrow_kernel(BwdArgs a, 
       prep(c);
       return true;
     }
-    if (!seek(c.q + nper, c)) return false;
+    if (!seek(c.q + 1, c)) return false;
     prep(c);
     return true;
   };
@@ -1191,7 +1232,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_narrow_kernel(BwdArgs a, 
   };
 
   Cur cs;
-  if (!seek(lidx, cs)) return;
+  if (!seek(0, cs)) return;
   prep(cs);
   Cur nx = cs, last = cs;
   bool have = true;
@@ -1239,7 +1280,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_narrow_kernel(BwdArgs a, 
     }
     epilogue(cs);
     if (mode == kWriteT) since_store = 1;
-    if (!seek(cs.q + nper, cs)) break;
+    if (!seek(cs.q + 1, cs)) break;
   }
   wait_vmcnt<0>();
 }

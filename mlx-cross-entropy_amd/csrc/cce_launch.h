@@ -54,7 +54,8 @@ struct BwdPlan {
   int64_t cap;              // slots per chunk: nrb * chunk_nvt
   size_t g_bytes;           // bytes of one G tile (128 x 128 x sizeof(T))
   // workspace byte offsets
-  size_t bits, counts, rb_start, slot_vt, slot_rb, vt_start, vt_slot, g_task, g_task_rb, gtile, colsum, de_acc;
+  size_t bits, counts, rb_start, slot_vt, slot_rb, vt_start, vt_slot, g_task, g_task_rb, own_rb, own_vt, gtile, colsum,
+      de_acc;
   size_t total_bytes;
 };
 
@@ -105,6 +106,8 @@ inline BwdPlan make_bwd_plan(size_t esize, int64_t N, int64_t D, int64_t V, bool
   P.vt_slot = take((size_t)P.cap * 4);
   P.g_task = take((size_t)P.cap * 4);
   P.g_task_rb = take((size_t)P.cap * 4);
+  P.own_rb = take((size_t)P.nrb * 4);
+  P.own_vt = take((size_t)cw * 4);
   P.gtile = want_g ? take((size_t)P.cap * P.g_bytes) : 0;
   P.colsum = want_db ? take((size_t)P.cap * kBwdVocab * sizeof(float)) : 0;
   P.de_acc = (want_de && P.n_chunks > 1) ? take((size_t)N * (size_t)D * sizeof(float)) : 0;
@@ -129,7 +132,7 @@ struct BwdArgs {
   void* dBias;  // output, dtype, or null
   // workspace (see BwdPlan); the lists are rebuilt for every chunk
   uint32_t* bits;     // [nrb][nwords] keep bitmap, bit b of word w = vocab tile 32 w + b
-  int* counts;        // [0] kept pairs of the chunk, [1] G tasks of the chunk
+  int* counts;        // [0] kept pairs, [1] G tasks, [2] tail item counter, [4] / [5] entries of own_rb / own_vt
   int* rb_start;      // [nrb + 1] first slot of each token block
   int* slot_vt;       // [cap] chunk-local vocab tile of each slot
   int* slot_rb;       // [cap] token block of each slot
@@ -137,6 +140,8 @@ struct BwdArgs {
   int* vt_slot;       // [cap] slots grouped by vocab tile, token blocks ascending
   int* g_task;        // [cap] first slot of each G task (up to 4 slots of one token block)
   int* g_task_rb;     // [cap] token block of each G task
+  int* own_rb;        // [nrb] token blocks with kept tiles, most tiles first (dE owners)
+  int* own_vt;        // [chunk_nvt] chunk vocab tiles with kept tiles, most first (dC owners)
   char* gtile;        // [cap][128 tokens][128 vocab] G tiles, token-major, dtype
   float* colsum;      // [cap][128] per-slot column sums of G (dBias)
   float* de_acc;      // [N, D] fp32, only when n_chunks > 1
