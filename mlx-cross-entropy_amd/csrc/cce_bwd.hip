@@ -605,7 +605,7 @@ struct SumGeoNarrow {
   static constexpr int GLW = G_BYTES / 1024 / 4;   // G loads per wave per stage (4)
   static constexpr int LPW = XLW + GLW;
   static constexpr int KE = 32 / ES;               // contraction elements per MFMA step
-  static constexpr int NSTORE = 4 * 2 * 4;         // output stores per wave per task
+  static constexpr int NSTORE = 4 * 2 * (ES == 2 ? 2 : 4);  // output stores per wave per task
   static_assert(X_BYTES == 32768 && KS * GTP == G_BYTES, "stage geometry");
   static_assert((STAGES - 2) * LPW + NSTORE < 64, "in-flight operations must fit vmcnt");
 };
@@ -674,6 +674,12 @@ __device__ __forceinline__ void dma16_s(const char* sbase, uint32_t voff, uint32
   asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(u),
                "s"(__builtin_amdgcn_readfirstlane(lds))
                : "memory", "m0");
+}
+
+// Two floats rounded to a 16-bit type, packed low-first into one dword.
+template <typename T>
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, (T)lo) | ((uint32_t)__builtin_bit_cast(uint16_t, (T)hi) << 16);
 }
 
 // Output of a finished dE / dC task: kWriteT stores the output dtype (single chunk,
@@ -872,20 +878,36 @@ __global__ __launch_bounds__(SumGeo<T>::NT, 1) void bwd_sum_kernel(BwdArgs a, in
 #pragma unroll
         for (int jj = 0; jj < 2; ++jj) {
           const int64_t m = wm * 64 + 32 * jj + n;
+          if constexpr (ES == 4) {
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const int64_t d = d00 + 32 * i + 8 * q;
-            const uint32_t off = d < D ? (uint32_t)((m * D + d) * ES) : 0x80000000u;
-            if constexpr (ES == 4) {
+            for (int q = 0; q < 4; ++q) {
+              const int64_t d = d00 + 32 * i + 8 * q;
+              const uint32_t off = d < D ? (uint32_t)((m * D + d) * ES) : 0x80000000u;
               const u32x4 v{__float_as_uint(acc[i][jj][4 * q]), __float_as_uint(acc[i][jj][4 * q + 1]),
                             __float_as_uint(acc[i][jj][4 * q + 2]), __float_as_uint(acc[i][jj][4 * q + 3])};
               __builtin_amdgcn_raw_buffer_store_b128(v, rs, off, 0, 0);
-            } else {
-              const T v0 = (T)acc[i][jj][4 * q], v1 = (T)acc[i][jj][4 * q + 1];
-              const T v2 = (T)acc[i][jj][4 * q + 2], v3 = (T)acc[i][jj][4 * q + 3];
-              const u32x2 v{(uint32_t)__builtin_bit_cast(uint16_t, v0) | ((uint32_t)__builtin_bit_cast(uint16_t, v1) << 16),
-                            (uint32_t)__builtin_bit_cast(uint16_t, v2) | ((uint32_t)__builtin_bit_cast(uint16_t, v3) << 16)};
-              __builtin_amdgcn_raw_buffer_store_b64(v, rs, off, 0, 0);
+            }
+          } else {
+            // Lane (n, h) holds columns 8 q + 4 h + 0..3 of its row; one lane swap
+            // between the halves per q pair gives every lane 8 consecutive columns:
+            // 16 p + 8 h + 0..7 for the pair (2 p, 2 p + 1), stored as 16 bytes.
+            uint32_t pk[4][2];
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+              for (int k = 0; k < 2; ++k) pk[q][k] = pack2<T>(acc[i][jj][4 * q + 2 * k], acc[i][jj][4 * q + 2 * k + 1]);
+#pragma unroll
+            for (int pq = 0; pq < 2; ++pq) {
+              u32x4 v;
+#pragma unroll
+              for (int k = 0; k < 2; ++k) {
+                const auto sw = __builtin_amdgcn_permlane32_swap(pk[2 * pq][k], pk[2 * pq + 1][k], false, false);
+                v[k] = sw[0];
+                v[2 + k] = sw[1];
+              }
+              const int64_t d = d00 - h * 4 + 32 * i + 16 * pq + 8 * h;
+              const uint32_t off = d < D ? (uint32_t)((m * D + d) * ES) : 0x80000000u;
+              __builtin_amdgcn_raw_buffer_store_b128(v, rs, off, 0, 0);
             }
           }
         }
@@ -943,7 +965,7 @@ __global__ __launch_bounds__(SumGeo<T>::NT, 1) void bwd_sum_kernel(BwdArgs a, in
   //   (task end: epilogue)
   // The epilogue's stores are the newest vector memory operations at the next
   // barrier, so it waits with vmcnt(NSTORE) and lets them drain in the background.
-  constexpr int NSTORE = 4 * 2 * 4;  // buffer stores per wave per kWriteT epilogue
+  constexpr int NSTORE = 4 * 2 * (ES == 2 ? 2 : 4);  // buffer stores per wave per kWriteT epilogue
   static_assert(NSTORE < 64, "vmcnt is 6 bits");
   issue_next(0);
   advance_next();
@@ -1183,20 +1205,36 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_narrow_kernel(BwdArgs a, 
 #pragma unroll
         for (int jj = 0; jj < 2; ++jj) {
           const int64_t m = wm * 64 + 32 * jj + n;
+          if constexpr (ES == 4) {
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const int64_t d = d00 + 32 * i + 8 * q;
-            const uint32_t off = d < D ? (uint32_t)((m * D + d) * ES) : 0x80000000u;
-            if constexpr (ES == 4) {
+            for (int q = 0; q < 4; ++q) {
+              const int64_t d = d00 + 32 * i + 8 * q;
+              const uint32_t off = d < D ? (uint32_t)((m * D + d) * ES) : 0x80000000u;
               const u32x4 v{__float_as_uint(acc[i][jj][4 * q]), __float_as_uint(acc[i][jj][4 * q + 1]),
                             __float_as_uint(acc[i][jj][4 * q + 2]), __float_as_uint(acc[i][jj][4 * q + 3])};
               __builtin_amdgcn_raw_buffer_store_b128(v, rs, off, 0, 0);
-            } else {
-              const T v0 = (T)acc[i][jj][4 * q], v1 = (T)acc[i][jj][4 * q + 1];
-              const T v2 = (T)acc[i][jj][4 * q + 2], v3 = (T)acc[i][jj][4 * q + 3];
-              const u32x2 v{(uint32_t)__builtin_bit_cast(uint16_t, v0) | ((uint32_t)__builtin_bit_cast(uint16_t, v1) << 16),
-                            (uint32_t)__builtin_bit_cast(uint16_t, v2) | ((uint32_t)__builtin_bit_cast(uint16_t, v3) << 16)};
-              __builtin_amdgcn_raw_buffer_store_b64(v, rs, off, 0, 0);
+            }
+          } else {
+            // Lane (n, h) holds columns 8 q + 4 h + 0..3 of its row; one lane swap
+            // between the halves per q pair gives every lane 8 consecutive columns:
+            // 16 p + 8 h + 0..7 for the pair (2 p, 2 p + 1), stored as 16 bytes.
+            uint32_t pk[4][2];
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+              for (int k = 0; k < 2; ++k) pk[q][k] = pack2<T>(acc[i][jj][4 * q + 2 * k], acc[i][jj][4 * q + 2 * k + 1]);
+#pragma unroll
+            for (int pq = 0; pq < 2; ++pq) {
+              u32x4 v;
+#pragma unroll
+              for (int k = 0; k < 2; ++k) {
+                const auto sw = __builtin_amdgcn_permlane32_swap(pk[2 * pq][k], pk[2 * pq + 1][k], false, false);
+                v[k] = sw[0];
+                v[2 + k] = sw[1];
+              }
+              const int64_t d = d00 - h * 4 + 32 * i + 16 * pq + 8 * h;
+              const uint32_t off = d < D ? (uint32_t)((m * D + d) * ES) : 0x80000000u;
+              __builtin_amdgcn_raw_buffer_store_b128(v, rs, off, 0, 0);
             }
           }
         }
