@@ -45,6 +45,12 @@ namespace cce {
 static_assert(kStatTile == kBwdVocab, "filter statistics are kept per backward vocabulary tile");
 static_assert(kBwdTokens == 128 && kBwdVocab == 128, "the G-tile kernels assume 128 x 128 tiles");
 
+// Two floats rounded to a 16-bit type, packed low-first into one dword.
+template <typename T>
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, (T)lo) | ((uint32_t)__builtin_bit_cast(uint16_t, (T)hi) << 16);
+}
+
 // ---------------------------------------------------------------- 1. filter
 // One wave per (token block rb, bitmap word w): bits b = 0..31 for vocab tiles 32 w + b.
 // Lanes hold two rows each; eight tiles' statistics are fetched before they are tested.
@@ -354,7 +360,7 @@ __device__ __forceinline__ void empty_owner(const BwdArgs& a, int chunk, int o) 
 using GLoopShape = NTMainLoop<__bf16, 4 * kBwdVocab, kBwdTokens, 4, 2>;
 constexpr int kGThreads = GLoopShape::NTHREADS;
 
-template <typename T, bool HAS_BIAS, bool WANT_G, bool WANT_DB>
+template <typename T, bool HAS_BIAS, bool WANT_G, bool WANT_DB, bool RAGGED>
 __global__ __launch_bounds__(kGThreads, 1) void bwd_g_kernel(BwdArgs a, int chunk) {
   using Loop = NTMainLoop<T, 4 * kBwdVocab, kBwdTokens, 4, 2>;  // A = 4 x 128 C rows, B = 128 E rows
   static_assert(Loop::NTHREADS == kGThreads, "one launch shape for every dtype");
@@ -374,7 +380,6 @@ __global__ __launch_bounds__(kGThreads, 1) void bwd_g_kernel(BwdArgs a, int chun
   const T* bias = reinterpret_cast<const T*>(a.bias);
   const char* E = reinterpret_cast<const char*>(a.e);
   const char* C = reinterpret_cast<const char*>(a.c);
-  const bool ragged = pitch % kSliceBytes != 0;
 
   struct Task {
     int s0, rb, cnt;
@@ -390,12 +395,7 @@ __global__ __launch_bounds__(kGThreads, 1) void bwd_g_kernel(BwdArgs a, int chun
   auto sources = [&](const Task& k) {
     return Loop::template make_src<kBwdVocab>(C, a.V, k.seg, E, a.N, (int64_t)k.rb * kBwdTokens, pitch, pitch, xcd);
   };
-  auto prefetch = [&](const typename Loop::template Src<4>& src) {
-    if (ragged)
-      Loop::template prefetch<true>(src, smem);
-    else
-      Loop::template prefetch<false>(src, smem);
-  };
+  auto prefetch = [&](const typename Loop::template Src<4>& src) { Loop::template prefetch<RAGGED>(src, smem); };
 
   // Once out of tasks, the workgroup zeroes owners without kept tiles, taking items
   // from a counter the compaction kernel reset (only when dE or dC is wanted).
@@ -430,10 +430,7 @@ __global__ __launch_bounds__(kGThreads, 1) void bwd_g_kernel(BwdArgs a, int chun
     for (int i = 0; i < TI; ++i)
 #pragma unroll
       for (int j = 0; j < TJ; ++j) w[i][j] = zero16();
-    if (ragged)
-      Loop::template consume<true>(src, smem, w);
-    else
-      Loop::template consume<false>(src, smem, w);
+    Loop::template consume<RAGGED>(src, smem, w);
 
     const int tn = t + (int)gridDim.x;
     Task nxt;
@@ -476,7 +473,8 @@ __global__ __launch_bounds__(kGThreads, 1) void bwd_g_kernel(BwdArgs a, int chun
       // zeros for C rows past V, and dC / dBias are never written there.  One
       // 32-column block i at a time: form its 32 G values per lane, store them
       // token-major (4 consecutive vocab columns per store), add their column sums.
-      char* gt = a.gtile + (size_t)slot * a.plan.g_bytes;
+      const __amdgpu_buffer_rsrc_t grs = __builtin_amdgcn_make_buffer_rsrc(
+          a.gtile + (size_t)slot * a.plan.g_bytes, (short)0, (int)a.plan.g_bytes, 0x00020000);
 #pragma unroll
       for (int i = 0; i < TI; ++i) {
         float gv[TJ][16];
@@ -495,25 +493,40 @@ __global__ __launch_bounds__(kGThreads, 1) void bwd_g_kernel(BwdArgs a, int chun
           }
         }
         if constexpr (WANT_G) {
-          // byte offsets within the 128 x 128 tile stay 32-bit: (64 wb + 32 j + n) rows
-          // of 128 ES bytes, plus (32 i + 8 q + 4 h) columns
-          const uint32_t lane_off = (uint32_t)((wb * 64 + n) * kBwdVocab * ES + h * 4 * ES);
+          // Buffer stores at 32-bit offsets within the 128 x 128 tile: row (token)
+          // 64 wb + 32 j + n of 128 ES bytes.  Lane (n, h) holds columns 32 i + 8 q +
+          // 4 h + 0..3; for 16-bit types one lane swap per q pair gives every lane the 8
+          // consecutive columns 32 i + 16 p + 8 h + 0..7 of the pair (2 p, 2 p + 1).
+          if constexpr (ES == 4) {
+            const uint32_t lane_off = (uint32_t)((wb * 64 + n) * kBwdVocab * ES + h * 4 * ES);
 #pragma unroll
-          for (int j = 0; j < TJ; ++j) {
+            for (int j = 0; j < TJ; ++j)
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              char* dst = gt + (lane_off + (uint32_t)((j * 32 * kBwdVocab + i * 32 + q * 8) * ES));
-              if constexpr (ES == 4) {
-                *reinterpret_cast<f32x4*>(dst) =
-                    f32x4{gv[j][q * 4], gv[j][q * 4 + 1], gv[j][q * 4 + 2], gv[j][q * 4 + 3]};
-              } else {
-                const T v0_ = (T)gv[j][q * 4], v1_ = (T)gv[j][q * 4 + 1];
-                const T v2_ = (T)gv[j][q * 4 + 2], v3_ = (T)gv[j][q * 4 + 3];
-                const uint32_t p0 = (uint32_t)__builtin_bit_cast(uint16_t, v0_) |
-                                    ((uint32_t)__builtin_bit_cast(uint16_t, v1_) << 16);
-                const uint32_t p1 = (uint32_t)__builtin_bit_cast(uint16_t, v2_) |
-                                    ((uint32_t)__builtin_bit_cast(uint16_t, v3_) << 16);
-                *reinterpret_cast<u32x2*>(dst) = u32x2{p0, p1};
+              for (int q = 0; q < 4; ++q) {
+                const f32x4 v{gv[j][q * 4], gv[j][q * 4 + 1], gv[j][q * 4 + 2], gv[j][q * 4 + 3]};
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), grs,
+                                                       lane_off + (uint32_t)((j * 32 * kBwdVocab + i * 32 + q * 8) * ES), 0, 0);
+              }
+          } else {
+            const uint32_t lane_off = (uint32_t)((wb * 64 + n) * kBwdVocab * ES + h * 8 * ES);
+#pragma unroll
+            for (int j = 0; j < TJ; ++j) {
+              uint32_t pk[4][2];
+#pragma unroll
+              for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int k = 0; k < 2; ++k) pk[q][k] = pack2<T>(gv[j][4 * q + 2 * k], gv[j][4 * q + 2 * k + 1]);
+#pragma unroll
+              for (int pq = 0; pq < 2; ++pq) {
+                u32x4 v;
+#pragma unroll
+                for (int k = 0; k < 2; ++k) {
+                  const auto sw = __builtin_amdgcn_permlane32_swap(pk[2 * pq][k], pk[2 * pq + 1][k], false, false);
+                  v[k] = sw[0];
+                  v[2 + k] = sw[1];
+                }
+                __builtin_amdgcn_raw_buffer_store_b128(v, grs,
+                                                       lane_off + (uint32_t)((j * 32 * kBwdVocab + i * 32 + pq * 16) * ES), 0, 0);
               }
             }
           }
@@ -674,12 +687,6 @@ __device__ __forceinline__ void dma16_s(const char* sbase, uint32_t voff, uint32
   asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(u),
                "s"(__builtin_amdgcn_readfirstlane(lds))
                : "memory", "m0");
-}
-
-// Two floats rounded to a 16-bit type, packed low-first into one dword.
-template <typename T>
-__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
-  return (uint32_t)__builtin_bit_cast(uint16_t, (T)lo) | ((uint32_t)__builtin_bit_cast(uint16_t, (T)hi) << 16);
 }
 
 // Output of a finished dE / dC task: kWriteT stores the output dtype (single chunk,
@@ -1342,14 +1349,18 @@ __global__ __launch_bounds__(kBwdVocab) void bwd_dbias_kernel(BwdArgs a, int chu
 template <typename T, bool HB>
 static void launch_g(const BwdArgs& a, int chunk, dim3 grid, hipStream_t s) {
   const bool g = a.dE != nullptr || a.dC != nullptr, db = a.dBias != nullptr;
-#define CCE_G(G, DB)                                                                                   \
-  if (g == G && db == DB) {                                                                            \
-    hipLaunchKernelGGL((bwd_g_kernel<T, HB, G, DB>), grid, dim3(kGThreads), 0, s, a, chunk);           \
+  const bool rg = (a.D * (int64_t)sizeof(T)) % kSliceBytes != 0;
+#define CCE_G(G, DB, RG)                                                                               \
+  if (g == G && db == DB && rg == RG) {                                                                \
+    hipLaunchKernelGGL((bwd_g_kernel<T, HB, G, DB, RG>), grid, dim3(kGThreads), 0, s, a, chunk);       \
     return;                                                                                            \
   }
-  CCE_G(true, true)
-  CCE_G(true, false)
-  CCE_G(false, true)
+  CCE_G(true, true, false)
+  CCE_G(true, false, false)
+  CCE_G(false, true, false)
+  CCE_G(true, true, true)
+  CCE_G(true, false, true)
+  CCE_G(false, true, true)
 #undef CCE_G
 }
 
