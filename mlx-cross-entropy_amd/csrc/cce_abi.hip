@@ -202,6 +202,8 @@ int cce_backward(int dtype, const void* e, const void* c, const void* bias, cons
   a.g_task_rb = reinterpret_cast<int*>(ws + P.g_task_rb);
   a.own_rb = reinterpret_cast<int*>(ws + P.own_rb);
   a.own_vt = reinterpret_cast<int*>(ws + P.own_vt);
+  a.dc_bin_start = reinterpret_cast<int*>(ws + P.dc_bin_start);
+  a.dc_bin_owner = reinterpret_cast<int*>(ws + P.dc_bin_owner);
   a.gtile = (dE || dC) ? ws + P.gtile : nullptr;
   a.colsum = dBias ? reinterpret_cast<float*>(ws + P.colsum) : nullptr;
   a.de_acc = (dE && P.n_chunks > 1) ? reinterpret_cast<float*>(ws + P.de_acc) : nullptr;

@@ -114,7 +114,9 @@ __device__ __forceinline__ int wave_incl_scan(int v) {
   return v;
 }
 
-// Exclusive prefix sum over the 1024 threads of a workgroup; `total` gets the sum.
+// Exclusive prefix sum over the NW waves of a workgroup (all threads call it);
+// `total` gets the sum.
+template <int NW = 16>
 __device__ __forceinline__ int block_excl_scan(int v, int* wsum, int& total) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int incl = wave_incl_scan(v);
@@ -122,7 +124,7 @@ __device__ __forceinline__ int block_excl_scan(int v, int* wsum, int& total) {
   __syncthreads();
   int wbase = 0, tot = 0;
 #pragma unroll
-  for (int w = 0; w < 16; ++w) {
+  for (int w = 0; w < NW; ++w) {
     const int x = wsum[w];
     wbase += w < wave ? x : 0;
     tot += x;
@@ -347,6 +349,95 @@ __device__ __forceinline__ void empty_owner(const BwdArgs& a, int chunk, int o) 
     *reinterpret_cast<u32x4*>(out + i) = u32x4{0u, 0u, 0u, 0u};
 }
 
+// ---------------------------------------------------------------- dC schedule
+// The dC sums run one D slice of kDcSliceCols columns per workgroup and deal the
+// chunk's dC owners (vocab tiles with kept blocks) to bins: workgroup v takes bin
+// v / nds at slice v % nds, so every slice of an owner runs at the same time, in
+// the same order, on one XCD.  With more slices than workgroups there is one bin
+// and workgroup v takes slices v, v + nwg, ...
+constexpr int kDcSliceCols = 256;
+__host__ __device__ inline int dc_bins(int nwg, int nds) {
+  return nds <= nwg ? (nwg / nds < kMaxDcBins ? nwg / nds : kMaxDcBins) : 0;
+}
+
+// Longest-processing-time-first dealing of the dC owners (own_vt: most kept blocks
+// first) to nbins bins: each owner goes to the bin with the least work so far.
+// Owners of equal size form a batch: the bins are ranked once by (work, index) and
+// owner t of the batch goes to the bin of rank t % nbins -- what dealing them one
+// at a time does, since equal additions keep the ranking.  A bin lists its owners
+// in dealing order.  Run by one workgroup of NT threads; smem holds its tables.
+template <int NT>
+__device__ void dc_schedule(const BwdArgs& a, int nbins, char* smem) {
+  constexpr int NW = NT / 64;
+  const int tid = threadIdx.x;
+  const int n = a.counts[5];
+  int* sz = reinterpret_cast<int*>(smem);  // [n] kept blocks of owner i
+  int* bst = sz + kCompactMaxVt;           // [batches + 1] first owner of each batch
+  int* bin = bst + kCompactMaxVt + 1;      // [n] bin of owner i
+  int* pos = bin + kCompactMaxVt;          // [n] place of owner i in its bin
+  int* work = pos + kCompactMaxVt;         // [nbins] work dealt so far, then bin starts
+  int* cnt = work + kMaxDcBins;            // [nbins] owners dealt so far
+  int* byrank = cnt + kMaxDcBins;          // [nbins] bin of each rank
+  int* wsum = byrank + kMaxDcBins;         // [NW]
+  for (int i = tid; i < n; i += NT) {
+    const int v = a.own_vt[i];
+    sz[i] = a.vt_start[v + 1] - a.vt_start[v];
+  }
+  for (int b = tid; b < kMaxDcBins; b += NT) {
+    work[b] = 0;
+    cnt[b] = 0;
+  }
+  __syncthreads();
+  const int per = (n + NT - 1) / NT;
+  const int i0 = min(n, tid * per), i1 = min(n, i0 + per);
+  int f = 0;
+  for (int i = i0; i < i1; ++i) f += (i == 0 || sz[i] != sz[i - 1]) ? 1 : 0;
+  int nb;
+  int p = block_excl_scan<NW>(f, wsum, nb);
+  for (int i = i0; i < i1; ++i)
+    if (i == 0 || sz[i] != sz[i - 1]) bst[p++] = i;
+  if (tid == 0) bst[nb] = n;
+  __syncthreads();
+  for (int bt = 0; bt < nb; ++bt) {
+    const int b0 = bst[bt], c = bst[bt + 1] - b0, s = sz[b0];
+    for (int b = tid; b < nbins; b += NT) {
+      const int wb = work[b];
+      int r = 0;
+      for (int b2 = 0; b2 < nbins; ++b2) {
+        const int w2 = work[b2];
+        r += (w2 < wb || (w2 == wb && b2 < b)) ? 1 : 0;
+      }
+      byrank[r] = b;
+    }
+    __syncthreads();
+    for (int t = tid; t < c; t += NT) {
+      const int b = byrank[t % nbins];
+      bin[b0 + t] = b;
+      pos[b0 + t] = cnt[b] + t / nbins;
+    }
+    __syncthreads();
+    const int full = c / nbins, rem = c - full * nbins;
+    for (int r = tid; r < nbins; r += NT) {
+      const int b = byrank[r];
+      const int add = full + (r < rem ? 1 : 0);
+      work[b] += add * s;
+      cnt[b] += add;
+    }
+    __syncthreads();
+  }
+  if (tid == 0) {
+    int acc = 0;
+    for (int b = 0; b < nbins; ++b) {
+      work[b] = acc;
+      a.dc_bin_start[b] = acc;
+      acc += cnt[b];
+    }
+    a.dc_bin_start[nbins] = acc;
+  }
+  __syncthreads();
+  for (int i = tid; i < n; i += NT) a.dc_bin_owner[work[bin[i]] + pos[i]] = a.own_vt[i];
+}
+
 // ---------------------------------------------------------------- 4. G tiles
 // Task = up to 4 consecutive slots of one token block (its kept vocab tiles in this
 // chunk).  The 128 x 128 logit tiles of the task's 4 vocab tiles are recomputed
@@ -397,11 +488,13 @@ __global__ __launch_bounds__(kGThreads, 1) void bwd_g_kernel(BwdArgs a, int chun
   };
   auto prefetch = [&](const typename Loop::template Src<4>& src) { Loop::template prefetch<RAGGED>(src, smem); };
 
-  // Once out of tasks, the workgroup zeroes owners without kept tiles, taking items
-  // from a counter the compaction kernel reset (only when dE or dC is wanted).
+  // Once out of tasks, the workgroup takes items from a counter the compaction
+  // kernel reset (only when dE or dC is wanted): first the dC schedule (when dC is
+  // wanted), then the owners without kept tiles, whose rows it zeroes.
   auto tail = [&]() {
     if constexpr (WANT_G) {
-      const int nitems = (int)a.plan.nrb + (min((int)a.plan.nvt, vlo + (int)a.plan.chunk_nvt) - vlo);
+      const int sched = a.dC != nullptr ? 1 : 0;
+      const int nitems = sched + (int)a.plan.nrb + (min((int)a.plan.nvt, vlo + (int)a.plan.chunk_nvt) - vlo);
       int* box = reinterpret_cast<int*>(smem);
       for (;;) {
         __syncthreads();  // box (and smem) free
@@ -409,7 +502,13 @@ __global__ __launch_bounds__(kGThreads, 1) void bwd_g_kernel(BwdArgs a, int chun
         __syncthreads();
         const int o = box[0];
         if (o >= nitems) break;
-        empty_owner<T, kGThreads>(a, chunk, o);
+        if (o < sched) {
+          const int nds = (int)((a.D + kDcSliceCols - 1) / kDcSliceCols);
+          const int nb = dc_bins((int)gridDim.x, nds);
+          dc_schedule<kGThreads>(a, nb > 0 ? nb : 1, smem + 256);  // its tables start past box
+        } else {
+          empty_owner<T, kGThreads>(a, chunk, o - sched);
+        }
       }
     }
   };
@@ -1035,6 +1134,14 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_narrow_kernel(BwdArgs a, 
   const int ntasks = ldu(a.counts, PHASE == 0 ? 4 : 5) * nds;
   const int* own = PHASE == 0 ? a.own_rb : a.own_vt;
   const int vwg = xcd * nper + lidx, nwg = (int)gridDim.x;  // workgroups numbered XCD-major
+  // dC: this workgroup's bin of the schedule the G kernel dealt, and its first D slice
+  static_assert(PHASE == 0 || S::DN == kDcSliceCols, "the dC schedule assumes this slice width");
+  const int dcb = dc_bins(nwg, nds);
+  const int dcm = dcb > 0 ? vwg / nds : 0;
+  const int ds0 = dcb > 0 ? vwg - dcm * nds : vwg;
+  const bool dc_mine = PHASE == 1 && (dcb > 0 ? dcm < dcb : ds0 < nds);
+  const int bstart = dc_mine ? ldu(a.dc_bin_start, dcm) : 0;
+  const int bcnt = dc_mine ? ldu(a.dc_bin_start, dcm + 1) - bstart : 0;
   const int64_t D = a.D;
   const int64_t pitch = D * ES;
   const char* X = reinterpret_cast<const char*>(PHASE == 0 ? a.c : a.e);
@@ -1092,13 +1199,23 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_narrow_kernel(BwdArgs a, 
     int64_t xrow;
   };
   auto seek = [&](int q, Cur& c) -> bool {
-    const int p = q * nwg + ((q & 1) ? nwg - 1 - vwg : vwg);
-    if (p >= ntasks) return false;
-    const int owner = ldu(own, p / nds);
+    int owner, ds;
+    if constexpr (PHASE == 0) {
+      const int p = q * nwg + ((q & 1) ? nwg - 1 - vwg : vwg);
+      if (p >= ntasks) return false;
+      owner = ldu(own, p / nds);
+      ds = p - (p / nds) * nds;
+    } else {  // the q-th owner of this workgroup's bin (then the same again at slice ds0 + nwg, ...)
+      if (bcnt == 0) return false;
+      const int t = q / bcnt;
+      ds = ds0 + t * nwg;
+      if (ds >= nds) return false;
+      owner = ldu(a.dc_bin_owner, bstart + (q - t * bcnt));
+    }
     const int b = ldu(PHASE == 0 ? a.rb_start : a.vt_start, owner);
     c.q = q;
     c.owner = owner;
-    c.ds = p - (p / nds) * nds;
+    c.ds = ds;
     c.b = b;
     c.cnt = ldu(PHASE == 0 ? a.rb_start : a.vt_start, owner + 1) - b;
     c.j = 0;

@@ -45,6 +45,7 @@ struct FwdArgs {
 constexpr size_t kWScratchBudget = size_t(2) << 30;  // bytes of G-tile scratch per chunk
 constexpr int kCompactMaxWords = 8192;                 // bitmap words one compaction holds in LDS
 constexpr int kCompactMaxVt = 4096;                    // vocabulary tiles per chunk (LDS counts)
+constexpr int kMaxDcBins = 256;                        // workgroup bins of the dC sums' schedule
 
 struct BwdPlan {
   int64_t nvt, nrb, total;  // vocab tiles, token blocks, pairs
@@ -54,8 +55,8 @@ struct BwdPlan {
   int64_t cap;              // slots per chunk: nrb * chunk_nvt
   size_t g_bytes;           // bytes of one G tile (128 x 128 x sizeof(T))
   // workspace byte offsets
-  size_t bits, counts, rb_start, slot_vt, slot_rb, vt_start, vt_slot, g_task, g_task_rb, own_rb, own_vt, gtile, colsum,
-      de_acc;
+  size_t bits, counts, rb_start, slot_vt, slot_rb, vt_start, vt_slot, g_task, g_task_rb, own_rb, own_vt, dc_bin_start,
+      dc_bin_owner, gtile, colsum, de_acc;
   size_t total_bytes;
 };
 
@@ -108,6 +109,8 @@ inline BwdPlan make_bwd_plan(size_t esize, int64_t N, int64_t D, int64_t V, bool
   P.g_task_rb = take((size_t)P.cap * 4);
   P.own_rb = take((size_t)P.nrb * 4);
   P.own_vt = take((size_t)cw * 4);
+  P.dc_bin_start = take((size_t)(kMaxDcBins + 1) * 4);
+  P.dc_bin_owner = take((size_t)cw * 4);
   P.gtile = want_g ? take((size_t)P.cap * P.g_bytes) : 0;
   P.colsum = want_db ? take((size_t)P.cap * kBwdVocab * sizeof(float)) : 0;
   P.de_acc = (want_de && P.n_chunks > 1) ? take((size_t)N * (size_t)D * sizeof(float)) : 0;
@@ -142,6 +145,8 @@ struct BwdArgs {
   int* g_task_rb;     // [cap] token block of each G task
   int* own_rb;        // [nrb] token blocks with kept tiles, most tiles first (dE owners)
   int* own_vt;        // [chunk_nvt] chunk vocab tiles with kept tiles, most first (dC owners)
+  int* dc_bin_start;  // [kMaxDcBins + 1] dC schedule: owners of bin m are dc_bin_owner[start[m] .. start[m + 1])
+  int* dc_bin_owner;  // [chunk_nvt]
   char* gtile;        // [cap][128 tokens][128 vocab] G tiles, token-major, dtype
   float* colsum;      // [cap][128] per-slot column sums of G (dBias)
   float* de_acc;      // [N, D] fp32, only when n_chunks > 1
