@@ -448,12 +448,20 @@ __device__ void dc_schedule(const BwdArgs& a, int nbins, char* smem) {
 // next task's pipeline fill before it forms G of the current one.  Tasks are taken
 // XCD-major (consecutive tasks on one XCD) so tasks that run together share C rows
 // in that XCD's L2.
-using GLoopShape = NTMainLoop<__bf16, 4 * kBwdVocab, kBwdTokens, 4, 2>;
-constexpr int kGThreads = GLoopShape::NTHREADS;
+#ifndef CCE_G_SLICE
+#define CCE_G_SLICE 128
+#endif
+#ifndef CCE_G_STAGES
+#define CCE_G_STAGES 2
+#endif
+constexpr int kGSlice = CCE_G_SLICE, kGStages = CCE_G_STAGES;
+template <typename T>
+using GLoop = NTMainLoop<T, 4 * kBwdVocab, kBwdTokens, 4, 2, kGSlice, kGStages>;  // A = 4 x 128 C rows, B = 128 E rows
+constexpr int kGThreads = GLoop<__bf16>::NTHREADS;
 
 template <typename T, bool HAS_BIAS, bool WANT_G, bool WANT_DB, bool RAGGED>
 __global__ __launch_bounds__(kGThreads, 1) void bwd_g_kernel(BwdArgs a, int chunk) {
-  using Loop = NTMainLoop<T, 4 * kBwdVocab, kBwdTokens, 4, 2>;  // A = 4 x 128 C rows, B = 128 E rows
+  using Loop = GLoop<T>;
   static_assert(Loop::NTHREADS == kGThreads, "one launch shape for every dtype");
   constexpr int TI = Loop::TI, TJ = Loop::TJ;
   static_assert(TI == 4 && TJ == 2, "wave tile: one vocab tile x 64 tokens");
@@ -536,7 +544,7 @@ __global__ __launch_bounds__(kGThreads, 1) void bwd_g_kernel(BwdArgs a, int chun
     if (tn < ntask) {
       load_task(tn, nxt);
       src = sources(nxt);
-      prefetch(src);  // stage 0 only; the epilogue below uses stage 1's bytes
+      prefetch(src);  // all stages but the last; the epilogue below uses the last one's bytes
     }
 
     // w[i][j][r]: vocab v0 + 32 i + 8 (r/4) + 4 h + r%4, token t0 + 64 wb + 32 j + n.
@@ -550,7 +558,8 @@ __global__ __launch_bounds__(kGThreads, 1) void bwd_g_kernel(BwdArgs a, int chun
 #pragma unroll
     for (int k = 1; k < 4; ++k) v0 = wa == k ? cur.seg[k] : v0;
     const int64_t t0 = (int64_t)cur.rb * kBwdTokens;
-    float* red = reinterpret_cast<float*>(smem + Loop::STAGE_BYTES);  // [2 wb][4 wa][128] column sums
+    float* red = reinterpret_cast<float*>(smem + (Loop::SMEM_BYTES - Loop::STAGE_BYTES));  // [2 wb][4 wa][128] column sums
+    static_assert(8 * kBwdVocab * sizeof(float) <= Loop::STAGE_BYTES, "column sums fit one stage");
     if (active) {
       float g[TJ], lz[TJ];
       int tl[TJ];
@@ -646,8 +655,8 @@ __global__ __launch_bounds__(kGThreads, 1) void bwd_g_kernel(BwdArgs a, int chun
       }
     }
     if constexpr (WANT_DB) {
-      // the two token halves' column sums meet in LDS (stage 1, which no DMA fills
-      // until the next task's main loop has passed its first barrier)
+      // the two token halves' column sums meet in LDS (the last stage, which no DMA
+      // fills until the next task's main loop has passed its first barrier)
       __syncthreads();
       if (active && wb == 0) {
         float* cs = a.colsum + (size_t)slot * kBwdVocab;
@@ -1466,7 +1475,7 @@ __global__ __launch_bounds__(kBwdVocab) void bwd_dbias_kernel(BwdArgs a, int chu
 template <typename T, bool HB>
 static void launch_g(const BwdArgs& a, int chunk, dim3 grid, hipStream_t s) {
   const bool g = a.dE != nullptr || a.dC != nullptr, db = a.dBias != nullptr;
-  const bool rg = (a.D * (int64_t)sizeof(T)) % kSliceBytes != 0;
+  const bool rg = (a.D * (int64_t)sizeof(T)) % kGSlice != 0;
 #define CCE_G(G, DB, RG)                                                                               \
   if (g == G && db == DB && rg == RG) {                                                                \
     hipLaunchKernelGGL((bwd_g_kernel<T, HB, G, DB, RG>), grid, dim3(kGThreads), 0, s, a, chunk);       \

@@ -141,30 +141,31 @@ __device__ __forceinline__ f32x16 zero16() {
 }
 
 // --------------------------------------------------------------- main loop
-// Stage geometry: every stage holds one kSliceBytes slice of the contraction
+// Stage geometry: every stage holds one SLICE-byte slice of the contraction
 // dim for all ROWS_A + ROWS_B rows, as 16-byte chunks stored in the order
 // chunk ^ f(row).  Measured on gfx950 with the MFMA fragment pattern (lane l
 // reads row l%32, chunk 2s + l/32), both orders below are free of LDS bank
 // conflicts (unswizzled 64-byte rows conflict 75% of the time).  One
 // global_load_lds_dwordx4 (64 lanes x 16 bytes, written contiguously) fills
-// 1024 / kSliceBytes whole rows, each lane group covering one row's slice with
-// a single kSliceBytes-wide request.
+// 1024 / SLICE whole rows, each lane group covering one row's slice with a
+// single SLICE-byte request.
 #ifndef CCE_SLICE_BYTES
 #define CCE_SLICE_BYTES 128
 #endif
 #ifndef CCE_STAGES
 #define CCE_STAGES 2
 #endif
-constexpr int kSliceBytes = CCE_SLICE_BYTES;
+constexpr int kSliceBytes = CCE_SLICE_BYTES;  // the forward's slice and stage count
 constexpr int kStages = CCE_STAGES;
-constexpr int kChunks = kSliceBytes / 16;
-static_assert(kSliceBytes == 64 || kSliceBytes == 128, "slice of 64 or 128 bytes");
 
+template <int SLICE>
 __device__ __forceinline__ uint32_t slice_swz(uint32_t row) {
-  return kSliceBytes == 128 ? ((row ^ (row >> 3)) & 7u) : ((row >> 2) & 3u);
+  static_assert(SLICE == 64 || SLICE == 128, "slice of 64 or 128 bytes");
+  return SLICE == 128 ? ((row ^ (row >> 3)) & 7u) : ((row >> 2) & 3u);
 }
+template <int SLICE>
 __device__ __forceinline__ uint32_t slice_off(uint32_t row, uint32_t chunk) {
-  return row * kSliceBytes + ((chunk ^ slice_swz(row)) << 4);
+  return row * SLICE + ((chunk ^ slice_swz<SLICE>(row)) << 4);
 }
 
 // Source of the zeros that pad a ragged last slice (contraction length not a
@@ -195,26 +196,27 @@ __device__ __forceinline__ void stage_barrier() {
 
 // The "NT" main loop: acc[TI][TJ] = A_blk . B_blk^T for a ROWS_A x ROWS_B block,
 // both operands row-major with the contraction contiguous, staged through LDS in
-// kStages stages of (ROWS_A + ROWS_B) x kSliceBytes by direct-to-LDS loads.
+// STAGES stages of (ROWS_A + ROWS_B) x SLICE bytes by direct-to-LDS loads.
 // make_src() computes one block pair's per-lane sources, prefetch() issues the
 // pipeline fill and consume() runs the contraction; run() / run_gather() do all
 // three.  The phase rotation of the slices (make_src) measured 5% faster in the
 // forward than all XCDs streaming the same slice.
-template <typename T, int ROWS_A, int ROWS_B, int WA, int WB>
+template <typename T, int ROWS_A, int ROWS_B, int WA, int WB, int SLICE = kSliceBytes, int STAGES = kStages>
 struct NTMainLoop {
+  static constexpr int kChunks = SLICE / 16;
   static constexpr int TI = ROWS_A / WA / 32;
   static constexpr int TJ = ROWS_B / WB / 32;
   static constexpr int ROWS = ROWS_A + ROWS_B;
-  static constexpr int RPL = 1024 / kSliceBytes;                 // rows filled by one LDS-DMA load
+  static constexpr int RPL = 1024 / SLICE;                 // rows filled by one LDS-DMA load
   static constexpr int NW = WA * WB;                             // waves (64 NW threads)
   static constexpr int NTHREADS = 64 * NW;
   static constexpr int LPW = ROWS / RPL / NW;                    // LDS-DMA loads per wave per stage
-  static constexpr int KSTEPS = kSliceBytes / 32;                // 32-byte MFMA steps per slice
-  static constexpr uint32_t STAGE_BYTES = ROWS * kSliceBytes;
-  static constexpr uint32_t SMEM_BYTES = kStages * STAGE_BYTES;
+  static constexpr int KSTEPS = SLICE / 32;                // 32-byte MFMA steps per slice
+  static constexpr uint32_t STAGE_BYTES = ROWS * SLICE;
+  static constexpr uint32_t SMEM_BYTES = STAGES * STAGE_BYTES;
   static_assert(LPW * RPL * NW == ROWS, "stage must split evenly over the waves");
   static_assert(ROWS_A % 32 == 0 && ROWS_B % 32 == 0, "rows must be multiples of 32");
-  static_assert((kStages - 1) * LPW < 64, "in-flight loads must fit vmcnt");
+  static_assert((STAGES - 1) * LPW < 64, "in-flight loads must fit vmcnt");
 
   // Per-lane sources of one operand block pair.  Load j of wave w fills rows
   // [r0, r0 + RPL) of a stage, r0 = (j * NW + w) * RPL, so which operand (and which
@@ -257,7 +259,7 @@ struct NTMainLoop {
     for (int j = 0; j < LPW; ++j) {
       const int r0 = (j * NW + wave) * RPL;
       const int row = r0 + lane / kChunks;
-      const uint32_t q = (uint32_t)(lane % kChunks) ^ slice_swz((uint32_t)row);
+      const uint32_t q = (uint32_t)(lane % kChunks) ^ slice_swz<SLICE>((uint32_t)row);
       src.qb[j] = q * 16;
       int64_t g;
       if (j * NW * RPL < ROWS_A) {
@@ -272,22 +274,22 @@ struct NTMainLoop {
       }
     }
     src.kbytes = kbytes;
-    src.KT = (int)((kbytes + kSliceBytes - 1) / kSliceBytes);
+    src.KT = (int)((kbytes + SLICE - 1) / SLICE);
     src.kskew = (int)(((int64_t)(phase8 & 7) * src.KT) >> 3);
     return src;
   }
 
   // LDS-DMA loads of slice kt (clamped to the last slice: harmless reloads into
-  // idle stages) into stage kt % kStages.
+  // idle stages) into stage kt % STAGES.
   template <bool RAGGED, int NSEG>
   static __device__ __forceinline__ void issue(const Src<NSEG>& src, int kt, char* smem) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t lds_w = (uint32_t)(wave * RPL * kSliceBytes);
+    const uint32_t lds_w = (uint32_t)(wave * RPL * SLICE);
     kt = kt < src.KT ? kt : src.KT - 1;
-    char* st = smem + (kt % kStages) * STAGE_BYTES;
+    char* st = smem + (kt % STAGES) * STAGE_BYTES;
     int kr = kt + src.kskew;  // slice actually loaded: rotated by the phase
     kr = kr < src.KT ? kr : kr - src.KT;
-    const int64_t k0 = (int64_t)kr * kSliceBytes;
+    const int64_t k0 = (int64_t)kr * SLICE;
 #pragma unroll
     for (int j = 0; j < LPW; ++j) {
       const int sg = j * NW * RPL < ROWS_A ? (j * NW * RPL) / (ROWS_A / NSEG) : NSEG;
@@ -302,18 +304,18 @@ struct NTMainLoop {
       }
       __builtin_amdgcn_global_load_lds(
           reinterpret_cast<const void*>(g),
-          (__attribute__((address_space(3))) void*)(st + lds_w + j * NW * RPL * kSliceBytes), 16, 0, 0);
+          (__attribute__((address_space(3))) void*)(st + lds_w + j * NW * RPL * SLICE), 16, 0, 0);
     }
   }
 
-  // Pipeline fill: the loads of the first kStages - 1 slices.  smem must be free
+  // Pipeline fill: the loads of the first STAGES - 1 slices.  smem must be free
   // (no wave still reads it); consume() then runs the contraction.  Issuing the
   // fill early lets its latency overlap other work (a persistent kernel's
   // epilogue of the previous tile).
   template <bool RAGGED, int NSEG>
   static __device__ __forceinline__ void prefetch(const Src<NSEG>& src, char* smem) {
 #pragma unroll
-    for (int p = 0; p < kStages - 1; ++p) issue<RAGGED>(src, p, smem);
+    for (int p = 0; p < STAGES - 1; ++p) issue<RAGGED>(src, p, smem);
   }
 
   // acc[TI][TJ] += A_blk . B_blk^T over the full contraction, after prefetch() of
@@ -321,8 +323,8 @@ struct NTMainLoop {
   // [wa*ROWS_A/WA, ...) and B rows [wb*ROWS_B/WB, ...).  Ends with a barrier, so
   // the caller may reuse smem immediately.
   //
-  // Iteration it consumes slice it (stage it % kStages, KSTEPS MFMA steps):
-  //   read fragments of step 1 | issue the LDS-DMA loads of slice it + kStages - 1
+  // Iteration it consumes slice it (stage it % STAGES, KSTEPS MFMA steps):
+  //   read fragments of step 1 | issue the LDS-DMA loads of slice it + STAGES - 1
   //   (into the stage freed by the previous iteration) | MFMAs of step 0
   //   step s >= 1: read fragments of step s+1 | MFMAs of step s
   //   wait for slice it+1 (vmcnt), barrier
@@ -343,9 +345,9 @@ struct NTMainLoop {
     const int KT = src.KT;
     auto frags = [&](const char* s, int ks, u32x4 (&af)[TI], u32x4 (&bf)[TJ]) {
 #pragma unroll
-      for (int ti = 0; ti < TI; ++ti) af[ti] = lds_ld16(s, slice_off(arow + ti * 32, ks * 2 + kg));
+      for (int ti = 0; ti < TI; ++ti) af[ti] = lds_ld16(s, slice_off<SLICE>(arow + ti * 32, ks * 2 + kg));
 #pragma unroll
-      for (int tj = 0; tj < TJ; ++tj) bf[tj] = lds_ld16(s, slice_off(brow + tj * 32, ks * 2 + kg));
+      for (int tj = 0; tj < TJ; ++tj) bf[tj] = lds_ld16(s, slice_off<SLICE>(brow + tj * 32, ks * 2 + kg));
     };
     auto mma = [&](const u32x4 (&af)[TI], const u32x4 (&bf)[TJ]) {
 #pragma unroll
@@ -356,16 +358,16 @@ struct NTMainLoop {
     static_assert(KSTEPS % 2 == 0, "fragments alternate between two register sets");
     constexpr int MF = TI * TJ * Traits<T>::kInstrPerStep;
     constexpr int NR = TI + TJ;
-    constexpr int INFLIGHT = (kStages - 2) * LPW;  // loads allowed in flight at the barrier
+    constexpr int INFLIGHT = (STAGES - 2) * LPW;  // loads allowed in flight at the barrier
 
     stage_barrier<INFLIGHT>();
     u32x4 fa0[TI], fb0[TJ], fa1[TI], fb1[TJ];
     frags(smem, 0, fa0, fb0);
     for (int it = 0; it < KT; ++it) {
-      const char* s = smem + (it % kStages) * STAGE_BYTES;
-      const char* sn = smem + ((it + 1) % kStages) * STAGE_BYTES;
+      const char* s = smem + (it % STAGES) * STAGE_BYTES;
+      const char* sn = smem + ((it + 1) % STAGES) * STAGE_BYTES;
       frags(s, 1, fa1, fb1);
-      issue<RAGGED>(src, it + kStages - 1, smem);
+      issue<RAGGED>(src, it + STAGES - 1, smem);
 #pragma unroll
       for (int ks = 0; ks + 1 < KSTEPS; ks += 2) {
         if (ks > 0) frags(s, ks + 1, fa1, fb1);
@@ -395,8 +397,8 @@ struct NTMainLoop {
 
   // acc[TI][TJ] = A_blk . B_blk^T over the full contraction length kbytes, where
   // A_blk = rows [a_row0, a_row0 + ROWS_A) of A (row pitch `pitch` bytes, rows past
-  // a_rows-1 clamped to the last row) and B_blk likewise.  smem holds kStages
-  // stages of (ROWS_A + ROWS_B) x kSliceBytes.
+  // a_rows-1 clamped to the last row) and B_blk likewise.  smem holds STAGES
+  // stages of (ROWS_A + ROWS_B) x SLICE.
   static __device__ __forceinline__ void run(const char* __restrict__ A, int64_t a_rows, int64_t a_row0,
                                              const char* __restrict__ B, int64_t b_rows, int64_t b_row0,
                                              int64_t pitch, int64_t kbytes, char* smem,
@@ -413,7 +415,7 @@ struct NTMainLoop {
                                                     int64_t pitch, int64_t kbytes, char* smem,
                                                     f32x16 (&acc)[TI][TJ], int phase8 = 0) {
     const auto src = make_src<A_SEG>(A, a_rows, a_seg0, B, b_rows, b_row0, pitch, kbytes, phase8);
-    if (kbytes % kSliceBytes == 0) {
+    if (kbytes % SLICE == 0) {
       prefetch<false>(src, smem);
       consume<false>(src, smem, acc);
     } else {
