@@ -7,6 +7,7 @@
 // lifted: ragged N and V are masked inside the kernels.  Rows must be 16-byte
 // multiples (D % 8 == 0 for 16-bit dtypes, D % 4 == 0 for fp32); the reference
 // requires D % 8 == 0 for every dtype.
+#include <cstdlib>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -207,6 +208,20 @@ int cce_backward(int dtype, const void* e, const void* c, const void* bias, cons
   a.gtile = (dE || dC) ? ws + P.gtile : nullptr;
   a.colsum = dBias ? reinterpret_cast<float*>(ws + P.colsum) : nullptr;
   a.de_acc = (dE && P.n_chunks > 1) ? reinterpret_cast<float*>(ws + P.de_acc) : nullptr;
+  if (P.perm_ok) {
+    a.perm = reinterpret_cast<int*>(ws + P.perm);
+    a.sort_buf = reinterpret_cast<uint32_t*>(ws + P.sort_buf);
+    a.rowbits = reinterpret_cast<uint32_t*>(ws + P.rowbits);
+    a.bits_p = reinterpret_cast<uint32_t*>(ws + P.bits_p);
+    a.t_perm = reinterpret_cast<int64_t*>(ws + P.t_perm);
+    a.lse_perm = reinterpret_cast<float*>(ws + P.lse_perm);
+    a.dnll_perm = reinterpret_cast<float*>(ws + P.dnll_perm);
+    a.e_perm = ws + P.e_perm;
+    a.de_perm = dE ? ws + P.de_perm : nullptr;
+  }
+  // Test hook: CCE_TEST_TOKEN_ORDER=input|sorted forces the token order of the backward.
+  a.perm_mode = 0;
+  if (const char* env = std::getenv("CCE_TEST_TOKEN_ORDER")) a.perm_mode = env[0] == 'i' ? 1 : env[0] == 's' ? 2 : 0;
   a.tile_stats = tile_stats;
   a.plan = P;
   a.num_cus = cus;

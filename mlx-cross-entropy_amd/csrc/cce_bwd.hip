@@ -77,7 +77,7 @@ __global__ __launch_bounds__(256) void bwd_filter_kernel(BwdArgs a) {
       tg[k] = t;
     }
   }
-  uint32_t word = 0;
+  uint32_t word = 0, rw[2] = {0u, 0u};  // the block's word and each row's own bits
   const int vt0 = w * 32;
   for (int b0 = 0; b0 < 32; b0 += 8) {
     if (vt0 + b0 >= nvt) break;
@@ -95,12 +95,40 @@ __global__ __launch_bounds__(256) void bwd_filter_kernel(BwdArgs a) {
       const int64_t v0 = (int64_t)vt * kBwdVocab;
       bool keep = false;
 #pragma unroll
-      for (int k = 0; k < 2; ++k)
-        keep = keep || (act[k] && ((tg[k] >= v0 && tg[k] < v0 + kBwdVocab) || (tm[u][k] - lz[k] >= a.filter_log_eps)));
-      if (__any(keep) && vt < nvt) word |= 1u << (b0 + u);
+      for (int k = 0; k < 2; ++k) {
+        const bool kk = vt < nvt && act[k] && ((tg[k] >= v0 && tg[k] < v0 + kBwdVocab) || (tm[u][k] - lz[k] >= a.filter_log_eps));
+        rw[k] |= kk ? 1u << (b0 + u) : 0u;
+        keep = keep || kk;
+      }
+      if (__any(keep)) word |= 1u << (b0 + u);
     }
   }
   if (lane == 0) a.bits[(size_t)rb * nw + w] = word;
+  if (a.rowbits) {
+#pragma unroll
+    for (int k = 0; k < 2; ++k)
+      if (row[k] < a.N) a.rowbits[(size_t)row[k] * nw + w] = rw[k];
+  }
+}
+
+// Keep bitmap of the sorted token blocks: block rb of the sorted order holds rows
+// perm[128 rb ..], and keeps a tile when one of them does (their per-row bits).
+__global__ __launch_bounds__(256) void bwd_filter_sorted_kernel(BwdArgs a) {
+  const int nrb = (int)a.plan.nrb, nw = (int)a.plan.nwords;
+  const int lane = threadIdx.x & 63;
+  const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (item >= nrb * nw) return;  // uniform per wave
+  const int rb = item / nw;
+  const int w = item - rb * nw;
+  uint32_t x = 0;
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int64_t p = (int64_t)rb * kBwdTokens + k * 64 + lane;
+    if (p < a.N) x |= a.rowbits[(size_t)min((int64_t)a.perm[p], a.N - 1) * nw + w];
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) x |= (uint32_t)__shfl_xor((int)x, o);
+  if (lane == 0) a.bits_p[(size_t)rb * nw + w] = x;
 }
 
 // Inclusive prefix sum across the 64 lanes of a wave.
@@ -132,6 +160,255 @@ __device__ __forceinline__ int block_excl_scan(int v, int* wsum, int& total) {
   __syncthreads();  // wsum may be rewritten by the next scan
   total = tot;
   return wbase + incl - v;
+}
+
+// ---------------------------------------------------------------- token order
+// The backward's token order: rows grouped by key = the vocab tile of the target,
+// or nvt for rows that get no gradient (ignored, target out of range, d_nll == 0).
+//   1. A stable LSD radix sort of (key << 16 | row), 4 key bits per pass.  Element
+//      i of a pass is held by thread i % 1024 in round i / 1024, so rounds, then
+//      waves, then lanes run in element order; a lane's place among the elements
+//      with its digit is the digit's start + the count in earlier (round, wave)
+//      pairs + the count in lower lanes of its wave (a ballot).
+//   2. Rows whose key has fewer than kSortHeadRun rows ("tail" rows: rare targets;
+//      run lengths are read off the sorted keys)
+//      are spread evenly over the token blocks, in sorted order: block b takes the
+//      tail rows [tb(b), tb(b + 1)), tb(b) = floor(min(128 b, N) nT / N), then the
+//      next head rows in sorted order.  Every block then holds a slice of the long
+//      runs (one or two keys) and a few rare keys, instead of the last blocks
+//      holding one key per row.
+// One workgroup of 1024 threads; perm[p] = input row at position p.
+constexpr int kSortMaxRounds = (int)(kPermMaxN / 1024);
+constexpr int kSortHeadRun = 16;
+template <int MAXR>  // rounds the elements of one thread can span: N <= 1024 MAXR
+__global__ __launch_bounds__(1024) void bwd_sort_rows_kernel(BwdArgs a) {
+  // the ping-pong buffers sit in LDS for up to 8 rounds (8192 rows), else in the workspace
+  constexpr int kLdsRows = MAXR <= 8 ? 8 * 1024 : 1;
+  __shared__ int hist[kPermMaxKey];                // first sorted position of each key, then its rows
+  __shared__ int cnt[MAXR * 16 * 16];              // [round][wave][digit], then exclusive prefixes
+  __shared__ int dstart[17];
+  __shared__ int tbl[kPermMaxN / kBwdTokens + 1];  // tail rows before each block
+  __shared__ uint32_t lbuf[2][kLdsRows];
+  static_assert(MAXR % 8 == 0 && MAXR <= kSortMaxRounds, "rounds in groups of 8");
+  const int N = (int)a.N, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nvt = (int)a.plan.nvt;
+  const int rounds = (N + 1023) >> 10;
+  const uint64_t lt = (1ull << lane) - 1ull;
+  uint32_t* buf0 = MAXR <= 8 ? lbuf[0] : a.sort_buf;
+  uint32_t* buf1 = MAXR <= 8 ? lbuf[1] : a.sort_buf + N;
+  // Exclusive prefix of cnt[stride * e + off] over e < n by wave `wave_id` (n <= 64 * 16);
+  // returns the total on every lane of that wave.
+  auto wave_prefix = [&](int n, int stride, int off) {
+    const int per = (n + 63) >> 6;
+    const int e0 = min(n, lane * per), e1 = min(n, e0 + per);
+    int sum = 0;
+    for (int e = e0; e < e1; ++e) sum += cnt[e * stride + off];
+    const int incl = wave_incl_scan(sum);
+    int run = incl - sum;
+    for (int e = e0; e < e1; ++e) {
+      const int c = cnt[e * stride + off];
+      cnt[e * stride + off] = run;
+      run += c;
+    }
+    return __shfl(incl, 63);
+  };
+  // This thread's elements, one per round (element r * 1024 + tid), kept in registers;
+  // global loads are issued in batches so that their latencies overlap.
+  uint32_t x[MAXR];
+  auto valid = [&](int r) { return r < rounds && r * 1024 + tid < N; };
+#pragma unroll
+  for (int r0 = 0; r0 < MAXR; r0 += 8) {
+    int64_t t[8];
+    float g[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      t[k] = valid(r0 + k) ? a.targets[(r0 + k) * 1024 + tid] : -1;
+      g[k] = valid(r0 + k) ? a.d_nll[(r0 + k) * 1024 + tid] : 0.f;
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const bool act = g[k] != 0.f && !(a.has_ignore && t[k] == a.ignore_index) && t[k] >= 0 && t[k] < a.V;
+      const uint32_t key = act ? (uint32_t)(t[k] >> 7) : (uint32_t)nvt;  // t / kBwdVocab
+      x[r0 + k] = (key << 16) | (uint32_t)((r0 + k) * 1024 + tid);
+    }
+  }
+  static_assert(kBwdVocab == 128, "key = target >> 7");
+  int bits = 1;
+  while ((1 << bits) <= nvt) ++bits;
+  const int passes = (bits + 3) >> 2;
+  for (int ps = 0; ps < passes; ++ps) {
+    uint32_t* dst = (ps & 1) ? buf0 : buf1;
+    const int sh = 16 + 4 * ps;
+#pragma unroll
+    for (int r = 0; r < MAXR; ++r) {
+      if (r >= rounds) break;
+      const int d = valid(r) ? (int)((x[r] >> sh) & 15u) : 16;
+      int mycnt = 0;  // lane dd < 16 stores the wave's count of digit dd
+#pragma unroll
+      for (int dd = 0; dd < 16; ++dd) {
+        const int c = __popcll(__ballot(d == dd));
+        mycnt = lane == dd ? c : mycnt;
+      }
+      if (lane < 16) cnt[(r * 16 + wave) * 16 + lane] = mycnt;
+    }
+    __syncthreads();
+    {  // wave dd: exclusive prefix of digit dd over the (round, wave) pairs, in order
+      const int tot = wave_prefix(rounds * 16, 16, wave);
+      if (lane == 0) dstart[wave] = tot;  // digit total, turned into starts below
+    }
+    __syncthreads();
+    if (tid == 0) {
+      int acc = 0;
+      for (int dd = 0; dd < 16; ++dd) {
+        const int c = dstart[dd];
+        dstart[dd] = acc;
+        acc += c;
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < MAXR; ++r) {
+      if (r >= rounds) break;
+      const int d = valid(r) ? (int)((x[r] >> sh) & 15u) : 16;
+      uint64_t mine = 0;
+#pragma unroll
+      for (int dd = 0; dd < 16; ++dd) {
+        const uint64_t m = __ballot(d == dd);
+        mine = d == dd ? m : mine;
+      }
+      if (valid(r)) dst[dstart[d] + cnt[(r * 16 + wave) * 16 + d] + __popcll(mine & lt)] = x[r];
+    }
+    __syncthreads();  // this pass's stores are visible to the workgroup (and cnt free)
+#pragma unroll
+    for (int r = 0; r < MAXR; ++r) x[r] = valid(r) ? dst[r * 1024 + tid] : 0u;
+  }
+  const uint32_t* fin = (passes & 1) ? buf1 : buf0;
+  // Rows per key from the runs of the sorted keys: the first element of a run records
+  // where it starts, the last one the run's length.
+  uint32_t nb[MAXR];
+#pragma unroll
+  for (int r = 0; r < MAXR; ++r) {
+    const int s = r * 1024 + tid;
+    nb[r] = (valid(r) && s > 0) ? fin[s - 1] : 0xFFFFFFFFu;
+  }
+#pragma unroll
+  for (int r = 0; r < MAXR; ++r)
+    if (valid(r) && (nb[r] >> 16) != (x[r] >> 16)) hist[x[r] >> 16] = r * 1024 + tid;
+#pragma unroll
+  for (int r = 0; r < MAXR; ++r) {
+    const int s = r * 1024 + tid;
+    nb[r] = (valid(r) && s + 1 < N) ? fin[s + 1] : 0xFFFFFFFFu;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < MAXR; ++r)
+    if (valid(r) && (nb[r] >> 16) != (x[r] >> 16)) hist[x[r] >> 16] = r * 1024 + tid + 1 - hist[x[r] >> 16];
+  __syncthreads();
+  // Head / tail ranks in sorted order (rounds, waves, lanes in order).
+#pragma unroll
+  for (int r = 0; r < MAXR; ++r) {
+    if (r >= rounds) break;
+    const bool head = valid(r) && hist[x[r] >> 16] >= kSortHeadRun;
+    const uint64_t m = __ballot(head);
+    if (lane == 0) cnt[r * 16 + wave] = __popcll(m);
+  }
+  __syncthreads();
+  if (wave == 0) {
+    const int tot = wave_prefix(rounds * 16, 1, 0);
+    if (lane == 0) dstart[16] = tot;  // head rows
+  }
+  __syncthreads();
+  const int nH = dstart[16], nT = N - nH;
+  const int nrb = (N + kBwdTokens - 1) / kBwdTokens;
+  for (int b = tid; b <= nrb; b += 1024) tbl[b] = (int)((int64_t)min(b * kBwdTokens, N) * nT / N);
+  __syncthreads();
+  auto tb = [&](int b) { return tbl[b]; };                              // tail rows before block b
+  auto hb = [&](int b) { return min(b * kBwdTokens, N) - tbl[b]; };   // head rows before block b
+#pragma unroll
+  for (int r = 0; r < MAXR; ++r) {
+    if (r >= rounds) break;
+    const int s = r * 1024 + tid;
+    const bool head = valid(r) && hist[x[r] >> 16] >= kSortHeadRun;
+    const uint64_t m = __ballot(head);
+    if (valid(r)) {
+      const int hr = cnt[r * 16 + wave] + __popcll(m & lt);  // head rank
+      int pos;
+      if (head) {  // last block b with hb(b) <= hr
+        int lo = 0, hi = nrb - 1;
+        while (lo < hi) {
+          const int mid = (lo + hi + 1) >> 1;
+          if (hb(mid) <= hr) lo = mid; else hi = mid - 1;
+        }
+        pos = lo * kBwdTokens + (tb(lo + 1) - tb(lo)) + (hr - hb(lo));
+      } else {  // last block b with tb(b) <= tail rank
+        const int tr = s - hr;
+        int lo = 0, hi = nrb - 1;
+        while (lo < hi) {
+          const int mid = (lo + hi + 1) >> 1;
+          if (tb(mid) <= tr) lo = mid; else hi = mid - 1;
+        }
+        pos = lo * kBwdTokens + (tr - tb(lo));
+      }
+      a.perm[pos] = (int)(x[r] & 0xFFFFu);
+    }
+  }
+}
+
+// Pointers of the per-row data the G kernel and the sums read and the dE rows they
+// write: the sorted copies when the compaction chose the sorted token order.
+struct RowData {
+  const char* e;
+  const int64_t* targets;
+  const float* lse;
+  const float* d_nll;
+  void* dE;
+};
+__device__ __forceinline__ RowData row_data(const BwdArgs& a) {
+  if (a.perm && ldu(a.counts, kPermFlag) != 0)
+    return RowData{reinterpret_cast<const char*>(a.e_perm), a.t_perm, a.lse_perm, a.dnll_perm, a.de_perm};
+  return RowData{reinterpret_cast<const char*>(a.e), a.targets, a.lse, a.d_nll, a.dE};
+}
+
+// Row copies between the input order and the sorted order, when the compaction
+// chose the sorted order: one wave per row, 8 loads of 16 bytes in flight per lane.
+__device__ __forceinline__ void copy_row(const char* __restrict__ src, char* __restrict__ dst, int64_t nb) {
+  const int lane = threadIdx.x & 63;
+  int64_t o = (int64_t)lane * 16;
+  for (; o + 7 * 1024 < nb; o += 8 * 1024) {
+    u32x4 v[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = *reinterpret_cast<const u32x4*>(src + o + k * 1024);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) *reinterpret_cast<u32x4*>(dst + o + k * 1024) = v[k];
+  }
+  for (; o < nb; o += 1024) *reinterpret_cast<u32x4*>(dst + o) = *reinterpret_cast<const u32x4*>(src + o);
+}
+
+// Row p of the sorted order gathered from row perm[p], with its target, lse and d_nll.
+template <typename T>
+__global__ __launch_bounds__(256) void bwd_permute_rows_kernel(BwdArgs a) {
+  if (ldu(a.counts, kPermFlag) == 0) return;
+  const int64_t p = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (p >= a.N) return;  // uniform per wave
+  const int64_t r = min((int64_t)a.perm[p], a.N - 1);  // a permutation of [0, N); the clamp only guards the reads
+  const int64_t nb = a.D * (int64_t)sizeof(T);          // a multiple of 16
+  copy_row(reinterpret_cast<const char*>(a.e) + r * nb, reinterpret_cast<char*>(a.e_perm) + p * nb, nb);
+  if ((threadIdx.x & 63) == 0) {
+    a.t_perm[p] = a.targets[r];
+    a.lse_perm[p] = a.lse[r];
+    a.dnll_perm[p] = a.d_nll[r];
+  }
+}
+
+// dE row perm[p] from row p of the sorted order.
+template <typename T>
+__global__ __launch_bounds__(256) void bwd_unpermute_rows_kernel(BwdArgs a) {
+  if (ldu(a.counts, kPermFlag) == 0) return;
+  const int64_t p = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (p >= a.N) return;
+  const int64_t r = min((int64_t)a.perm[p], a.N - 1);
+  const int64_t nb = a.D * (int64_t)sizeof(T);
+  copy_row(reinterpret_cast<const char*>(a.de_perm) + p * nb, reinterpret_cast<char*>(a.dE) + r * nb, nb);
 }
 
 // Writes to out[] the owners o < n with size(o) > 0, largest size first (a counting
@@ -178,7 +455,9 @@ __device__ __forceinline__ int order_by_size(int n, F size, int* out, int* hist,
 // popcounts in that (row-major) order gives every kept pair its slot, so slots run
 // by token block, then vocab tile.  Per vocab tile the kept token blocks are listed
 // in vt_slot (ascending), and the G tasks cut every token block's slots into runs
-// of at most 4.  Last, the owners of the dE and dC sums (token blocks, vocab tiles)
+// of at most 4.  The token blocks are those of the input order or of the sorted
+// order (the first chunk picks one for all chunks).  Last, the owners of the dE and
+// dC sums (token blocks, vocab tiles)
 // that hold kept tiles are listed by descending tile count.
 __global__ __launch_bounds__(1024) void bwd_compact_kernel(BwdArgs a, int chunk) {
   __shared__ uint32_t bm[kCompactMaxWords];
@@ -194,9 +473,43 @@ __global__ __launch_bounds__(1024) void bwd_compact_kernel(BwdArgs a, int chunk)
   const int cwd = (nv + 31) >> 5;
   const int E = nrb * cwd;
 
+  // Token order (decided by the first chunk for all of them): the sorted blocks'
+  // bitmap when it keeps at least 10% fewer pairs than the input blocks' (or as the
+  // test hook perm_mode forces).
+  __shared__ int sorted;
+  if (chunk == 0) {
+    int flag = 0;
+    if (a.perm && a.perm_mode != 1) {
+      if (a.perm_mode == 2) {
+        flag = 1;
+      } else {
+        int cn = 0, cs = 0;
+        for (int e = tid; e < nrb * nw; e += 1024) {
+          const int w = e % nw;
+          const int inside = nvt - w * 32;
+          const uint32_t m = inside < 32 ? (1u << inside) - 1u : ~0u;
+          cn += __builtin_popcount(a.bits[e] & m);
+          cs += __builtin_popcount(a.bits_p[e] & m);
+        }
+        int tn, ts;
+        block_excl_scan(cn, wsum, tn);
+        block_excl_scan(cs, wsum, ts);
+        flag = (int64_t)ts * 10 <= (int64_t)tn * 9 ? 1 : 0;
+      }
+    }
+    if (tid == 0) {
+      sorted = flag;
+      a.counts[kPermFlag] = flag;
+    }
+  } else if (tid == 0) {
+    sorted = a.counts[kPermFlag];
+  }
+  __syncthreads();
+  const uint32_t* bsrc = sorted ? a.bits_p : a.bits;
+
   for (int e = tid; e < E; e += 1024) {
     const int rb = e / cwd, wl = e - rb * cwd;
-    uint32_t x = a.bits[(size_t)rb * nw + wlo + wl];
+    uint32_t x = bsrc[(size_t)rb * nw + wlo + wl];
     const int inside = nv - wl * 32;
     if (inside < 32) x &= (1u << inside) - 1u;
     bm[e] = x;
@@ -322,7 +635,7 @@ __device__ __forceinline__ void empty_owner(const BwdArgs& a, int chunk, int o) 
     const int64_t row0 = (int64_t)o * kBwdTokens;
     const int64_t n = (a.N - row0 < kBwdTokens ? a.N - row0 : kBwdTokens) * D;  // elements
     if (!multi) {
-      T* out = reinterpret_cast<T*>(a.dE) + row0 * D;
+      T* out = reinterpret_cast<T*>(row_data(a).dE) + row0 * D;
       for (int64_t i = (int64_t)threadIdx.x * (16 / sizeof(T)); i < n; i += NT * (16 / sizeof(T)))
         *reinterpret_cast<u32x4*>(out + i) = u32x4{0u, 0u, 0u, 0u};
     } else if (first) {
@@ -331,7 +644,7 @@ __device__ __forceinline__ void empty_owner(const BwdArgs& a, int chunk, int o) 
         *reinterpret_cast<f32x4*>(acc + i) = f32x4{0.f, 0.f, 0.f, 0.f};
     } else {
       const float* acc = a.de_acc + row0 * D;
-      T* out = reinterpret_cast<T*>(a.dE) + row0 * D;
+      T* out = reinterpret_cast<T*>(row_data(a).dE) + row0 * D;
       for (int64_t i = (int64_t)threadIdx.x * 4; i < n; i += NT * 4) {
         const f32x4 x = *reinterpret_cast<const f32x4*>(acc + i);
 #pragma unroll
@@ -477,7 +790,8 @@ __global__ __launch_bounds__(kGThreads, 1) void bwd_g_kernel(BwdArgs a, int chun
   const int h = lane >> 5;
   const int64_t pitch = a.D * (int64_t)ES;
   const T* bias = reinterpret_cast<const T*>(a.bias);
-  const char* E = reinterpret_cast<const char*>(a.e);
+  const RowData rd = row_data(a);
+  const char* E = rd.e;
   const char* C = reinterpret_cast<const char*>(a.c);
 
   struct Task {
@@ -570,9 +884,9 @@ __global__ __launch_bounds__(kGThreads, 1) void bwd_g_kernel(BwdArgs a, int chun
         lz[j] = INFINITY;
         tl[j] = -4096;
         if (tok < a.N) {
-          const int64_t tg = a.targets[tok];
-          g[j] = (a.has_ignore && tg == a.ignore_index) ? 0.f : a.d_nll[tok];
-          if (g[j] != 0.f) lz[j] = a.lse[tok] * kLog2e;
+          const int64_t tg = rd.targets[tok];
+          g[j] = (a.has_ignore && tg == a.ignore_index) ? 0.f : rd.d_nll[tok];
+          if (g[j] != 0.f) lz[j] = rd.lse[tok] * kLog2e;
           const int64_t loc = tg - v0;
           if (loc >= 0 && loc < kBwdVocab) tl[j] = (int)loc - 4 * h;
         }
@@ -832,7 +1146,8 @@ __global__ __launch_bounds__(SumGeo<T>::NT, 1) void bwd_sum_kernel(BwdArgs a, in
   const int vwg = xcd * nper + lidx, nwg = (int)gridDim.x;  // workgroups numbered XCD-major
   const int64_t D = a.D;
   const int64_t pitch = D * ES;
-  const char* X = reinterpret_cast<const char*>(PHASE == 0 ? a.c : a.e);
+  const RowData rd = row_data(a);
+  const char* X = PHASE == 0 ? reinterpret_cast<const char*>(a.c) : rd.e;
   const int64_t xrows = PHASE == 0 ? a.V : a.N;
   const int mode = (PHASE == 0 && a.plan.n_chunks > 1)
                        ? (chunk == 0 ? kStoreF32 : (chunk == (int)a.plan.n_chunks - 1 ? kFinishT : kAddF32))
@@ -983,7 +1298,7 @@ __global__ __launch_bounds__(SumGeo<T>::NT, 1) void bwd_sum_kernel(BwdArgs a, in
     const int64_t orow0 = (int64_t)(PHASE == 0 ? c.owner : vlo + c.owner) * 128;
     const int64_t orows = PHASE == 0 ? a.N : a.V;
     const int64_t nrows = orows - orow0 < 128 ? orows - orow0 : 128;
-    T* out = reinterpret_cast<T*>(PHASE == 0 ? a.dE : a.dC) + orow0 * D;
+    T* out = reinterpret_cast<T*>(PHASE == 0 ? rd.dE : a.dC) + orow0 * D;
     const int64_t d00 = (int64_t)c.ds * S::DN + wd * 128 + h * 4;
     if (mode == kWriteT) {
       const __amdgpu_buffer_rsrc_t rs =
@@ -1153,7 +1468,8 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_narrow_kernel(BwdArgs a, 
   const int bcnt = dc_mine ? ldu(a.dc_bin_start, dcm + 1) - bstart : 0;
   const int64_t D = a.D;
   const int64_t pitch = D * ES;
-  const char* X = reinterpret_cast<const char*>(PHASE == 0 ? a.c : a.e);
+  const RowData rd = row_data(a);
+  const char* X = PHASE == 0 ? reinterpret_cast<const char*>(a.c) : rd.e;
   const int64_t xrows = PHASE == 0 ? a.V : a.N;
   const int mode = (PHASE == 0 && a.plan.n_chunks > 1)
                        ? (chunk == 0 ? kStoreF32 : (chunk == (int)a.plan.n_chunks - 1 ? kFinishT : kAddF32))
@@ -1328,7 +1644,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_narrow_kernel(BwdArgs a, 
     const int64_t orow0 = (int64_t)(PHASE == 0 ? c.owner : vlo + c.owner) * 128;
     const int64_t orows = PHASE == 0 ? a.N : a.V;
     const int64_t nrows = orows - orow0 < 128 ? orows - orow0 : 128;
-    T* out = reinterpret_cast<T*>(PHASE == 0 ? a.dE : a.dC) + orow0 * D;
+    T* out = reinterpret_cast<T*>(PHASE == 0 ? rd.dE : a.dC) + orow0 * D;
     const int64_t d00 = (int64_t)c.ds * S::DN + wd * 128 + h * 4;
     if (mode == kWriteT) {
       const __amdgpu_buffer_rsrc_t rs =
@@ -1508,9 +1824,25 @@ template <typename T>
 static hipError_t backward_typed(const BwdArgs& a, hipStream_t s) {
   const BwdPlan& P = a.plan;
   const int items = (int)(P.nrb * P.nwords);
+  const bool sorted_ok = a.perm != nullptr;  // the workspace holds the sorted token order
+  hipError_t err;
+  if (sorted_ok) {
+    if (a.N <= 8 * 1024)
+      hipLaunchKernelGGL(bwd_sort_rows_kernel<8>, dim3(1), dim3(1024), 0, s, a);
+    else if (a.N <= 16 * 1024)
+      hipLaunchKernelGGL(bwd_sort_rows_kernel<16>, dim3(1), dim3(1024), 0, s, a);
+    else if (a.N <= 32 * 1024)
+      hipLaunchKernelGGL(bwd_sort_rows_kernel<32>, dim3(1), dim3(1024), 0, s, a);
+    else
+      hipLaunchKernelGGL(bwd_sort_rows_kernel<kSortMaxRounds>, dim3(1), dim3(1024), 0, s, a);
+    if ((err = hipGetLastError()) != hipSuccess) return err;
+  }
   hipLaunchKernelGGL(bwd_filter_kernel, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, s, a);
-  hipError_t err = hipGetLastError();
-  if (err != hipSuccess) return err;
+  if ((err = hipGetLastError()) != hipSuccess) return err;
+  if (sorted_ok) {
+    hipLaunchKernelGGL(bwd_filter_sorted_kernel, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, s, a);
+    if ((err = hipGetLastError()) != hipSuccess) return err;
+  }
   const bool want_de = a.dE != nullptr, want_dc = a.dC != nullptr, want_db = a.dBias != nullptr;
   const int cus = a.num_cus > 0 ? a.num_cus : 256;
   const int gp = (cus + 7) / 8 * 8;  // persistent grids: a multiple of the 8 XCDs
@@ -1520,6 +1852,10 @@ static hipError_t backward_typed(const BwdArgs& a, hipStream_t s) {
     hipLaunchKernelGGL(bwd_compact_kernel, dim3(1), dim3(1024), 0, s, a, chunk);
     if ((err = hipGetLastError()) != hipSuccess) return err;
     if (!(want_de || want_dc || want_db)) continue;
+    if (chunk == 0 && sorted_ok) {  // the sorted rows, if the compaction chose them
+      hipLaunchKernelGGL((bwd_permute_rows_kernel<T>), dim3((unsigned)((a.N + 3) / 4)), dim3(256), 0, s, a);
+      if ((err = hipGetLastError()) != hipSuccess) return err;
+    }
     if (a.bias)
       launch_g<T, true>(a, chunk, dim3(gp), s);
     else
@@ -1540,6 +1876,10 @@ static hipError_t backward_typed(const BwdArgs& a, hipStream_t s) {
       hipLaunchKernelGGL((bwd_dbias_kernel<T>), dim3((unsigned)nv), dim3(kBwdVocab), 0, s, a, chunk);
       if ((err = hipGetLastError()) != hipSuccess) return err;
     }
+  }
+  if (sorted_ok && want_de) {
+    hipLaunchKernelGGL((bwd_unpermute_rows_kernel<T>), dim3((unsigned)((a.N + 3) / 4)), dim3(256), 0, s, a);
+    if ((err = hipGetLastError()) != hipSuccess) return err;
   }
   return hipGetLastError();
 }

@@ -46,6 +46,14 @@ constexpr size_t kWScratchBudget = size_t(2) << 30;  // bytes of G-tile scratch 
 constexpr int kCompactMaxWords = 8192;                 // bitmap words one compaction holds in LDS
 constexpr int kCompactMaxVt = 4096;                    // vocabulary tiles per chunk (LDS counts)
 constexpr int kMaxDcBins = 256;                        // workgroup bins of the dC sums' schedule
+// Token order of the backward.  The token blocks of the tile filter can be formed
+// from the rows grouped by the vocabulary tile of their target: with a peaked
+// softmax a block then keeps a few tiles instead of one per distinct target.  The
+// grouping (a stable sort, then the rows of rare targets spread evenly over the
+// blocks) runs in one workgroup on 16-bit (tile, row) keys.
+constexpr int64_t kPermMaxN = 65536;   // rows the sort handles
+constexpr int64_t kPermMaxKey = 16384; // tiles + 1 (the key of rows without gradient)
+constexpr int kPermFlag = 15;          // counts[kPermFlag]: 1 when the backward runs on sorted rows
 
 struct BwdPlan {
   int64_t nvt, nrb, total;  // vocab tiles, token blocks, pairs
@@ -54,9 +62,11 @@ struct BwdPlan {
   int64_t n_chunks;
   int64_t cap;              // slots per chunk: nrb * chunk_nvt
   size_t g_bytes;           // bytes of one G tile (128 x 128 x sizeof(T))
+  bool perm_ok;             // the sorted token order is available (N and tile count in range)
   // workspace byte offsets
   size_t bits, counts, rb_start, slot_vt, slot_rb, vt_start, vt_slot, g_task, g_task_rb, own_rb, own_vt, dc_bin_start,
       dc_bin_owner, gtile, colsum, de_acc;
+  size_t perm, sort_buf, rowbits, bits_p, t_perm, lse_perm, dnll_perm, e_perm, de_perm;  // sorted order (perm_ok)
   size_t total_bytes;
 };
 
@@ -114,6 +124,18 @@ inline BwdPlan make_bwd_plan(size_t esize, int64_t N, int64_t D, int64_t V, bool
   P.gtile = want_g ? take((size_t)P.cap * P.g_bytes) : 0;
   P.colsum = want_db ? take((size_t)P.cap * kBwdVocab * sizeof(float)) : 0;
   P.de_acc = (want_de && P.n_chunks > 1) ? take((size_t)N * (size_t)D * sizeof(float)) : 0;
+  P.perm_ok = N <= kPermMaxN && P.nvt + 1 <= kPermMaxKey && (want_g || want_db);
+  if (P.perm_ok) {
+    P.perm = take((size_t)N * 4);
+    P.sort_buf = take((size_t)N * 8);
+    P.rowbits = take((size_t)N * P.nwords * 4);
+    P.bits_p = take((size_t)P.nrb * P.nwords * 4);
+    P.t_perm = take((size_t)N * 8);
+    P.lse_perm = take((size_t)N * 4);
+    P.dnll_perm = take((size_t)N * 4);
+    P.e_perm = take((size_t)N * (size_t)D * esize);
+    P.de_perm = want_de ? take((size_t)N * (size_t)D * esize) : 0;
+  }
   P.total_bytes = off;
   return P;
 }
@@ -153,6 +175,19 @@ struct BwdArgs {
   int64_t* tile_stats;  // [2] or null
   BwdPlan plan;
   int num_cus;
+  // sorted token order (plan.perm_ok; null otherwise).  Row p of the sorted order is
+  // row perm[p] of the input; when counts[kPermFlag] is set the G kernel and the
+  // sums read e_perm / t_perm / lse_perm / dnll_perm and write dE rows to de_perm.
+  int* perm;            // [N]
+  uint32_t* sort_buf;   // [2 N] radix-sort ping-pong of (key << 16 | row)
+  uint32_t* rowbits;    // [N][nwords] keep bits of every row (input order)
+  uint32_t* bits_p;     // [nrb][nwords] keep bitmap of the sorted token blocks
+  int64_t* t_perm;      // [N]
+  float* lse_perm;      // [N]
+  float* dnll_perm;     // [N]
+  void* e_perm;         // [N, D] dtype
+  void* de_perm;        // [N, D] dtype, when dE is wanted
+  int perm_mode;        // 0: sorted order when it keeps >= 10% fewer tiles, 1: never, 2: always
 };
 
 // dtype: 0 f32, 1 f16, 2 bf16.  Return hipError_t of the launches.

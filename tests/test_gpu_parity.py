@@ -297,11 +297,43 @@ def _peaked(dev, N=512, D=256, V=8192, boost=12.0, dtype=torch.bfloat16, seed=5)
     return e, c, t
 
 
-def test_filtered_backward_matches_filter_emulation(m, cuda):
-    """Kept-tile set is exact against the kernel's own fp32 statistics; gradients match the oracle over it."""
+def _sorted_rows(tt, d_nll, V, ignore_index=-100, head_run=16):
+    """The token order the backward may run its tile filter in: rows sorted (stably) by
+    the 128-column vocabulary tile of their target, rows without gradient (ignored,
+    out-of-range target, d_nll == 0) keyed past the last tile; then the rows whose key
+    has fewer than head_run rows are spread evenly over the 128-row blocks (block b
+    takes tail rows [tb(b), tb(b+1)), tb(b) = floor(min(128 b, N) nT / N), followed by
+    the next rows of the longer runs).  Returns perm: position p holds input row perm[p]."""
+    N = len(tt)
+    nvt = (V + 127) // 128
+    act = (d_nll != 0) & (tt != ignore_index) & (tt >= 0) & (tt < V)
+    key = np.where(act, tt // 128, nvt)
+    srt = np.argsort(key, kind="stable")
+    head = np.bincount(key, minlength=nvt + 1)[key[srt]] >= head_run
+    heads, tails = srt[head], srt[~head]
+    nT = len(tails)
+    nrb = (N + 127) // 128
+    tb = [min(128 * b, N) * nT // N for b in range(nrb + 1)]
+    perm = np.empty(N, dtype=np.int64)
+    h = 0
+    for b in range(nrb):
+        p0 = 128 * b
+        nt = tb[b + 1] - tb[b]
+        perm[p0:p0 + nt] = tails[tb[b]:tb[b + 1]]
+        nh = min(128 * (b + 1), N) - p0 - nt
+        perm[p0 + nt:p0 + nt + nh] = heads[h:h + nh]
+        h += nh
+    return perm
+
+
+@pytest.mark.parametrize("order", ["input", "sorted"])
+def test_filtered_backward_matches_filter_emulation(m, cuda, order, monkeypatch):
+    """Kept-tile set is exact against the kernel's own fp32 statistics (token blocks of the
+    input order, or of the rows sorted by target tile); gradients match the oracle over it."""
+    monkeypatch.setenv("CCE_TEST_TOKEN_ORDER", order)
     e, c, t = _peaked(cuda)
     tm, _, _, lse, _ = m._ext.forward(e, c, t, None, -100)
-    N = e.shape[0]
+    N, V = e.shape[0], c.shape[0]
     d_nll = torch.full((N,), 1.0 / N, device=cuda)
     stats = torch.zeros(2, dtype=torch.int64, device=cuda)
     dE, dC, _ = m._ext.backward(e, c, t, lse, tm, d_nll, None, -100, m.FILTER_LOG_EPS, True, True, False,
@@ -309,16 +341,24 @@ def test_filtered_backward_matches_filter_emulation(m, cuda):
     torch.cuda.synchronize()
     tm_np, lse_np = tm.cpu().numpy(), lse.cpu().numpy()
     tt = t.cpu().numpy()
-    keep = O.keep_mask(tm_np, lse_np, tt, np.full(N, 1.0 / N), eps=np.float32(m.FILTER_LOG_EPS))
+    dn = np.full(N, 1.0 / N)
+    perm = _sorted_rows(tt, dn, V) if order == "sorted" else np.arange(N)
+    keep = O.keep_mask(tm_np[:, perm], lse_np[perm], tt[perm], dn[perm], eps=np.float32(m.FILTER_LOG_EPS))
     # the kernel's comparison is fp32 (tile_max - lse >= eps): replay it in fp32
     hot = (tm_np - lse_np[None, :]).astype(np.float32) >= np.float32(m.FILTER_LOG_EPS)
     kept, total = stats.tolist()
     assert total == keep.size
     assert kept == int(keep.sum()), (kept, int(keep.sum()))
     assert 0 < kept < total
-    print(f"filter: kept {kept}/{total} tiles (skip {1 - kept / total:.3f}); hot fraction {hot.mean():.4f}")
+    if order == "sorted":  # the peaked Zipf case is the one the sorted order is for
+        keep_in = O.keep_mask(tm_np, lse_np, tt, dn, eps=np.float32(m.FILTER_LOG_EPS))
+        assert kept * 10 <= int(keep_in.sum()) * 9, (kept, int(keep_in.sum()))
+    print(f"filter ({order} order): kept {kept}/{total} tiles (skip {1 - kept / total:.3f}); "
+          f"hot fraction {hot.mean():.4f}")
     ee, cc = f64(e), f64(c)
-    fE, fC, _ = O.grads_filtered(ee, cc, tt, keep, 128, 128, None, d_nll=np.full(N, 1.0 / N))
+    fE_p, fC, _ = O.grads_filtered(ee[perm], cc, tt[perm], keep, 128, 128, None, d_nll=dn[perm])
+    fE = np.empty_like(fE_p)
+    fE[perm] = fE_p
     emu = [O.rel_fro(f64(dE), fE), O.rel_fro(f64(dC), fC)]
     print(f"kernel vs filter emulation: dE {emu[0]:.3e} dC {emu[1]:.3e}")
     assert emu[0] < 2e-2 and emu[1] < 2e-2  # bf16 tolerance against the same kept-tile set
@@ -462,12 +502,20 @@ def test_config_c3_full_size_moderate_peak_sampled_grads(m, cuda):
     kept, total = m.last_tile_stats()
     dE, dC = e2.grad, c2.grad
 
-    # kept-tile set, from the kernel's fp32 statistics (float32 comparison, as on the GPU)
+    # kept-tile set, from the kernel's fp32 statistics (float32 comparison, as on the GPU),
+    # over the token blocks of the rows sorted by target tile: with this peaked Zipf input
+    # they keep far fewer tiles than the input-order blocks, so the backward runs on them
     tn = t.cpu().numpy()
     d_nll = np.full(N, np.float32(1.0 / N), dtype=np.float32)
-    keep = O.keep_mask(tm.cpu().numpy(), lse.cpu().numpy(), tn, d_nll)
-    print(f"c3 boost 12: loss {loss.item():.4f} kept {kept}/{total} (cpu predicate {int(keep.sum())})")
-    assert int(keep.sum()) == kept and total == keep.size
+    tm_np, lse_np = tm.cpu().numpy(), lse.cpu().numpy()
+    keep_in = O.keep_mask(tm_np, lse_np, tn, d_nll)
+    perm = _sorted_rows(tn, d_nll, V)
+    keep = O.keep_mask(tm_np[:, perm], lse_np[perm], tn[perm], d_nll[perm])
+    blk = np.empty(N, dtype=np.int64)
+    blk[perm] = np.arange(N) // 128  # token block of every row in the sorted order
+    print(f"c3 boost 12: loss {loss.item():.4f} kept {kept}/{total} (cpu predicate: sorted order "
+          f"{int(keep.sum())}, input order {int(keep_in.sum())})")
+    assert int(keep.sum()) == kept and total == keep.size and kept * 10 <= int(keep_in.sum()) * 9
 
     cc = f64(c)
     lse64 = f64(lse)
@@ -481,7 +529,7 @@ def test_config_c3_full_size_moderate_peak_sampled_grads(m, cuda):
     np.testing.assert_allclose(lse64[rows], ref_lse, rtol=0, atol=8 * ulp)
     G = g * np.exp(S - ref_lse[:, None])
     G[np.arange(len(rows)), tn[rows]] -= g
-    mask = np.repeat(keep[:, rows // 128], 128, axis=0)[:V].T  # [rows, V]
+    mask = np.repeat(keep[:, blk[rows]], 128, axis=0)[:V].T  # [rows, V]
     refE = np.where(mask, G, 0.0) @ cc
     errE = O.rel_fro(f64(dE[rows]), refE)
 
@@ -493,7 +541,7 @@ def test_config_c3_full_size_moderate_peak_sampled_grads(m, cuda):
     Sc = ee @ cc[vs].T  # [N, len(vs)]
     Gc = g * np.exp(Sc - lse64[:, None])
     Gc -= g * (tn[:, None] == vs[None, :])
-    maskc = np.repeat(keep[vs // 128, :], 128, axis=1)[:, :N].T  # [N, len(vs)]
+    maskc = keep[vs // 128][:, blk].T  # [N, len(vs)]
     refC = np.where(maskc, Gc, 0.0).T @ ee
     errC = O.rel_fro(f64(dC[vs]), refC)
 
