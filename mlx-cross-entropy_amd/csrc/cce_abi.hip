@@ -217,7 +217,6 @@ int cce_backward(int dtype, const void* e, const void* c, const void* bias, cons
     a.lse_perm = reinterpret_cast<float*>(ws + P.lse_perm);
     a.dnll_perm = reinterpret_cast<float*>(ws + P.dnll_perm);
     a.e_perm = ws + P.e_perm;
-    a.de_perm = dE ? ws + P.de_perm : nullptr;
   }
   // Test hook: CCE_TEST_TOKEN_ORDER=input|sorted forces the token order of the backward.
   a.perm_mode = 0;

@@ -354,23 +354,24 @@ __global__ __launch_bounds__(1024) void bwd_sort_rows_kernel(BwdArgs a) {
   }
 }
 
-// Pointers of the per-row data the G kernel and the sums read and the dE rows they
-// write: the sorted copies when the compaction chose the sorted token order.
+// Pointers of the per-row data the G kernel and the sums read -- the sorted copies
+// when the compaction chose the sorted token order -- and the map from the row
+// order they work in to the rows of dE (perm; null for the input order).
 struct RowData {
   const char* e;
   const int64_t* targets;
   const float* lse;
   const float* d_nll;
-  void* dE;
+  const int* map;
 };
 __device__ __forceinline__ RowData row_data(const BwdArgs& a) {
   if (a.perm && ldu(a.counts, kPermFlag) != 0)
-    return RowData{reinterpret_cast<const char*>(a.e_perm), a.t_perm, a.lse_perm, a.dnll_perm, a.de_perm};
-  return RowData{reinterpret_cast<const char*>(a.e), a.targets, a.lse, a.d_nll, a.dE};
+    return RowData{reinterpret_cast<const char*>(a.e_perm), a.t_perm, a.lse_perm, a.dnll_perm, a.perm};
+  return RowData{reinterpret_cast<const char*>(a.e), a.targets, a.lse, a.d_nll, nullptr};
 }
 
-// Row copies between the input order and the sorted order, when the compaction
-// chose the sorted order: one wave per row, 8 loads of 16 bytes in flight per lane.
+// Row copy into the sorted order, when the compaction chose it: one wave per row,
+// 8 loads of 16 bytes in flight per lane.
 __device__ __forceinline__ void copy_row(const char* __restrict__ src, char* __restrict__ dst, int64_t nb) {
   const int lane = threadIdx.x & 63;
   int64_t o = (int64_t)lane * 16;
@@ -398,17 +399,6 @@ __global__ __launch_bounds__(256) void bwd_permute_rows_kernel(BwdArgs a) {
     a.lse_perm[p] = a.lse[r];
     a.dnll_perm[p] = a.d_nll[r];
   }
-}
-
-// dE row perm[p] from row p of the sorted order.
-template <typename T>
-__global__ __launch_bounds__(256) void bwd_unpermute_rows_kernel(BwdArgs a) {
-  if (ldu(a.counts, kPermFlag) == 0) return;
-  const int64_t p = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (p >= a.N) return;
-  const int64_t r = min((int64_t)a.perm[p], a.N - 1);
-  const int64_t nb = a.D * (int64_t)sizeof(T);
-  copy_row(reinterpret_cast<const char*>(a.de_perm) + p * nb, reinterpret_cast<char*>(a.dE) + r * nb, nb);
 }
 
 // Writes to out[] the owners o < n with size(o) > 0, largest size first (a counting
@@ -633,22 +623,28 @@ __device__ __forceinline__ void empty_owner(const BwdArgs& a, int chunk, int o) 
     const bool first = chunk == 0, last = chunk == (int)a.plan.n_chunks - 1;
     if (multi && !first && !last) return;
     const int64_t row0 = (int64_t)o * kBwdTokens;
-    const int64_t n = (a.N - row0 < kBwdTokens ? a.N - row0 : kBwdTokens) * D;  // elements
+    const int64_t nrows = a.N - row0 < kBwdTokens ? a.N - row0 : kBwdTokens;
+    const int* map = row_data(a).map;  // dE row of each row of the block (null: the same)
+    T* dE = reinterpret_cast<T*>(a.dE);
     if (!multi) {
-      T* out = reinterpret_cast<T*>(row_data(a).dE) + row0 * D;
-      for (int64_t i = (int64_t)threadIdx.x * (16 / sizeof(T)); i < n; i += NT * (16 / sizeof(T)))
-        *reinterpret_cast<u32x4*>(out + i) = u32x4{0u, 0u, 0u, 0u};
+      for (int64_t r = 0; r < nrows; ++r) {
+        T* out = dE + (map ? (int64_t)map[row0 + r] : row0 + r) * D;
+        for (int64_t i = (int64_t)threadIdx.x * (16 / sizeof(T)); i < D; i += NT * (16 / sizeof(T)))
+          *reinterpret_cast<u32x4*>(out + i) = u32x4{0u, 0u, 0u, 0u};
+      }
     } else if (first) {
       float* acc = a.de_acc + row0 * D;
-      for (int64_t i = (int64_t)threadIdx.x * 4; i < n; i += NT * 4)
+      for (int64_t i = (int64_t)threadIdx.x * 4; i < nrows * D; i += NT * 4)
         *reinterpret_cast<f32x4*>(acc + i) = f32x4{0.f, 0.f, 0.f, 0.f};
     } else {
-      const float* acc = a.de_acc + row0 * D;
-      T* out = reinterpret_cast<T*>(row_data(a).dE) + row0 * D;
-      for (int64_t i = (int64_t)threadIdx.x * 4; i < n; i += NT * 4) {
-        const f32x4 x = *reinterpret_cast<const f32x4*>(acc + i);
+      for (int64_t r = 0; r < nrows; ++r) {
+        const float* acc = a.de_acc + (row0 + r) * D;
+        T* out = dE + (map ? (int64_t)map[row0 + r] : row0 + r) * D;
+        for (int64_t i = (int64_t)threadIdx.x * 4; i < D; i += NT * 4) {
+          const f32x4 x = *reinterpret_cast<const f32x4*>(acc + i);
 #pragma unroll
-        for (int k = 0; k < 4; ++k) out[i + k] = (T)x[k];
+          for (int k = 0; k < 4; ++k) out[i + k] = (T)x[k];
+        }
       }
     }
     return;
@@ -1298,11 +1294,21 @@ __global__ __launch_bounds__(SumGeo<T>::NT, 1) void bwd_sum_kernel(BwdArgs a, in
     const int64_t orow0 = (int64_t)(PHASE == 0 ? c.owner : vlo + c.owner) * 128;
     const int64_t orows = PHASE == 0 ? a.N : a.V;
     const int64_t nrows = orows - orow0 < 128 ? orows - orow0 : 128;
-    T* out = reinterpret_cast<T*>(PHASE == 0 ? rd.dE : a.dC) + orow0 * D;
+    // dE rows of the sorted order go to dE row map[row] (the whole of dE is then one
+    // buffer, under 2^31 bytes when the sorted order is available); rows past the
+    // owner's end get an out-of-range offset, so every lane issues every store.
+    const int* map = PHASE == 0 ? rd.map : nullptr;
+    T* out = reinterpret_cast<T*>(PHASE == 0 ? a.dE : a.dC) + (map ? 0 : orow0 * D);
+    uint32_t rowoff[2];
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      const int64_t m = wm * 64 + 32 * jj + n;
+      rowoff[jj] = m >= nrows ? 0x80000000u : (uint32_t)((map ? (int64_t)map[orow0 + m] : m) * D * ES);
+    }
     const int64_t d00 = (int64_t)c.ds * S::DN + wd * 128 + h * 4;
     if (mode == kWriteT) {
-      const __amdgpu_buffer_rsrc_t rs =
-          __builtin_amdgcn_make_buffer_rsrc(out, (short)0, (int)(nrows * D * ES), 0x00020000);
+      const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+          out, (short)0, (int)((map ? a.N : nrows) * D * ES), 0x00020000);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
 #pragma unroll
@@ -1312,7 +1318,7 @@ __global__ __launch_bounds__(SumGeo<T>::NT, 1) void bwd_sum_kernel(BwdArgs a, in
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
               const int64_t d = d00 + 32 * i + 8 * q;
-              const uint32_t off = d < D ? (uint32_t)((m * D + d) * ES) : 0x80000000u;
+              const uint32_t off = d < D ? rowoff[jj] + (uint32_t)(d * ES) : 0x80000000u;
               const u32x4 v{__float_as_uint(acc[i][jj][4 * q]), __float_as_uint(acc[i][jj][4 * q + 1]),
                             __float_as_uint(acc[i][jj][4 * q + 2]), __float_as_uint(acc[i][jj][4 * q + 3])};
               __builtin_amdgcn_raw_buffer_store_b128(v, rs, off, 0, 0);
@@ -1336,7 +1342,7 @@ __global__ __launch_bounds__(SumGeo<T>::NT, 1) void bwd_sum_kernel(BwdArgs a, in
                 v[2 + k] = sw[1];
               }
               const int64_t d = d00 - h * 4 + 32 * i + 16 * pq + 8 * h;
-              const uint32_t off = d < D ? (uint32_t)((m * D + d) * ES) : 0x80000000u;
+              const uint32_t off = d < D ? rowoff[jj] + (uint32_t)(d * ES) : 0x80000000u;
               __builtin_amdgcn_raw_buffer_store_b128(v, rs, off, 0, 0);
             }
           }
@@ -1362,8 +1368,9 @@ __global__ __launch_bounds__(SumGeo<T>::NT, 1) void bwd_sum_kernel(BwdArgs a, in
               *cp = *cp + v;
             } else {
               v = *cp + v;
+              T* orow = out + (map ? (int64_t)map[orow0 + m] : m) * D;
 #pragma unroll
-              for (int k = 0; k < 4; ++k) out[m * D + d + k] = (T)v[k];
+              for (int k = 0; k < 4; ++k) orow[d + k] = (T)v[k];
             }
           }
         }
@@ -1644,11 +1651,21 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_narrow_kernel(BwdArgs a, 
     const int64_t orow0 = (int64_t)(PHASE == 0 ? c.owner : vlo + c.owner) * 128;
     const int64_t orows = PHASE == 0 ? a.N : a.V;
     const int64_t nrows = orows - orow0 < 128 ? orows - orow0 : 128;
-    T* out = reinterpret_cast<T*>(PHASE == 0 ? rd.dE : a.dC) + orow0 * D;
+    // dE rows of the sorted order go to dE row map[row] (the whole of dE is then one
+    // buffer, under 2^31 bytes when the sorted order is available); rows past the
+    // owner's end get an out-of-range offset, so every lane issues every store.
+    const int* map = PHASE == 0 ? rd.map : nullptr;
+    T* out = reinterpret_cast<T*>(PHASE == 0 ? a.dE : a.dC) + (map ? 0 : orow0 * D);
+    uint32_t rowoff[2];
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      const int64_t m = wm * 64 + 32 * jj + n;
+      rowoff[jj] = m >= nrows ? 0x80000000u : (uint32_t)((map ? (int64_t)map[orow0 + m] : m) * D * ES);
+    }
     const int64_t d00 = (int64_t)c.ds * S::DN + wd * 128 + h * 4;
     if (mode == kWriteT) {
-      const __amdgpu_buffer_rsrc_t rs =
-          __builtin_amdgcn_make_buffer_rsrc(out, (short)0, (int)(nrows * D * ES), 0x00020000);
+      const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+          out, (short)0, (int)((map ? a.N : nrows) * D * ES), 0x00020000);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
 #pragma unroll
@@ -1658,7 +1675,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_narrow_kernel(BwdArgs a, 
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
               const int64_t d = d00 + 32 * i + 8 * q;
-              const uint32_t off = d < D ? (uint32_t)((m * D + d) * ES) : 0x80000000u;
+              const uint32_t off = d < D ? rowoff[jj] + (uint32_t)(d * ES) : 0x80000000u;
               const u32x4 v{__float_as_uint(acc[i][jj][4 * q]), __float_as_uint(acc[i][jj][4 * q + 1]),
                             __float_as_uint(acc[i][jj][4 * q + 2]), __float_as_uint(acc[i][jj][4 * q + 3])};
               __builtin_amdgcn_raw_buffer_store_b128(v, rs, off, 0, 0);
@@ -1682,7 +1699,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_narrow_kernel(BwdArgs a, 
                 v[2 + k] = sw[1];
               }
               const int64_t d = d00 - h * 4 + 32 * i + 16 * pq + 8 * h;
-              const uint32_t off = d < D ? (uint32_t)((m * D + d) * ES) : 0x80000000u;
+              const uint32_t off = d < D ? rowoff[jj] + (uint32_t)(d * ES) : 0x80000000u;
               __builtin_amdgcn_raw_buffer_store_b128(v, rs, off, 0, 0);
             }
           }
@@ -1708,8 +1725,9 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_narrow_kernel(BwdArgs a, 
               *cp = *cp + v;
             } else {
               v = *cp + v;
+              T* orow = out + (map ? (int64_t)map[orow0 + m] : m) * D;
 #pragma unroll
-              for (int k = 0; k < 4; ++k) out[m * D + d + k] = (T)v[k];
+              for (int k = 0; k < 4; ++k) orow[d + k] = (T)v[k];
             }
           }
         }
@@ -1876,10 +1894,6 @@ static hipError_t backward_typed(const BwdArgs& a, hipStream_t s) {
       hipLaunchKernelGGL((bwd_dbias_kernel<T>), dim3((unsigned)nv), dim3(kBwdVocab), 0, s, a, chunk);
       if ((err = hipGetLastError()) != hipSuccess) return err;
     }
-  }
-  if (sorted_ok && want_de) {
-    hipLaunchKernelGGL((bwd_unpermute_rows_kernel<T>), dim3((unsigned)((a.N + 3) / 4)), dim3(256), 0, s, a);
-    if ((err = hipGetLastError()) != hipSuccess) return err;
   }
   return hipGetLastError();
 }

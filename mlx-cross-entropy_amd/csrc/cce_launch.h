@@ -66,7 +66,7 @@ struct BwdPlan {
   // workspace byte offsets
   size_t bits, counts, rb_start, slot_vt, slot_rb, vt_start, vt_slot, g_task, g_task_rb, own_rb, own_vt, dc_bin_start,
       dc_bin_owner, gtile, colsum, de_acc;
-  size_t perm, sort_buf, rowbits, bits_p, t_perm, lse_perm, dnll_perm, e_perm, de_perm;  // sorted order (perm_ok)
+  size_t perm, sort_buf, rowbits, bits_p, t_perm, lse_perm, dnll_perm, e_perm;  // sorted order (perm_ok)
   size_t total_bytes;
 };
 
@@ -124,7 +124,9 @@ inline BwdPlan make_bwd_plan(size_t esize, int64_t N, int64_t D, int64_t V, bool
   P.gtile = want_g ? take((size_t)P.cap * P.g_bytes) : 0;
   P.colsum = want_db ? take((size_t)P.cap * kBwdVocab * sizeof(float)) : 0;
   P.de_acc = (want_de && P.n_chunks > 1) ? take((size_t)N * (size_t)D * sizeof(float)) : 0;
-  P.perm_ok = N <= kPermMaxN && P.nvt + 1 <= kPermMaxKey && (want_g || want_db);
+  // (dE rows are then written through the map with one buffer over all of dE: < 2^31 bytes)
+  P.perm_ok = N <= kPermMaxN && P.nvt + 1 <= kPermMaxKey && (want_g || want_db) &&
+              (double)N * (double)D * (double)esize < 2147483648.0;
   if (P.perm_ok) {
     P.perm = take((size_t)N * 4);
     P.sort_buf = take((size_t)N * 8);
@@ -134,7 +136,6 @@ inline BwdPlan make_bwd_plan(size_t esize, int64_t N, int64_t D, int64_t V, bool
     P.lse_perm = take((size_t)N * 4);
     P.dnll_perm = take((size_t)N * 4);
     P.e_perm = take((size_t)N * (size_t)D * esize);
-    P.de_perm = want_de ? take((size_t)N * (size_t)D * esize) : 0;
   }
   P.total_bytes = off;
   return P;
@@ -177,7 +178,7 @@ struct BwdArgs {
   int num_cus;
   // sorted token order (plan.perm_ok; null otherwise).  Row p of the sorted order is
   // row perm[p] of the input; when counts[kPermFlag] is set the G kernel and the
-  // sums read e_perm / t_perm / lse_perm / dnll_perm and write dE rows to de_perm.
+  // sums read e_perm / t_perm / lse_perm / dnll_perm and write dE row perm[p] for p.
   int* perm;            // [N]
   uint32_t* sort_buf;   // [2 N] radix-sort ping-pong of (key << 16 | row)
   uint32_t* rowbits;    // [N][nwords] keep bits of every row (input order)
@@ -186,7 +187,6 @@ struct BwdArgs {
   float* lse_perm;      // [N]
   float* dnll_perm;     // [N]
   void* e_perm;         // [N, D] dtype
-  void* de_perm;        // [N, D] dtype, when dE is wanted
   int perm_mode;        // 0: sorted order when it keeps >= 10% fewer tiles, 1: never, 2: always
 };
 
