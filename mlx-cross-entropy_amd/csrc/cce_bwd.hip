@@ -54,10 +54,9 @@ __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
 // ---------------------------------------------------------------- 1. filter
 // One wave per (token block rb, bitmap word w): bits b = 0..31 for vocab tiles 32 w + b.
 // Lanes hold two rows each; eight tiles' statistics are fetched before they are tested.
-__global__ __launch_bounds__(256) void bwd_filter_kernel(BwdArgs a) {
+__device__ __forceinline__ void filter_item(const BwdArgs& a, int item) {
   const int nrb = (int)a.plan.nrb, nw = (int)a.plan.nwords, nvt = (int)a.plan.nvt;
   const int lane = threadIdx.x & 63;
-  const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (item >= nrb * nw) return;  // uniform per wave
   const int rb = item / nw;
   const int w = item - rb * nw;
@@ -109,6 +108,10 @@ __global__ __launch_bounds__(256) void bwd_filter_kernel(BwdArgs a) {
     for (int k = 0; k < 2; ++k)
       if (row[k] < a.N) a.rowbits[(size_t)row[k] * nw + w] = rw[k];
   }
+}
+
+__global__ __launch_bounds__(256) void bwd_filter_kernel(BwdArgs a) {
+  filter_item(a, blockIdx.x * 4 + (threadIdx.x >> 6));
 }
 
 // Keep bitmap of the sorted token blocks: block rb of the sorted order holds rows
@@ -181,7 +184,7 @@ __device__ __forceinline__ int block_excl_scan(int v, int* wsum, int& total) {
 constexpr int kSortMaxRounds = (int)(kPermMaxN / 1024);
 constexpr int kSortHeadRun = 16;
 template <int MAXR>  // rounds the elements of one thread can span: N <= 1024 MAXR
-__global__ __launch_bounds__(1024) void bwd_sort_rows_kernel(BwdArgs a) {
+__device__ void sort_rows(const BwdArgs& a) {
   // the ping-pong buffers sit in LDS for up to 8 rounds (8192 rows), else in the workspace
   constexpr int kLdsRows = MAXR <= 8 ? 8 * 1024 : 1;
   __shared__ int hist[kPermMaxKey];                // first sorted position of each key, then its rows
@@ -354,6 +357,17 @@ __global__ __launch_bounds__(1024) void bwd_sort_rows_kernel(BwdArgs a) {
   }
 }
 
+// The sort and the filter in one launch: workgroup 0 sorts (one CU) while the
+// others run the filter items, 16 per workgroup (one per wave).
+template <int MAXR>
+__global__ __launch_bounds__(1024) void bwd_filter_sort_kernel(BwdArgs a) {
+  if (blockIdx.x == 0) {
+    sort_rows<MAXR>(a);
+    return;
+  }
+  filter_item(a, (blockIdx.x - 1) * 16 + (threadIdx.x >> 6));
+}
+
 // Pointers of the per-row data the G kernel and the sums read -- the sorted copies
 // when the compaction chose the sorted token order -- and the map from the row
 // order they work in to the rows of dE (perm; null for the input order).
@@ -385,14 +399,11 @@ __device__ __forceinline__ void copy_row(const char* __restrict__ src, char* __r
   for (; o < nb; o += 1024) *reinterpret_cast<u32x4*>(dst + o) = *reinterpret_cast<const u32x4*>(src + o);
 }
 
-// Row p of the sorted order gathered from row perm[p], with its target, lse and d_nll.
-template <typename T>
-__global__ __launch_bounds__(256) void bwd_permute_rows_kernel(BwdArgs a) {
-  if (ldu(a.counts, kPermFlag) == 0) return;
-  const int64_t p = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+// Row p of the sorted order gathered from row perm[p], with its target, lse and d_nll
+// (by one wave; rows of nb bytes).
+__device__ __forceinline__ void permute_row(const BwdArgs& a, int64_t p, int64_t nb) {
   if (p >= a.N) return;  // uniform per wave
   const int64_t r = min((int64_t)a.perm[p], a.N - 1);  // a permutation of [0, N); the clamp only guards the reads
-  const int64_t nb = a.D * (int64_t)sizeof(T);          // a multiple of 16
   copy_row(reinterpret_cast<const char*>(a.e) + r * nb, reinterpret_cast<char*>(a.e_perm) + p * nb, nb);
   if ((threadIdx.x & 63) == 0) {
     a.t_perm[p] = a.targets[r];
@@ -450,6 +461,13 @@ __device__ __forceinline__ int order_by_size(int n, F size, int* out, int* hist,
 // dC sums (token blocks, vocab tiles)
 // that hold kept tiles are listed by descending tile count.
 __global__ __launch_bounds__(1024) void bwd_compact_kernel(BwdArgs a, int chunk) {
+  // Workgroups past the first copy the rows into the sorted order (16 rows each, one
+  // per wave) while the first compacts: the copy does not wait for the choice of
+  // order, and is only read if the sorted order is chosen.
+  if (blockIdx.x > 0) {
+    permute_row(a, (int64_t)(blockIdx.x - 1) * 16 + (threadIdx.x >> 6), a.D * (int64_t)(a.plan.g_bytes >> 14));
+    return;
+  }
   __shared__ uint32_t bm[kCompactMaxWords];
   __shared__ int pre[kCompactMaxWords + 1];
   __shared__ int vcnt[kCompactMaxVt];
@@ -1845,17 +1863,18 @@ static hipError_t backward_typed(const BwdArgs& a, hipStream_t s) {
   const bool sorted_ok = a.perm != nullptr;  // the workspace holds the sorted token order
   hipError_t err;
   if (sorted_ok) {
+    const dim3 fg((unsigned)(1 + (items + 15) / 16));
     if (a.N <= 8 * 1024)
-      hipLaunchKernelGGL(bwd_sort_rows_kernel<8>, dim3(1), dim3(1024), 0, s, a);
+      hipLaunchKernelGGL(bwd_filter_sort_kernel<8>, fg, dim3(1024), 0, s, a);
     else if (a.N <= 16 * 1024)
-      hipLaunchKernelGGL(bwd_sort_rows_kernel<16>, dim3(1), dim3(1024), 0, s, a);
+      hipLaunchKernelGGL(bwd_filter_sort_kernel<16>, fg, dim3(1024), 0, s, a);
     else if (a.N <= 32 * 1024)
-      hipLaunchKernelGGL(bwd_sort_rows_kernel<32>, dim3(1), dim3(1024), 0, s, a);
+      hipLaunchKernelGGL(bwd_filter_sort_kernel<32>, fg, dim3(1024), 0, s, a);
     else
-      hipLaunchKernelGGL(bwd_sort_rows_kernel<kSortMaxRounds>, dim3(1), dim3(1024), 0, s, a);
-    if ((err = hipGetLastError()) != hipSuccess) return err;
+      hipLaunchKernelGGL(bwd_filter_sort_kernel<kSortMaxRounds>, fg, dim3(1024), 0, s, a);
+  } else {
+    hipLaunchKernelGGL(bwd_filter_kernel, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, s, a);
   }
-  hipLaunchKernelGGL(bwd_filter_kernel, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, s, a);
   if ((err = hipGetLastError()) != hipSuccess) return err;
   if (sorted_ok) {
     hipLaunchKernelGGL(bwd_filter_sorted_kernel, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, s, a);
@@ -1867,13 +1886,11 @@ static hipError_t backward_typed(const BwdArgs& a, hipStream_t s) {
   for (int chunk = 0; chunk < (int)P.n_chunks; ++chunk) {
     const int vlo = chunk * (int)P.chunk_nvt;
     const int nv = (int)(P.nvt - vlo < P.chunk_nvt ? P.nvt - vlo : P.chunk_nvt);
-    hipLaunchKernelGGL(bwd_compact_kernel, dim3(1), dim3(1024), 0, s, a, chunk);
+    // chunk 0 also copies the rows into the sorted order (extra workgroups)
+    const unsigned cg = 1 + (chunk == 0 && sorted_ok ? (unsigned)((a.N + 15) / 16) : 0u);
+    hipLaunchKernelGGL(bwd_compact_kernel, dim3(cg), dim3(1024), 0, s, a, chunk);
     if ((err = hipGetLastError()) != hipSuccess) return err;
     if (!(want_de || want_dc || want_db)) continue;
-    if (chunk == 0 && sorted_ok) {  // the sorted rows, if the compaction chose them
-      hipLaunchKernelGGL((bwd_permute_rows_kernel<T>), dim3((unsigned)((a.N + 3) / 4)), dim3(256), 0, s, a);
-      if ((err = hipGetLastError()) != hipSuccess) return err;
-    }
     if (a.bias)
       launch_g<T, true>(a, chunk, dim3(gp), s);
     else
