@@ -115,11 +115,16 @@ def main():
         step()
     torch.cuda.synchronize()
     log(f"bench: warmup {args.warmup} done")
-    kept, total = cce.last_tile_stats(dev)
+    fs = cce.last_filter_stats(dev)
+    kept, total, kept_in = fs["kept"], fs["total"], fs["kept_input_order"]
     skip = 1.0 - kept / total
+    skip_in = 1.0 - kept_in / total
 
+    # Timed steps: HIP events bracket the forward pair (the roofline kernels) on the
+    # stream it runs on; the backward is timed in a few extra steps after the timed
+    # region, so that only two event records fall inside it per step.
     torch.cuda.reset_peak_memory_stats(dev)
-    _ext.set_timing(True)
+    _ext.set_timing(True, kinds=("forward",))
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
@@ -127,9 +132,13 @@ def main():
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     tm = _ext.timings_ms()
-    _ext.set_timing(False)
     peak_mem = torch.cuda.max_memory_allocated(dev)
     log(f"bench: {args.steps} steps in {elapsed:.3f} s")
+    _ext.set_timing(True, kinds=("backward",))
+    for i in range(min(args.steps, 5)):
+        step()
+    tm["backward"] = _ext.timings_ms()["backward"]
+    _ext.set_timing(False)
     if args.calib_copy_mib > 0:
         src = torch.empty(args.calib_copy_mib << 20, dtype=torch.uint8, device=dev)
         dst = torch.empty_like(src)
@@ -144,7 +153,11 @@ def main():
     peak = PEAK_TFLOPS[dt]
     fwd_flops = 2.0 * N * D * V
     achieved = fwd_flops / (fwd_ms * 1e-3) / 1e12
-    step_flops = workloads.flops(N, D, V, skip)
+    # Non-filtered FLOPs: the forward plus the backward's three GEMMs over the tiles the
+    # 2^-12 filter keeps with token blocks taken in input order; the backward may
+    # group the rows by target tile and then computes fewer tiles (performed_flops).
+    step_flops = workloads.flops(N, D, V, skip_in)
+    performed_flops = workloads.flops(N, D, V, skip)
     dense_flops = workloads.flops(N, D, V, 0.0)
 
     out = {
@@ -162,14 +175,19 @@ def main():
         "data": "synthetic (seeded torch.Generator on device; random-init classifier rows)",
         "config": {"workload": f"{w['name']}: {w['description']}", "N": N, "D": D, "V": V, "reduction": red,
                    "bias": b is not None, "grads": "dE,dC" + (",dBias" if b is not None else ""),
-                   "filter": "2^-12 (128x128 tiles)" if feps is not None else "off"},
+                   "filter": "2^-12 (128x128 tiles)" if feps is not None else "off",
+                   "backward_token_order": "grouped by target tile when it keeps >=10% fewer tiles"},
         "roofline": {"bound": "mfma", "kernel": "cce forward (fwd_tile_kernel + lse_kernel)",
                      "achieved": achieved, "peak": peak, "unit": "TFLOP/s", "frac": achieved / peak,
                      "traffic": traffic_from_profiles(args.workload, args.filter),
                      "flops_per_launch": fwd_flops, "avg_launch_ms": fwd_ms},
-        "step": {"fwd_ms": fwd_ms, "bwd_ms": bwd_ms, "tile_skip": skip, "kept_tiles": kept, "total_tiles": total,
+        "step": {"fwd_ms": fwd_ms, "bwd_ms": bwd_ms, "tile_skip_input_order": skip_in,
+                 "kept_tiles_input_order": kept_in, "total_tiles": total,
+                 "rows_grouped_by_target": bool(fs["sorted_rows"]), "tile_skip": skip, "kept_tiles": kept,
                  "algorithmic_flops": step_flops, "tflops": step_flops / (ms * 1e-3) / 1e12,
                  "mfma_frac": step_flops / (ms * 1e-3) / 1e12 / peak,
+                 "performed_flops": performed_flops,
+                 "mfma_frac_performed": performed_flops / (ms * 1e-3) / 1e12 / peak,
                  "dense_flops": dense_flops,
                  "peak_mem_gb": peak_mem / 2 ** 30, "logits_bytes_if_materialised": 4.0 * N * V},
         "cpu_baseline": None,

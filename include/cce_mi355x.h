@@ -102,7 +102,10 @@ size_t cce_backward_workspace_size(int dtype, int64_t N, int64_t D, int64_t V,
  * workgroup that owns it and written once.  Every output element is written, so the
  * outputs need no zero-fill.  Rows of dE/dC/dBias that no kept tile touches are 0.
  * The workspace must stay untouched until the backward's work on the stream ends.
- * tile_stats (nullable, device int64[2]) receives {kept tiles, total tiles}.
+ * tile_stats (nullable, device int64[3]) receives {kept tiles, total tiles, kept tiles
+ * of the input-order token blocks}.  The backward may form its 128-row token blocks
+ * from the rows sorted by the vocabulary tile of their target (when that keeps at
+ * least 10% fewer tiles); the first entry counts the blocks it used.
  */
 int cce_backward(int dtype, const void* e, const void* c, const void* bias,
                  const int64_t* targets, int64_t ignore_index, int has_ignore,

@@ -487,23 +487,20 @@ __global__ __launch_bounds__(1024) void bwd_compact_kernel(BwdArgs a, int chunk)
   __shared__ int sorted;
   if (chunk == 0) {
     int flag = 0;
-    if (a.perm && a.perm_mode != 1) {
-      if (a.perm_mode == 2) {
-        flag = 1;
-      } else {
-        int cn = 0, cs = 0;
-        for (int e = tid; e < nrb * nw; e += 1024) {
-          const int w = e % nw;
-          const int inside = nvt - w * 32;
-          const uint32_t m = inside < 32 ? (1u << inside) - 1u : ~0u;
-          cn += __builtin_popcount(a.bits[e] & m);
-          cs += __builtin_popcount(a.bits_p[e] & m);
-        }
-        int tn, ts;
-        block_excl_scan(cn, wsum, tn);
-        block_excl_scan(cs, wsum, ts);
-        flag = (int64_t)ts * 10 <= (int64_t)tn * 9 ? 1 : 0;
+    if (a.perm) {
+      int cn = 0, cs = 0;
+      for (int e = tid; e < nrb * nw; e += 1024) {
+        const int w = e % nw;
+        const int inside = nvt - w * 32;
+        const uint32_t m = inside < 32 ? (1u << inside) - 1u : ~0u;
+        cn += __builtin_popcount(a.bits[e] & m);
+        cs += __builtin_popcount(a.bits_p[e] & m);
       }
+      int tn, ts;
+      block_excl_scan(cn, wsum, tn);
+      block_excl_scan(cs, wsum, ts);
+      flag = a.perm_mode == 1 ? 0 : a.perm_mode == 2 ? 1 : ((int64_t)ts * 10 <= (int64_t)tn * 9 ? 1 : 0);
+      if (tid == 0 && a.tile_stats) a.tile_stats[2] = tn;  // kept pairs of the input-order blocks
     }
     if (tid == 0) {
       sorted = flag;
@@ -611,12 +608,14 @@ __global__ __launch_bounds__(1024) void bwd_compact_kernel(BwdArgs a, int chunk)
     a.counts[0] = kept;
     a.counts[1] = ntask;
     a.counts[2] = 0;  // next owner-without-kept-tiles item (taken by the G kernel's tail)
-    if (a.tile_stats) {
+    if (a.tile_stats) {  // [2]: already set from the whole bitmap when the sorted order was available
       if (chunk == 0) {
         a.tile_stats[0] = kept;
         a.tile_stats[1] = a.plan.total;
+        if (!a.perm) a.tile_stats[2] = kept;
       } else {
         a.tile_stats[0] += kept;
+        if (!a.perm) a.tile_stats[2] += kept;
       }
     }
   }

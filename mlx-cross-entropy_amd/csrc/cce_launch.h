@@ -173,7 +173,7 @@ struct BwdArgs {
   char* gtile;        // [cap][128 tokens][128 vocab] G tiles, token-major, dtype
   float* colsum;      // [cap][128] per-slot column sums of G (dBias)
   float* de_acc;      // [N, D] fp32, only when n_chunks > 1
-  int64_t* tile_stats;  // [2] or null
+  int64_t* tile_stats;  // [3] or null: kept pairs, all pairs, kept pairs of the input-order token blocks
   BwdPlan plan;
   int num_cus;
   // sorted token order (plan.perm_ok; null otherwise).  Row p of the sorted order is

@@ -37,6 +37,7 @@ __all__ = [
     "LinearCrossEntropy",
     "FILTER_LOG_EPS",
     "last_tile_stats",
+    "last_filter_stats",
 ]
 
 _REDUCTIONS = ("none", "sum", "mean")
@@ -45,12 +46,21 @@ _last_stats = {}
 
 def last_tile_stats(device=None):
     """(kept, total) backward tiles of the most recent backward on `device` (synchronises)."""
+    st = last_filter_stats(device)
+    return None if st is None else (st["kept"], st["total"])
+
+
+def last_filter_stats(device=None):
+    """Tile-filter counts of the most recent backward on `device` (synchronises):
+    kept / total 128x128 tiles, and kept_input_order, the tiles the filter keeps with
+    token blocks taken in input order (equal to kept unless the backward grouped the
+    rows by target tile)."""
     dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
     t = _last_stats.get(dev)
     if t is None:
         return None
-    kept, total = t.tolist()
-    return int(kept), int(total)
+    kept, total, kept_in = (int(x) for x in t.tolist())
+    return {"kept": kept, "total": total, "kept_input_order": kept_in, "sorted_rows": kept != kept_in}
 
 
 class _CCEFunction(torch.autograd.Function):
@@ -83,7 +93,7 @@ class _CCEFunction(torch.autograd.Function):
         want_db = bias is not None and ctx.needs_input_grad[2] and grad_bias
         if not (want_de or want_dc or want_db):
             return None, None, None, None, None, None, None, None, None
-        stats = torch.empty((2,), dtype=torch.int64, device=e.device)
+        stats = torch.empty((3,), dtype=torch.int64, device=e.device)
         dE, dC, dB = _ext.backward(e, c, targets, lse, tile_max, d_nll, bias, ignore_index, filter_eps,
                                    want_de, want_dc, want_db, tile_stats=stats)
         _last_stats[e.device] = stats

@@ -54,9 +54,11 @@ _lib = None
 _timing = {"on": False, "forward": [], "backward": []}
 
 
-def set_timing(on):
-    """Enable/disable event timing of the library calls and clear recorded events."""
+def set_timing(on, kinds=("forward", "backward")):
+    """Enable/disable event timing of the library calls (of the given kinds) and clear
+    recorded events."""
     _timing["on"] = bool(on)
+    _timing["kinds"] = tuple(kinds)
     _timing["forward"].clear()
     _timing["backward"].clear()
 
@@ -68,7 +70,7 @@ def timings_ms():
 
 
 def _event_pair(kind):
-    if not _timing["on"]:
+    if not _timing["on"] or kind not in _timing.get("kinds", ("forward", "backward")):
         return None
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     _timing[kind].append((a, b))
@@ -202,7 +204,8 @@ def backward(e, c, targets, lse, tile_max, d_nll, bias=None, ignore_index=-100,
 
     d_nll is the fp32 cotangent of the per-token loss [N].  filter_eps=None or
     -inf disables the 2^-12 tile filter.  tile_stats, if given, is a device
-    int64[2] tensor that receives (kept tiles, total tiles).
+    int64[3] tensor that receives (kept tiles, total tiles, kept tiles of the
+    input-order token blocks).
     """
     code = _prep(e, c, targets, bias)
     e = e.contiguous()

@@ -335,7 +335,7 @@ def test_filtered_backward_matches_filter_emulation(m, cuda, order, monkeypatch)
     tm, _, _, lse, _ = m._ext.forward(e, c, t, None, -100)
     N, V = e.shape[0], c.shape[0]
     d_nll = torch.full((N,), 1.0 / N, device=cuda)
-    stats = torch.zeros(2, dtype=torch.int64, device=cuda)
+    stats = torch.zeros(3, dtype=torch.int64, device=cuda)
     dE, dC, _ = m._ext.backward(e, c, t, lse, tm, d_nll, None, -100, m.FILTER_LOG_EPS, True, True, False,
                                 tile_stats=stats)
     torch.cuda.synchronize()
@@ -346,13 +346,14 @@ def test_filtered_backward_matches_filter_emulation(m, cuda, order, monkeypatch)
     keep = O.keep_mask(tm_np[:, perm], lse_np[perm], tt[perm], dn[perm], eps=np.float32(m.FILTER_LOG_EPS))
     # the kernel's comparison is fp32 (tile_max - lse >= eps): replay it in fp32
     hot = (tm_np - lse_np[None, :]).astype(np.float32) >= np.float32(m.FILTER_LOG_EPS)
-    kept, total = stats.tolist()
+    kept, total, kept_in = stats.tolist()
+    keep_in = O.keep_mask(tm_np, lse_np, tt, dn, eps=np.float32(m.FILTER_LOG_EPS))
     assert total == keep.size
     assert kept == int(keep.sum()), (kept, int(keep.sum()))
+    assert kept_in == int(keep_in.sum()), (kept_in, int(keep_in.sum()))
     assert 0 < kept < total
     if order == "sorted":  # the peaked Zipf case is the one the sorted order is for
-        keep_in = O.keep_mask(tm_np, lse_np, tt, dn, eps=np.float32(m.FILTER_LOG_EPS))
-        assert kept * 10 <= int(keep_in.sum()) * 9, (kept, int(keep_in.sum()))
+        assert kept * 10 <= kept_in * 9, (kept, kept_in)
     print(f"filter ({order} order): kept {kept}/{total} tiles (skip {1 - kept / total:.3f}); "
           f"hot fraction {hot.mean():.4f}")
     ee, cc = f64(e), f64(c)
@@ -378,10 +379,10 @@ def test_filter_disabled_is_dense(m, cuda):
     e, c, t = _peaked(cuda, N=256, V=4096)
     tm, _, _, lse, _ = m._ext.forward(e, c, t, None, -100)
     d_nll = torch.full((256,), 1.0 / 256, device=cuda)
-    stats = torch.zeros(2, dtype=torch.int64, device=cuda)
+    stats = torch.zeros(3, dtype=torch.int64, device=cuda)
     m._ext.backward(e, c, t, lse, tm, d_nll, None, -100, None, True, True, False, tile_stats=stats)
-    kept, total = stats.tolist()
-    assert kept == total == 2 * 32
+    kept, total, kept_in = stats.tolist()
+    assert kept == total == kept_in == 2 * 32
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
@@ -499,23 +500,27 @@ def test_config_c3_full_size_moderate_peak_sampled_grads(m, cuda):
     loss = m.linear_cross_entropy(e2, c2, t)
     loss.backward()
     torch.cuda.synchronize()
-    kept, total = m.last_tile_stats()
+    fs = m.last_filter_stats()
+    kept, total = fs["kept"], fs["total"]
     dE, dC = e2.grad, c2.grad
 
     # kept-tile set, from the kernel's fp32 statistics (float32 comparison, as on the GPU),
-    # over the token blocks of the rows sorted by target tile: with this peaked Zipf input
-    # they keep far fewer tiles than the input-order blocks, so the backward runs on them
+    # over the token blocks the backward used: with this peaked Zipf input the rows
+    # grouped by target tile keep far fewer tiles than the input-order blocks, so the
+    # backward picks them unless a test hook forces the order
     tn = t.cpu().numpy()
     d_nll = np.full(N, np.float32(1.0 / N), dtype=np.float32)
     tm_np, lse_np = tm.cpu().numpy(), lse.cpu().numpy()
     keep_in = O.keep_mask(tm_np, lse_np, tn, d_nll)
-    perm = _sorted_rows(tn, d_nll, V)
+    perm = _sorted_rows(tn, d_nll, V) if fs["sorted_rows"] else np.arange(N)
     keep = O.keep_mask(tm_np[:, perm], lse_np[perm], tn[perm], d_nll[perm])
     blk = np.empty(N, dtype=np.int64)
-    blk[perm] = np.arange(N) // 128  # token block of every row in the sorted order
-    print(f"c3 boost 12: loss {loss.item():.4f} kept {kept}/{total} (cpu predicate: sorted order "
-          f"{int(keep.sum())}, input order {int(keep_in.sum())})")
-    assert int(keep.sum()) == kept and total == keep.size and kept * 10 <= int(keep_in.sum()) * 9
+    blk[perm] = np.arange(N) // 128  # token block of every row in the order used
+    print(f"c3 boost 12: loss {loss.item():.4f} kept {kept}/{total} (cpu predicate: order used "
+          f"{int(keep.sum())}, input order {int(keep_in.sum())}, rows grouped {fs['sorted_rows']})")
+    assert int(keep.sum()) == kept and total == keep.size and fs["kept_input_order"] == int(keep_in.sum())
+    if not os.environ.get("CCE_TEST_TOKEN_ORDER"):
+        assert fs["sorted_rows"] and kept * 10 <= int(keep_in.sum()) * 9
 
     cc = f64(c)
     lse64 = f64(lse)
