@@ -15,20 +15,32 @@
 //
 //   1. bwd_filter_kernel   keep bit per (token block, vocabulary tile) of 128 x 128:
 //                          some row with d_nll != 0 has its target in the tile or
-//                          tile_max - lse >= filter_log_eps.
+//                          tile_max - lse >= filter_log_eps; also each row's own
+//                          keep bits.  When the token order below is available the
+//                          same launch (bwd_filter_sort_kernel) sorts the rows by
+//                          the vocabulary tile of their target in one extra
+//                          workgroup, and bwd_filter_sorted_kernel ORs the row bits
+//                          over the blocks of the sorted order.
 //   per chunk of vocabulary tiles (one chunk unless the problem is large):
-//   2. bwd_compact_kernel  one workgroup turns the chunk's bitmap (held in LDS)
-//                          into slots in (token block, vocab tile) order, the same
-//                          slots grouped by vocab tile, and the G task list.
+//   2. bwd_compact_kernel  one workgroup picks the token order (the first chunk: the
+//                          sorted blocks when they keep >= 10% fewer tiles), turns
+//                          the chunk's bitmap (held in LDS) into slots in (token
+//                          block, vocab tile) order, the same slots grouped by vocab
+//                          tile, the G task list and the sums' owner orders; the
+//                          launch's other workgroups copy E rows (and per-row data)
+//                          into the sorted order meanwhile.
 //   3. empty_owner         owners (row blocks of dE / dC) without kept tiles get
 //                          zeros (and the fp32 dE carry is started / finished);
-//                          done by the G kernel's workgroups once out of tasks.
+//                          done by the G kernel's workgroups once out of tasks,
+//                          after the first of them deals the dC schedule.
 //   4. bwd_g_kernel        per task (one token block, up to 4 of its kept vocab
 //                          tiles): recompute the 512 x 128 logits on MFMA, form G,
 //                          store each 128 x 128 G tile token-major in the input
 //                          dtype, plus fp32 column sums for dBias.
 //   5. bwd_sum_kernel<0>   dE = sum over a token block's kept tiles of G_j . C_j;
-//      bwd_sum_kernel<1>   dC = sum over a vocab tile's kept blocks of G_j^T . E_j.
+//      (or the narrow      written to the dE rows of the block (through the sorted
+//      geometry)           order's permutation when it is used);
+//      bwd_sum_narrow<1>   dC = sum over a vocab tile's kept blocks of G_j^T . E_j.
 //                          Persistent, software-pipelined GEMMs over the gathered
 //                          tile lists: E / C rows stream into LDS by DMA in their
 //                          natural [k][d] layout and are read as MFMA fragments

@@ -77,12 +77,15 @@ class _CCEFunction(torch.autograd.Function):
         ctx.save_for_backward(e, c, bias, targets, lse, tile_max, scale)
         ctx.cce = (ignore_index, reduction, filter_eps, grad_c, grad_bias)
         ctx.mark_non_differentiable(lse)
+        ctx.set_materialize_grads(False)  # no zero-filled cotangent for lse (it has no gradient)
         return loss, lse
 
     @staticmethod
     def backward(ctx, grad_loss, _grad_lse):
         e, c, bias, targets, lse, tile_max, scale = ctx.saved_tensors
         ignore_index, reduction, filter_eps, grad_c, grad_bias = ctx.cce
+        if grad_loss is None:
+            return None, None, None, None, None, None, None, None, None
         N = e.shape[0]
         if reduction == "none":
             d_nll = grad_loss.to(torch.float32).reshape(N)
