@@ -83,6 +83,22 @@ int cce_forward(int dtype, const void* e, const void* c, const void* bias,
                 float* tile_max, float* tile_sum_exp, float* neg_target_logit,
                 float* lse, float* nll, void* hip_stream);
 
+/*
+ * As cce_forward, and also fills zero_bytes bytes at zero_buf with zeros, spread over
+ * the tile kernel's work (that kernel is MFMA-bound and leaves HBM write bandwidth
+ * idle).  For the dC buffer a later cce_backward_ex(..., CCE_BWD_DC_ZEROED) writes:
+ * that backward then writes only the dC rows of vocabulary tiles with kept tiles.
+ * zero_buf must be 16-byte aligned and zero_bytes a multiple of 16 (NULL / 0: none).
+ * Replaces the same reference interfaces as cce_forward; the zero fill stands in for
+ * the zero fill of the outputs the reference's backward accumulates into
+ * (csrc/cce/cce.cpp:315-327 fill_zero_f32; reference/_fused_backward.py:1649 init_value=0.0).
+ */
+int cce_forward_ex(int dtype, const void* e, const void* c, const void* bias,
+                   const int64_t* targets, int64_t ignore_index, int has_ignore,
+                   int64_t N, int64_t D, int64_t V,
+                   float* tile_max, float* tile_sum_exp, float* neg_target_logit,
+                   float* lse, float* nll, void* zero_buf, int64_t zero_bytes, void* hip_stream);
+
 /* Bytes of device workspace cce_backward needs for these sizes and outputs. */
 size_t cce_backward_workspace_size(int dtype, int64_t N, int64_t D, int64_t V,
                                    int want_dE, int want_dC, int want_dBias);
@@ -115,6 +131,19 @@ int cce_backward(int dtype, const void* e, const void* c, const void* bias,
                  void* dE, void* dC, void* dBias,
                  void* workspace, size_t workspace_bytes,
                  int64_t* tile_stats, void* hip_stream);
+
+/* Flags of cce_backward_ex. */
+#define CCE_BWD_DC_ZEROED 1 /* dC already holds zeros (e.g. from cce_forward_ex) */
+
+/* As cce_backward, with flags (CCE_BWD_*).  Same reference interfaces as cce_backward. */
+int cce_backward_ex(int dtype, const void* e, const void* c, const void* bias,
+                    const int64_t* targets, int64_t ignore_index, int has_ignore,
+                    int64_t N, int64_t D, int64_t V,
+                    const float* lse, const float* tile_max, const float* d_nll,
+                    float filter_log_eps,
+                    void* dE, void* dC, void* dBias,
+                    void* workspace, size_t workspace_bytes,
+                    int64_t* tile_stats, int flags, void* hip_stream);
 
 /* Reduction modes of cce_reduce_loss. */
 #define CCE_REDUCE_SUM 1

@@ -107,6 +107,14 @@ int64_t cce_num_vocab_tiles(int64_t V) { return V <= 0 ? 0 : (V + cce::kStatTile
 int cce_forward(int dtype, const void* e, const void* c, const void* bias, const int64_t* targets,
                 int64_t ignore_index, int has_ignore, int64_t N, int64_t D, int64_t V, float* tile_max,
                 float* tile_sum_exp, float* neg_target_logit, float* lse, float* nll, void* hip_stream) {
+  return cce_forward_ex(dtype, e, c, bias, targets, ignore_index, has_ignore, N, D, V, tile_max, tile_sum_exp,
+                        neg_target_logit, lse, nll, nullptr, 0, hip_stream);
+}
+
+int cce_forward_ex(int dtype, const void* e, const void* c, const void* bias, const int64_t* targets,
+                   int64_t ignore_index, int has_ignore, int64_t N, int64_t D, int64_t V, float* tile_max,
+                   float* tile_sum_exp, float* neg_target_logit, float* lse, float* nll, void* zero_buf,
+                   int64_t zero_bytes, void* hip_stream) {
   g_err[0] = 0;
   int rc = check_common("cce_forward", dtype, e, c, targets, N, D, V);
   if (rc != CCE_OK) return rc;
@@ -115,6 +123,9 @@ int cce_forward(int dtype, const void* e, const void* c, const void* bias, const
                 "[cce_forward] tile_max, tile_sum_exp, neg_target_logit, lse and nll must be non-null");
   if (bias && !aligned(bias, elem_size(dtype)))
     return fail(CCE_ERR_INVALID_ARGUMENT, "[cce_forward] bias is not aligned to its element size");
+  if (zero_bytes < 0 || zero_bytes % 16 != 0 || (zero_bytes > 0 && (!zero_buf || !aligned(zero_buf, 16))))
+    return fail(CCE_ERR_INVALID_ARGUMENT,
+                "[cce_forward] zero_buf must be 16-byte aligned and zero_bytes a non-negative multiple of 16");
   const int cus = num_cus_current();
   if (cus <= 0) return fail(CCE_ERR_NO_DEVICE, "[cce_forward] no HIP device is available");
 
@@ -134,6 +145,8 @@ int cce_forward(int dtype, const void* e, const void* c, const void* bias, const
   a.lse = lse;
   a.nll = nll;
   a.num_cus = cus;
+  a.zero_buf = zero_bytes > 0 ? zero_buf : nullptr;
+  a.zero_units = zero_bytes / 16;
   hipError_t err = cce::launch_forward(dtype, a, reinterpret_cast<hipStream_t>(hip_stream));
   if (err != hipSuccess)
     return fail(CCE_ERR_LAUNCH, "[cce_forward] kernel launch failed: %s", hipGetErrorString(err));
@@ -151,7 +164,17 @@ int cce_backward(int dtype, const void* e, const void* c, const void* bias, cons
                  int64_t ignore_index, int has_ignore, int64_t N, int64_t D, int64_t V, const float* lse,
                  const float* tile_max, const float* d_nll, float filter_log_eps, void* dE, void* dC, void* dBias,
                  void* workspace, size_t workspace_bytes, int64_t* tile_stats, void* hip_stream) {
+  return cce_backward_ex(dtype, e, c, bias, targets, ignore_index, has_ignore, N, D, V, lse, tile_max, d_nll,
+                         filter_log_eps, dE, dC, dBias, workspace, workspace_bytes, tile_stats, 0, hip_stream);
+}
+
+int cce_backward_ex(int dtype, const void* e, const void* c, const void* bias, const int64_t* targets,
+                    int64_t ignore_index, int has_ignore, int64_t N, int64_t D, int64_t V, const float* lse,
+                    const float* tile_max, const float* d_nll, float filter_log_eps, void* dE, void* dC,
+                    void* dBias, void* workspace, size_t workspace_bytes, int64_t* tile_stats, int flags,
+                    void* hip_stream) {
   g_err[0] = 0;
+  if (flags & ~CCE_BWD_DC_ZEROED) return fail(CCE_ERR_INVALID_ARGUMENT, "[cce_backward] unknown flags 0x%x", flags);
   int rc = check_common("cce_backward", dtype, e, c, targets, N, D, V);
   if (rc != CCE_OK) return rc;
   if (!lse || !tile_max || !d_nll)
@@ -222,6 +245,7 @@ int cce_backward(int dtype, const void* e, const void* c, const void* bias, cons
   a.perm_mode = 0;
   if (const char* env = std::getenv("CCE_TEST_TOKEN_ORDER")) a.perm_mode = env[0] == 'i' ? 1 : env[0] == 's' ? 2 : 0;
   a.tile_stats = tile_stats;
+  a.dc_zeroed = (flags & CCE_BWD_DC_ZEROED) ? 1 : 0;
   a.plan = P;
   a.num_cus = cus;
 

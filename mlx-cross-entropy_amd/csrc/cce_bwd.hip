@@ -837,11 +837,14 @@ __global__ __launch_bounds__(kGThreads, 1) void bwd_g_kernel(BwdArgs a, int chun
 
   // Once out of tasks, the workgroup takes items from a counter the compaction
   // kernel reset (only when dE or dC is wanted): first the dC schedule (when dC is
-  // wanted), then the owners without kept tiles, whose rows it zeroes.
+  // wanted), then the owners without kept tiles, whose rows it zeroes (dC rows only
+  // when dC did not come zeroed).
   auto tail = [&]() {
     if constexpr (WANT_G) {
       const int sched = a.dC != nullptr ? 1 : 0;
-      const int nitems = sched + (int)a.plan.nrb + (min((int)a.plan.nvt, vlo + (int)a.plan.chunk_nvt) - vlo);
+      // dC rows of vocab tiles without kept tiles need zeros unless dC came zeroed
+      const int nitems = sched + (int)a.plan.nrb +
+                         (a.dc_zeroed ? 0 : min((int)a.plan.nvt, vlo + (int)a.plan.chunk_nvt) - vlo);
       int* box = reinterpret_cast<int*>(smem);
       for (;;) {
         __syncthreads();  // box (and smem) free

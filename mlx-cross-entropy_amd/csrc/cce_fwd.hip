@@ -168,9 +168,27 @@ __global__ __launch_bounds__(FwdLoop<T>::NTHREADS, 1) void fwd_tile_kernel(FwdAr
     }
   };
 
+  // Zero fill riding along (zero_buf, if any): this workgroup's share [z0, z1) of the
+  // 16-byte units, one piece after each tile's epilogue (the next tile's first DMA
+  // stage is then in flight) and the rest after its last tile.
+  const int r_begin = (int)((int64_t)xcd * sc.rounds / 8);
+  const int64_t z0 = (int64_t)blockIdx.x * a.zero_units / gridDim.x;
+  const int64_t z1 = ((int64_t)blockIdx.x + 1) * a.zero_units / gridDim.x;
+  const int64_t zpiece = ((z1 - z0 + max(1, r_end - r_begin) - 1) / max(1, r_end - r_begin) + Loop::NTHREADS - 1) /
+                         Loop::NTHREADS * Loop::NTHREADS;
+  int64_t zc = z0;
+  auto zero_upto = [&](int64_t lim) {
+    u32x4* zb = reinterpret_cast<u32x4*>(a.zero_buf);
+    for (int64_t u = zc + threadIdx.x; u < lim; u += Loop::NTHREADS) zb[u] = u32x4{0u, 0u, 0u, 0u};
+    zc = lim;
+  };
+
   int tb = 0, vb = 0;
-  int r = next_round((int)((int64_t)xcd * sc.rounds / 8), tb, vb);
-  if (r >= r_end) return;
+  int r = next_round(r_begin, tb, vb);
+  if (r >= r_end) {
+    zero_upto(z1);
+    return;
+  }
   auto src = sources(tb, vb);
   Loop::template prefetch<RAGGED>(src, smem);
   int64_t tg[TJ];
@@ -195,6 +213,7 @@ __global__ __launch_bounds__(FwdLoop<T>::NTHREADS, 1) void fwd_tile_kernel(FwdAr
       targets(tbn, tgn);
     }
     fwd_epilogue<T, HAS_BIAS>(a, sc.nvt, acc, tb, vb, tg);
+    zero_upto(min(zc + zpiece, z1));
     if (rn >= r_end) break;
     r = rn;
     tb = tbn;
@@ -202,6 +221,7 @@ __global__ __launch_bounds__(FwdLoop<T>::NTHREADS, 1) void fwd_tile_kernel(FwdAr
 #pragma unroll
     for (int j = 0; j < TJ; ++j) tg[j] = tgn[j];
   }
+  zero_upto(z1);
 }
 
 __device__ __forceinline__ void lse_merge(float& M, float& S, float m, float s) {

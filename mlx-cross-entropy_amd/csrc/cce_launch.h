@@ -33,6 +33,8 @@ struct FwdArgs {
   float* lse;
   float* nll;
   int num_cus;  // compute units of the device (the persistent forward runs one workgroup per CU)
+  void* zero_buf;       // filled with zeros alongside the tiles (null: none)
+  int64_t zero_units;   // 16-byte units of zero_buf
 };
 
 // Backward work plan.  Kept (token block, vocabulary tile) pairs are found by the
@@ -188,6 +190,7 @@ struct BwdArgs {
   float* dnll_perm;     // [N]
   void* e_perm;         // [N, D] dtype
   int perm_mode;        // 0: sorted order when it keeps >= 10% fewer tiles, 1: never, 2: always
+  int dc_zeroed;        // dC already holds zeros: only rows of vocab tiles with kept tiles are written
 };
 
 // dtype: 0 f32, 1 f16, 2 bf16.  Return hipError_t of the launches.

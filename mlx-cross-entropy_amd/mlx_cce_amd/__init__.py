@@ -67,8 +67,12 @@ class _CCEFunction(torch.autograd.Function):
     """Autograd glue: replaces the reference's mx.custom_function + vjp (mlx_cce/__init__.py:21-51)."""
 
     @staticmethod
-    def forward(ctx, e, c, bias, targets, ignore_index, reduction, filter_eps, grad_c, grad_bias):
-        tile_max, _tse, _ntl, lse, nll = _ext.forward(e, c, targets, bias, ignore_index)
+    def forward(ctx, e, c, bias, targets, ignore_index, reduction, filter_eps, grad_c, grad_bias, zero_dc):
+        # dC will be wanted (zero_dc: grad mode on and c requires grad): let the forward's
+        # tile kernel zero it (its HBM writes idle there), so the backward writes only the
+        # rows of vocabulary tiles it keeps.
+        ctx.dc_zeroed = torch.empty_like(c) if (zero_dc and c.is_contiguous()) else None
+        tile_max, _tse, _ntl, lse, nll = _ext.forward(e, c, targets, bias, ignore_index, zero_out=ctx.dc_zeroed)
         if reduction == "none":
             loss = nll
             scale = None
@@ -85,7 +89,7 @@ class _CCEFunction(torch.autograd.Function):
         e, c, bias, targets, lse, tile_max, scale = ctx.saved_tensors
         ignore_index, reduction, filter_eps, grad_c, grad_bias = ctx.cce
         if grad_loss is None:
-            return None, None, None, None, None, None, None, None, None
+            return None, None, None, None, None, None, None, None, None, None
         N = e.shape[0]
         if reduction == "none":
             d_nll = grad_loss.to(torch.float32).reshape(N)
@@ -95,12 +99,13 @@ class _CCEFunction(torch.autograd.Function):
         want_dc = ctx.needs_input_grad[1] and grad_c
         want_db = bias is not None and ctx.needs_input_grad[2] and grad_bias
         if not (want_de or want_dc or want_db):
-            return None, None, None, None, None, None, None, None, None
+            return None, None, None, None, None, None, None, None, None, None
         stats = torch.empty((3,), dtype=torch.int64, device=e.device)
+        dc_zeroed, ctx.dc_zeroed = ctx.dc_zeroed, None  # used once (a second backward zeroes its own)
         dE, dC, dB = _ext.backward(e, c, targets, lse, tile_max, d_nll, bias, ignore_index, filter_eps,
-                                   want_de, want_dc, want_db, tile_stats=stats)
+                                   want_de, want_dc, want_db, tile_stats=stats, dc_zeroed=dc_zeroed)
         _last_stats[e.device] = stats
-        return dE, dC, dB, None, None, None, None, None, None
+        return dE, dC, dB, None, None, None, None, None, None, None
 
 
 def _cce(e, c, targets, bias, reduction, ignore_index, filter_eps, grad_c=True, grad_bias=True):
@@ -108,7 +113,9 @@ def _cce(e, c, targets, bias, reduction, ignore_index, filter_eps, grad_c=True, 
         raise ValueError(f"Unknown reduction: {reduction!r}")
     if bias is not None and bias.dtype != e.dtype:
         bias = bias.to(e.dtype)
-    loss, lse = _CCEFunction.apply(e, c, bias, targets, ignore_index, reduction, filter_eps, grad_c, grad_bias)
+    zero_dc = bool(grad_c and torch.is_grad_enabled() and c.requires_grad)
+    loss, lse = _CCEFunction.apply(e, c, bias, targets, ignore_index, reduction, filter_eps, grad_c, grad_bias,
+                                   zero_dc)
     return loss, lse
 
 

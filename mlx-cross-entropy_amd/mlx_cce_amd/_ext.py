@@ -40,12 +40,17 @@ SIGNATURES = {
     "cce_backward_workspace_size": (ctypes.c_size_t, [_INT, _I64, _I64, _I64, _INT, _INT, _INT]),
     "cce_backward": (_INT, [_INT, _P, _P, _P, _P, _I64, _INT, _I64, _I64, _I64, _P, _P, _P, ctypes.c_float,
                             _P, _P, _P, _P, ctypes.c_size_t, _P, _P]),
+    "cce_forward_ex": (_INT, [_INT, _P, _P, _P, _P, _I64, _INT, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _I64,
+                              _P]),
+    "cce_backward_ex": (_INT, [_INT, _P, _P, _P, _P, _I64, _INT, _I64, _I64, _I64, _P, _P, _P, ctypes.c_float,
+                               _P, _P, _P, _P, ctypes.c_size_t, _P, _INT, _P]),
     "cce_reduce_loss": (_INT, [_P, _P, _I64, _INT, _I64, _INT, _P, _P, _P]),
     "cce_broadcast_grad": (_INT, [_P, _P, _I64, _P, _P]),
 }
 
 CCE_REDUCE_SUM = 1
 CCE_REDUCE_MEAN = 2
+CCE_BWD_DC_ZEROED = 1
 
 _lib = None
 
@@ -153,11 +158,13 @@ def _prep(e, c, targets, bias):
     return DTYPE_CODES[e.dtype]
 
 
-def forward(e, c, targets, bias=None, ignore_index=-100):
+def forward(e, c, targets, bias=None, ignore_index=-100, zero_out=None):
     """Run the fused forward.  Returns (tile_max, tile_sum_exp, neg_target_logit, lse, nll).
 
     tile_max / tile_sum_exp are [ceil(V/128), N] fp32 (vocab-tile major);
     nll is the per-token loss, 0 on rows whose target equals ignore_index.
+    zero_out (optional, a contiguous device tensor of a multiple of 16 bytes) is
+    filled with zeros by the forward's tile kernel (cce_forward_ex).
     """
     code = _prep(e, c, targets, bias)
     e = e.contiguous()
@@ -180,10 +187,19 @@ def forward(e, c, targets, bias=None, ignore_index=-100):
         ev = _event_pair("forward")
         if ev:
             ev[0].record()
-        rc = lib().cce_forward(code, _ptr(e), _ptr(c), _ptr(bias), _ptr(targets),
-                               int(ignore_index) if has_ignore else 0, 1 if has_ignore else 0,
-                               N, D, V, _ptr(tile_max), _ptr(tile_sum_exp), _ptr(neg_tl), _ptr(lse), _ptr(nll),
-                               ctypes.c_void_p(stream))
+        if zero_out is not None:
+            if not zero_out.is_contiguous() or zero_out.device != e.device:
+                raise ValueError("[cce_forward] zero_out must be a contiguous tensor on the device of e")
+            rc = lib().cce_forward_ex(code, _ptr(e), _ptr(c), _ptr(bias), _ptr(targets),
+                                      int(ignore_index) if has_ignore else 0, 1 if has_ignore else 0,
+                                      N, D, V, _ptr(tile_max), _ptr(tile_sum_exp), _ptr(neg_tl), _ptr(lse),
+                                      _ptr(nll), _ptr(zero_out), zero_out.numel() * zero_out.element_size(),
+                                      ctypes.c_void_p(stream))
+        else:
+            rc = lib().cce_forward(code, _ptr(e), _ptr(c), _ptr(bias), _ptr(targets),
+                                   int(ignore_index) if has_ignore else 0, 1 if has_ignore else 0,
+                                   N, D, V, _ptr(tile_max), _ptr(tile_sum_exp), _ptr(neg_tl), _ptr(lse), _ptr(nll),
+                                   ctypes.c_void_p(stream))
         if ev:
             ev[1].record()
     if rc != CCE_OK:
@@ -199,13 +215,16 @@ def workspace_size(e, c, want_de, want_dc, want_db):
 
 
 def backward(e, c, targets, lse, tile_max, d_nll, bias=None, ignore_index=-100,
-             filter_eps=FILTER_LOG_EPS, want_de=True, want_dc=True, want_db=True, tile_stats=None):
+             filter_eps=FILTER_LOG_EPS, want_de=True, want_dc=True, want_db=True, tile_stats=None,
+             dc_zeroed=None):
     """Run the filtered backward.  Returns (dE, dC, dBias), each None when not wanted.
 
     d_nll is the fp32 cotangent of the per-token loss [N].  filter_eps=None or
     -inf disables the 2^-12 tile filter.  tile_stats, if given, is a device
     int64[3] tensor that receives (kept tiles, total tiles, kept tiles of the
-    input-order token blocks).
+    input-order token blocks).  dc_zeroed, if given, is a tensor like c that
+    already holds zeros (from forward(..., zero_out=)): it becomes dC, and only its
+    rows of vocabulary tiles with kept tiles are written (cce_backward_ex).
     """
     code = _prep(e, c, targets, bias)
     e = e.contiguous()
@@ -222,7 +241,13 @@ def backward(e, c, targets, lse, tile_max, d_nll, bias=None, ignore_index=-100,
     if d_nll.shape != (N,) or lse.shape != (N,):
         raise ValueError("[cce_backward] lse and d_nll must be [N]")
     dE = torch.empty_like(e) if want_de else None
-    dC = torch.empty_like(c) if want_dc else None
+    if dc_zeroed is not None and want_dc:
+        if dc_zeroed.shape != c.shape or dc_zeroed.dtype != c.dtype or not dc_zeroed.is_contiguous():
+            raise ValueError("[cce_backward] dc_zeroed must be a contiguous tensor like c")
+        dC = dc_zeroed
+    else:
+        dc_zeroed = None
+        dC = torch.empty_like(c) if want_dc else None
     dB = torch.empty_like(bias) if want_db else None
     ws_bytes = workspace_size(e, c, want_de, want_dc, want_db)
     ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=e.device)
@@ -233,11 +258,12 @@ def backward(e, c, targets, lse, tile_max, d_nll, bias=None, ignore_index=-100,
         ev = _event_pair("backward")
         if ev:
             ev[0].record()
-        rc = lib().cce_backward(code, _ptr(e), _ptr(c), _ptr(bias), _ptr(targets),
-                                int(ignore_index) if has_ignore else 0, 1 if has_ignore else 0,
-                                N, D, V, _ptr(lse), _ptr(tile_max), _ptr(d_nll), ctypes.c_float(eps),
-                                _ptr(dE), _ptr(dC), _ptr(dB), _ptr(ws), ctypes.c_size_t(ws_bytes),
-                                _ptr(tile_stats), ctypes.c_void_p(stream))
+        rc = lib().cce_backward_ex(code, _ptr(e), _ptr(c), _ptr(bias), _ptr(targets),
+                                   int(ignore_index) if has_ignore else 0, 1 if has_ignore else 0,
+                                   N, D, V, _ptr(lse), _ptr(tile_max), _ptr(d_nll), ctypes.c_float(eps),
+                                   _ptr(dE), _ptr(dC), _ptr(dB), _ptr(ws), ctypes.c_size_t(ws_bytes),
+                                   _ptr(tile_stats), CCE_BWD_DC_ZEROED if dc_zeroed is not None else 0,
+                                   ctypes.c_void_p(stream))
         if ev:
             ev[1].record()
     if rc != CCE_OK:

@@ -385,6 +385,40 @@ def test_filter_disabled_is_dense(m, cuda):
     assert kept == total == kept_in == 2 * 32
 
 
+@pytest.mark.parametrize("chunked", [False, True])
+def test_forward_zero_fill_and_backward_into_zeroed_dc(m, cuda, chunked, monkeypatch):
+    """cce_forward_ex fills its buffer with zeros (every byte, whatever it held) and leaves
+    the forward's outputs unchanged; cce_backward_ex with CCE_BWD_DC_ZEROED writes only the
+    kept vocabulary tiles' dC rows into it, and the result equals the ordinary backward's
+    dC bit for bit (filtered, so that most rows are left untouched)."""
+    if chunked:
+        monkeypatch.setenv("CCE_TEST_CHUNK_VT", "32")
+    e, c, t = _peaked(cuda, N=384, D=256, V=9000, seed=13)
+    plain = m._ext.forward(e, c, t, None, -100)
+    buf = torch.full_like(c, float("nan"))
+    outs = m._ext.forward(e, c, t, None, -100, zero_out=buf)
+    torch.cuda.synchronize()
+    assert int((buf.view(torch.int16) != 0).sum()) == 0
+    for x, y in zip(outs, plain):
+        assert torch.equal(x, y)
+    tm, _, _, lse, _ = plain
+    d_nll = torch.full((384,), 1.0 / 384, device=cuda)
+    _, dC_ref, _ = m._ext.backward(e, c, t, lse, tm, d_nll, None, -100, m.FILTER_LOG_EPS, True, True, False)
+    stats = torch.zeros(3, dtype=torch.int64, device=cuda)
+    _, dC, _ = m._ext.backward(e, c, t, lse, tm, d_nll, None, -100, m.FILTER_LOG_EPS, True, True, False,
+                               tile_stats=stats, dc_zeroed=buf)
+    torch.cuda.synchronize()
+    assert dC.data_ptr() == buf.data_ptr()
+    kept, total, _ = stats.tolist()
+    assert 0 < kept < total
+    assert torch.equal(dC.view(torch.int16), dC_ref.view(torch.int16))
+    # the autograd path uses it: same gradients as through the ordinary backward
+    e2 = e.detach().clone().requires_grad_(True)
+    c2 = c.detach().clone().requires_grad_(True)
+    m.linear_cross_entropy(e2, c2, t).backward()
+    assert torch.equal(c2.grad.view(torch.int16), dC_ref.view(torch.int16))
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("filtered", [False, True])
 @pytest.mark.parametrize("de_sums", ["narrow", "wide"])
