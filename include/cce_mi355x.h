@@ -145,6 +145,49 @@ int cce_backward_ex(int dtype, const void* e, const void* c, const void* bias,
                     void* workspace, size_t workspace_bytes,
                     int64_t* tile_stats, int flags, void* hip_stream);
 
+/*
+ * Quantized classifier rows.  The reference's callers pass an lm_head / tied
+ * embedding stored with MLX's affine group quantization through mx.dequantize
+ * before the loss (README.md:84-95,136; examples/mlx_lm_lora_test.py:16-21),
+ * materialising the [V, D] rows.  These entry points take the quantized rows
+ * instead and dequantize chunk_rows of them at a time into a caller-provided
+ * scratch (0 selects 32768 rows; otherwise a multiple of 4096).
+ *   weight   [V, D * bits / 32] uint32: code j of a word in bits [j * bits, (j + 1) * bits)
+ *   scales, qbiases  [V, D / group_size] dtype;  w = scale * q + bias
+ *   bits 2, 4 or 8; group_size 32, 64 or 128; D % group_size == 0
+ * Dequantized values: fp32 product scale * q, fp32 add of the bias, rounded to
+ * dtype to nearest-even; the quantized passes equal the plain passes over
+ * cce_dequantize's output bit for bit.  The rows carry no gradient (no dC).
+ */
+/* rows x D dequantized into out [rows, D] dtype (16-byte aligned); mx.dequantize's
+ * affine mode, which the reference's callers run before the loss. */
+int cce_dequantize(int dtype, const uint32_t* weight, const void* scales, const void* qbiases, int group_size,
+                   int bits, int64_t rows, int64_t D, void* out, void* hip_stream);
+
+/* Bytes of scratch cce_forward_q needs: min(chunk_rows, V) rows of D dtype elements. */
+size_t cce_forward_q_scratch_size(int dtype, int64_t V, int64_t D, int64_t chunk_rows);
+
+/* As cce_forward with quantized classifier rows (reference: the same interfaces
+ * as cce_forward, fed by mx.dequantize's output). */
+int cce_forward_q(int dtype, const void* e, const uint32_t* weight, const void* scales, const void* qbiases,
+                  int group_size, int bits, const void* bias, const int64_t* targets, int64_t ignore_index,
+                  int has_ignore, int64_t N, int64_t D, int64_t V, float* tile_max, float* tile_sum_exp,
+                  float* neg_target_logit, float* lse, float* nll, void* scratch, size_t scratch_bytes,
+                  int64_t chunk_rows, void* hip_stream);
+
+/* Workspace bytes of cce_backward_q (includes one chunk of dequantized rows). */
+size_t cce_backward_q_workspace_size(int dtype, int64_t N, int64_t D, int64_t V, int want_dE, int want_dBias,
+                                     int64_t chunk_rows);
+
+/* As cce_backward with quantized classifier rows: dE and dBias only (reference:
+ * the same interfaces as cce_backward; the frozen-head mode compute_all_grads=False
+ * of csrc/bindings.cpp:15-56 returns no dC either). */
+int cce_backward_q(int dtype, const void* e, const uint32_t* weight, const void* scales, const void* qbiases,
+                   int group_size, int bits, const void* bias, const int64_t* targets, int64_t ignore_index,
+                   int has_ignore, int64_t N, int64_t D, int64_t V, const float* lse, const float* tile_max,
+                   const float* d_nll, float filter_log_eps, void* dE, void* dBias, void* workspace,
+                   size_t workspace_bytes, int64_t chunk_rows, int64_t* tile_stats, void* hip_stream);
+
 /* Reduction modes of cce_reduce_loss. */
 #define CCE_REDUCE_SUM 1
 #define CCE_REDUCE_MEAN 2

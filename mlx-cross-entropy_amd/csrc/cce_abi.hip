@@ -86,6 +86,34 @@ int check_common(const char* fn, int dtype, const void* e, const void* c, const 
   return CCE_OK;
 }
 
+// Checks of quantized classifier rows (the layout of MLX's affine quantization).
+int check_quant(const char* fn, int dtype, const uint32_t* wq, const void* scales, const void* qbiases,
+                int group_size, int bits, int64_t D) {
+  if (!wq || !scales || !qbiases)
+    return fail(CCE_ERR_INVALID_ARGUMENT, "[%s] weight, scales and biases must be non-null", fn);
+  if (bits != 2 && bits != 4 && bits != 8)
+    return fail(CCE_ERR_INVALID_ARGUMENT, "[%s] bits must be 2, 4 or 8, got %d", fn, bits);
+  if (group_size != 32 && group_size != 64 && group_size != 128)
+    return fail(CCE_ERR_INVALID_ARGUMENT, "[%s] group_size must be 32, 64 or 128, got %d", fn, group_size);
+  if (D % group_size != 0)
+    return fail(CCE_ERR_INVALID_ARGUMENT, "[%s] D must be a multiple of group_size (%d), got D=%lld", fn, group_size,
+                (long long)D);
+  if (!aligned(wq, 4) || !aligned(scales, elem_size(dtype)) || !aligned(qbiases, elem_size(dtype)))
+    return fail(CCE_ERR_INVALID_ARGUMENT, "[%s] weight, scales or biases not aligned to their element size", fn);
+  return CCE_OK;
+}
+
+int64_t quant_chunk_rows(int64_t chunk_rows) {
+  return chunk_rows == 0 ? cce::kQuantDefaultChunkRows : chunk_rows;
+}
+
+int check_chunk_rows(const char* fn, int64_t chunk_rows) {
+  if (chunk_rows < 0 || chunk_rows % cce::kQuantChunkAlign != 0 || chunk_rows > ((int64_t)1 << 30))
+    return fail(CCE_ERR_INVALID_ARGUMENT, "[%s] chunk_rows must be a positive multiple of %lld (or 0), got %lld", fn,
+                (long long)cce::kQuantChunkAlign, (long long)chunk_rows);
+  return CCE_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -168,15 +196,18 @@ int cce_backward(int dtype, const void* e, const void* c, const void* bias, cons
                          filter_log_eps, dE, dC, dBias, workspace, workspace_bytes, tile_stats, 0, hip_stream);
 }
 
-int cce_backward_ex(int dtype, const void* e, const void* c, const void* bias, const int64_t* targets,
-                    int64_t ignore_index, int has_ignore, int64_t N, int64_t D, int64_t V, const float* lse,
-                    const float* tile_max, const float* d_nll, float filter_log_eps, void* dE, void* dC,
-                    void* dBias, void* workspace, size_t workspace_bytes, int64_t* tile_stats, int flags,
-                    void* hip_stream) {
-  g_err[0] = 0;
-  if (flags & ~CCE_BWD_DC_ZEROED) return fail(CCE_ERR_INVALID_ARGUMENT, "[cce_backward] unknown flags 0x%x", flags);
-  int rc = check_common("cce_backward", dtype, e, c, targets, N, D, V);
-  if (rc != CCE_OK) return rc;
+}  // extern "C"
+
+namespace {
+
+// The backward over plain (q == null) or quantized classifier rows.  Quantized rows
+// reserve the scratch of one chunk in the workspace, and the chunks are capped at
+// q->chunk_rows rows.
+int backward_impl(int dtype, const void* e, const void* c, const void* bias, const int64_t* targets,
+                  int64_t ignore_index, int has_ignore, int64_t N, int64_t D, int64_t V, const float* lse,
+                  const float* tile_max, const float* d_nll, float filter_log_eps, void* dE, void* dC, void* dBias,
+                  void* workspace, size_t workspace_bytes, int64_t* tile_stats, int flags, const cce::QuantRows* q,
+                  void* hip_stream) {
   if (!lse || !tile_max || !d_nll)
     return fail(CCE_ERR_INVALID_ARGUMENT, "[cce_backward] lse, tile_max and d_nll must be non-null");
   if (dBias && !bias)
@@ -187,7 +218,8 @@ int cce_backward_ex(int dtype, const void* e, const void* c, const void* bias, c
     return fail(CCE_ERR_INVALID_ARGUMENT, "[cce_backward] gradient outputs must be 16-byte aligned");
   if (std::isnan(filter_log_eps))
     return fail(CCE_ERR_INVALID_ARGUMENT, "[cce_backward] filter_log_eps must not be NaN");
-  const cce::BwdPlan P = cce::make_bwd_plan(elem_size(dtype), N, D, V, dE != nullptr, dC != nullptr, dBias != nullptr);
+  const cce::BwdPlan P = cce::make_bwd_plan(elem_size(dtype), N, D, V, dE != nullptr, dC != nullptr, dBias != nullptr,
+                                            q ? q->chunk_rows / cce::kBwdVocab : 0, q != nullptr);
   if (!workspace || workspace_bytes < P.total_bytes)
     return fail(CCE_ERR_WORKSPACE, "[cce_backward] workspace of %zu bytes required, %zu given", P.total_bytes,
                 workspace ? workspace_bytes : (size_t)0);
@@ -248,11 +280,129 @@ int cce_backward_ex(int dtype, const void* e, const void* c, const void* bias, c
   a.dc_zeroed = (flags & CCE_BWD_DC_ZEROED) ? 1 : 0;
   a.plan = P;
   a.num_cus = cus;
+  if (q) {
+    a.q = *q;
+    a.q.scratch = ws + P.qrows;
+  }
 
   const hipError_t err = cce::launch_backward(dtype, a, s);
   if (err != hipSuccess)
     return fail(CCE_ERR_LAUNCH, "[cce_backward] kernel launch failed: %s", hipGetErrorString(err));
   return CCE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int cce_backward_ex(int dtype, const void* e, const void* c, const void* bias, const int64_t* targets,
+                    int64_t ignore_index, int has_ignore, int64_t N, int64_t D, int64_t V, const float* lse,
+                    const float* tile_max, const float* d_nll, float filter_log_eps, void* dE, void* dC,
+                    void* dBias, void* workspace, size_t workspace_bytes, int64_t* tile_stats, int flags,
+                    void* hip_stream) {
+  g_err[0] = 0;
+  if (flags & ~CCE_BWD_DC_ZEROED) return fail(CCE_ERR_INVALID_ARGUMENT, "[cce_backward] unknown flags 0x%x", flags);
+  const int rc = check_common("cce_backward", dtype, e, c, targets, N, D, V);
+  if (rc != CCE_OK) return rc;
+  return backward_impl(dtype, e, c, bias, targets, ignore_index, has_ignore, N, D, V, lse, tile_max, d_nll,
+                       filter_log_eps, dE, dC, dBias, workspace, workspace_bytes, tile_stats, flags, nullptr,
+                       hip_stream);
+}
+
+int cce_dequantize(int dtype, const uint32_t* weight, const void* scales, const void* qbiases, int group_size,
+                   int bits, int64_t rows, int64_t D, void* out, void* hip_stream) {
+  g_err[0] = 0;
+  if (dtype != CCE_DTYPE_F32 && dtype != CCE_DTYPE_F16 && dtype != CCE_DTYPE_BF16)
+    return fail(CCE_ERR_UNSUPPORTED_DTYPE, "[cce_dequantize] unsupported dtype code %d", dtype);
+  if (rows <= 0 || D <= 0 || rows >= ((int64_t)1 << 31))
+    return fail(CCE_ERR_INVALID_ARGUMENT, "[cce_dequantize] rows and D must be positive (rows below 2^31), got %lld, %lld",
+                (long long)rows, (long long)D);
+  int rc = check_quant("cce_dequantize", dtype, weight, scales, qbiases, group_size, bits, D);
+  if (rc != CCE_OK) return rc;
+  if (!out || !aligned(out, 16)) return fail(CCE_ERR_INVALID_ARGUMENT, "[cce_dequantize] out must be 16-byte aligned");
+  if (num_cus_current() <= 0) return fail(CCE_ERR_NO_DEVICE, "[cce_dequantize] no HIP device is available");
+  cce::QuantRows q{weight, scales, qbiases, group_size, bits, nullptr, 0};
+  const hipError_t err = cce::launch_dequantize(dtype, q, 0, rows, D, out, reinterpret_cast<hipStream_t>(hip_stream));
+  if (err != hipSuccess)
+    return fail(CCE_ERR_LAUNCH, "[cce_dequantize] kernel launch failed: %s", hipGetErrorString(err));
+  return CCE_OK;
+}
+
+size_t cce_forward_q_scratch_size(int dtype, int64_t V, int64_t D, int64_t chunk_rows) {
+  if (V <= 0 || D <= 0 || chunk_rows < 0 || chunk_rows % cce::kQuantChunkAlign != 0) return 0;
+  if (dtype != CCE_DTYPE_F32 && dtype != CCE_DTYPE_F16 && dtype != CCE_DTYPE_BF16) return 0;
+  const int64_t rows = quant_chunk_rows(chunk_rows) < V ? quant_chunk_rows(chunk_rows) : V;
+  return (size_t)rows * (size_t)D * elem_size(dtype);
+}
+
+int cce_forward_q(int dtype, const void* e, const uint32_t* weight, const void* scales, const void* qbiases,
+                  int group_size, int bits, const void* bias, const int64_t* targets, int64_t ignore_index,
+                  int has_ignore, int64_t N, int64_t D, int64_t V, float* tile_max, float* tile_sum_exp,
+                  float* neg_target_logit, float* lse, float* nll, void* scratch, size_t scratch_bytes,
+                  int64_t chunk_rows, void* hip_stream) {
+  g_err[0] = 0;
+  // c is not read on this path: check the shapes with e standing in for it
+  int rc = check_common("cce_forward_q", dtype, e, e, targets, N, D, V);
+  if (rc != CCE_OK) return rc;
+  if ((rc = check_quant("cce_forward_q", dtype, weight, scales, qbiases, group_size, bits, D)) != CCE_OK) return rc;
+  if ((rc = check_chunk_rows("cce_forward_q", chunk_rows)) != CCE_OK) return rc;
+  if (!tile_max || !tile_sum_exp || !neg_target_logit || !lse || !nll)
+    return fail(CCE_ERR_INVALID_ARGUMENT,
+                "[cce_forward_q] tile_max, tile_sum_exp, neg_target_logit, lse and nll must be non-null");
+  if (bias && !aligned(bias, elem_size(dtype)))
+    return fail(CCE_ERR_INVALID_ARGUMENT, "[cce_forward_q] bias is not aligned to its element size");
+  const size_t need = cce_forward_q_scratch_size(dtype, V, D, chunk_rows);
+  if (!scratch || scratch_bytes < need || !aligned(scratch, 256))
+    return fail(CCE_ERR_WORKSPACE, "[cce_forward_q] scratch of %zu bytes (256-byte aligned) required, %zu given", need,
+                scratch ? scratch_bytes : (size_t)0);
+  const int cus = num_cus_current();
+  if (cus <= 0) return fail(CCE_ERR_NO_DEVICE, "[cce_forward_q] no HIP device is available");
+
+  cce::FwdArgs a{};
+  a.e = e;
+  a.c = nullptr;
+  a.bias = bias;
+  a.targets = targets;
+  a.ignore_index = ignore_index;
+  a.has_ignore = has_ignore ? 1 : 0;
+  a.N = N;
+  a.D = D;
+  a.V = V;
+  a.tile_max = tile_max;
+  a.tile_sum_exp = tile_sum_exp;
+  a.neg_target_logit = neg_target_logit;
+  a.lse = lse;
+  a.nll = nll;
+  a.num_cus = cus;
+  cce::QuantRows q{weight, scales, qbiases, group_size, bits, scratch, quant_chunk_rows(chunk_rows)};
+  const hipError_t err = cce::launch_forward_q(dtype, a, q, reinterpret_cast<hipStream_t>(hip_stream));
+  if (err != hipSuccess)
+    return fail(CCE_ERR_LAUNCH, "[cce_forward_q] kernel launch failed: %s", hipGetErrorString(err));
+  return CCE_OK;
+}
+
+size_t cce_backward_q_workspace_size(int dtype, int64_t N, int64_t D, int64_t V, int want_dE, int want_dBias,
+                                     int64_t chunk_rows) {
+  if (N <= 0 || D <= 0 || V <= 0 || chunk_rows < 0 || chunk_rows % cce::kQuantChunkAlign != 0) return 0;
+  if (dtype != CCE_DTYPE_F32 && dtype != CCE_DTYPE_F16 && dtype != CCE_DTYPE_BF16) return 0;
+  return cce::make_bwd_plan(elem_size(dtype), N, D, V, want_dE != 0, false, want_dBias != 0,
+                            quant_chunk_rows(chunk_rows) / cce::kBwdVocab, true)
+      .total_bytes;
+}
+
+int cce_backward_q(int dtype, const void* e, const uint32_t* weight, const void* scales, const void* qbiases,
+                   int group_size, int bits, const void* bias, const int64_t* targets, int64_t ignore_index,
+                   int has_ignore, int64_t N, int64_t D, int64_t V, const float* lse, const float* tile_max,
+                   const float* d_nll, float filter_log_eps, void* dE, void* dBias, void* workspace,
+                   size_t workspace_bytes, int64_t chunk_rows, int64_t* tile_stats, void* hip_stream) {
+  g_err[0] = 0;
+  int rc = check_common("cce_backward_q", dtype, e, e, targets, N, D, V);
+  if (rc != CCE_OK) return rc;
+  if ((rc = check_quant("cce_backward_q", dtype, weight, scales, qbiases, group_size, bits, D)) != CCE_OK) return rc;
+  if ((rc = check_chunk_rows("cce_backward_q", chunk_rows)) != CCE_OK) return rc;
+  cce::QuantRows q{weight, scales, qbiases, group_size, bits, nullptr, quant_chunk_rows(chunk_rows)};
+  return backward_impl(dtype, e, nullptr, bias, targets, ignore_index, has_ignore, N, D, V, lse, tile_max, d_nll,
+                       filter_log_eps, dE, nullptr, dBias, workspace, workspace_bytes, tile_stats, 0, &q, hip_stream);
 }
 
 int cce_reduce_loss(const float* nll, const int64_t* targets, int64_t ignore_index, int has_ignore, int64_t N,

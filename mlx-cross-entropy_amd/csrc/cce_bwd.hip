@@ -48,6 +48,7 @@
 //                          way), output rows written once in the output dtype.
 //   6. bwd_dbias_kernel    dBias = sum of the column sums of a vocab tile's slots.
 #include <cstdlib>
+#include <type_traits>
 
 #include "cce_device.h"
 #include "cce_launch.h"
@@ -1897,24 +1898,35 @@ static hipError_t backward_typed(const BwdArgs& a, hipStream_t s) {
   const bool want_de = a.dE != nullptr, want_dc = a.dC != nullptr, want_db = a.dBias != nullptr;
   const int cus = a.num_cus > 0 ? a.num_cus : 256;
   const int gp = (cus + 7) / 8 * 8;  // persistent grids: a multiple of the 8 XCDs
+  const int dtype = sizeof(T) == 4 ? 0 : (std::is_same<T, _Float16>::value ? 1 : 2);
   for (int chunk = 0; chunk < (int)P.n_chunks; ++chunk) {
     const int vlo = chunk * (int)P.chunk_nvt;
     const int nv = (int)(P.nvt - vlo < P.chunk_nvt ? P.nvt - vlo : P.chunk_nvt);
+    // Quantized classifier rows: dequantize this chunk's rows into the scratch and
+    // let c address it at global row numbers (only the G kernel and the dE sums read c).
+    BwdArgs ac = a;
+    if (a.q.wq != nullptr && (want_de || want_db)) {
+      const int64_t r0 = (int64_t)vlo * kBwdVocab;
+      const int64_t r1 = (int64_t)(vlo + nv) * kBwdVocab < a.V ? (int64_t)(vlo + nv) * kBwdVocab : a.V;
+      err = launch_dequantize(dtype, a.q, r0, r1 - r0, a.D, a.q.scratch, s);
+      if (err != hipSuccess) return err;
+      ac.c = reinterpret_cast<const char*>(a.q.scratch) - r0 * a.D * (int64_t)sizeof(T);
+    }
     // chunk 0 also copies the rows into the sorted order (extra workgroups)
     const unsigned cg = 1 + (chunk == 0 && sorted_ok ? (unsigned)((a.N + 15) / 16) : 0u);
     hipLaunchKernelGGL(bwd_compact_kernel, dim3(cg), dim3(1024), 0, s, a, chunk);
     if ((err = hipGetLastError()) != hipSuccess) return err;
     if (!(want_de || want_dc || want_db)) continue;
     if (a.bias)
-      launch_g<T, true>(a, chunk, dim3(gp), s);
+      launch_g<T, true>(ac, chunk, dim3(gp), s);
     else
-      launch_g<T, false>(a, chunk, dim3(gp), s);
+      launch_g<T, false>(ac, chunk, dim3(gp), s);
     if ((err = hipGetLastError()) != hipSuccess) return err;
     if (want_de) {
       if (use_wide_de_sums(P, a.D, gp))
-        hipLaunchKernelGGL((bwd_sum_kernel<T, 0>), dim3(gp), dim3(SumGeo<T>::NT), 0, s, a, chunk);
+        hipLaunchKernelGGL((bwd_sum_kernel<T, 0>), dim3(gp), dim3(SumGeo<T>::NT), 0, s, ac, chunk);
       else
-        hipLaunchKernelGGL((bwd_sum_narrow_kernel<T, 0>), dim3(gp), dim3(SumGeoNarrow<T>::NT), 0, s, a, chunk);
+        hipLaunchKernelGGL((bwd_sum_narrow_kernel<T, 0>), dim3(gp), dim3(SumGeoNarrow<T>::NT), 0, s, ac, chunk);
       if ((err = hipGetLastError()) != hipSuccess) return err;
     }
     if (want_dc) {

@@ -41,10 +41,11 @@ using FwdLoop = NTMainLoop<T, kFwdVocab, kFwdTokens, 2, kFwdWB>;  // A = C rows 
 // at the same time; the XCDs sweep the vocabulary in step, so they share C blocks
 // in the infinity cache.
 struct FwdSched {
-  int ntb, nvb;     // token / vocabulary blocks
+  int ntb, nvb;     // token / vocabulary blocks (the launch covers blocks vb0 .. vb0 + nvb - 1)
   int gt, gv, ngv;  // round shape, vocabulary groups
   int rounds;       // R
-  int nvt;          // statistic tiles
+  int nvt;          // statistic tiles of the whole vocabulary
+  int vb0;          // first vocabulary block (a chunk of dequantized rows; 0 otherwise)
 };
 
 // Epilogue of one tile, registers only: bias, ragged-vocabulary mask, per token
@@ -149,6 +150,7 @@ __global__ __launch_bounds__(FwdLoop<T>::NTHREADS, 1) void fwd_tile_kernel(FwdAr
       vb = (r % sc.ngv) * sc.gv + sv;
       if (tb < sc.ntb && vb < sc.nvb) break;
     }
+    vb += sc.vb0;
     return r;
   };
   const int64_t pitch = a.D * (int64_t)sizeof(T);
@@ -281,11 +283,14 @@ __global__ __launch_bounds__(64 * kLseSplits) void lse_kernel(FwdArgs a, int nvt
   }
 }
 
+// The tile kernel over vocabulary blocks [vb0, vb0 + nvb): a.c must address the
+// rows of those blocks at their global row numbers.
 template <typename T>
-static hipError_t forward_typed(const FwdArgs& a, hipStream_t s) {
+static hipError_t launch_tiles(const FwdArgs& a, int vb0, int nvb, hipStream_t s) {
   FwdSched sc{};
   sc.ntb = (int)((a.N + kFwdTokens - 1) / kFwdTokens);
-  sc.nvb = (int)((a.V + kFwdVocab - 1) / kFwdVocab);
+  sc.nvb = nvb;
+  sc.vb0 = vb0;
   sc.nvt = (int)((a.V + kStatTile - 1) / kStatTile);
   // members per XCD; a round is gt token blocks x gv vocabulary blocks
   const int cpx = a.num_cus / 8 > 0 ? a.num_cus / 8 : 1;
@@ -309,10 +314,40 @@ static hipError_t forward_typed(const FwdArgs& a, hipStream_t s) {
     else
       hipLaunchKernelGGL((fwd_tile_kernel<T, false, false>), grid, block, 0, s, a, sc);
   }
-  hipError_t err = hipGetLastError();
-  if (err != hipSuccess) return err;
-  hipLaunchKernelGGL(lse_kernel, dim3((unsigned)((a.N + 63) / 64)), dim3(64 * kLseSplits), 0, s, a, sc.nvt);
   return hipGetLastError();
+}
+
+template <typename T>
+static hipError_t launch_lse(const FwdArgs& a, hipStream_t s) {
+  const int nvt = (int)((a.V + kStatTile - 1) / kStatTile);
+  hipLaunchKernelGGL(lse_kernel, dim3((unsigned)((a.N + 63) / 64)), dim3(64 * kLseSplits), 0, s, a, nvt);
+  return hipGetLastError();
+}
+
+template <typename T>
+static hipError_t forward_typed(const FwdArgs& a, hipStream_t s) {
+  hipError_t err = launch_tiles<T>(a, 0, (int)((a.V + kFwdVocab - 1) / kFwdVocab), s);
+  if (err != hipSuccess) return err;
+  return launch_lse<T>(a, s);
+}
+
+// Quantized classifier rows: per chunk of q.chunk_rows rows (whole vocabulary
+// blocks), dequantize into q.scratch, then run the tile kernel on the chunk's blocks
+// with c addressing the scratch at global row numbers; one lse merge at the end.
+template <typename T>
+static hipError_t forward_q_typed(int dtype, const FwdArgs& a, const QuantRows& q, hipStream_t s) {
+  static_assert(kQuantChunkAlign % kFwdVocab == 0, "chunks hold whole vocabulary blocks");
+  const int64_t row_bytes = a.D * (int64_t)sizeof(T);
+  for (int64_t v0 = 0; v0 < a.V; v0 += q.chunk_rows) {
+    const int64_t rows = a.V - v0 < q.chunk_rows ? a.V - v0 : q.chunk_rows;
+    hipError_t err = launch_dequantize(dtype, q, v0, rows, a.D, q.scratch, s);
+    if (err != hipSuccess) return err;
+    FwdArgs ac = a;
+    ac.c = reinterpret_cast<const char*>(q.scratch) - v0 * row_bytes;
+    err = launch_tiles<T>(ac, (int)(v0 / kFwdVocab), (int)((rows + kFwdVocab - 1) / kFwdVocab), s);
+    if (err != hipSuccess) return err;
+  }
+  return launch_lse<T>(a, s);
 }
 
 // Reduced loss of cce_loss (mlx_cce/__init__.py:72-76): one workgroup sums nll in a
@@ -380,6 +415,17 @@ hipError_t launch_forward(int dtype, const FwdArgs& a, hipStream_t s) {
       return forward_typed<_Float16>(a, s);
     default:
       return forward_typed<__bf16>(a, s);
+  }
+}
+
+hipError_t launch_forward_q(int dtype, const FwdArgs& a, const QuantRows& q, hipStream_t s) {
+  switch (dtype) {
+    case 0:
+      return forward_q_typed<float>(dtype, a, q, s);
+    case 1:
+      return forward_q_typed<_Float16>(dtype, a, q, s);
+    default:
+      return forward_q_typed<__bf16>(dtype, a, q, s);
   }
 }
 

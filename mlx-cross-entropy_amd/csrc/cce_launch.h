@@ -37,6 +37,25 @@ struct FwdArgs {
   int64_t zero_units;   // 16-byte units of zero_buf
 };
 
+// Classifier rows stored with affine group quantization (the layout of MLX's
+// mx.quantize / mx.dequantize, mlx >= 0.22, which the reference's callers apply
+// before the loss: README.md:90-95, examples/mlx_lm_lora_test.py:16-21): row r of
+// the [rows, D] weight is D * bits / 32 uint32 words, element j of a word in bits
+// [j * bits, (j + 1) * bits); scales and biases are [rows, D / group_size] in the
+// compute dtype; w = scale * q + bias.  The passes dequantize chunk_rows rows at a
+// time into `scratch` ([chunk_rows, D], compute dtype) and run on that chunk.
+struct QuantRows {
+  const uint32_t* wq;  // null: the classifier rows are plain
+  const void* scales;
+  const void* biases;
+  int group_size;      // 32, 64 or 128
+  int bits;            // 2, 4 or 8
+  void* scratch;
+  int64_t chunk_rows;  // a multiple of kQuantChunkAlign
+};
+constexpr int64_t kQuantChunkAlign = 4096;         // rows: whole 32-tile chunks of the backward
+constexpr int64_t kQuantDefaultChunkRows = 32768;  // 256 MiB of bf16 scratch at D = 4096
+
 // Backward work plan.  Kept (token block, vocabulary tile) pairs are found by the
 // filter as a bitmap, one bit per pair, rows by token block.  The vocabulary is
 // cut into chunks of `chunk_nvt` tiles (one chunk unless the problem is large);
@@ -69,13 +88,16 @@ struct BwdPlan {
   size_t bits, counts, rb_start, slot_vt, slot_rb, vt_start, vt_slot, g_task, g_task_rb, own_rb, own_vt, dc_bin_start,
       dc_bin_owner, gtile, colsum, de_acc;
   size_t perm, sort_buf, rowbits, bits_p, t_perm, lse_perm, dnll_perm, e_perm;  // sorted order (perm_ok)
+  size_t qrows;  // dequantized classifier rows of one chunk (quantized classifier only)
   size_t total_bytes;
 };
 
 inline size_t plan_align(size_t x) { return (x + 255) & ~size_t(255); }
 
+// max_chunk_nvt > 0 caps the chunk width (a multiple of 32 tiles); quant reserves the
+// scratch of one chunk's dequantized classifier rows.
 inline BwdPlan make_bwd_plan(size_t esize, int64_t N, int64_t D, int64_t V, bool want_de, bool want_dc,
-                             bool want_db) {
+                             bool want_db, int64_t max_chunk_nvt = 0, bool quant = false) {
   BwdPlan P{};
   P.nvt = (V + kBwdVocab - 1) / kBwdVocab;
   P.nrb = (N + kBwdTokens - 1) / kBwdTokens;
@@ -93,6 +115,7 @@ inline BwdPlan make_bwd_plan(size_t esize, int64_t N, int64_t D, int64_t V, bool
   const int64_t by_lds = 32 * (kCompactMaxWords / P.nrb);
   cw = cw < by_lds ? cw : by_lds;
   cw = cw < kCompactMaxVt ? cw : kCompactMaxVt;
+  if (max_chunk_nvt > 0 && max_chunk_nvt < cw) cw = max_chunk_nvt;
   // Test hook: CCE_TEST_CHUNK_VT narrows the chunks (rounded down to a multiple of 32)
   // so that the multi-chunk path runs at small sizes.
   if (const char* env = std::getenv("CCE_TEST_CHUNK_VT")) {
@@ -139,6 +162,7 @@ inline BwdPlan make_bwd_plan(size_t esize, int64_t N, int64_t D, int64_t V, bool
     P.dnll_perm = take((size_t)N * 4);
     P.e_perm = take((size_t)N * (size_t)D * esize);
   }
+  P.qrows = quant ? take((size_t)P.chunk_nvt * kBwdVocab * (size_t)D * esize) : 0;
   P.total_bytes = off;
   return P;
 }
@@ -191,10 +215,16 @@ struct BwdArgs {
   void* e_perm;         // [N, D] dtype
   int perm_mode;        // 0: sorted order when it keeps >= 10% fewer tiles, 1: never, 2: always
   int dc_zeroed;        // dC already holds zeros: only rows of vocab tiles with kept tiles are written
+  QuantRows q;          // q.wq set: c is unused; every chunk first dequantizes its rows into q.scratch
 };
 
 // dtype: 0 f32, 1 f16, 2 bf16.  Return hipError_t of the launches.
 hipError_t launch_forward(int dtype, const FwdArgs& a, hipStream_t s);
+// As launch_forward with the classifier rows in q (a.c unused).
+hipError_t launch_forward_q(int dtype, const FwdArgs& a, const QuantRows& q, hipStream_t s);
+// Rows [row0, row0 + rows) of q dequantized into out ([rows, D], dtype).
+hipError_t launch_dequantize(int dtype, const QuantRows& q, int64_t row0, int64_t rows, int64_t D, void* out,
+                             hipStream_t s);
 hipError_t launch_backward(int dtype, const BwdArgs& a, hipStream_t s);
 hipError_t launch_reduce_loss(const float* nll, const int64_t* targets, int64_t ignore_index, int has_ignore,
                               int64_t N, int mode, float* loss, float* scale, hipStream_t s);

@@ -19,6 +19,10 @@ API mirrors (reference file:line):
     cce_forward_raw        csrc/bindings.cpp:58-69
     cce_backward_raw       csrc/bindings.cpp:71-86
     LinearCrossEntropy     reference/__init__.py:88-118
+
+Quantized classifier rows (the reference's callers run mx.dequantize first,
+README.md:84-95): pass a ``QuantizedWeight`` as ``c``; the library dequantizes a
+bounded chunk of rows at a time (see ``quant.py``).
 """
 
 __version__ = "0.1.0"
@@ -27,6 +31,7 @@ import torch
 
 from . import _ext
 from ._ext import FILTER_LOG_EPS, cce_backward_raw, cce_forward_raw
+from .quant import QuantizedWeight, dequantize, quantize
 
 __all__ = [
     "linear_cross_entropy",
@@ -38,6 +43,9 @@ __all__ = [
     "FILTER_LOG_EPS",
     "last_tile_stats",
     "last_filter_stats",
+    "QuantizedWeight",
+    "quantize",
+    "dequantize",
 ]
 
 _REDUCTIONS = ("none", "sum", "mean")
@@ -68,11 +76,17 @@ class _CCEFunction(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, e, c, bias, targets, ignore_index, reduction, filter_eps, grad_c, grad_bias, zero_dc):
+        # Quantized classifier rows (a QuantizedWeight, not a tensor): no gradient for them.
+        ctx.qw = c if isinstance(c, QuantizedWeight) else None
         # dC will be wanted (zero_dc: grad mode on and c requires grad): let the forward's
         # tile kernel zero it (its HBM writes idle there), so the backward writes only the
         # rows of vocabulary tiles it keeps.
-        ctx.dc_zeroed = torch.empty_like(c) if (zero_dc and c.is_contiguous()) else None
-        tile_max, _tse, _ntl, lse, nll = _ext.forward(e, c, targets, bias, ignore_index, zero_out=ctx.dc_zeroed)
+        ctx.dc_zeroed = torch.empty_like(c) if (zero_dc and ctx.qw is None and c.is_contiguous()) else None
+        if ctx.qw is not None:
+            tile_max, _tse, _ntl, lse, nll = _ext.forward_q(e, c, targets, bias, ignore_index)
+            c = None
+        else:
+            tile_max, _tse, _ntl, lse, nll = _ext.forward(e, c, targets, bias, ignore_index, zero_out=ctx.dc_zeroed)
         if reduction == "none":
             loss = nll
             scale = None
@@ -101,6 +115,11 @@ class _CCEFunction(torch.autograd.Function):
         if not (want_de or want_dc or want_db):
             return None, None, None, None, None, None, None, None, None, None
         stats = torch.empty((3,), dtype=torch.int64, device=e.device)
+        if ctx.qw is not None:
+            dE, dB = _ext.backward_q(e, ctx.qw, targets, lse, tile_max, d_nll, bias, ignore_index, filter_eps,
+                                     want_de, want_db, tile_stats=stats)
+            _last_stats[e.device] = stats
+            return dE, None, dB, None, None, None, None, None, None, None
         dc_zeroed, ctx.dc_zeroed = ctx.dc_zeroed, None  # used once (a second backward zeroes its own)
         dE, dC, dB = _ext.backward(e, c, targets, lse, tile_max, d_nll, bias, ignore_index, filter_eps,
                                    want_de, want_dc, want_db, tile_stats=stats, dc_zeroed=dc_zeroed)
@@ -113,7 +132,7 @@ def _cce(e, c, targets, bias, reduction, ignore_index, filter_eps, grad_c=True, 
         raise ValueError(f"Unknown reduction: {reduction!r}")
     if bias is not None and bias.dtype != e.dtype:
         bias = bias.to(e.dtype)
-    zero_dc = bool(grad_c and torch.is_grad_enabled() and c.requires_grad)
+    zero_dc = bool(grad_c and torch.is_grad_enabled() and isinstance(c, torch.Tensor) and c.requires_grad)
     loss, lse = _CCEFunction.apply(e, c, bias, targets, ignore_index, reduction, filter_eps, grad_c, grad_bias,
                                    zero_dc)
     return loss, lse

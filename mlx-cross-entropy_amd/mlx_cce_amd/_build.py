@@ -19,7 +19,7 @@ CSRC = os.path.join(PROJECT_DIR, "csrc")
 INCLUDE = os.path.join(REPO_DIR, "include")
 LIB_NAME = "libcce_mi355x.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
-SOURCES = ["cce_fwd.hip", "cce_bwd.hip", "cce_abi.hip"]
+SOURCES = ["cce_fwd.hip", "cce_bwd.hip", "cce_quant.hip", "cce_abi.hip"]
 ARCH = os.environ.get("CCE_OFFLOAD_ARCH", "gfx950")
 
 COMMON_FLAGS = [

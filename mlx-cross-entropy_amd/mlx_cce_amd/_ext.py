@@ -44,6 +44,13 @@ SIGNATURES = {
                               _P]),
     "cce_backward_ex": (_INT, [_INT, _P, _P, _P, _P, _I64, _INT, _I64, _I64, _I64, _P, _P, _P, ctypes.c_float,
                                _P, _P, _P, _P, ctypes.c_size_t, _P, _INT, _P]),
+    "cce_dequantize": (_INT, [_INT, _P, _P, _P, _INT, _INT, _I64, _I64, _P, _P]),
+    "cce_forward_q_scratch_size": (ctypes.c_size_t, [_INT, _I64, _I64, _I64]),
+    "cce_forward_q": (_INT, [_INT, _P, _P, _P, _P, _INT, _INT, _P, _P, _I64, _INT, _I64, _I64, _I64, _P, _P, _P, _P,
+                             _P, _P, ctypes.c_size_t, _I64, _P]),
+    "cce_backward_q_workspace_size": (ctypes.c_size_t, [_INT, _I64, _I64, _I64, _INT, _INT, _I64]),
+    "cce_backward_q": (_INT, [_INT, _P, _P, _P, _P, _INT, _INT, _P, _P, _I64, _INT, _I64, _I64, _I64, _P, _P, _P,
+                              ctypes.c_float, _P, _P, _P, ctypes.c_size_t, _I64, _P, _P]),
     "cce_reduce_loss": (_INT, [_P, _P, _I64, _INT, _I64, _INT, _P, _P, _P]),
     "cce_broadcast_grad": (_INT, [_P, _P, _I64, _P, _P]),
 }
@@ -269,6 +276,136 @@ def backward(e, c, targets, lse, tile_max, d_nll, bias=None, ignore_index=-100,
     if rc != CCE_OK:
         _raise(rc, "cce_backward")
     return dE, dC, dB
+
+
+# --------------------------------------------------------------------------
+# Quantized classifier rows (MLX affine group quantization; see quant.py).
+
+def _quant_parts(qw, D=None):
+    w, sc, bi = qw.weight, qw.scales, qw.biases
+    if w.dtype not in (torch.int32, torch.uint32):
+        raise TypeError(f"[cce] quantized weight must be int32/uint32 words, got {w.dtype}")
+    if sc.dtype not in DTYPE_CODES or bi.dtype != sc.dtype:
+        raise TypeError("[cce] scales and biases must share one float dtype")
+    if w.dim() != 2 or sc.dim() != 2 or bi.shape != sc.shape or sc.shape[0] != w.shape[0]:
+        raise ValueError("[cce] weight [V, D*bits/32], scales and biases [V, D/group_size] expected")
+    Dq = w.shape[1] * 32 // qw.bits
+    if D is not None and Dq != D:
+        raise ValueError(f"[cut_cross_entropy] quantized rows hold D={Dq}, e has D={D}")
+    if sc.shape[1] * qw.group_size != Dq:
+        raise ValueError("[cce] scales.shape[1] * group_size must equal D")
+    return w.contiguous(), sc.contiguous(), bi.contiguous(), Dq
+
+
+def dequantize(qw):
+    """Dense [V, D] rows (dtype of the scales) of a QuantizedWeight (cce_dequantize)."""
+    w, sc, bi, D = _quant_parts(qw)
+    _check_device("weight", w, None)
+    _check_device("scales", sc, w.device)
+    _check_device("biases", bi, w.device)
+    V = w.shape[0]
+    out = torch.empty((V, D), dtype=sc.dtype, device=w.device)
+    with torch.cuda.device(w.device):
+        stream = torch.cuda.current_stream(w.device).cuda_stream
+        rc = lib().cce_dequantize(DTYPE_CODES[sc.dtype], _ptr(w), _ptr(sc), _ptr(bi), qw.group_size, qw.bits, V, D,
+                                  _ptr(out), ctypes.c_void_p(stream))
+    if rc != CCE_OK:
+        _raise(rc, "cce_dequantize")
+    return out
+
+
+def _prep_q(e, qw, targets, bias):
+    if e.dim() != 2:
+        raise ValueError(f"[cut_cross_entropy] e must be 2D [B, D], got {e.dim()}D")
+    if targets.dim() != 1 or targets.shape[0] != e.shape[0]:
+        raise ValueError("[cut_cross_entropy] targets must be 1D [B] with B = e.shape[0]")
+    w, sc, bi, _ = _quant_parts(qw, e.shape[1])
+    V = w.shape[0]
+    if bias is not None and (bias.dim() != 1 or bias.shape[0] != V):
+        raise ValueError("[cut_cross_entropy] bias must be 1D [V]")
+    if e.dtype not in DTYPE_CODES:
+        raise RuntimeError(f"CCE: unsupported dtype {e.dtype}")
+    if sc.dtype != e.dtype or (bias is not None and bias.dtype != e.dtype):
+        raise TypeError(f"[cut_cross_entropy] e, the scales and bias must share one dtype, got {e.dtype}, {sc.dtype}")
+    dev = e.device
+    _check_device("e", e, None)
+    for name, t in (("weight", w), ("scales", sc), ("biases", bi), ("targets", targets)):
+        _check_device(name, t, dev)
+    if bias is not None:
+        _check_device("bias", bias, dev)
+    return DTYPE_CODES[e.dtype], w, sc, bi, V
+
+
+def forward_q(e, qw, targets, bias=None, ignore_index=-100, chunk_rows=0):
+    """forward() with quantized classifier rows (cce_forward_q): returns the same five tensors."""
+    code, w, sc, bi, V = _prep_q(e, qw, targets, bias)
+    e = e.contiguous()
+    targets = targets.to(torch.int64).contiguous()
+    if bias is not None:
+        bias = bias.contiguous()
+    N, D = e.shape
+    nvt = (V + STAT_TILE - 1) // STAT_TILE
+    f32 = dict(dtype=torch.float32, device=e.device)
+    tile_max = torch.empty((nvt, N), **f32)
+    tile_sum_exp = torch.empty((nvt, N), **f32)
+    neg_tl = torch.empty((N,), **f32)
+    lse = torch.empty((N,), **f32)
+    nll = torch.empty((N,), **f32)
+    sbytes = int(lib().cce_forward_q_scratch_size(code, V, D, int(chunk_rows)))
+    scratch = torch.empty((max(sbytes, 1),), dtype=torch.uint8, device=e.device)
+    has_ignore = ignore_index is not None
+    with torch.cuda.device(e.device):
+        stream = torch.cuda.current_stream(e.device).cuda_stream
+        ev = _event_pair("forward")
+        if ev:
+            ev[0].record()
+        rc = lib().cce_forward_q(code, _ptr(e), _ptr(w), _ptr(sc), _ptr(bi), qw.group_size, qw.bits, _ptr(bias),
+                                 _ptr(targets), int(ignore_index) if has_ignore else 0, 1 if has_ignore else 0,
+                                 N, D, V, _ptr(tile_max), _ptr(tile_sum_exp), _ptr(neg_tl), _ptr(lse), _ptr(nll),
+                                 _ptr(scratch), ctypes.c_size_t(sbytes), int(chunk_rows), ctypes.c_void_p(stream))
+        if ev:
+            ev[1].record()
+    if rc != CCE_OK:
+        _raise(rc, "cce_forward_q")
+    return tile_max, tile_sum_exp, neg_tl, lse, nll
+
+
+def backward_q(e, qw, targets, lse, tile_max, d_nll, bias=None, ignore_index=-100, filter_eps=FILTER_LOG_EPS,
+               want_de=True, want_db=True, tile_stats=None, chunk_rows=0):
+    """backward() with quantized classifier rows (cce_backward_q): returns (dE, dBias); the rows get no gradient."""
+    code, w, sc, bi, V = _prep_q(e, qw, targets, bias)
+    e = e.contiguous()
+    targets = targets.to(torch.int64).contiguous()
+    if bias is not None:
+        bias = bias.contiguous()
+    want_db = bool(want_db and bias is not None)
+    N, D = e.shape
+    lse = lse.contiguous()
+    tile_max = tile_max.contiguous()
+    d_nll = d_nll.to(torch.float32).contiguous()
+    if d_nll.shape != (N,) or lse.shape != (N,):
+        raise ValueError("[cce_backward] lse and d_nll must be [N]")
+    dE = torch.empty_like(e) if want_de else None
+    dB = torch.empty_like(bias) if want_db else None
+    ws_bytes = int(lib().cce_backward_q_workspace_size(code, N, D, V, int(want_de), int(want_db), int(chunk_rows)))
+    ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=e.device)
+    eps = -math.inf if filter_eps is None else float(filter_eps)
+    has_ignore = ignore_index is not None
+    with torch.cuda.device(e.device):
+        stream = torch.cuda.current_stream(e.device).cuda_stream
+        ev = _event_pair("backward")
+        if ev:
+            ev[0].record()
+        rc = lib().cce_backward_q(code, _ptr(e), _ptr(w), _ptr(sc), _ptr(bi), qw.group_size, qw.bits, _ptr(bias),
+                                  _ptr(targets), int(ignore_index) if has_ignore else 0, 1 if has_ignore else 0,
+                                  N, D, V, _ptr(lse), _ptr(tile_max), _ptr(d_nll), ctypes.c_float(eps),
+                                  _ptr(dE), _ptr(dB), _ptr(ws), ctypes.c_size_t(ws_bytes), int(chunk_rows),
+                                  _ptr(tile_stats), ctypes.c_void_p(stream))
+        if ev:
+            ev[1].record()
+    if rc != CCE_OK:
+        _raise(rc, "cce_backward_q")
+    return dE, dB
 
 
 # --------------------------------------------------------------------------

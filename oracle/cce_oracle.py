@@ -24,6 +24,15 @@ below every tolerance it checks:
   (mlx_cce/__init__.py:61).
 * ``grads_filtered``: the gradients restricted to kept tiles (what a filtered
   backward computes).
+* ``dequantize``: affine group dequantization of quantized classifier rows, the
+  layout of MLX's mx.quantize / mx.dequantize (mlx >= 0.22, absent here), which the
+  reference's callers apply before the loss (README.md:84-95,136;
+  examples/mlx_lm_lora_test.py:16-21): code j of a uint32 word in bits
+  [j bits, (j + 1) bits), w = scale q + bias.  The product and the add are float32
+  (the library's rounding).  Pinned by a pure-Python bit-by-bit brute force, by
+  cases exact in any rounding order (power-of-two scales, small integer biases),
+  and by a planted code-order mistake; MLX's own rounding of scale q + bias is
+  parity unpinned (MLX cannot run here).
 
 How each function is pinned (tests/test_oracle.py): pure-Python brute force on
 tiny inputs, an independent float64 torch autograd of materialised logits,
@@ -230,3 +239,19 @@ def rel_fro(got, ref):
     if den == 0.0:
         return 0.0 if num == 0.0 else float("inf")
     return float(num / den)
+
+
+def dequantize(words, scales, biases, group_size, bits):
+    """float32 [V, D] rows from quantized words [V, D bits / 32] (uint32 bit patterns,
+    any integer dtype) and scales / biases [V, D / group_size]: code j of a word in
+    bits [j bits, (j + 1) bits), w = float32(float32(scale) q) + float32(bias)."""
+    w = np.asarray(words).astype(np.int64) & 0xFFFFFFFF
+    V, W = w.shape
+    epw = 32 // bits
+    shifts = np.arange(epw, dtype=np.int64) * bits
+    q = ((w[:, :, None] >> shifts) & ((1 << bits) - 1)).reshape(V, W * epw)
+    D = W * epw
+    s = np.repeat(np.asarray(scales, dtype=np.float32), group_size, axis=1)[:, :D]
+    b = np.repeat(np.asarray(biases, dtype=np.float32), group_size, axis=1)[:, :D]
+    return (s * q.astype(np.float32)).astype(np.float32) + b
+
