@@ -1,6 +1,6 @@
 """Benchmark: Cut Cross-Entropy fwd+bwd on one MI355X.
 
-python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c3] [--filter on|off]
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c3] [--filter on|off] [--quantize BITS]
 
 A step is one forward + backward (dE and dC, dBias when the workload has a bias)
 of linear_cross_entropy over one batch of synthetic input already resident in
@@ -12,6 +12,10 @@ forward kernel pair (tile kernel + lse combine, timed with HIP events on the
 stream they run on) against the bf16 MFMA peak; `cpu_baseline` is the float32
 torch-CPU restatement of the reference's materialised-logits path timed on a
 bounded slice of the same workload on this host.
+
+--quantize BITS (2, 4 or 8; not the default) stores the classifier rows in affine
+groups of 64 and passes them to the loss quantized (the frozen-head case: dE and dBias,
+no dC); the library dequantizes a bounded chunk of rows at a time.
 """
 
 import argparse
@@ -67,6 +71,8 @@ def main():
     ap.add_argument("--workload", default="c3", choices=["c1", "c2", "c3", "c4", "c5"])
     ap.add_argument("--filter", default="on", choices=["on", "off"])
     ap.add_argument("--cpu-baseline", default="on", choices=["on", "off"])
+    ap.add_argument("--quantize", type=int, default=0, choices=[0, 2, 4, 8],
+                    help="classifier rows in BITS-bit affine groups of 64 (frozen head: no dC)")
     ap.add_argument("--cpu-rows", type=int, default=1024)
     ap.add_argument("--cpu-budget", type=float, default=12.0)
     ap.add_argument("--calib-copy-mib", type=int, default=0,
@@ -94,7 +100,8 @@ def main():
     N, D, V = w["N"], w["D"], w["V"]
     dt = {torch.bfloat16: "bf16", torch.float16: "f16", torch.float32: "f32"}[w["dtype"]]
     e = w["e"].reshape(N, D).detach().requires_grad_(True)
-    c = w["c"].detach().requires_grad_(True)
+    qw = cce.quantize(w["c"].detach(), group_size=64, bits=args.quantize) if args.quantize else None
+    c = qw if qw is not None else w["c"].detach().requires_grad_(True)
     b = w["bias"].detach().requires_grad_(True) if w["bias"] is not None else None
     t = w["targets"].reshape(N)
     red = w["reduction"]
@@ -103,7 +110,8 @@ def main():
 
     def step():
         e.grad = None
-        c.grad = None
+        if qw is None:
+            c.grad = None
         if b is not None:
             b.grad = None
         loss = cce.linear_cross_entropy(e, c, t, b, reduction=red, ignore_index=w["ignore_index"], filter_eps=feps)
@@ -156,9 +164,10 @@ def main():
     # Non-filtered FLOPs: the forward plus the backward's three GEMMs over the tiles the
     # 2^-12 filter keeps with token blocks taken in input order; the backward may
     # group the rows by target tile and then computes fewer tiles (performed_flops).
-    step_flops = workloads.flops(N, D, V, skip_in)
-    performed_flops = workloads.flops(N, D, V, skip)
-    dense_flops = workloads.flops(N, D, V, 0.0)
+    want_dc = qw is None
+    step_flops = workloads.flops(N, D, V, skip_in, want_dc)
+    performed_flops = workloads.flops(N, D, V, skip, want_dc)
+    dense_flops = workloads.flops(N, D, V, 0.0, want_dc)
 
     out = {
         "metric": METRIC,
@@ -174,12 +183,17 @@ def main():
         "dtype": dt,
         "data": "synthetic (seeded torch.Generator on device; random-init classifier rows)",
         "config": {"workload": f"{w['name']}: {w['description']}", "N": N, "D": D, "V": V, "reduction": red,
-                   "bias": b is not None, "grads": "dE,dC" + (",dBias" if b is not None else ""),
+                   "bias": b is not None,
+                   "grads": ("dE,dC" if qw is None else "dE") + (",dBias" if b is not None else ""),
+                   "classifier_rows": (f"{args.quantize}-bit affine groups of 64, dequantized in chunks of 32768 rows"
+                                       if qw is not None else "dense"),
                    "filter": "2^-12 (128x128 tiles)" if feps is not None else "off",
                    "backward_token_order": "grouped by target tile when it keeps >=10% fewer tiles"},
-        "roofline": {"bound": "mfma", "kernel": "cce forward (fwd_tile_kernel + lse_kernel)",
+        "roofline": {"bound": "mfma",
+                     "kernel": ("cce forward (fwd_tile_kernel + lse_kernel)" if qw is None else
+                                "cce forward (dequant_kernel per chunk + fwd_tile_kernel + lse_kernel)"),
                      "achieved": achieved, "peak": peak, "unit": "TFLOP/s", "frac": achieved / peak,
-                     "traffic": traffic_from_profiles(args.workload, args.filter),
+                     "traffic": traffic_from_profiles(args.workload, args.filter) if qw is None else None,
                      "flops_per_launch": fwd_flops, "avg_launch_ms": fwd_ms},
         "step": {"fwd_ms": fwd_ms, "bwd_ms": bwd_ms, "tile_skip_input_order": skip_in,
                  "kept_tiles_input_order": kept_in, "total_tiles": total,

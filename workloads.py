@@ -94,9 +94,10 @@ def make(name, device="cpu", scale=1.0, dtype=None, target_boost=40.0):
                 reduction=cfg["reduction"], ignore_index=IGNORE, dtype=dt, description=NAMES[name])
 
 
-def flops(N, D, V, skip=0.0):
-    """Algorithmic MFMA work of one fwd+bwd: 2NDV forward + 6NDV(1 - skip) backward."""
-    return 2.0 * N * D * V + 6.0 * N * D * V * (1.0 - skip)
+def flops(N, D, V, skip=0.0, want_dc=True):
+    """Algorithmic MFMA work of one fwd+bwd: 2NDV forward + 6NDV(1 - skip) backward
+    (recompute, dE and dC; 4NDV(1 - skip) without dC)."""
+    return 2.0 * N * D * V + (6.0 if want_dc else 4.0) * N * D * V * (1.0 - skip)
 
 
 def min_bytes(N, D, V, esize=2, bias=False):
