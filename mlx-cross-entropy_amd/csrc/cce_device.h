@@ -280,7 +280,11 @@ struct NTMainLoop {
   }
 
   // LDS-DMA loads of slice kt (clamped to the last slice: harmless reloads into
-  // idle stages) into stage kt % STAGES.
+  // idle stages) into stage kt % STAGES.  Issued as inline assembly in the saddr
+  // form (a scalar base plus the lane's 32-bit offset): the compiler then does not
+  // count these loads, so it keeps exact lgkmcnt waits for the fragment reads (with
+  // compiler-visible LDS-DMA in flight it waits for all of them), and the stage
+  // barriers order the DMA against the reads of its stage.
   template <bool RAGGED, int NSEG>
   static __device__ __forceinline__ void issue(const Src<NSEG>& src, int kt, char* smem) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -293,18 +297,16 @@ struct NTMainLoop {
 #pragma unroll
     for (int j = 0; j < LPW; ++j) {
       const int sg = j * NW * RPL < ROWS_A ? (j * NW * RPL) / (ROWS_A / NSEG) : NSEG;
-      // The per-lane offset passes through an empty asm so its zero extension stays
-      // next to the load: the address is then a scalar base plus a 32-bit VGPR (the
-      // saddr form), not a 64-bit VGPR pair kept live per load across the loop.
-      uint32_t o = src.off[j];
-      asm("" : "+v"(o));
-      const char* g = (src.segb[sg] + k0) + o;
+      const uint32_t lds = __builtin_amdgcn_readfirstlane(lds_addr(st + lds_w + j * NW * RPL * SLICE));
       if constexpr (RAGGED) {
+        const char* g = (src.segb[sg] + k0) + src.off[j];
         if (k0 + (int64_t)src.qb[j] >= src.kbytes) g = reinterpret_cast<const char*>(g_zero16);
+        asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory");
+      } else {
+        asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(src.off[j]),
+                     "s"(src.segb[sg] + k0), "s"(lds)
+                     : "memory");
       }
-      __builtin_amdgcn_global_load_lds(
-          reinterpret_cast<const void*>(g),
-          (__attribute__((address_space(3))) void*)(st + lds_w + j * NW * RPL * SLICE), 16, 0, 0);
     }
   }
 
