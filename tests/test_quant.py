@@ -311,3 +311,46 @@ def test_quantized_rows_get_no_gradient(cuda):
     ee = e.detach().clone().requires_grad_(True)
     m.linear_cross_entropy(ee, qw, t).backward()
     assert ee.grad is not None and not qw.weight.requires_grad and qw.scales.grad is None
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype,D,gs,bits", [(torch.bfloat16, 96, 32, 4), (torch.float16, 160, 32, 8),
+                                               (torch.float32, 64, 32, 2)])
+def test_quantized_ragged_shapes_multi_chunk(cuda, dtype, D, gs, bits, monkeypatch):
+    """Rows that are not a whole number of 128-byte slices (the zero-padded slice path),
+    N not a multiple of the 128-row block, several chunks, ignore_index=None:
+    the quantized passes equal the plain passes over the dequantized rows (forward to
+    1e-5 across chunks, backward bit for bit with the same chunks)."""
+    import mlx_cce_amd as m
+    monkeypatch.setenv("CCE_TEST_CHUNK_VT", "32")
+    qw = _gpu_quant(cuda, 8500, D, gs, bits, dtype, seed=D + bits)
+    g = torch.Generator(device=cuda).manual_seed(31)
+    e = torch.randn((333, D), generator=g, device=cuda).to(dtype)
+    t = torch.randint(0, 8500, (333,), generator=g, device=cuda)
+    cd = m.dequantize(qw)
+    plain = m._ext.forward(e, cd, t, None, None)
+    quant = m._ext.forward_q(e, qw, t, None, None, chunk_rows=4096)
+    torch.cuda.synchronize()
+    for x, y in zip(quant, plain):
+        torch.testing.assert_close(x, y, rtol=1e-5, atol=2e-5)
+    tm, _, _, lse, _ = plain
+    d_nll = torch.full((333,), 1.0 / 333, device=cuda)
+    dE_p, _, _ = m._ext.backward(e, cd, t, lse, tm, d_nll, None, None, m.FILTER_LOG_EPS, True, False, False)
+    dE_q, _ = m._ext.backward_q(e, qw, t, lse, tm, d_nll, None, None, m.FILTER_LOG_EPS, True, False,
+                                chunk_rows=4096)
+    torch.cuda.synchronize()
+    bits_of = lambda x: x.view(torch.int16) if x.element_size() == 2 else x.view(torch.int32)
+    assert torch.equal(bits_of(dE_q), bits_of(dE_p))
+
+
+@pytest.mark.gpu
+def test_quantized_rejects_bad_layouts(cuda):
+    import mlx_cce_amd as m
+    qw = _gpu_quant(cuda, 300, 128, 64, 4, torch.bfloat16, seed=40)
+    e = torch.randn((16, 96), device=cuda).to(torch.bfloat16)
+    t = torch.zeros((16,), dtype=torch.int64, device=cuda)
+    with pytest.raises(ValueError):
+        m.linear_cross_entropy(e, qw, t)  # D mismatch
+    e = torch.randn((16, 128), device=cuda).to(torch.float16)
+    with pytest.raises(TypeError):
+        m.linear_cross_entropy(e, qw, t)  # dtype of e differs from the scales
