@@ -63,7 +63,13 @@ constexpr int64_t kQuantDefaultChunkRows = 32768;  // 256 MiB of bf16 scratch at
 // order, and every slot's 128 x 128 G tile lives in a scratch of `cap` slots.
 // A chunk holds every token block of its vocabulary tiles, so dC and dBias of a
 // chunk are final when its sums end; dE is carried between chunks in fp32.
-constexpr size_t kWScratchBudget = size_t(2) << 30;  // bytes of G-tile scratch per chunk
+// G-tile scratch per chunk.  A chunk holds every pair it may keep, so the budget sets
+// the chunk width: 16 GiB keeps a 70B-class head (N = 32768, V = 128256: 8.4 GB) in one
+// chunk, which saves the fp32 dE carry between chunks (at that size 1.5 of 4.5 ms).
+#ifndef CCE_G_SCRATCH_GIB
+#define CCE_G_SCRATCH_GIB 16
+#endif
+constexpr size_t kWScratchBudget = size_t(CCE_G_SCRATCH_GIB) << 30;
 constexpr int kCompactMaxWords = 8192;                 // bitmap words one compaction holds in LDS
 constexpr int kCompactMaxVt = 4096;                    // vocabulary tiles per chunk (LDS counts)
 constexpr int kMaxDcBins = 256;                        // workgroup bins of the dC sums' schedule

@@ -510,6 +510,44 @@ def test_config_c3_full_size_properties(m, cuda):
     assert 0 < kept < total and torch.isfinite(e2.grad).all() and torch.isfinite(c2.grad).all()
 
 
+def test_config_c5_full_size_properties(m, cuda):
+    """c5 at full size (N=32768, D=8192, V=128256, bf16, reduction sum, the last 410
+    positions of each sequence ignored): lse / nll of sampled rows against float64
+    (computed with torch on the device in vocabulary chunks: a host float64 copy of C
+    would be 8.4 GB), within 32 / 48 ulp; the backward keeps 0 < kept < total tiles,
+    gives finite gradients and exactly zero dE rows for the ignored positions."""
+    w = workloads.make("c5", device="cuda")
+    N, D = w["N"], w["D"]
+    e = w["e"].reshape(N, D)
+    c, t = w["c"], w["targets"].reshape(N)
+    assert w["reduction"] == "sum"
+    tm, ts, ntl, lse, nll = m._ext.forward(e, c, t, None, -100)
+    rows = torch.arange(5, N, 1021, device=cuda)
+    rows = rows[t[rows] != -100]
+    er = e[rows].double()
+    lse_ref = torch.full((len(rows),), -math.inf, dtype=torch.float64, device=cuda)
+    for v0 in range(0, c.shape[0], 16384):
+        lse_ref = torch.logaddexp(lse_ref, torch.logsumexp(er @ c[v0:v0 + 16384].double().T, dim=1))
+    tgt = (er * c[t[rows]].double()).sum(1)
+    # fp32 accumulation of 8192-term dot products (target logits ~40): measured up to
+    # 12 ulp of lse (1.1e-6 relative); bounds 32 / 48 ulp (c3, D = 4096: 8 / 16)
+    ulp = np.spacing(np.float32(lse_ref.abs().max().item()))
+    np.testing.assert_allclose(f64(lse[rows]), f64(lse_ref), rtol=0, atol=32 * ulp)
+    assert np.abs(f64(nll[rows]) - f64(lse_ref - tgt)).max() < 48 * ulp
+    del tm, ts, ntl, lse, nll
+    e2 = e.detach().clone().requires_grad_(True)
+    c2 = c.detach().clone().requires_grad_(True)
+    loss = m.linear_cross_entropy(e2, c2, t, reduction="sum")
+    loss.backward()
+    torch.cuda.synchronize()
+    kept, total = m.last_tile_stats()
+    print(f"c5: loss {loss.item():.3e} kept {kept}/{total} skip {1 - kept / total:.4f}")
+    assert 0 < kept < total and torch.isfinite(e2.grad).all() and torch.isfinite(c2.grad).all()
+    ign = t == -100
+    assert int(ign.sum()) == 8 * 410
+    assert int((e2.grad[ign].view(torch.int16) != 0).sum()) == 0
+
+
 def test_config_c3_full_size_moderate_peak_sampled_grads(m, cuda):
     """c3 at full size (N=8192, D=4096, V=128256, bf16, filter on) with the target boost
     lowered from 40 to 12 so the softmax is peaked but the gradients are not ~0.
