@@ -1871,6 +1871,19 @@ static bool use_wide_de_sums(const BwdPlan& P, int64_t D, int grid) {
   return rw * 512 * 85 < rn * 256 * 100;
 }
 
+// dC sums: the narrow geometry suits the filtered backward (owners keep one or two
+// token blocks, so tasks are short); with the filter off every owner keeps all of its
+// token blocks and the wide geometry runs ~35% faster.  The kept counts are not known
+// on the host, so the choice follows the filter setting.
+static bool use_wide_dc_sums(const BwdArgs& a) {
+  // Test hook: CCE_TEST_DC_SUMS=wide|narrow forces a geometry.
+  if (const char* env = std::getenv("CCE_TEST_DC_SUMS")) {
+    if (env[0] == 'w') return true;
+    if (env[0] == 'n') return false;
+  }
+  return !(a.filter_log_eps > -INFINITY);
+}
+
 template <typename T>
 static hipError_t backward_typed(const BwdArgs& a, hipStream_t s) {
   const BwdPlan& P = a.plan;
@@ -1930,7 +1943,10 @@ static hipError_t backward_typed(const BwdArgs& a, hipStream_t s) {
       if ((err = hipGetLastError()) != hipSuccess) return err;
     }
     if (want_dc) {
-      hipLaunchKernelGGL((bwd_sum_narrow_kernel<T, 1>), dim3(gp), dim3(SumGeoNarrow<T>::NT), 0, s, a, chunk);
+      if (use_wide_dc_sums(a))
+        hipLaunchKernelGGL((bwd_sum_kernel<T, 1>), dim3(gp), dim3(SumGeo<T>::NT), 0, s, a, chunk);
+      else
+        hipLaunchKernelGGL((bwd_sum_narrow_kernel<T, 1>), dim3(gp), dim3(SumGeoNarrow<T>::NT), 0, s, a, chunk);
       if ((err = hipGetLastError()) != hipSuccess) return err;
     }
     if (want_db) {

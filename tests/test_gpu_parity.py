@@ -425,8 +425,10 @@ def test_forward_zero_fill_and_backward_into_zeroed_dc(m, cuda, chunked, monkeyp
 def test_vocabulary_chunks(m, cuda, dtype, filtered, de_sums, monkeypatch):
     """Several vocabulary chunks (forced narrow through CCE_TEST_CHUNK_VT): dE carried in fp32
     between chunks, dC / dBias final per chunk; equal to the single-chunk result and the oracle.
-    Both dE-sum geometries (CCE_TEST_DE_SUMS); D = 264 leaves a ragged column slice in each."""
+    Both sum geometries, for dE and dC together (CCE_TEST_DE_SUMS, CCE_TEST_DC_SUMS); D = 264
+    leaves a ragged column slice in each."""
     monkeypatch.setenv("CCE_TEST_DE_SUMS", de_sums)
+    monkeypatch.setenv("CCE_TEST_DC_SUMS", de_sums)
     N, D, V = 300, 264, 9000
     if filtered:
         e, c, t = _peaked(cuda, N=N, D=D, V=V, dtype=dtype, seed=11)
