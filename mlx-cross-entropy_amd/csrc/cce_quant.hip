@@ -31,22 +31,22 @@ __device__ __forceinline__ float affine(float s, float q, float b) {
   return s * q + b;
 }
 
-// Rows are blockIdx.x (chunk-local); words of a row are split over blockIdx.y.
+// Rows are blockIdx.x (chunk-local); words of a row are split over blockIdx.y.  W
+// (words per row) and G (groups per row) come from the host and group_size is a power
+// of two, so the indexing needs no 64-bit division.
 template <typename T, int BITS>
 __global__ __launch_bounds__(256) void dequant_kernel(const uint32_t* __restrict__ wq, const T* __restrict__ scales,
-                                                      const T* __restrict__ biases, int64_t D, int group_size,
-                                                      T* __restrict__ out) {
+                                                      const T* __restrict__ biases, int W, int G, int gshift,
+                                                      int64_t D, T* __restrict__ out) {
   constexpr int EPW = 32 / BITS;  // codes per word
   typedef T vec_t __attribute__((ext_vector_type(EPW)));
-  const int64_t W = D / EPW;      // words per row
-  const int64_t w = (int64_t)blockIdx.y * 256 + threadIdx.x;
+  const int w = (int)blockIdx.y * 256 + (int)threadIdx.x;
   if (w >= W) return;
   const int64_t r = blockIdx.x;
-  const int64_t G = D / group_size;
   const uint32_t word = wq[r * W + w];
-  const int64_t d0 = w * EPW;
-  const float s = to_f32(scales[r * G + d0 / group_size]);
-  const float b = to_f32(biases[r * G + d0 / group_size]);
+  const int d0 = w * EPW;
+  const float s = to_f32(scales[r * G + (d0 >> gshift)]);
+  const float b = to_f32(biases[r * G + (d0 >> gshift)]);
   vec_t v;
 #pragma unroll
   for (int j = 0; j < EPW; ++j) {
@@ -60,22 +60,24 @@ template <typename T>
 static hipError_t dequantize_typed(const QuantRows& q, int64_t row0, int64_t rows, int64_t D, void* out,
                                    hipStream_t s) {
   if (rows <= 0) return hipSuccess;
-  const int64_t words = D * q.bits / 32;
+  const int64_t words = D * q.bits / 32;  // D < 2^22 elements (8 MiB rows): fits int
   const dim3 grid((unsigned)rows, (unsigned)((words + 255) / 256));
   const uint32_t* wq = q.wq + row0 * words;
   const int64_t g = D / q.group_size;
+  const int gshift = q.group_size == 32 ? 5 : q.group_size == 64 ? 6 : 7;
   const T* sc = reinterpret_cast<const T*>(q.scales) + row0 * g;
   const T* bi = reinterpret_cast<const T*>(q.biases) + row0 * g;
   T* o = reinterpret_cast<T*>(out);
+  const int W = (int)words, G = (int)g;
   switch (q.bits) {
     case 2:
-      hipLaunchKernelGGL((dequant_kernel<T, 2>), grid, dim3(256), 0, s, wq, sc, bi, D, q.group_size, o);
+      hipLaunchKernelGGL((dequant_kernel<T, 2>), grid, dim3(256), 0, s, wq, sc, bi, W, G, gshift, D, o);
       break;
     case 4:
-      hipLaunchKernelGGL((dequant_kernel<T, 4>), grid, dim3(256), 0, s, wq, sc, bi, D, q.group_size, o);
+      hipLaunchKernelGGL((dequant_kernel<T, 4>), grid, dim3(256), 0, s, wq, sc, bi, W, G, gshift, D, o);
       break;
     case 8:
-      hipLaunchKernelGGL((dequant_kernel<T, 8>), grid, dim3(256), 0, s, wq, sc, bi, D, q.group_size, o);
+      hipLaunchKernelGGL((dequant_kernel<T, 8>), grid, dim3(256), 0, s, wq, sc, bi, W, G, gshift, D, o);
       break;
     default:
       return hipErrorInvalidValue;
