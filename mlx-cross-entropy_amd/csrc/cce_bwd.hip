@@ -196,6 +196,19 @@ __device__ __forceinline__ int block_excl_scan(int v, int* wsum, int& total) {
 // One workgroup of 1024 threads; perm[p] = input row at position p.
 constexpr int kSortMaxRounds = (int)(kPermMaxN / 1024);
 constexpr int kSortHeadRun = 16;
+// Lanes of the wave whose 5-bit value d (a 4-bit digit, or 16 for no element) equals
+// v: five ballots, one per bit, intersected with the bit or its complement as v has it.
+// Every lane must call this (the ballots span the wave).
+__device__ __forceinline__ uint64_t digit_lanes(int d, int v) {
+  uint64_t m = ~0ull;
+#pragma unroll
+  for (int k = 0; k < 5; ++k) {
+    const uint64_t b = __ballot((d >> k) & 1);
+    m &= ((v >> k) & 1) ? b : ~b;
+  }
+  return m;
+}
+
 template <int MAXR>  // rounds the elements of one thread can span: N <= 1024 MAXR
 __device__ void sort_rows(const BwdArgs& a) {
   // the ping-pong buffers sit in LDS for up to 8 rounds (8192 rows), else in the workspace
@@ -259,13 +272,9 @@ __device__ void sort_rows(const BwdArgs& a) {
     for (int r = 0; r < MAXR; ++r) {
       if (r >= rounds) break;
       const int d = valid(r) ? (int)((x[r] >> sh) & 15u) : 16;
-      int mycnt = 0;  // lane dd < 16 stores the wave's count of digit dd
-#pragma unroll
-      for (int dd = 0; dd < 16; ++dd) {
-        const int c = __popcll(__ballot(d == dd));
-        mycnt = lane == dd ? c : mycnt;
-      }
-      if (lane < 16) cnt[(r * 16 + wave) * 16 + lane] = mycnt;
+      // lane dd < 16 stores the wave's count of digit dd (lanes of digit dd: digit_lanes(dd))
+      const uint64_t m = digit_lanes(d, lane);
+      if (lane < 16) cnt[(r * 16 + wave) * 16 + lane] = __popcll(m);
     }
     __syncthreads();
     {  // wave dd: exclusive prefix of digit dd over the (round, wave) pairs, in order
@@ -286,12 +295,7 @@ __device__ void sort_rows(const BwdArgs& a) {
     for (int r = 0; r < MAXR; ++r) {
       if (r >= rounds) break;
       const int d = valid(r) ? (int)((x[r] >> sh) & 15u) : 16;
-      uint64_t mine = 0;
-#pragma unroll
-      for (int dd = 0; dd < 16; ++dd) {
-        const uint64_t m = __ballot(d == dd);
-        mine = d == dd ? m : mine;
-      }
+      const uint64_t mine = digit_lanes(d, d);  // the lanes holding this lane's digit
       if (valid(r)) dst[dstart[d] + cnt[(r * 16 + wave) * 16 + d] + __popcll(mine & lt)] = x[r];
     }
     __syncthreads();  // this pass's stores are visible to the workgroup (and cnt free)
