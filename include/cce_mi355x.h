@@ -99,6 +99,27 @@ int cce_forward_ex(int dtype, const void* e, const void* c, const void* bias,
                    float* tile_max, float* tile_sum_exp, float* neg_target_logit,
                    float* lse, float* nll, void* zero_buf, int64_t zero_bytes, void* hip_stream);
 
+/* Bytes of device workspace cce_forward_ws uses for these sizes: a copy of E in
+ * MFMA fragment order, ceil(N / 256) * 256 rows of ceil(D * elem / 128) * 128 bytes. */
+size_t cce_forward_workspace_size(int dtype, int64_t N, int64_t D);
+
+/*
+ * As cce_forward_ex, with a caller-owned workspace of cce_forward_workspace_size()
+ * bytes (16-byte aligned).  The forward first rewrites E into the workspace in the
+ * order the MFMA B operand is read, then its tile kernel loads the E fragments
+ * straight into registers and stages only the C rows through the LDS (a third of
+ * the LDS traffic saved).  Results are bit-identical to cce_forward_ex.
+ * workspace NULL: same as cce_forward_ex.  The workspace must stay untouched until
+ * the forward's work on the stream ends.  Replaces the same reference interfaces as
+ * cce_forward (csrc/bindings.cpp:58-69, cce.cpp:123-145, cce.cpp:207-277).
+ */
+int cce_forward_ws(int dtype, const void* e, const void* c, const void* bias,
+                   const int64_t* targets, int64_t ignore_index, int has_ignore,
+                   int64_t N, int64_t D, int64_t V,
+                   float* tile_max, float* tile_sum_exp, float* neg_target_logit,
+                   float* lse, float* nll, void* zero_buf, int64_t zero_bytes,
+                   void* workspace, size_t workspace_bytes, void* hip_stream);
+
 /* Bytes of device workspace cce_backward needs for these sizes and outputs. */
 size_t cce_backward_workspace_size(int dtype, int64_t N, int64_t D, int64_t V,
                                    int want_dE, int want_dC, int want_dBias);

@@ -139,10 +139,24 @@ int cce_forward(int dtype, const void* e, const void* c, const void* bias, const
                         neg_target_logit, lse, nll, nullptr, 0, hip_stream);
 }
 
+size_t cce_forward_workspace_size(int dtype, int64_t N, int64_t D) {
+  if (N <= 0 || D <= 0) return 0;
+  if (dtype != CCE_DTYPE_F32 && dtype != CCE_DTYPE_F16 && dtype != CCE_DTYPE_BF16) return 0;
+  return cce::e_frag_bytes(N, D * (int64_t)elem_size(dtype));
+}
+
 int cce_forward_ex(int dtype, const void* e, const void* c, const void* bias, const int64_t* targets,
                    int64_t ignore_index, int has_ignore, int64_t N, int64_t D, int64_t V, float* tile_max,
                    float* tile_sum_exp, float* neg_target_logit, float* lse, float* nll, void* zero_buf,
                    int64_t zero_bytes, void* hip_stream) {
+  return cce_forward_ws(dtype, e, c, bias, targets, ignore_index, has_ignore, N, D, V, tile_max, tile_sum_exp,
+                        neg_target_logit, lse, nll, zero_buf, zero_bytes, nullptr, 0, hip_stream);
+}
+
+int cce_forward_ws(int dtype, const void* e, const void* c, const void* bias, const int64_t* targets,
+                   int64_t ignore_index, int has_ignore, int64_t N, int64_t D, int64_t V, float* tile_max,
+                   float* tile_sum_exp, float* neg_target_logit, float* lse, float* nll, void* zero_buf,
+                   int64_t zero_bytes, void* workspace, size_t workspace_bytes, void* hip_stream) {
   g_err[0] = 0;
   int rc = check_common("cce_forward", dtype, e, c, targets, N, D, V);
   if (rc != CCE_OK) return rc;
@@ -154,6 +168,12 @@ int cce_forward_ex(int dtype, const void* e, const void* c, const void* bias, co
   if (zero_bytes < 0 || zero_bytes % 16 != 0 || (zero_bytes > 0 && (!zero_buf || !aligned(zero_buf, 16))))
     return fail(CCE_ERR_INVALID_ARGUMENT,
                 "[cce_forward] zero_buf must be 16-byte aligned and zero_bytes a non-negative multiple of 16");
+  if (workspace) {
+    const size_t need = cce::e_frag_bytes(N, D * (int64_t)elem_size(dtype));
+    if (workspace_bytes < need || !aligned(workspace, 16))
+      return fail(CCE_ERR_WORKSPACE, "[cce_forward] workspace must be 16-byte aligned and hold %zu bytes, got %zu",
+                  need, workspace_bytes);
+  }
   const int cus = num_cus_current();
   if (cus <= 0) return fail(CCE_ERR_NO_DEVICE, "[cce_forward] no HIP device is available");
 
@@ -175,6 +195,7 @@ int cce_forward_ex(int dtype, const void* e, const void* c, const void* bias, co
   a.num_cus = cus;
   a.zero_buf = zero_bytes > 0 ? zero_buf : nullptr;
   a.zero_units = zero_bytes / 16;
+  a.e_frag = workspace;
   hipError_t err = cce::launch_forward(dtype, a, reinterpret_cast<hipStream_t>(hip_stream));
   if (err != hipSuccess)
     return fail(CCE_ERR_LAUNCH, "[cce_forward] kernel launch failed: %s", hipGetErrorString(err));

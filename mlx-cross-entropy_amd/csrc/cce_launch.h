@@ -35,7 +35,17 @@ struct FwdArgs {
   int num_cus;  // compute units of the device (the persistent forward runs one workgroup per CU)
   void* zero_buf;       // filled with zeros alongside the tiles (null: none)
   int64_t zero_units;   // 16-byte units of zero_buf
+  void* e_frag;         // E in MFMA fragment order (e_frag_bytes(); null: E staged through LDS)
 };
+
+// Bytes of the fragment-order copy of E that the forward's register-operand main
+// loop reads: every 32-row token block of the whole 256-token tiles, the row
+// bytes rounded up to the 128-byte slice.
+inline size_t e_frag_bytes(int64_t N, int64_t row_bytes) {
+  const int64_t blocks = (N + 255) / 256 * 8;
+  const int64_t slices = (row_bytes + 127) / 128;
+  return (size_t)(blocks * slices * 4096);
+}
 
 // Classifier rows stored with affine group quantization (the layout of MLX's
 // mx.quantize / mx.dequantize, mlx >= 0.22, which the reference's callers apply

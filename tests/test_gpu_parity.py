@@ -631,3 +631,29 @@ def test_config_c3_full_size_moderate_peak_sampled_grads(m, cuda):
     assert errE < 2e-2 and errC < 2e-2
     assert rel_ip < 5e-3
     assert torch.isfinite(dE).all() and torch.isfinite(dC).all()
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("N,D,V", [(1, 8, 1), (300, 40, 1000), (513, 136, 2050), (1024, 512, 4096),
+                                   (2304, 4096, 1280)])
+def test_forward_e_fragments_bit_identical(m, cuda, dtype, N, D, V):
+    """cce_forward_ws (E fragments in registers from the fragment-order copy) returns
+    exactly what cce_forward_ex (both operands through the LDS) returns: same MFMA
+    sequence on the same operands.  Covers ragged N (token blocks past N read the
+    copy's zero rows), a row length off the 128-byte slice (zero-padded fragments)
+    and a contraction long enough for many pipeline rounds."""
+    g = torch.Generator(device=cuda).manual_seed(N + D + V)
+    e = torch.randn((N, D), generator=g, device=cuda).to(dtype)
+    c = (torch.randn((V, D), generator=g, device=cuda) * 0.05).to(dtype)
+    t = torch.randint(0, V, (N,), generator=g, device=cuda)
+    t[::7] = -100
+    zero = torch.full((V * D,), 7.0, device=cuda, dtype=torch.float32)
+    outs_lds = m._ext.forward(e, c, t, e_frag=False)
+    outs_reg = m._ext.forward(e, c, t, zero_out=zero, e_frag=True)
+    torch.cuda.synchronize()
+    valid = t != -100  # neg_target_logit is left unwritten on ignored rows
+    for k, (a, b) in enumerate(zip(outs_lds, outs_reg)):
+        if k == 2:
+            a, b = a[valid], b[valid]
+        assert torch.equal(torch.nan_to_num(a, nan=1e30), torch.nan_to_num(b, nan=1e30)), k
+    assert int(torch.count_nonzero(zero)) == 0
