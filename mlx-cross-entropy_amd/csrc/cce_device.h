@@ -301,11 +301,11 @@ struct NTMainLoop {
       if constexpr (RAGGED) {
         const char* g = (src.segb[sg] + k0) + src.off[j];
         if (k0 + (int64_t)src.qb[j] >= src.kbytes) g = reinterpret_cast<const char*>(g_zero16);
-        asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory");
+        asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
       } else {
         asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(src.off[j]),
                      "s"(src.segb[sg] + k0), "s"(lds)
-                     : "memory");
+                     : "memory", "m0");
       }
     }
   }

@@ -55,6 +55,17 @@ def test_version_and_geometry(ext):
         assert lib.cce_num_vocab_tiles(V) == math.ceil(V / 128)
 
 
+def test_forward_workspace_size(ext):
+    """Fragment-order copy of E: whole 256-token tiles x row bytes rounded up to the
+    128-byte slice; zero for empty shapes and unknown dtypes."""
+    lib = ext.lib()
+    assert lib.cce_forward_workspace_size(2, 8192, 4096) == 8192 * 8192
+    assert lib.cce_forward_workspace_size(0, 300, 40) == 512 * 256  # fp32 rows of 160 B -> 2 slices
+    assert lib.cce_forward_workspace_size(1, 1, 8) == 256 * 128
+    assert lib.cce_forward_workspace_size(2, 0, 4096) == 0
+    assert lib.cce_forward_workspace_size(7, 8192, 4096) == 0
+
+
 def test_workspace_size_layout(ext):
     lib = ext.lib()
     N, D, V = 1000, 64, 3000
