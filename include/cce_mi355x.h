@@ -99,30 +99,27 @@ int cce_forward_ex(int dtype, const void* e, const void* c, const void* bias,
                    float* tile_max, float* tile_sum_exp, float* neg_target_logit,
                    float* lse, float* nll, void* zero_buf, int64_t zero_bytes, void* hip_stream);
 
-/* Bytes of device workspace cce_forward_ws uses for these sizes: a copy of E in
- * MFMA fragment order, ceil(N / 256) * 256 rows of ceil(D * elem / 128) * 128 bytes. */
-size_t cce_forward_workspace_size(int dtype, int64_t N, int64_t D);
-
 /*
- * As cce_forward_ex, with a caller-owned workspace of cce_forward_workspace_size()
- * bytes (16-byte aligned).  The forward first rewrites E into the workspace in the
- * order the MFMA B operand is read, then its tile kernel loads the E fragments
- * straight into registers and stages only the C rows through the LDS (a third of
- * the LDS traffic saved).  Results are bit-identical to cce_forward_ex.
- * workspace NULL: same as cce_forward_ex.  The workspace must stay untouched until
- * the forward's work on the stream ends.  Replaces the same reference interfaces as
- * cce_forward (csrc/bindings.cpp:58-69, cce.cpp:123-145, cce.cpp:207-277).
+ * Bytes of the default device workspace of cce_backward for these sizes and outputs.
+ * The backward holds the G tiles of the kept (128-row, 128-column) pairs in passes of
+ * a bounded size (a 512 MiB budget of G tiles by default, at least 2 tiles per 128-row
+ * block): the workspace is O(budget + N*D + V), never O(N*V).  Reference interface
+ * replaced: the output-sized accumulators of cce.cpp:315-340 (zero_alloc dE / dC).
  */
-int cce_forward_ws(int dtype, const void* e, const void* c, const void* bias,
-                   const int64_t* targets, int64_t ignore_index, int has_ignore,
-                   int64_t N, int64_t D, int64_t V,
-                   float* tile_max, float* tile_sum_exp, float* neg_target_logit,
-                   float* lse, float* nll, void* zero_buf, int64_t zero_bytes,
-                   void* workspace, size_t workspace_bytes, void* hip_stream);
-
-/* Bytes of device workspace cce_backward needs for these sizes and outputs. */
 size_t cce_backward_workspace_size(int dtype, int64_t N, int64_t D, int64_t V,
                                    int want_dE, int want_dC, int want_dBias);
+
+/*
+ * As cce_backward_workspace_size, for passes of at most max_g_tiles G tiles (0: the
+ * default budget; values below 2 tiles per 128-row block are raised to that, values
+ * above the default are lowered to it) and vocabulary chunks of at most
+ * max_chunk_tiles 128-column tiles (0: the library's choice; else a multiple of 32).
+ * A cce_backward_ex given a workspace of this size and the same max_chunk_tiles runs
+ * exactly these passes.  Same reference interface as above.
+ */
+size_t cce_backward_workspace_size_ex(int dtype, int64_t N, int64_t D, int64_t V,
+                                      int want_dE, int want_dC, int want_dBias, int64_t max_g_tiles,
+                                      int64_t max_chunk_tiles);
 
 /*
  * Backward pass.  Replaces cce_backward_raw (csrc/bindings.cpp:71-86, cce.cpp:152-179),
@@ -135,9 +132,14 @@ size_t cce_backward_workspace_size(int dtype, int64_t N, int64_t D, int64_t V,
  * (reference predicate: cce.metal:191-204).  filter_log_eps = -INFINITY keeps all tiles.
  * dE/dC/dBias are written in `dtype`; pass NULL for any gradient not wanted.
  * No atomics: kept tiles' G blocks are staged (bf16/fp16/fp32, the input dtype) in
- * the workspace, then every output row block is summed in fp32 registers by the one
- * workgroup that owns it and written once.  Every output element is written, so the
- * outputs need no zero-fill.  Rows of dE/dC/dBias that no kept tile touches are 0.
+ * the workspace, one pass of a bounded number of them at a time, then every output
+ * row block is summed in fp32 registers by the one workgroup that owns it and written
+ * once (dE through an fp32 carry in the workspace when the kept tiles take more than
+ * one pass).  Every output element is written, so the outputs need no zero-fill.
+ * Rows of dE/dC/dBias that no kept tile touches are 0.
+ * The plan depends only on the sizes, the outputs asked for and workspace_bytes: the
+ * default plan when the workspace holds cce_backward_workspace_size() bytes, else
+ * smaller passes (CCE_ERR_WORKSPACE below the least size).
  * The workspace must stay untouched until the backward's work on the stream ends.
  * tile_stats (nullable, device int64[3]) receives {kept tiles, total tiles, kept tiles
  * of the input-order token blocks}.  The backward may form its 128-row token blocks
@@ -154,9 +156,20 @@ int cce_backward(int dtype, const void* e, const void* c, const void* bias,
                  int64_t* tile_stats, void* hip_stream);
 
 /* Flags of cce_backward_ex. */
-#define CCE_BWD_DC_ZEROED 1 /* dC already holds zeros (e.g. from cce_forward_ex) */
+#define CCE_BWD_DC_ZEROED 1       /* dC already holds zeros (e.g. from cce_forward_ex) */
+/* Overrides of choices the backward otherwise makes itself (for tests and tuning;
+ * results agree to rounding either way): */
+#define CCE_BWD_TOKENS_INPUT 2    /* token blocks of 128 rows in input order */
+#define CCE_BWD_TOKENS_SORTED 4   /* token blocks of the rows grouped by target tile, when available */
+#define CCE_BWD_DE_SUMS_WIDE 8    /* dE sums in 512-column tasks */
+#define CCE_BWD_DE_SUMS_NARROW 16 /* dE sums in 256-column tasks */
+#define CCE_BWD_DC_SUMS_WIDE 32   /* dC sums in 512-column tasks */
+#define CCE_BWD_DC_SUMS_NARROW 64 /* dC sums in 256-column tasks */
 
-/* As cce_backward, with flags (CCE_BWD_*).  Same reference interfaces as cce_backward. */
+/* As cce_backward, with flags (CCE_BWD_*) and vocabulary chunks of at most
+ * max_chunk_tiles tiles (0: the library's choice; else a multiple of 32; the workspace
+ * size is then cce_backward_workspace_size_ex's with the same value).  Same reference
+ * interfaces as cce_backward. */
 int cce_backward_ex(int dtype, const void* e, const void* c, const void* bias,
                     const int64_t* targets, int64_t ignore_index, int has_ignore,
                     int64_t N, int64_t D, int64_t V,
@@ -164,7 +177,7 @@ int cce_backward_ex(int dtype, const void* e, const void* c, const void* bias,
                     float filter_log_eps,
                     void* dE, void* dC, void* dBias,
                     void* workspace, size_t workspace_bytes,
-                    int64_t* tile_stats, int flags, void* hip_stream);
+                    int64_t* tile_stats, int flags, int64_t max_chunk_tiles, void* hip_stream);
 
 /*
  * Quantized classifier rows.  The reference's callers pass an lm_head / tied

@@ -139,24 +139,10 @@ int cce_forward(int dtype, const void* e, const void* c, const void* bias, const
                         neg_target_logit, lse, nll, nullptr, 0, hip_stream);
 }
 
-size_t cce_forward_workspace_size(int dtype, int64_t N, int64_t D) {
-  if (N <= 0 || D <= 0) return 0;
-  if (dtype != CCE_DTYPE_F32 && dtype != CCE_DTYPE_F16 && dtype != CCE_DTYPE_BF16) return 0;
-  return cce::e_frag_bytes(N, D * (int64_t)elem_size(dtype));
-}
-
 int cce_forward_ex(int dtype, const void* e, const void* c, const void* bias, const int64_t* targets,
                    int64_t ignore_index, int has_ignore, int64_t N, int64_t D, int64_t V, float* tile_max,
                    float* tile_sum_exp, float* neg_target_logit, float* lse, float* nll, void* zero_buf,
                    int64_t zero_bytes, void* hip_stream) {
-  return cce_forward_ws(dtype, e, c, bias, targets, ignore_index, has_ignore, N, D, V, tile_max, tile_sum_exp,
-                        neg_target_logit, lse, nll, zero_buf, zero_bytes, nullptr, 0, hip_stream);
-}
-
-int cce_forward_ws(int dtype, const void* e, const void* c, const void* bias, const int64_t* targets,
-                   int64_t ignore_index, int has_ignore, int64_t N, int64_t D, int64_t V, float* tile_max,
-                   float* tile_sum_exp, float* neg_target_logit, float* lse, float* nll, void* zero_buf,
-                   int64_t zero_bytes, void* workspace, size_t workspace_bytes, void* hip_stream) {
   g_err[0] = 0;
   int rc = check_common("cce_forward", dtype, e, c, targets, N, D, V);
   if (rc != CCE_OK) return rc;
@@ -168,12 +154,6 @@ int cce_forward_ws(int dtype, const void* e, const void* c, const void* bias, co
   if (zero_bytes < 0 || zero_bytes % 16 != 0 || (zero_bytes > 0 && (!zero_buf || !aligned(zero_buf, 16))))
     return fail(CCE_ERR_INVALID_ARGUMENT,
                 "[cce_forward] zero_buf must be 16-byte aligned and zero_bytes a non-negative multiple of 16");
-  if (workspace) {
-    const size_t need = cce::e_frag_bytes(N, D * (int64_t)elem_size(dtype));
-    if (workspace_bytes < need || !aligned(workspace, 16))
-      return fail(CCE_ERR_WORKSPACE, "[cce_forward] workspace must be 16-byte aligned and hold %zu bytes, got %zu",
-                  need, workspace_bytes);
-  }
   const int cus = num_cus_current();
   if (cus <= 0) return fail(CCE_ERR_NO_DEVICE, "[cce_forward] no HIP device is available");
 
@@ -195,7 +175,6 @@ int cce_forward_ws(int dtype, const void* e, const void* c, const void* bias, co
   a.num_cus = cus;
   a.zero_buf = zero_bytes > 0 ? zero_buf : nullptr;
   a.zero_units = zero_bytes / 16;
-  a.e_frag = workspace;
   hipError_t err = cce::launch_forward(dtype, a, reinterpret_cast<hipStream_t>(hip_stream));
   if (err != hipSuccess)
     return fail(CCE_ERR_LAUNCH, "[cce_forward] kernel launch failed: %s", hipGetErrorString(err));
@@ -204,9 +183,16 @@ int cce_forward_ws(int dtype, const void* e, const void* c, const void* bias, co
 
 size_t cce_backward_workspace_size(int dtype, int64_t N, int64_t D, int64_t V, int want_dE, int want_dC,
                                    int want_dBias) {
-  if (N <= 0 || D <= 0 || V <= 0) return 0;
+  return cce_backward_workspace_size_ex(dtype, N, D, V, want_dE, want_dC, want_dBias, 0, 0);
+}
+
+size_t cce_backward_workspace_size_ex(int dtype, int64_t N, int64_t D, int64_t V, int want_dE, int want_dC,
+                                      int want_dBias, int64_t max_g_tiles, int64_t max_chunk_tiles) {
+  if (N <= 0 || D <= 0 || V <= 0 || max_g_tiles < 0 || max_chunk_tiles < 0 || max_chunk_tiles % 32 != 0) return 0;
   if (dtype != CCE_DTYPE_F32 && dtype != CCE_DTYPE_F16 && dtype != CCE_DTYPE_BF16) return 0;
-  return cce::make_bwd_plan(elem_size(dtype), N, D, V, want_dE != 0, want_dC != 0, want_dBias != 0).total_bytes;
+  return cce::make_bwd_plan(elem_size(dtype), N, D, V, want_dE != 0, want_dC != 0, want_dBias != 0,
+                            max_chunk_tiles, false, max_g_tiles)
+      .total_bytes;
 }
 
 int cce_backward(int dtype, const void* e, const void* c, const void* bias, const int64_t* targets,
@@ -214,7 +200,7 @@ int cce_backward(int dtype, const void* e, const void* c, const void* bias, cons
                  const float* tile_max, const float* d_nll, float filter_log_eps, void* dE, void* dC, void* dBias,
                  void* workspace, size_t workspace_bytes, int64_t* tile_stats, void* hip_stream) {
   return cce_backward_ex(dtype, e, c, bias, targets, ignore_index, has_ignore, N, D, V, lse, tile_max, d_nll,
-                         filter_log_eps, dE, dC, dBias, workspace, workspace_bytes, tile_stats, 0, hip_stream);
+                         filter_log_eps, dE, dC, dBias, workspace, workspace_bytes, tile_stats, 0, 0, hip_stream);
 }
 
 }  // extern "C"
@@ -227,8 +213,8 @@ namespace {
 int backward_impl(int dtype, const void* e, const void* c, const void* bias, const int64_t* targets,
                   int64_t ignore_index, int has_ignore, int64_t N, int64_t D, int64_t V, const float* lse,
                   const float* tile_max, const float* d_nll, float filter_log_eps, void* dE, void* dC, void* dBias,
-                  void* workspace, size_t workspace_bytes, int64_t* tile_stats, int flags, const cce::QuantRows* q,
-                  void* hip_stream) {
+                  void* workspace, size_t workspace_bytes, int64_t* tile_stats, int flags, int64_t max_chunk_tiles,
+                  const cce::QuantRows* q, void* hip_stream) {
   if (!lse || !tile_max || !d_nll)
     return fail(CCE_ERR_INVALID_ARGUMENT, "[cce_backward] lse, tile_max and d_nll must be non-null");
   if (dBias && !bias)
@@ -239,11 +225,21 @@ int backward_impl(int dtype, const void* e, const void* c, const void* bias, con
     return fail(CCE_ERR_INVALID_ARGUMENT, "[cce_backward] gradient outputs must be 16-byte aligned");
   if (std::isnan(filter_log_eps))
     return fail(CCE_ERR_INVALID_ARGUMENT, "[cce_backward] filter_log_eps must not be NaN");
-  const cce::BwdPlan P = cce::make_bwd_plan(elem_size(dtype), N, D, V, dE != nullptr, dC != nullptr, dBias != nullptr,
-                                            q ? q->chunk_rows / cce::kBwdVocab : 0, q != nullptr);
-  if (!workspace || workspace_bytes < P.total_bytes)
-    return fail(CCE_ERR_WORKSPACE, "[cce_backward] workspace of %zu bytes required, %zu given", P.total_bytes,
-                workspace ? workspace_bytes : (size_t)0);
+  // The plan is a function of the sizes, the wanted outputs and the workspace size
+  // only: the default plan when the workspace holds it, else smaller passes.
+  const size_t es = elem_size(dtype);
+  int64_t qcv = q ? q->chunk_rows / cce::kBwdVocab : 0;
+  if (max_chunk_tiles > 0 && (qcv == 0 || max_chunk_tiles < qcv)) qcv = max_chunk_tiles;
+  bool fits = false;
+  const cce::BwdPlan P = cce::plan_for_workspace(es, N, D, V, dE != nullptr, dC != nullptr, dBias != nullptr, qcv,
+                                                 q != nullptr, workspace ? workspace_bytes : 0, fits);
+  if (!workspace || !fits) {
+    const size_t least = cce::make_bwd_plan_cap(es, N, D, V, dE != nullptr, dC != nullptr, dBias != nullptr, 1, false,
+                                                qcv, q != nullptr)
+                             .total_bytes;
+    return fail(CCE_ERR_WORKSPACE, "[cce_backward] workspace of %zu bytes required (at least %zu), %zu given",
+                P.total_bytes, least, workspace ? workspace_bytes : (size_t)0);
+  }
   if (!aligned(workspace, 256))
     return fail(CCE_ERR_WORKSPACE, "[cce_backward] workspace must be 256-byte aligned");
   const int cus = num_cus_current();
@@ -270,6 +266,7 @@ int backward_impl(int dtype, const void* e, const void* c, const void* bias, con
   a.dBias = dBias;
   a.bits = reinterpret_cast<uint32_t*>(ws + P.bits);
   a.counts = reinterpret_cast<int*>(ws + P.counts);
+  a.pinfo = reinterpret_cast<int*>(ws + P.pinfo);
   a.rb_start = reinterpret_cast<int*>(ws + P.rb_start);
   a.slot_vt = reinterpret_cast<int*>(ws + P.slot_vt);
   a.slot_rb = reinterpret_cast<int*>(ws + P.slot_rb);
@@ -283,7 +280,7 @@ int backward_impl(int dtype, const void* e, const void* c, const void* bias, con
   a.dc_bin_owner = reinterpret_cast<int*>(ws + P.dc_bin_owner);
   a.gtile = (dE || dC) ? ws + P.gtile : nullptr;
   a.colsum = dBias ? reinterpret_cast<float*>(ws + P.colsum) : nullptr;
-  a.de_acc = (dE && P.n_chunks > 1) ? reinterpret_cast<float*>(ws + P.de_acc) : nullptr;
+  a.de_acc = P.carry ? reinterpret_cast<float*>(ws + P.de_acc) : nullptr;
   if (P.perm_ok) {
     a.perm = reinterpret_cast<int*>(ws + P.perm);
     a.sort_buf = reinterpret_cast<uint32_t*>(ws + P.sort_buf);
@@ -294,9 +291,9 @@ int backward_impl(int dtype, const void* e, const void* c, const void* bias, con
     a.dnll_perm = reinterpret_cast<float*>(ws + P.dnll_perm);
     a.e_perm = ws + P.e_perm;
   }
-  // Test hook: CCE_TEST_TOKEN_ORDER=input|sorted forces the token order of the backward.
-  a.perm_mode = 0;
-  if (const char* env = std::getenv("CCE_TEST_TOKEN_ORDER")) a.perm_mode = env[0] == 'i' ? 1 : env[0] == 's' ? 2 : 0;
+  a.perm_mode = (flags & CCE_BWD_TOKENS_INPUT) ? 1 : (flags & CCE_BWD_TOKENS_SORTED) ? 2 : 0;
+  a.de_geo = (flags & CCE_BWD_DE_SUMS_WIDE) ? 1 : (flags & CCE_BWD_DE_SUMS_NARROW) ? 2 : 0;
+  a.dc_geo = (flags & CCE_BWD_DC_SUMS_WIDE) ? 1 : (flags & CCE_BWD_DC_SUMS_NARROW) ? 2 : 0;
   a.tile_stats = tile_stats;
   a.dc_zeroed = (flags & CCE_BWD_DC_ZEROED) ? 1 : 0;
   a.plan = P;
@@ -320,14 +317,24 @@ int cce_backward_ex(int dtype, const void* e, const void* c, const void* bias, c
                     int64_t ignore_index, int has_ignore, int64_t N, int64_t D, int64_t V, const float* lse,
                     const float* tile_max, const float* d_nll, float filter_log_eps, void* dE, void* dC,
                     void* dBias, void* workspace, size_t workspace_bytes, int64_t* tile_stats, int flags,
-                    void* hip_stream) {
+                    int64_t max_chunk_tiles, void* hip_stream) {
   g_err[0] = 0;
-  if (flags & ~CCE_BWD_DC_ZEROED) return fail(CCE_ERR_INVALID_ARGUMENT, "[cce_backward] unknown flags 0x%x", flags);
+  constexpr int kKnown = CCE_BWD_DC_ZEROED | CCE_BWD_TOKENS_INPUT | CCE_BWD_TOKENS_SORTED | CCE_BWD_DE_SUMS_WIDE |
+                         CCE_BWD_DE_SUMS_NARROW | CCE_BWD_DC_SUMS_WIDE | CCE_BWD_DC_SUMS_NARROW;
+  if (flags & ~kKnown) return fail(CCE_ERR_INVALID_ARGUMENT, "[cce_backward] unknown flags 0x%x", flags);
+  if ((flags & CCE_BWD_TOKENS_INPUT) && (flags & CCE_BWD_TOKENS_SORTED))
+    return fail(CCE_ERR_INVALID_ARGUMENT, "[cce_backward] CCE_BWD_TOKENS_INPUT and CCE_BWD_TOKENS_SORTED exclude each other");
+  if (((flags & CCE_BWD_DE_SUMS_WIDE) && (flags & CCE_BWD_DE_SUMS_NARROW)) ||
+      ((flags & CCE_BWD_DC_SUMS_WIDE) && (flags & CCE_BWD_DC_SUMS_NARROW)))
+    return fail(CCE_ERR_INVALID_ARGUMENT, "[cce_backward] a sums geometry flag pair excludes each other");
+  if (max_chunk_tiles < 0 || (max_chunk_tiles > 0 && max_chunk_tiles % 32 != 0))
+    return fail(CCE_ERR_INVALID_ARGUMENT, "[cce_backward] max_chunk_tiles must be 0 or a positive multiple of 32, got %lld",
+                (long long)max_chunk_tiles);
   const int rc = check_common("cce_backward", dtype, e, c, targets, N, D, V);
   if (rc != CCE_OK) return rc;
   return backward_impl(dtype, e, c, bias, targets, ignore_index, has_ignore, N, D, V, lse, tile_max, d_nll,
-                       filter_log_eps, dE, dC, dBias, workspace, workspace_bytes, tile_stats, flags, nullptr,
-                       hip_stream);
+                       filter_log_eps, dE, dC, dBias, workspace, workspace_bytes, tile_stats, flags, max_chunk_tiles,
+                       nullptr, hip_stream);
 }
 
 int cce_dequantize(int dtype, const uint32_t* weight, const void* scales, const void* qbiases, int group_size,
@@ -423,7 +430,8 @@ int cce_backward_q(int dtype, const void* e, const uint32_t* weight, const void*
   if ((rc = check_chunk_rows("cce_backward_q", chunk_rows)) != CCE_OK) return rc;
   cce::QuantRows q{weight, scales, qbiases, group_size, bits, nullptr, quant_chunk_rows(chunk_rows)};
   return backward_impl(dtype, e, nullptr, bias, targets, ignore_index, has_ignore, N, D, V, lse, tile_max, d_nll,
-                       filter_log_eps, dE, nullptr, dBias, workspace, workspace_bytes, tile_stats, 0, &q, hip_stream);
+                       filter_log_eps, dE, nullptr, dBias, workspace, workspace_bytes, tile_stats, 0, 0, &q,
+                       hip_stream);
 }
 
 int cce_reduce_loss(const float* nll, const int64_t* targets, int64_t ignore_index, int has_ignore, int64_t N,

@@ -47,7 +47,6 @@
 //                          with ds_read_b64_tr_b16 (dC reads G transposed the same
 //                          way), output rows written once in the output dtype.
 //   6. bwd_dbias_kernel    dBias = sum of the column sums of a vocab tile's slots.
-#include <cstdlib>
 #include <type_traits>
 
 #include "cce_device.h"
@@ -429,12 +428,13 @@ __device__ __forceinline__ void permute_row(const BwdArgs& a, int64_t p, int64_t
   }
 }
 
-// Writes to out[] the owners o < n with size(o) > 0, largest size first (a counting
-// sort over LDS buckets; sizes past the last bucket share it, and the order among
-// equal sizes is not fixed), and returns how many there are.  All 1024 threads call it.
+// Writes to out[] the owners base + o (o < n) with size(o) > 0, largest size first (a
+// counting sort over LDS buckets; sizes past the last bucket share it, and the order
+// among equal sizes is not fixed), and returns how many there are.  All 1024 threads
+// call it.
 constexpr int kOrderBuckets = 4096;
 template <typename F>
-__device__ __forceinline__ int order_by_size(int n, F size, int* out, int* hist, int* wsum) {
+__device__ __forceinline__ int order_by_size(int n, F size, int* out, int base, int* hist, int* wsum) {
   const int tid = threadIdx.x;
   auto bucket = [](int sz) { return kOrderBuckets - 1 - min(sz, kOrderBuckets - 1); };
   for (int i = tid; i < kOrderBuckets; i += 1024) hist[i] = 0;
@@ -461,7 +461,7 @@ __device__ __forceinline__ int order_by_size(int n, F size, int* out, int* hist,
   __syncthreads();
   for (int o = tid; o < n; o += 1024) {
     const int sz = size(o);
-    if (sz > 0) out[atomicAdd(&hist[bucket(sz)], 1)] = o;
+    if (sz > 0) out[atomicAdd(&hist[bucket(sz)], 1)] = base + o;
   }
   __syncthreads();  // hist free for the next call
   return total;
@@ -469,14 +469,20 @@ __device__ __forceinline__ int order_by_size(int n, F size, int* out, int* hist,
 
 // ---------------------------------------------------------------- 2. compaction
 // One workgroup of 1024 threads per chunk.  The chunk's bitmap (token block rb,
-// word wl) sits in LDS as bm[rb * cwd + wl]; an exclusive scan of the word
-// popcounts in that (row-major) order gives every kept pair its slot, so slots run
-// by token block, then vocab tile.  Per vocab tile the kept token blocks are listed
-// in vt_slot (ascending), and the G tasks cut every token block's slots into runs
-// of at most 4.  The token blocks are those of the input order or of the sorted
-// order (the first chunk picks one for all chunks).  Last, the owners of the dE and
-// dC sums (token blocks, vocab tiles)
-// that hold kept tiles are listed by descending tile count.
+// word wl) sits in LDS as bm[rb * cwd + wl], with each row's kept count before every
+// word (pre).  The chunk's tiles are cut into passes by the exclusive prefix P[v] of
+// their kept counts: tile v belongs to pass floor(P[v] / (cap - nrb)) (one pass when
+// the chunk fits the G scratch), so every pass keeps fewer than cap pairs.  Slots run
+// by pass, then token block, then vocab tile: slot(rb, v) = first slot of (pass,
+// rb) + the kept tiles of row rb in the pass before v.  Per vocab tile the kept token
+// blocks are listed in vt_slot (ascending), the G tasks cut every (pass, token block)
+// run of slots into runs of at most 4, and per pass the owners of the dE and dC sums
+// (token blocks, vocab tiles) that hold kept tiles are listed by descending tile
+// count.  The pass table gets every pass's ranges, counts and dE write mode; passes
+// past the last one the data needs are marked empty.  The token blocks are those of
+// the input order or of the sorted order (the first chunk picks one for all chunks).
+constexpr int kRbsLds = 8192;  // (pass, token block) slot starts held in LDS when they fit
+
 __global__ __launch_bounds__(1024) void bwd_compact_kernel(BwdArgs a, int chunk) {
   // Workgroups past the first copy the rows into the sorted order (16 rows each, one
   // per wave) while the first compacts: the copy does not wait for the choice of
@@ -486,12 +492,17 @@ __global__ __launch_bounds__(1024) void bwd_compact_kernel(BwdArgs a, int chunk)
     return;
   }
   __shared__ uint32_t bm[kCompactMaxWords];
-  __shared__ int pre[kCompactMaxWords + 1];
-  __shared__ int vcnt[kCompactMaxVt];
-  __shared__ int hist[kOrderBuckets];
+  __shared__ int pre[kCompactMaxWords];     // kept tiles of row rb before word wl
+  __shared__ int vpre[kCompactMaxVt + 1];   // kept pairs of the chunk's tiles before tile v
+  __shared__ int pvt[kCompactMaxVt + 1];    // first tile of each pass (nv from the pass after the last on)
+  __shared__ int rbs_l[kRbsLds + 1];        // rb_start, when the chunk's (pass, block) pairs fit
+  __shared__ int hist[kCompactMaxVt + 1];   // the G-task run indices before each pass (kbp), then order_by_size's
   __shared__ int wsum[16];
+  static_assert(kOrderBuckets <= kCompactMaxVt, "order_by_size's buckets fit hist");
+  int* kbp = hist;  // G-task run indices of the passes before pass p (free again once the tasks are written)
   const int tid = threadIdx.x;
   const int nrb = (int)a.plan.nrb, nw = (int)a.plan.nwords, nvt = (int)a.plan.nvt;
+  const int maxp = (int)a.plan.max_passes;
   const int vlo = chunk * (int)a.plan.chunk_nvt;
   const int nv = min(nvt, vlo + (int)a.plan.chunk_nvt) - vlo;
   const int wlo = vlo >> 5;  // chunks start on a word boundary
@@ -500,7 +511,7 @@ __global__ __launch_bounds__(1024) void bwd_compact_kernel(BwdArgs a, int chunk)
 
   // Token order (decided by the first chunk for all of them): the sorted blocks'
   // bitmap when it keeps at least 10% fewer pairs than the input blocks' (or as the
-  // test hook perm_mode forces).
+  // caller forces with perm_mode).
   __shared__ int sorted;
   if (chunk == 0) {
     int flag = 0;
@@ -537,136 +548,255 @@ __global__ __launch_bounds__(1024) void bwd_compact_kernel(BwdArgs a, int chunk)
     bm[e] = x;
   }
   __syncthreads();
-
-  // slots: exclusive scan of popcounts, each thread over a contiguous run of words
-  const int per = (E + 1023) >> 10;
-  const int e0 = min(E, tid * per), e1 = min(E, e0 + per);
-  int cnt = 0;
-  for (int e = e0; e < e1; ++e) cnt += __builtin_popcount(bm[e]);
-  int kept;
-  int pos = block_excl_scan(cnt, wsum, kept);
-  for (int e = e0; e < e1; ++e) {
-    pre[e] = pos;
-    pos += __builtin_popcount(bm[e]);
+  for (int rb = tid; rb < nrb; rb += 1024) {
+    int acc = 0;
+    for (int wl = 0; wl < cwd; ++wl) {
+      pre[rb * cwd + wl] = acc;
+      acc += __builtin_popcount(bm[rb * cwd + wl]);
+    }
   }
-  if (tid == 0) pre[E] = kept;
+  // kept pairs per tile, then their exclusive prefix (each thread a contiguous run of tiles)
+  int kept;
+  {
+    const int pv = (nv + 1023) >> 10;
+    const int v0 = min(nv, tid * pv), v1 = min(nv, v0 + pv);
+    int vs = 0;
+    for (int v = v0; v < v1; ++v) {
+      const int wl = v >> 5, bit = v & 31;
+      int c = 0;
+      for (int rb = 0; rb < nrb; ++rb) c += (bm[rb * cwd + wl] >> bit) & 1u;
+      vpre[v] = c;
+      vs += c;
+    }
+    int vp = block_excl_scan(vs, wsum, kept);
+    for (int v = v0; v < v1; ++v) {
+      const int c = vpre[v];
+      vpre[v] = vp;
+      vp += c;
+    }
+    if (tid == 0) vpre[nv] = kept;
+  }
   __syncthreads();
 
-  for (int rb = tid; rb < nrb; rb += 1024) a.rb_start[rb] = pre[rb * cwd];
-  if (tid == 0) a.rb_start[nrb] = kept;
+  // Passes.  With max_passes > 1 the plan has cap >= 2 nrb, so consecutive tiles
+  // (at most nrb pairs each) never skip a pass, and every pass holds a tile.
+  const int cp = maxp > 1 ? (int)(a.plan.cap - nrb) : 0x7fffffff;
+  auto pass_of = [&](int v) { return vpre[v] / cp; };
+  for (int v = tid; v < nv; v += 1024) {
+    const int p = pass_of(v);
+    if (v == 0 || pass_of(v - 1) != p) pvt[p] = v;
+  }
+  const int npass = pass_of(nv - 1) + 1;  // <= maxp
+  for (int p = npass + tid; p <= maxp; p += 1024) pvt[p] = nv;
+  __syncthreads();
+  // kept tiles of row rb before tile x (0 <= x <= nv), and of row rb in pass p
+  auto rowpre = [&](int rb, int x) -> int {
+    const int wl = x >> 5;
+    if (wl >= cwd) return pre[rb * cwd + cwd - 1] + __builtin_popcount(bm[rb * cwd + cwd - 1]);
+    return pre[rb * cwd + wl] + __builtin_popcount(bm[rb * cwd + wl] & ((1u << (x & 31)) - 1u));
+  };
+  auto pcnt = [&](int p, int rb) { return rowpre(rb, pvt[p + 1]) - rowpre(rb, pvt[p]); };
+
+  // First slot of every (pass, token block): an exclusive scan in that order; and
+  // the most kept tiles of one block in each pass (hist, before it holds kbp).
+  const int I = npass * nrb;
+  for (int p = tid; p < npass; p += 1024) hist[p] = 0;
+  {
+    const int per = (I + 1023) >> 10;
+    const int i0 = min(I, tid * per), i1 = min(I, i0 + per);
+    int sum = 0;
+    for (int i = i0; i < i1; ++i) sum += pcnt(i / nrb, i % nrb);
+    int tot;
+    int pos = block_excl_scan(sum, wsum, tot);  // its barriers order the zeroing of hist before the maxima
+    for (int i = i0; i < i1; ++i) {
+      const int c = pcnt(i / nrb, i % nrb);
+      a.rb_start[i] = pos;
+      if (I <= kRbsLds) rbs_l[i] = pos;
+      atomicMax(&hist[i / nrb], c);
+      pos += c;
+    }
+  }
+  for (int i = I + tid; i <= maxp * nrb; i += 1024) a.rb_start[i] = kept;
+  if (tid == 0 && I <= kRbsLds) rbs_l[I] = kept;
+  __syncthreads();
+  auto rbs = [&](int i) { return I <= kRbsLds ? rbs_l[i] : a.rb_start[i]; };  // i <= I
+  auto slot_of = [&](int p, int rb, int v) { return rbs(p * nrb + rb) + rowpre(rb, v) - rowpre(rb, pvt[p]); };
+
+  // slot lists
   for (int e = tid; e < E; e += 1024) {
     uint32_t x = bm[e];
-    int sl = pre[e];
     const int rb = e / cwd;
     const int vb = (e - rb * cwd) * 32;
     while (x) {
-      const int b = __builtin_ctz(x);
+      const int v = vb + __builtin_ctz(x);
       x &= x - 1u;
-      a.slot_vt[sl] = vb + b;
+      const int sl = slot_of(pass_of(v), rb, v);
+      a.slot_vt[sl] = v;
       a.slot_rb[sl] = rb;
-      ++sl;
     }
   }
+  // per vocab tile: its kept token blocks, ascending, as slots
+  for (int v = tid; v < nv; v += 1024) {
+    a.vt_start[v] = vpre[v];
+    const int p = pass_of(v);
+    const int wl = v >> 5, bit = v & 31;
+    int q = vpre[v];
+    for (int rb = 0; rb < nrb; ++rb)
+      if ((bm[rb * cwd + wl] >> bit) & 1u) a.vt_slot[q++] = slot_of(p, rb, v);
+  }
+  if (tid == 0) a.vt_start[nv] = kept;
 
-  // G tasks: runs of at most 4 consecutive slots of one token block, ordered by run
-  // index first and token block second.  Tasks that run at the same time then read
+  // G tasks: runs of at most 4 consecutive slots of one (pass, token block), ordered by
+  // pass, then run index, then token block.  Tasks that run at the same time then read
   // the same vocabulary tiles when the lists are dense, and every block's first run
-  // (its lowest, most shared tiles) is taken early.  Thread k (one per run index,
-  // kb <= 1024 of them) counts the blocks with more than k runs, the counts are
-  // scanned, and thread k writes its column.
-  const int kb = (nv + 3) >> 2;
-  int colc = 0;
-  if (tid < kb)
-    for (int rb = 0; rb < nrb; ++rb) colc += ((pre[(rb + 1) * cwd] - pre[rb * cwd] + 3) >> 2) > tid;
+  // (its lowest, most shared tiles) is taken early.  Item (p, k) -- run index k of
+  // pass p, k < ceil(most kept tiles of a block in the pass / 4), at least one item
+  // per pass -- counts the blocks with more than k runs; the counts are scanned and
+  // every item writes its column.
+  {
+    const int pp = (npass + 1023) >> 10;
+    const int p0 = min(npass, tid * pp), p1 = min(npass, p0 + pp);
+    int kb[4];  // this thread's passes' item counts (pp <= 4: npass <= 4096)
+    int sum = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      kb[q] = p0 + q < p1 ? max(1, (hist[p0 + q] + 3) >> 2) : 0;
+      sum += kb[q];
+    }
+    int J;
+    int pos = block_excl_scan(sum, wsum, J);  // its barriers order the reads of hist before the writes of kbp
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if (p0 + q < p1) kbp[p0 + q] = pos;
+      pos += kb[q];
+    }
+    if (tid == 0) kbp[npass] = J;
+  }
+  __syncthreads();
+  const int J = kbp[npass];
+  auto item_pass = [&](int j) {  // the pass p < npass with kbp[p] <= j < kbp[p + 1]
+    int lo = 0, hi = npass - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (kbp[mid] <= j) lo = mid; else hi = mid - 1;
+    }
+    return lo;
+  };
   int ntask;
-  int tb = block_excl_scan(colc, wsum, ntask);
-  if (tid < kb) {
-    for (int rb = 0; rb < nrb; ++rb) {
-      const int first = pre[rb * cwd];
-      if (((pre[(rb + 1) * cwd] - first + 3) >> 2) > tid) {
-        a.g_task[tb] = first + 4 * tid;
-        a.g_task_rb[tb] = rb;
-        ++tb;
+  {
+    const int pj = (J + 1023) >> 10;
+    const int j0 = min(J, tid * pj), j1 = min(J, j0 + pj);
+    int cnt = 0;
+    for (int j = j0; j < j1; ++j) {
+      const int p = item_pass(j), k4 = 4 * (j - kbp[p]);
+      int prev = rbs(p * nrb);
+      for (int rb = 0; rb < nrb; ++rb) {
+        const int next = rbs(p * nrb + rb + 1);
+        cnt += next - prev > k4 ? 1 : 0;
+        prev = next;
+      }
+    }
+    int tb = block_excl_scan(cnt, wsum, ntask);
+    for (int j = j0; j < j1; ++j) {
+      const int p = item_pass(j), k4 = 4 * (j - kbp[p]);
+      if (k4 == 0) {  // the pass's first item: its tasks start here
+        a.pinfo[p * kPassInts + kPiTask0] = tb;
+        if (p > 0) a.pinfo[(p - 1) * kPassInts + kPiTask1] = tb;
+      }
+      int prev = rbs(p * nrb);
+      for (int rb = 0; rb < nrb; ++rb) {
+        const int next = rbs(p * nrb + rb + 1);
+        if (next - prev > k4) {
+          a.g_task[tb] = prev + k4;
+          a.g_task_rb[tb] = rb;
+          ++tb;
+        }
+        prev = next;
       }
     }
   }
+  if (tid == 0) a.pinfo[(npass - 1) * kPassInts + kPiTask1] = ntask;
 
-  // per vocab tile: kept token blocks, ascending, as slots
-  const int pv = (nv + 1023) >> 10;
-  const int v0 = min(nv, tid * pv), v1 = min(nv, v0 + pv);
-  int vs = 0;
-  for (int v = v0; v < v1; ++v) {
-    const int wl = v >> 5, bit = v & 31;
-    int c = 0;
-    for (int rb = 0; rb < nrb; ++rb) c += (bm[rb * cwd + wl] >> bit) & 1u;
-    vcnt[v] = c;
-    vs += c;
-  }
-  int vtot;
-  int vp = block_excl_scan(vs, wsum, vtot);
-  for (int v = v0; v < v1; ++v) {
-    a.vt_start[v] = vp;
-    const int wl = v >> 5, bit = v & 31;
-    const uint32_t low = (1u << bit) - 1u;
-    int p = vp;
-    for (int rb = 0; rb < nrb; ++rb) {
-      const uint32_t x = bm[rb * cwd + wl];
-      if ((x >> bit) & 1u) a.vt_slot[p++] = pre[rb * cwd + wl] + __builtin_popcount(x & low);
+  // the owners of every pass's sums, most kept tiles first
+  for (int p = 0; p < npass; ++p) {
+    const int n_rb = order_by_size(nrb, [&](int rb) { return rbs(p * nrb + rb + 1) - rbs(p * nrb + rb); },
+                                   a.own_rb + (size_t)p * nrb, 0, hist, wsum);
+    const int vt0 = pvt[p];
+    const int n_vt = order_by_size(pvt[p + 1] - vt0, [&](int i) { return vpre[vt0 + i + 1] - vpre[vt0 + i]; },
+                                   a.own_vt + vt0, vt0, hist, wsum);
+    if (tid == 0) {
+      a.pinfo[p * kPassInts + kPiOwnRb] = n_rb;
+      a.pinfo[p * kPassInts + kPiOwnVt] = n_vt;
     }
-    vp += vcnt[v];
   }
-  // (the barriers of the scan above made every vcnt entry visible)
-  const int n_own_rb = order_by_size(nrb, [&](int rb) { return pre[(rb + 1) * cwd] - pre[rb * cwd]; }, a.own_rb, hist, wsum);
-  const int n_own_vt = order_by_size(nv, [&](int v) { return vcnt[v]; }, a.own_vt, hist, wsum);
-  if (tid == 0) {
-    a.counts[4] = n_own_rb;
-    a.counts[5] = n_own_vt;
-    a.vt_start[nv] = vtot;
-    a.counts[0] = kept;
-    a.counts[1] = ntask;
-    a.counts[2] = 0;  // next owner-without-kept-tiles item (taken by the G kernel's tail)
-    if (a.tile_stats) {  // [2]: already set from the whole bitmap when the sorted order was available
-      if (chunk == 0) {
-        a.tile_stats[0] = kept;
-        a.tile_stats[1] = a.plan.total;
-        if (!a.perm) a.tile_stats[2] = kept;
-      } else {
-        a.tile_stats[0] += kept;
-        if (!a.perm) a.tile_stats[2] += kept;
-      }
+  // the rest of the pass table
+  const bool multi = a.plan.n_chunks > 1 || npass > 1;
+  const int last_chunk = (int)a.plan.n_chunks - 1;
+  for (int p = tid; p < maxp; p += 1024) {
+    int* pi = a.pinfo + p * kPassInts;
+    pi[kPiTail] = 0;
+    if (p < npass) {
+      pi[kPiVt0] = pvt[p];
+      pi[kPiVt1] = pvt[p + 1];
+      pi[kPiS0] = rbs(p * nrb);
+      pi[kPiS1] = rbs((p + 1) * nrb);
+      pi[kPiDeMode] = !multi ? kWriteT
+                             : (chunk == 0 && p == 0) ? kStoreF32
+                                                      : (chunk == last_chunk && p == npass - 1) ? kFinishT : kAddF32;
+    } else {
+      pi[kPiVt0] = nv;
+      pi[kPiVt1] = nv;
+      pi[kPiS0] = kept;
+      pi[kPiS1] = kept;
+      pi[kPiTask0] = ntask;
+      pi[kPiTask1] = ntask;
+      pi[kPiOwnRb] = 0;
+      pi[kPiOwnVt] = 0;
+      pi[kPiDeMode] = -1;
+    }
+  }
+  if (tid == 0 && a.tile_stats) {  // [2]: already set from the whole bitmap when the sorted order was available
+    if (chunk == 0) {
+      a.tile_stats[0] = kept;
+      a.tile_stats[1] = a.plan.total;
+      if (!a.perm) a.tile_stats[2] = kept;
+    } else {
+      a.tile_stats[0] += kept;
+      if (!a.perm) a.tile_stats[2] += kept;
     }
   }
 }
 
 // ---------------------------------------------------------------- 3. owners without kept tiles
-// Item o: token block rb = o < nrb (dE rows), then the chunk's vocab tiles (dC
-// rows).  With one chunk, an empty owner's rows are zero.  With several, dE goes
-// through the fp32 carry: the first chunk zeroes an empty block's carry rows, the
-// last converts them to the output dtype (blocks with kept tiles are stored / added
-// / finished by the dE sums themselves).  NT threads work on one item.  The G
-// kernel's workgroups take these items once they run out of G tasks.
+// Item o of a pass: token block rb = o < nrb (dE rows), then the pass's vocab tiles
+// (dC rows).  In the pass's dE write mode, a block without kept tiles in the pass
+// gets zero dE rows (kWriteT: one pass over everything), zero carry rows (kStoreF32:
+// the first pass), its carry converted to the output dtype (kFinishT: the last
+// pass), or nothing (kAddF32); blocks with kept tiles are stored / added / finished by
+// the dE sums themselves.  A vocab tile of the pass without kept blocks gets zero dC
+// rows.  NT threads work on one item.  The G kernel's workgroups take these items
+// once they run out of G tasks.
 template <typename T, int NT>
-__device__ __forceinline__ void empty_owner(const BwdArgs& a, int chunk, int o) {
-  const int nrb = (int)a.plan.nrb, nvt = (int)a.plan.nvt;
+__device__ __forceinline__ void empty_owner(const BwdArgs& a, int chunk, int pass, int o) {
+  const int nrb = (int)a.plan.nrb;
+  const int* pi = a.pinfo + pass * kPassInts;
   const int vlo = chunk * (int)a.plan.chunk_nvt;
-  const int nv = min(nvt, vlo + (int)a.plan.chunk_nvt) - vlo;
   const int64_t D = a.D;
   if (o < nrb) {
-    if (!a.dE || ldu(a.rb_start, o + 1) != ldu(a.rb_start, o)) return;
-    const bool multi = a.plan.n_chunks > 1;
-    const bool first = chunk == 0, last = chunk == (int)a.plan.n_chunks - 1;
-    if (multi && !first && !last) return;
+    if (!a.dE || ldu(a.rb_start, pass * nrb + o + 1) != ldu(a.rb_start, pass * nrb + o)) return;
+    const int mode = ldu(pi, kPiDeMode);
+    if (mode == kAddF32) return;
     const int64_t row0 = (int64_t)o * kBwdTokens;
     const int64_t nrows = a.N - row0 < kBwdTokens ? a.N - row0 : kBwdTokens;
     const int* map = row_data(a).map;  // dE row of each row of the block (null: the same)
     T* dE = reinterpret_cast<T*>(a.dE);
-    if (!multi) {
+    if (mode == kWriteT) {
       for (int64_t r = 0; r < nrows; ++r) {
         T* out = dE + (map ? (int64_t)map[row0 + r] : row0 + r) * D;
         for (int64_t i = (int64_t)threadIdx.x * (16 / sizeof(T)); i < D; i += NT * (16 / sizeof(T)))
           *reinterpret_cast<u32x4*>(out + i) = u32x4{0u, 0u, 0u, 0u};
       }
-    } else if (first) {
+    } else if (mode == kStoreF32) {
       float* acc = a.de_acc + row0 * D;
       for (int64_t i = (int64_t)threadIdx.x * 4; i < nrows * D; i += NT * 4)
         *reinterpret_cast<f32x4*>(acc + i) = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -683,8 +813,8 @@ __device__ __forceinline__ void empty_owner(const BwdArgs& a, int chunk, int o) 
     }
     return;
   }
-  const int v = o - nrb;
-  if (v >= nv || !a.dC || ldu(a.vt_start, v + 1) != ldu(a.vt_start, v)) return;
+  const int v = ldu(pi, kPiVt0) + (o - nrb);
+  if (v >= ldu(pi, kPiVt1) || !a.dC || ldu(a.vt_start, v + 1) != ldu(a.vt_start, v)) return;
   const int64_t row0 = (int64_t)(vlo + v) * kBwdVocab;
   const int64_t n = (a.V - row0 < kBwdVocab ? a.V - row0 : kBwdVocab) * D;
   T* out = reinterpret_cast<T*>(a.dC) + row0 * D;
@@ -703,17 +833,19 @@ __host__ __device__ inline int dc_bins(int nwg, int nds) {
   return nds <= nwg ? (nwg / nds < kMaxDcBins ? nwg / nds : kMaxDcBins) : 0;
 }
 
-// Longest-processing-time-first dealing of the dC owners (own_vt: most kept blocks
-// first) to nbins bins: each owner goes to the bin with the least work so far.
+// Longest-processing-time-first dealing of the dC owners of a pass (own_vt: most kept
+// blocks first) to nbins bins: each owner goes to the bin with the least work so far.
 // Owners of equal size form a batch: the bins are ranked once by (work, index) and
 // owner t of the batch goes to the bin of rank t % nbins -- what dealing them one
 // at a time does, since equal additions keep the ranking.  A bin lists its owners
 // in dealing order.  Run by one workgroup of NT threads; smem holds its tables.
 template <int NT>
-__device__ void dc_schedule(const BwdArgs& a, int nbins, char* smem) {
+__device__ void dc_schedule(const BwdArgs& a, int pass, int nbins, char* smem) {
   constexpr int NW = NT / 64;
   const int tid = threadIdx.x;
-  const int n = a.counts[5];
+  const int* pi = a.pinfo + pass * kPassInts;
+  const int n = ldu(pi, kPiOwnVt);
+  const int* own_vt = a.own_vt + ldu(pi, kPiVt0);
   int* sz = reinterpret_cast<int*>(smem);  // [n] kept blocks of owner i
   int* bst = sz + kCompactMaxVt;           // [batches + 1] first owner of each batch
   int* bin = bst + kCompactMaxVt + 1;      // [n] bin of owner i
@@ -723,7 +855,7 @@ __device__ void dc_schedule(const BwdArgs& a, int nbins, char* smem) {
   int* byrank = cnt + kMaxDcBins;          // [nbins] bin of each rank
   int* wsum = byrank + kMaxDcBins;         // [NW]
   for (int i = tid; i < n; i += NT) {
-    const int v = a.own_vt[i];
+    const int v = own_vt[i];
     sz[i] = a.vt_start[v + 1] - a.vt_start[v];
   }
   for (int b = tid; b < kMaxDcBins; b += NT) {
@@ -778,7 +910,7 @@ __device__ void dc_schedule(const BwdArgs& a, int nbins, char* smem) {
     a.dc_bin_start[nbins] = acc;
   }
   __syncthreads();
-  for (int i = tid; i < n; i += NT) a.dc_bin_owner[work[bin[i]] + pos[i]] = a.own_vt[i];
+  for (int i = tid; i < n; i += NT) a.dc_bin_owner[work[bin[i]] + pos[i]] = own_vt[i];
 }
 
 // ---------------------------------------------------------------- 4. G tiles
@@ -803,14 +935,19 @@ using GLoop = NTMainLoop<T, 4 * kBwdVocab, kBwdTokens, 4, 2, kGSlice, kGStages>;
 constexpr int kGThreads = GLoop<__bf16>::NTHREADS;
 
 template <typename T, bool HAS_BIAS, bool WANT_G, bool WANT_DB, bool RAGGED>
-__global__ __launch_bounds__(kGThreads, 1) void bwd_g_kernel(BwdArgs a, int chunk) {
+__global__ __launch_bounds__(kGThreads, 1) void bwd_g_kernel(BwdArgs a, int chunk, int pass) {
   using Loop = GLoop<T>;
   static_assert(Loop::NTHREADS == kGThreads, "one launch shape for every dtype");
   constexpr int TI = Loop::TI, TJ = Loop::TJ;
   static_assert(TI == 4 && TJ == 2, "wave tile: one vocab tile x 64 tokens");
   __shared__ __attribute__((aligned(16))) char smem[Loop::SMEM_BYTES];
   constexpr int ES = sizeof(T);
-  const int ntask = ldu(a.counts, 1);
+  const int* pi = a.pinfo + pass * kPassInts;
+  if (ldu(pi, kPiDeMode) < 0) return;  // past the passes the data needs
+  const int task0 = ldu(pi, kPiTask0);
+  const int ntask = ldu(pi, kPiTask1) - task0;
+  const int s0 = ldu(pi, kPiS0);  // the scratch holds slot s at s - s0
+  const int* rb_start = a.rb_start + pass * (int)a.plan.nrb;
   const int vlo = chunk * (int)a.plan.chunk_nvt;
   const int xcd = (int)(blockIdx.x & 7), lidx = (int)(blockIdx.x >> 3), nper = (int)(gridDim.x >> 3);
   const int lane = threadIdx.x & 63;
@@ -829,9 +966,9 @@ __global__ __launch_bounds__(kGThreads, 1) void bwd_g_kernel(BwdArgs a, int chun
     int64_t seg[4];
   };
   auto load_task = [&](int t, Task& k) {
-    k.s0 = ldu(a.g_task, t);
-    k.rb = ldu(a.g_task_rb, t);
-    k.cnt = min(4, ldu(a.rb_start, k.rb + 1) - k.s0);
+    k.s0 = ldu(a.g_task, task0 + t);
+    k.rb = ldu(a.g_task_rb, task0 + t);
+    k.cnt = min(4, ldu(rb_start, k.rb + 1) - k.s0);
 #pragma unroll
     for (int i = 0; i < 4; ++i) k.seg[i] = (int64_t)(vlo + ldu(a.slot_vt, k.s0 + (i < k.cnt ? i : k.cnt - 1))) * kBwdVocab;
   };
@@ -840,29 +977,28 @@ __global__ __launch_bounds__(kGThreads, 1) void bwd_g_kernel(BwdArgs a, int chun
   };
   auto prefetch = [&](const typename Loop::template Src<4>& src) { Loop::template prefetch<RAGGED>(src, smem); };
 
-  // Once out of tasks, the workgroup takes items from a counter the compaction
-  // kernel reset (only when dE or dC is wanted): first the dC schedule (when dC is
-  // wanted), then the owners without kept tiles, whose rows it zeroes (dC rows only
-  // when dC did not come zeroed).
+  // Once out of tasks, the workgroup takes items from the pass's counter, which the
+  // compaction kernel reset (only when dE or dC is wanted): first the dC schedule
+  // (when dC is wanted), then the owners without kept tiles in the pass, whose rows it
+  // zeroes or finishes (dC rows only when dC did not come zeroed).
   auto tail = [&]() {
     if constexpr (WANT_G) {
       const int sched = a.dC != nullptr ? 1 : 0;
       // dC rows of vocab tiles without kept tiles need zeros unless dC came zeroed
-      const int nitems = sched + (int)a.plan.nrb +
-                         (a.dc_zeroed ? 0 : min((int)a.plan.nvt, vlo + (int)a.plan.chunk_nvt) - vlo);
+      const int nitems = sched + (int)a.plan.nrb + (a.dc_zeroed ? 0 : ldu(pi, kPiVt1) - ldu(pi, kPiVt0));
       int* box = reinterpret_cast<int*>(smem);
       for (;;) {
         __syncthreads();  // box (and smem) free
-        if (threadIdx.x == 0) box[0] = atomicAdd(&a.counts[2], 1);
+        if (threadIdx.x == 0) box[0] = atomicAdd(&a.pinfo[pass * kPassInts + kPiTail], 1);
         __syncthreads();
         const int o = box[0];
         if (o >= nitems) break;
         if (o < sched) {
           const int nds = (int)((a.D + kDcSliceCols - 1) / kDcSliceCols);
           const int nb = dc_bins((int)gridDim.x, nds);
-          dc_schedule<kGThreads>(a, nb > 0 ? nb : 1, smem + 256);  // its tables start past box
+          dc_schedule<kGThreads>(a, pass, nb > 0 ? nb : 1, smem + 256);  // its tables start past box
         } else {
-          empty_owner<T, kGThreads>(a, chunk, o - sched);
+          empty_owner<T, kGThreads>(a, chunk, pass, o - sched);
         }
       }
     }
@@ -929,7 +1065,7 @@ __global__ __launch_bounds__(kGThreads, 1) void bwd_g_kernel(BwdArgs a, int chun
       // 32-column block i at a time: form its 32 G values per lane, store them
       // token-major (4 consecutive vocab columns per store), add their column sums.
       const __amdgpu_buffer_rsrc_t grs = __builtin_amdgcn_make_buffer_rsrc(
-          a.gtile + (size_t)slot * a.plan.g_bytes, (short)0, (int)a.plan.g_bytes, 0x00020000);
+          a.gtile + (size_t)(slot - s0) * a.plan.g_bytes, (short)0, (int)a.plan.g_bytes, 0x00020000);
 #pragma unroll
       for (int i = 0; i < TI; ++i) {
         float gv[TJ][16];
@@ -1006,7 +1142,7 @@ __global__ __launch_bounds__(kGThreads, 1) void bwd_g_kernel(BwdArgs a, int chun
       // fills until the next task's main loop has passed its first barrier)
       __syncthreads();
       if (active && wb == 0) {
-        float* cs = a.colsum + (size_t)slot * kBwdVocab;
+        float* cs = a.colsum + (size_t)(slot - s0) * kBwdVocab;
         for (int c = lane; c < kBwdVocab; c += 64) cs[c] = red[wa * kBwdVocab + c] + red[(4 + wa) * kBwdVocab + c];
       }
       __syncthreads();
@@ -1144,9 +1280,8 @@ __device__ __forceinline__ void dma16_s(const char* sbase, uint32_t voff, uint32
                : "memory", "m0");
 }
 
-// Output of a finished dE / dC task: kWriteT stores the output dtype (single chunk,
-// and always for dC); the fp32 modes carry dE between chunks.
-enum WriteMode { kWriteT = 0, kStoreF32 = 1, kAddF32 = 2, kFinishT = 3 };
+// Output of a finished dE / dC task: kWriteT stores the output dtype (one pass over
+// everything, and always for dC); the fp32 modes carry dE between passes (WriteMode).
 
 // Persistent owner-computes sums.  PHASE 0 (dE): owner = token block rb, tiles =
 // its slots rb_start[rb] .. rb_start[rb + 1]; A-side rows = C rows of each slot's
@@ -1166,25 +1301,27 @@ enum WriteMode { kWriteT = 0, kStoreF32 = 1, kAddF32 = 2, kFinishT = 3 };
 // wave-uniform base plus a per-lane constant computed once: DMA sources in the
 // saddr form, fragment reads as constant LDS offsets.
 template <typename T, int PHASE>
-__global__ __launch_bounds__(SumGeo<T>::NT, 1) void bwd_sum_kernel(BwdArgs a, int chunk) {
+__global__ __launch_bounds__(SumGeo<T>::NT, 1) void bwd_sum_kernel(BwdArgs a, int chunk, int pass) {
   using S = SumGeo<T>;
   __shared__ __attribute__((aligned(16))) char smem[S::STAGES * S::STAGE];
   constexpr int ES = S::ES;
   const int nrb = (int)a.plan.nrb, nds = (int)((a.D + S::DN - 1) / S::DN);
   const int vlo = chunk * (int)a.plan.chunk_nvt;
-  const int nv = min((int)a.plan.nvt, vlo + (int)a.plan.chunk_nvt) - vlo;
   const int xcd = (int)(blockIdx.x & 7), lidx = (int)(blockIdx.x >> 3), nper = (int)(gridDim.x >> 3);
-  const int ntasks = ldu(a.counts, PHASE == 0 ? 4 : 5) * nds;
-  const int* own = PHASE == 0 ? a.own_rb : a.own_vt;
+  const int* pi = a.pinfo + pass * kPassInts;
+  const int pmode = ldu(pi, kPiDeMode);
+  if (pmode < 0) return;  // past the passes the data needs
+  const int s0 = ldu(pi, kPiS0);  // the G scratch holds slot s at s - s0
+  const int ntasks = ldu(pi, PHASE == 0 ? kPiOwnRb : kPiOwnVt) * nds;
+  const int* own = PHASE == 0 ? a.own_rb + pass * nrb : a.own_vt + ldu(pi, kPiVt0);
+  const int* ostart = PHASE == 0 ? a.rb_start + pass * nrb : a.vt_start;  // an owner's slots / vt_slot entries
   const int vwg = xcd * nper + lidx, nwg = (int)gridDim.x;  // workgroups numbered XCD-major
   const int64_t D = a.D;
   const int64_t pitch = D * ES;
   const RowData rd = row_data(a);
   const char* X = PHASE == 0 ? reinterpret_cast<const char*>(a.c) : rd.e;
   const int64_t xrows = PHASE == 0 ? a.V : a.N;
-  const int mode = (PHASE == 0 && a.plan.n_chunks > 1)
-                       ? (chunk == 0 ? kStoreF32 : (chunk == (int)a.plan.n_chunks - 1 ? kFinishT : kAddF32))
-                       : kWriteT;
+  const int mode = PHASE == 0 ? pmode : kWriteT;
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1238,12 +1375,12 @@ __global__ __launch_bounds__(SumGeo<T>::NT, 1) void bwd_sum_kernel(BwdArgs a, in
     const int p = q * nwg + ((q & 1) ? nwg - 1 - vwg : vwg);
     if (p >= ntasks) return false;
     const int owner = ldu(own, p / nds);
-    const int b = ldu(PHASE == 0 ? a.rb_start : a.vt_start, owner);
+    const int b = ldu(ostart, owner);
     c.q = q;
     c.owner = owner;
     c.ds = p - (p / nds) * nds;
     c.b = b;
-    c.cnt = ldu(PHASE == 0 ? a.rb_start : a.vt_start, owner + 1) - b;
+    c.cnt = ldu(ostart, owner + 1) - b;
     c.j = 0;
     c.h = 0;
     return true;
@@ -1290,7 +1427,8 @@ __global__ __launch_bounds__(SumGeo<T>::NT, 1) void bwd_sum_kernel(BwdArgs a, in
         dma16(src, sb + (wave * S::XLW + j) * 1024);
       }
     }
-    const char* gbase = a.gtile + (size_t)c.slot * a.plan.g_bytes + (PHASE == 0 ? c.h * 128 : c.h * S::KS * S::GTP);
+    const char* gbase =
+        a.gtile + (size_t)(c.slot - s0) * a.plan.g_bytes + (PHASE == 0 ? c.h * 128 : c.h * S::KS * S::GTP);
 #pragma unroll
     for (int j = 0; j < S::GLW; ++j) dma16_s(gbase, goff[j], sb + S::X_BYTES + (wave * S::GLW + j) * 1024);
   };
@@ -1491,16 +1629,20 @@ __global__ __launch_bounds__(SumGeo<T>::NT, 1) void bwd_sum_kernel(BwdArgs a, in
 
 // As bwd_sum_kernel, in the narrow geometry (one 4-wave pipeline of 48 KiB stages).
 template <typename T, int PHASE>
-__global__ __launch_bounds__(kThreads, 1) void bwd_sum_narrow_kernel(BwdArgs a, int chunk) {
+__global__ __launch_bounds__(kThreads, 1) void bwd_sum_narrow_kernel(BwdArgs a, int chunk, int pass) {
   using S = SumGeoNarrow<T>;
   __shared__ __attribute__((aligned(16))) char smem[S::STAGES * S::STAGE];
   constexpr int ES = S::ES;
   const int nrb = (int)a.plan.nrb, nds = (int)((a.D + S::DN - 1) / S::DN);
   const int vlo = chunk * (int)a.plan.chunk_nvt;
-  const int nv = min((int)a.plan.nvt, vlo + (int)a.plan.chunk_nvt) - vlo;
   const int xcd = (int)(blockIdx.x & 7), lidx = (int)(blockIdx.x >> 3), nper = (int)(gridDim.x >> 3);
-  const int ntasks = ldu(a.counts, PHASE == 0 ? 4 : 5) * nds;
-  const int* own = PHASE == 0 ? a.own_rb : a.own_vt;
+  const int* pi = a.pinfo + pass * kPassInts;
+  const int pmode = ldu(pi, kPiDeMode);
+  if (pmode < 0) return;  // past the passes the data needs
+  const int s0 = ldu(pi, kPiS0);  // the G scratch holds slot s at s - s0
+  const int ntasks = ldu(pi, PHASE == 0 ? kPiOwnRb : kPiOwnVt) * nds;
+  const int* own = PHASE == 0 ? a.own_rb + pass * nrb : a.own_vt + ldu(pi, kPiVt0);
+  const int* ostart = PHASE == 0 ? a.rb_start + pass * nrb : a.vt_start;  // an owner's slots / vt_slot entries
   const int vwg = xcd * nper + lidx, nwg = (int)gridDim.x;  // workgroups numbered XCD-major
   // dC: this workgroup's bin of the schedule the G kernel dealt, and its first D slice
   static_assert(PHASE == 0 || S::DN == kDcSliceCols, "the dC schedule assumes this slice width");
@@ -1515,9 +1657,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_narrow_kernel(BwdArgs a, 
   const RowData rd = row_data(a);
   const char* X = PHASE == 0 ? reinterpret_cast<const char*>(a.c) : rd.e;
   const int64_t xrows = PHASE == 0 ? a.V : a.N;
-  const int mode = (PHASE == 0 && a.plan.n_chunks > 1)
-                       ? (chunk == 0 ? kStoreF32 : (chunk == (int)a.plan.n_chunks - 1 ? kFinishT : kAddF32))
-                       : kWriteT;
+  const int mode = PHASE == 0 ? pmode : kWriteT;
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1581,12 +1721,12 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_narrow_kernel(BwdArgs a, 
       if (ds >= nds) return false;
       owner = ldu(a.dc_bin_owner, bstart + (q - t * bcnt));
     }
-    const int b = ldu(PHASE == 0 ? a.rb_start : a.vt_start, owner);
+    const int b = ldu(ostart, owner);
     c.q = q;
     c.owner = owner;
     c.ds = ds;
     c.b = b;
-    c.cnt = ldu(PHASE == 0 ? a.rb_start : a.vt_start, owner + 1) - b;
+    c.cnt = ldu(ostart, owner + 1) - b;
     c.j = 0;
     c.h = 0;
     return true;
@@ -1633,7 +1773,8 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_narrow_kernel(BwdArgs a, 
         dma16(src, sb + (wave * S::XLW + j) * 1024);
       }
     }
-    const char* gbase = a.gtile + (size_t)c.slot * a.plan.g_bytes + (PHASE == 0 ? c.h * 128 : c.h * S::KS * S::GTP);
+    const char* gbase =
+        a.gtile + (size_t)(c.slot - s0) * a.plan.g_bytes + (PHASE == 0 ? c.h * 128 : c.h * S::KS * S::GTP);
 #pragma unroll
     for (int j = 0; j < S::GLW; ++j) dma16_s(gbase, goff[j], sb + S::X_BYTES + (wave * S::GLW + j) * 1024);
   };
@@ -1828,28 +1969,29 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_narrow_kernel(BwdArgs a, 
 }
 
 // ---------------------------------------------------------------- 6. dBias
-// One workgroup per vocab tile of the chunk: the sum of its slots' column sums.
+// One workgroup per vocab tile of the pass: the sum of its slots' column sums.
 template <typename T>
-__global__ __launch_bounds__(kBwdVocab) void bwd_dbias_kernel(BwdArgs a, int chunk) {
+__global__ __launch_bounds__(kBwdVocab) void bwd_dbias_kernel(BwdArgs a, int chunk, int pass) {
+  const int* pi = a.pinfo + pass * kPassInts;
   const int vlo = chunk * (int)a.plan.chunk_nvt;
-  const int nv = min((int)a.plan.nvt, vlo + (int)a.plan.chunk_nvt) - vlo;
-  const int v = (int)blockIdx.x;
-  if (v >= nv) return;
+  const int v = ldu(pi, kPiVt0) + (int)blockIdx.x;
+  if (v >= ldu(pi, kPiVt1)) return;
+  const int s0 = ldu(pi, kPiS0);
   const int b = ldu(a.vt_start, v), e = ldu(a.vt_start, v + 1);
   float sum = 0.f;
-  for (int k = b; k < e; ++k) sum += a.colsum[(size_t)ldu(a.vt_slot, k) * kBwdVocab + threadIdx.x];
+  for (int k = b; k < e; ++k) sum += a.colsum[(size_t)(ldu(a.vt_slot, k) - s0) * kBwdVocab + threadIdx.x];
   const int64_t col = (int64_t)(vlo + v) * kBwdVocab + threadIdx.x;
   if (col < a.V) reinterpret_cast<T*>(a.dBias)[col] = (T)sum;
 }
 
 // ---------------------------------------------------------------- launch
 template <typename T, bool HB>
-static void launch_g(const BwdArgs& a, int chunk, dim3 grid, hipStream_t s) {
+static void launch_g(const BwdArgs& a, int chunk, int pass, dim3 grid, hipStream_t s) {
   const bool g = a.dE != nullptr || a.dC != nullptr, db = a.dBias != nullptr;
   const bool rg = (a.D * (int64_t)sizeof(T)) % kGSlice != 0;
 #define CCE_G(G, DB, RG)                                                                               \
   if (g == G && db == DB && rg == RG) {                                                                \
-    hipLaunchKernelGGL((bwd_g_kernel<T, HB, G, DB, RG>), grid, dim3(kGThreads), 0, s, a, chunk);       \
+    hipLaunchKernelGGL((bwd_g_kernel<T, HB, G, DB, RG>), grid, dim3(kGThreads), 0, s, a, chunk, pass); \
     return;                                                                                            \
   }
   CCE_G(true, true, false)
@@ -1863,14 +2005,11 @@ static void launch_g(const BwdArgs& a, int chunk, dim3 grid, hipStream_t s) {
 
 // dE sums: the wide geometry (512 columns per task, measured 0.85x the time of two
 // narrow tasks) unless it leaves so few tasks that the narrow one finishes in fewer
-// rounds of equal tasks over the persistent grid.
-static bool use_wide_de_sums(const BwdPlan& P, int64_t D, int grid) {
-  // Test hook: CCE_TEST_DE_SUMS=wide|narrow forces a geometry.
-  if (const char* env = std::getenv("CCE_TEST_DE_SUMS")) {
-    if (env[0] == 'w') return true;
-    if (env[0] == 'n') return false;
-  }
-  const int64_t tw = P.nrb * ((D + 511) / 512), tn = P.nrb * ((D + 255) / 256);
+// rounds of equal tasks over the persistent grid.  a.de_geo forces one (1 wide, 2 narrow).
+static bool use_wide_de_sums(const BwdArgs& a, int grid) {
+  if (a.de_geo != 0) return a.de_geo == 1;
+  const BwdPlan& P = a.plan;
+  const int64_t tw = P.nrb * ((a.D + 511) / 512), tn = P.nrb * ((a.D + 255) / 256);
   const int64_t rw = (tw + grid - 1) / grid, rn = (tn + grid - 1) / grid;
   return rw * 512 * 85 < rn * 256 * 100;
 }
@@ -1878,13 +2017,9 @@ static bool use_wide_de_sums(const BwdPlan& P, int64_t D, int grid) {
 // dC sums: the narrow geometry suits the filtered backward (owners keep one or two
 // token blocks, so tasks are short); with the filter off every owner keeps all of its
 // token blocks and the wide geometry runs ~35% faster.  The kept counts are not known
-// on the host, so the choice follows the filter setting.
+// on the host, so the choice follows the filter setting.  a.dc_geo forces one.
 static bool use_wide_dc_sums(const BwdArgs& a) {
-  // Test hook: CCE_TEST_DC_SUMS=wide|narrow forces a geometry.
-  if (const char* env = std::getenv("CCE_TEST_DC_SUMS")) {
-    if (env[0] == 'w') return true;
-    if (env[0] == 'n') return false;
-  }
+  if (a.dc_geo != 0) return a.dc_geo == 1;
   return !(a.filter_log_eps > -INFINITY);
 }
 
@@ -1916,6 +2051,7 @@ static hipError_t backward_typed(const BwdArgs& a, hipStream_t s) {
   const int cus = a.num_cus > 0 ? a.num_cus : 256;
   const int gp = (cus + 7) / 8 * 8;  // persistent grids: a multiple of the 8 XCDs
   const int dtype = sizeof(T) == 4 ? 0 : (std::is_same<T, _Float16>::value ? 1 : 2);
+  const bool wide_de = use_wide_de_sums(a, gp), wide_dc = use_wide_dc_sums(a);
   for (int chunk = 0; chunk < (int)P.n_chunks; ++chunk) {
     const int vlo = chunk * (int)P.chunk_nvt;
     const int nv = (int)(P.nvt - vlo < P.chunk_nvt ? P.nvt - vlo : P.chunk_nvt);
@@ -1934,28 +2070,32 @@ static hipError_t backward_typed(const BwdArgs& a, hipStream_t s) {
     hipLaunchKernelGGL(bwd_compact_kernel, dim3(cg), dim3(1024), 0, s, a, chunk);
     if ((err = hipGetLastError()) != hipSuccess) return err;
     if (!(want_de || want_dc || want_db)) continue;
-    if (a.bias)
-      launch_g<T, true>(ac, chunk, dim3(gp), s);
-    else
-      launch_g<T, false>(ac, chunk, dim3(gp), s);
-    if ((err = hipGetLastError()) != hipSuccess) return err;
-    if (want_de) {
-      if (use_wide_de_sums(P, a.D, gp))
-        hipLaunchKernelGGL((bwd_sum_kernel<T, 0>), dim3(gp), dim3(SumGeo<T>::NT), 0, s, ac, chunk);
+    // Every pass the chunk may need; passes past the data's last return at once.
+    for (int pass = 0; pass < (int)P.max_passes; ++pass) {
+      if (a.bias)
+        launch_g<T, true>(ac, chunk, pass, dim3(gp), s);
       else
-        hipLaunchKernelGGL((bwd_sum_narrow_kernel<T, 0>), dim3(gp), dim3(SumGeoNarrow<T>::NT), 0, s, ac, chunk);
+        launch_g<T, false>(ac, chunk, pass, dim3(gp), s);
       if ((err = hipGetLastError()) != hipSuccess) return err;
-    }
-    if (want_dc) {
-      if (use_wide_dc_sums(a))
-        hipLaunchKernelGGL((bwd_sum_kernel<T, 1>), dim3(gp), dim3(SumGeo<T>::NT), 0, s, a, chunk);
-      else
-        hipLaunchKernelGGL((bwd_sum_narrow_kernel<T, 1>), dim3(gp), dim3(SumGeoNarrow<T>::NT), 0, s, a, chunk);
-      if ((err = hipGetLastError()) != hipSuccess) return err;
-    }
-    if (want_db) {
-      hipLaunchKernelGGL((bwd_dbias_kernel<T>), dim3((unsigned)nv), dim3(kBwdVocab), 0, s, a, chunk);
-      if ((err = hipGetLastError()) != hipSuccess) return err;
+      if (want_de) {
+        if (wide_de)
+          hipLaunchKernelGGL((bwd_sum_kernel<T, 0>), dim3(gp), dim3(SumGeo<T>::NT), 0, s, ac, chunk, pass);
+        else
+          hipLaunchKernelGGL((bwd_sum_narrow_kernel<T, 0>), dim3(gp), dim3(SumGeoNarrow<T>::NT), 0, s, ac, chunk,
+                             pass);
+        if ((err = hipGetLastError()) != hipSuccess) return err;
+      }
+      if (want_dc) {
+        if (wide_dc)
+          hipLaunchKernelGGL((bwd_sum_kernel<T, 1>), dim3(gp), dim3(SumGeo<T>::NT), 0, s, a, chunk, pass);
+        else
+          hipLaunchKernelGGL((bwd_sum_narrow_kernel<T, 1>), dim3(gp), dim3(SumGeoNarrow<T>::NT), 0, s, a, chunk, pass);
+        if ((err = hipGetLastError()) != hipSuccess) return err;
+      }
+      if (want_db) {
+        hipLaunchKernelGGL((bwd_dbias_kernel<T>), dim3((unsigned)nv), dim3(kBwdVocab), 0, s, a, chunk, pass);
+        if ((err = hipGetLastError()) != hipSuccess) return err;
+      }
     }
   }
   return hipGetLastError();

@@ -32,230 +32,6 @@ constexpr int kFwdWB = CCE_FWD_WB;
 template <typename T>
 using FwdLoop = NTMainLoop<T, kFwdVocab, kFwdTokens, 2, kFwdWB>;  // A = C rows (vocab), B = E rows (tokens)
 
-// ------------------------------------------------ E in MFMA fragment order
-// e_frag_kernel rewrites E so that one 32-byte K step of one 32-token block is
-// 1 KiB laid out exactly as the MFMA B operand wants it: lane l's 16 bytes are
-// row 32 b + l % 32, bytes [32 s + 16 (l / 32), +16) of that row.  Unit
-// ((b * KT * 4 + s) * 64 + l) * 16 of the copy holds them; rows past N and bytes
-// past the row end are zero.  A wave then loads its B fragments straight into
-// registers, 1 KiB contiguous per instruction, and only the C rows go through
-// the LDS.  Workgroup w copies slice w % KT of token block w / KT (32 rows x 128
-// bytes in, 4 KiB contiguous out).
-__global__ __launch_bounds__(256) void e_frag_kernel(const char* __restrict__ E, u32x4* __restrict__ out, int64_t N,
-                                                     int64_t row_bytes, uint32_t KT) {
-  const uint32_t w = blockIdx.x;
-  const uint32_t b = w / KT, kt = w - b * KT;
-  const int t = threadIdx.x;
-  const int lane = t & 63;
-  const int64_t row = (int64_t)b * 32 + (lane & 31);
-  const int64_t byte = (int64_t)kt * 128 + (t >> 6) * 32 + (lane >> 5) * 16;
-  u32x4 v = u32x4{0u, 0u, 0u, 0u};
-  if (row < N && byte < row_bytes) v = gld16(E + row * row_bytes + byte);
-  out[(size_t)w * 256 + t] = v;
-}
-
-// Main loop of the forward with the B operand (E rows) taken from the fragment
-// copy in registers and only the A operand (C rows) staged through the LDS.
-// Per 32-byte step a workgroup then moves 32 KiB of fragment reads and 8 KiB of
-// DMA writes through the LDS instead of 48 + 16 KiB.  Same wave layout and
-// accumulator layout as FwdLoop (waves 2 along the vocabulary x 4 along the
-// tokens, 128 x 64 per wave), same slice order, same MFMA sequence: results are
-// bit-identical to FwdLoop's.
-//
-// B fragments run 3 steps ahead in a ring of 4 slots (slot = step % 4): step g
-// issues the loads of step g + 3, then waits for its own.  Both the C DMA and
-// the B loads are inline assembly, so every vmcnt wait is explicit; each count
-// is the number of vector-memory instructions issued after the one awaited, in
-// program order (the pipeline fill issues the same pattern as the steady state):
-//   steps 0-2 of a slice: 10 (2 B steps, the slice's 4 DMA loads, 1 B step),
-//   step 3: 6 (3 B steps), stage barrier (DMA of the next slice): 8 with 2
-//   stages.  Other loads or stores issued in between only make a wait stricter.
-// The wait statements take the slot registers as in/out operands, so no use of
-// a slot can be scheduled above its wait.
-template <typename T>
-struct FwdFragLoop {
-  static constexpr int ROWS_A = kFwdVocab;
-  static constexpr int SLICE = 128;
-  static constexpr int STAGES = 2;
-  static constexpr int WA = 2, WB = kFwdWB, NW = WA * WB;
-  static constexpr int NTHREADS = 64 * NW;
-  static constexpr int TI = ROWS_A / WA / 32;
-  static constexpr int TJ = kFwdTokens / WB / 32;
-  static constexpr int RPL = 1024 / SLICE;
-  static constexpr int LPW = ROWS_A / RPL / NW;  // DMA loads per wave per slice
-  static constexpr int KSTEPS = SLICE / 32;
-  static constexpr uint32_t STAGE_BYTES = ROWS_A * SLICE;
-  static constexpr uint32_t SMEM_BYTES = STAGES * STAGE_BYTES;
-  static constexpr int PD = 3;  // B prefetch distance in steps
-  static_assert(KSTEPS == 4 && PD + 1 == KSTEPS, "ring slot = step within the slice");
-  static_assert(LPW == 4 && TJ == 2, "wait counts below assume 4 DMA and 2 B loads per step");
-  static constexpr int kWaitStep = 2 * TJ + LPW + TJ;  // steps 0-2
-  static constexpr int kWaitLast = PD * TJ;            // step 3
-  static constexpr int kWaitStage = KSTEPS * TJ;       // DMA of the next slice (2 stages)
-  static constexpr int kWaitFirst = PD * TJ;           // DMA of slice 0, before the loop
-
-  struct Src {
-    const char* abase;     // first C row of the block
-    uint32_t off[LPW];     // per-lane DMA offsets
-    uint32_t qb[LPW];      // chunk byte offset of each DMA lane (ragged tail test)
-    const char* bbase;     // fragment copy of this wave's first token block
-    uint32_t boff[TJ];     // lane offset of each token block
-    int64_t kbytes;
-    int KT, kskew;
-    u32x4 ring[KSTEPS][TJ];
-  };
-
-  static __device__ __forceinline__ Src make_src(const char* __restrict__ C, int64_t V, int64_t v0,
-                                                 const char* __restrict__ Ef, int64_t tb, int64_t pitch,
-                                                 int phase8) {
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    constexpr int kChunks = SLICE / 16;
-    Src src;
-    src.abase = C + v0 * pitch;
-#pragma unroll
-    for (int j = 0; j < LPW; ++j) {
-      const int row = (j * NW + wave) * RPL + lane / kChunks;
-      const uint32_t q = (uint32_t)(lane % kChunks) ^ slice_swz<SLICE>((uint32_t)row);
-      src.qb[j] = q * 16;
-      int64_t g = v0 + row;
-      g = g < V ? g : V - 1;
-      src.off[j] = (uint32_t)((g - v0) * pitch) + q * 16;
-    }
-    src.kbytes = pitch;
-    src.KT = (int)((pitch + SLICE - 1) / SLICE);
-    src.kskew = (int)(((int64_t)(phase8 & 7) * src.KT) >> 3);
-    const int wb = wave / WA;
-    const int64_t blk_bytes = (int64_t)src.KT * KSTEPS * 1024;
-    src.bbase = Ef + (tb * (kFwdTokens / 32) + wb * TJ) * blk_bytes;
-#pragma unroll
-    for (int tj = 0; tj < TJ; ++tj) src.boff[tj] = (uint32_t)(tj * blk_bytes) + (uint32_t)lane * 16u;
-    return src;
-  }
-
-  // slice kt of the contraction as loaded (rotated by the phase)
-  static __device__ __forceinline__ int rot(const Src& src, int kt) {
-    kt = kt < src.KT ? kt : src.KT - 1;
-    const int kr = kt + src.kskew;
-    return kr < src.KT ? kr : kr - src.KT;
-  }
-
-  template <bool RAGGED>
-  static __device__ __forceinline__ void issue_a(const Src& src, int kt, char* smem) {
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t lds_w = (uint32_t)(wave * RPL * SLICE);
-    const int kc = kt < src.KT ? kt : src.KT - 1;
-    char* st = smem + (kc % STAGES) * STAGE_BYTES;
-    const int64_t k0 = (int64_t)rot(src, kt) * SLICE;
-#pragma unroll
-    for (int j = 0; j < LPW; ++j) {
-      const uint32_t lds = __builtin_amdgcn_readfirstlane(lds_addr(st + lds_w + j * NW * RPL * SLICE));
-      if constexpr (RAGGED) {
-        const char* g = (src.abase + k0) + src.off[j];
-        if (k0 + (int64_t)src.qb[j] >= src.kbytes) g = reinterpret_cast<const char*>(g_zero16);
-        asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
-      } else {
-        asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(src.off[j]), "s"(src.abase + k0),
-                     "s"(lds)
-                     : "memory", "m0");
-      }
-    }
-  }
-
-  // B fragments of global step g (SLOT = g % 4) into ring slot SLOT; steps past the
-  // end reload the last step, so every step issues the same loads.
-  template <int SLOT>
-  static __device__ __forceinline__ void issue_b(Src& src, int g) {
-    const int last = src.KT * KSTEPS - 1;
-    g = g < last ? g : last;
-    const int sa = rot(src, g / KSTEPS) * KSTEPS + (g % KSTEPS);
-    const char* sb = src.bbase + (int64_t)sa * 1024;
-#pragma unroll
-    for (int tj = 0; tj < TJ; ++tj)
-      asm volatile("global_load_dwordx4 %0, %1, %2" : "=v"(src.ring[SLOT][tj]) : "v"(src.boff[tj]), "s"(sb));
-  }
-
-  template <int N>
-  static __device__ __forceinline__ void wait_slot(u32x4 (&b)[TJ]) {
-    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
-    asm volatile("s_waitcnt vmcnt(%2)" : "+v"(b[0]), "+v"(b[1]) : "n"(N));
-  }
-
-  template <bool RAGGED>
-  static __device__ __forceinline__ void prefetch(Src& src, char* smem) {
-#pragma unroll
-    for (int p = 0; p < STAGES - 1; ++p) issue_a<RAGGED>(src, p, smem);
-    issue_b<0>(src, 0);
-    issue_b<1>(src, 1);
-    issue_b<2>(src, 2);
-  }
-
-  template <bool RAGGED>
-  static __device__ __forceinline__ void consume(Src& src, char* smem, f32x16 (&acc)[TI][TJ]) {
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int wa = wave % WA;
-    const int arow = wa * (ROWS_A / WA) + (lane & 31);
-    const int kg = lane >> 5;
-    const int KT = src.KT;
-    auto frags = [&](const char* s, int ks, u32x4 (&af)[TI]) {
-#pragma unroll
-      for (int ti = 0; ti < TI; ++ti) af[ti] = lds_ld16(s, slice_off<SLICE>(arow + ti * 32, ks * 2 + kg));
-    };
-    auto mma = [&](const u32x4 (&af)[TI], const u32x4 (&bf)[TJ]) {
-#pragma unroll
-      for (int ti = 0; ti < TI; ++ti)
-#pragma unroll
-        for (int tj = 0; tj < TJ; ++tj) acc[ti][tj] = Traits<T>::mfma(af[ti], bf[tj], acc[ti][tj]);
-    };
-    constexpr int MF = TI * TJ * Traits<T>::kInstrPerStep;
-    constexpr int NR = TI;
-
-    stage_barrier<kWaitFirst>();
-    u32x4 fa0[TI], fa1[TI];
-    frags(smem, 0, fa0);
-    for (int it = 0; it < KT; ++it) {
-      const char* s = smem + (it % STAGES) * STAGE_BYTES;
-      const char* sn = smem + ((it + 1) % STAGES) * STAGE_BYTES;
-      const int g0 = it * KSTEPS;
-      frags(s, 1, fa1);
-      issue_a<RAGGED>(src, it + STAGES - 1, smem);
-      // step 0
-      issue_b<3>(src, g0 + 3);
-      wait_slot<kWaitStep>(src.ring[0]);
-      mma(fa0, src.ring[0]);
-      __builtin_amdgcn_sched_group_barrier(0x100, NR, 0);
-      sched_interleave<0, MF, 0, 0, 0>();
-      // step 1
-      frags(s, 2, fa0);
-      issue_b<0>(src, g0 + 4);
-      wait_slot<kWaitStep>(src.ring[1]);
-      mma(fa1, src.ring[1]);
-      sched_interleave<0, MF, NR, 0, 0>();
-      // step 2
-      frags(s, 3, fa1);
-      issue_b<1>(src, g0 + 5);
-      wait_slot<kWaitStep>(src.ring[2]);
-      mma(fa0, src.ring[2]);
-      sched_interleave<0, MF, NR, 0, 0>();
-      // step 3
-      issue_b<2>(src, g0 + 6);
-      __builtin_amdgcn_sched_barrier(0);
-      stage_barrier<kWaitStage>();  // slice it+1 has landed in every wave's share of its stage
-      __builtin_amdgcn_sched_barrier(0);
-      frags(sn, 0, fa0);
-      wait_slot<kWaitLast>(src.ring[3]);
-      mma(fa1, src.ring[3]);
-      sched_interleave<0, MF, NR, 0, 0>();
-    }
-    // drain: the ring's last loads (clamped reloads) stay live until they land
-    asm volatile("s_waitcnt vmcnt(0)"
-                 : "+v"(src.ring[0][0]), "+v"(src.ring[0][1]), "+v"(src.ring[1][0]), "+v"(src.ring[1][1]),
-                   "+v"(src.ring[2][0]), "+v"(src.ring[2][1]), "+v"(src.ring[3][0]), "+v"(src.ring[3][1]));
-    __syncthreads();
-  }
-};
-
 // Persistent schedule of the forward tiles.  The grid is 8 * cpx workgroups, one
 // per CU: the hardware deals workgroups to the 8 XCDs round-robin, so workgroup b
 // runs on XCD b % 8 as that XCD's member s = b / 8.  Tiles are grouped in rounds of
@@ -359,12 +135,9 @@ __device__ __forceinline__ void fwd_epilogue(const FwdArgs& a, int nvt, f32x16 (
   }
 }
 
-// FRAG: E fragments from the fragment-order copy a.e_frag (FwdFragLoop);
-// otherwise both operands through the LDS (FwdLoop).
-template <typename T, bool HAS_BIAS, bool RAGGED, bool FRAG>
+template <typename T, bool HAS_BIAS, bool RAGGED>
 __global__ __launch_bounds__(FwdLoop<T>::NTHREADS, 1) void fwd_tile_kernel(FwdArgs a, FwdSched sc) {
-  using Loop = std::conditional_t<FRAG, FwdFragLoop<T>, FwdLoop<T>>;
-  static_assert(Loop::NTHREADS == FwdLoop<T>::NTHREADS, "one block shape");
+  using Loop = FwdLoop<T>;
   constexpr int TI = Loop::TI, TJ = Loop::TJ;
   __shared__ __attribute__((aligned(16))) char smem[Loop::SMEM_BYTES];
 
@@ -386,13 +159,8 @@ __global__ __launch_bounds__(FwdLoop<T>::NTHREADS, 1) void fwd_tile_kernel(FwdAr
   const char* C = reinterpret_cast<const char*>(a.c);
   const char* E = reinterpret_cast<const char*>(a.e);
   auto sources = [&](int tb, int vb) {
-    if constexpr (FRAG) {
-      return Loop::make_src(C, a.V, (int64_t)vb * kFwdVocab, reinterpret_cast<const char*>(a.e_frag), tb, pitch,
-                            xcd);
-    } else {
-      const int64_t seg[1] = {(int64_t)vb * kFwdVocab};
-      return Loop::template make_src<kFwdVocab>(C, a.V, seg, E, a.N, (int64_t)tb * kFwdTokens, pitch, pitch, xcd);
-    }
+    const int64_t seg[1] = {(int64_t)vb * kFwdVocab};
+    return Loop::template make_src<kFwdVocab>(C, a.V, seg, E, a.N, (int64_t)tb * kFwdTokens, pitch, pitch, xcd);
   };
   // targets of this lane's tokens (clamped reads past N; the epilogue ignores them)
   auto targets = [&](int tb, int64_t (&tg)[TJ]) {
@@ -517,25 +285,20 @@ __global__ __launch_bounds__(64 * kLseSplits) void lse_kernel(FwdArgs a, int nvt
   }
 }
 
-// The register-operand loop (FRAG) runs without a bias only: with the bias
-// epilogue's extra live values the compiler spills registers of that kernel, and
-// a spilled ring slot would copy a register whose load is still in flight.
-template <typename T, bool FRAG>
+template <typename T>
 static void launch_tile_variant(const FwdArgs& a, const FwdSched& sc, bool bias, bool ragged, dim3 grid, dim3 block,
                                 hipStream_t s) {
-  if constexpr (!FRAG) {
-    if (bias) {
-      if (ragged)
-        hipLaunchKernelGGL((fwd_tile_kernel<T, true, true, false>), grid, block, 0, s, a, sc);
-      else
-        hipLaunchKernelGGL((fwd_tile_kernel<T, true, false, false>), grid, block, 0, s, a, sc);
-      return;
-    }
+  if (bias) {
+    if (ragged)
+      hipLaunchKernelGGL((fwd_tile_kernel<T, true, true>), grid, block, 0, s, a, sc);
+    else
+      hipLaunchKernelGGL((fwd_tile_kernel<T, true, false>), grid, block, 0, s, a, sc);
+  } else {
+    if (ragged)
+      hipLaunchKernelGGL((fwd_tile_kernel<T, false, true>), grid, block, 0, s, a, sc);
+    else
+      hipLaunchKernelGGL((fwd_tile_kernel<T, false, false>), grid, block, 0, s, a, sc);
   }
-  if (ragged)
-    hipLaunchKernelGGL((fwd_tile_kernel<T, false, true, FRAG>), grid, block, 0, s, a, sc);
-  else
-    hipLaunchKernelGGL((fwd_tile_kernel<T, false, false, FRAG>), grid, block, 0, s, a, sc);
 }
 
 // The tile kernel over vocabulary blocks [vb0, vb0 + nvb): a.c must address the
@@ -558,10 +321,7 @@ static hipError_t launch_tiles(const FwdArgs& a, int vb0, int nvb, hipStream_t s
   sc.rounds = (int)rounds;
   const dim3 grid(8 * cpx), block(FwdLoop<T>::NTHREADS);
   const bool ragged = (a.D * (int64_t)sizeof(T)) % kSliceBytes != 0;
-  if (a.e_frag && !a.bias)
-    launch_tile_variant<T, true>(a, sc, a.bias != nullptr, ragged, grid, block, s);
-  else
-    launch_tile_variant<T, false>(a, sc, a.bias != nullptr, ragged, grid, block, s);
+  launch_tile_variant<T>(a, sc, a.bias != nullptr, ragged, grid, block, s);
   return hipGetLastError();
 }
 
@@ -574,16 +334,6 @@ static hipError_t launch_lse(const FwdArgs& a, hipStream_t s) {
 
 template <typename T>
 static hipError_t forward_typed(const FwdArgs& a, hipStream_t s) {
-  if (a.e_frag && !a.bias) {
-    const int64_t row_bytes = a.D * (int64_t)sizeof(T);
-    const int64_t KT = (row_bytes + 127) / 128;
-    const int64_t wgs = (a.N + 255) / 256 * 8 * KT;
-    if (wgs > INT32_MAX) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(e_frag_kernel, dim3((unsigned)wgs), dim3(256), 0, s, reinterpret_cast<const char*>(a.e),
-                       reinterpret_cast<u32x4*>(a.e_frag), a.N, row_bytes, (uint32_t)KT);
-    hipError_t err = hipGetLastError();
-    if (err != hipSuccess) return err;
-  }
   hipError_t err = launch_tiles<T>(a, 0, (int)((a.V + kFwdVocab - 1) / kFwdVocab), s);
   if (err != hipSuccess) return err;
   return launch_lse<T>(a, s);

@@ -6,8 +6,6 @@
 #include <stdint.h>
 #include <stdlib.h>
 
-#include <cstdlib>
-
 namespace cce {
 
 // Forward workgroup tile: 256 tokens x 256 vocabulary rows.
@@ -35,17 +33,7 @@ struct FwdArgs {
   int num_cus;  // compute units of the device (the persistent forward runs one workgroup per CU)
   void* zero_buf;       // filled with zeros alongside the tiles (null: none)
   int64_t zero_units;   // 16-byte units of zero_buf
-  void* e_frag;         // E in MFMA fragment order (e_frag_bytes(); null: E staged through LDS)
 };
-
-// Bytes of the fragment-order copy of E that the forward's register-operand main
-// loop reads: every 32-row token block of the whole 256-token tiles, the row
-// bytes rounded up to the 128-byte slice.
-inline size_t e_frag_bytes(int64_t N, int64_t row_bytes) {
-  const int64_t blocks = (N + 255) / 256 * 8;
-  const int64_t slices = (row_bytes + 127) / 128;
-  return (size_t)(blocks * slices * 4096);
-}
 
 // Classifier rows stored with affine group quantization (the layout of MLX's
 // mx.quantize / mx.dequantize, mlx >= 0.22, which the reference's callers apply
@@ -67,19 +55,30 @@ constexpr int64_t kQuantChunkAlign = 4096;         // rows: whole 32-tile chunks
 constexpr int64_t kQuantDefaultChunkRows = 32768;  // 256 MiB of bf16 scratch at D = 4096
 
 // Backward work plan.  Kept (token block, vocabulary tile) pairs are found by the
-// filter as a bitmap, one bit per pair, rows by token block.  The vocabulary is
-// cut into chunks of `chunk_nvt` tiles (one chunk unless the problem is large);
-// per chunk the kept pairs get consecutive "slots" in (token block, vocab tile)
-// order, and every slot's 128 x 128 G tile lives in a scratch of `cap` slots.
-// A chunk holds every token block of its vocabulary tiles, so dC and dBias of a
-// chunk are final when its sums end; dE is carried between chunks in fp32.
-// G-tile scratch per chunk.  A chunk holds every pair it may keep, so the budget sets
-// the chunk width: 16 GiB keeps a 70B-class head (N = 32768, V = 128256: 8.4 GB) in one
-// chunk, which saves the fp32 dE carry between chunks (at that size 1.5 of 4.5 ms).
-#ifndef CCE_G_SCRATCH_GIB
-#define CCE_G_SCRATCH_GIB 16
+// filter as a bitmap, one bit per pair, rows by token block.  Two levels cut the
+// work so that every scratch buffer has a bounded size:
+//   * chunks: the vocabulary in runs of `chunk_nvt` tiles, fixed on the host by the
+//     compaction's LDS limits only (one chunk unless N and V are large);
+//   * passes: a chunk's tiles in runs chosen on the device by kept-pair count, so
+//     that one pass keeps at most `cap` pairs.  Pass p holds the tiles v whose
+//     exclusive prefix of kept pairs P[v] lies in [p (cap - nrb), (p + 1)(cap - nrb)):
+//     a tile keeps at most nrb pairs, so a pass keeps fewer than cap.  The host
+//     launches `max_passes` passes per chunk (the dense worst case); passes past
+//     the last one the data needs find nothing to do and return at once.
+// Per chunk the kept pairs get "slots" ordered by (pass, token block, vocab tile);
+// a pass's G tiles live in a scratch of `cap` tiles (slot s at s - first slot of
+// the pass).  A pass holds every token block of its tiles, so dC and dBias of a
+// pass are final when its sums end; dE is carried between passes and chunks in
+// fp32 when the backward takes more than one pass.
+// G-tile budget of one pass, in MiB (the default workspace; a smaller workspace
+// gives smaller passes, down to 2 tiles per token block).  512 MiB holds a quarter of
+// the Llama-3 8B head's tiles (N = 8192, V = 128256: 2.1 GB of bf16 G when nothing is
+// skipped), so a backward launches at most 4 passes there; each pass past the ones the
+// data needs costs one empty launch per kernel (about 4.5 us).
+#ifndef CCE_G_SCRATCH_MIB
+#define CCE_G_SCRATCH_MIB 512
 #endif
-constexpr size_t kWScratchBudget = size_t(CCE_G_SCRATCH_GIB) << 30;
+constexpr size_t kGScratchBudget = size_t(CCE_G_SCRATCH_MIB) << 20;
 constexpr int kCompactMaxWords = 8192;                 // bitmap words one compaction holds in LDS
 constexpr int kCompactMaxVt = 4096;                    // vocabulary tiles per chunk (LDS counts)
 constexpr int kMaxDcBins = 256;                        // workgroup bins of the dC sums' schedule
@@ -92,17 +91,39 @@ constexpr int64_t kPermMaxN = 65536;   // rows the sort handles
 constexpr int64_t kPermMaxKey = 16384; // tiles + 1 (the key of rows without gradient)
 constexpr int kPermFlag = 15;          // counts[kPermFlag]: 1 when the backward runs on sorted rows
 
+// Pass table: kPassInts ints per pass of the current chunk, written by the compaction.
+constexpr int kPassInts = 16;
+enum PassField {
+  kPiVt0 = 0,      // chunk-local vocabulary tiles [vt0, vt1) of the pass
+  kPiVt1 = 1,
+  kPiS0 = 2,       // slots [s0, s1); the G scratch holds slot s at index s - s0
+  kPiS1 = 3,
+  kPiTask0 = 4,    // G tasks [task0, task1) in g_task / g_task_rb
+  kPiTask1 = 5,
+  kPiOwnRb = 6,    // dE owners: own_rb[p * nrb + i], i < this count
+  kPiOwnVt = 7,    // dC owners: own_vt[vt0 + i], i < this count
+  kPiTail = 8,     // item counter of the G kernel's tail (zeroed by the compaction)
+  kPiDeMode = 9,   // -1: no work (past the passes the data needs); else a dE write mode (WriteMode)
+};
+// dE write mode of a pass: one pass over everything writes dE directly; with more
+// passes (or chunks) dE is summed in an fp32 carry: the first pass stores it, the
+// middle ones add to it, the last one adds and writes dE.
+enum WriteMode { kWriteT = 0, kStoreF32 = 1, kAddF32 = 2, kFinishT = 3 };
+
 struct BwdPlan {
   int64_t nvt, nrb, total;  // vocab tiles, token blocks, pairs
   int64_t nwords;           // 32-bit bitmap words per token block: ceil(nvt / 32)
   int64_t chunk_nvt;        // vocab tiles per chunk (a multiple of 32 unless it is nvt)
   int64_t n_chunks;
-  int64_t cap;              // slots per chunk: nrb * chunk_nvt
+  int64_t chunk_pairs;      // nrb * chunk_nvt: the most pairs one chunk may keep
+  int64_t cap;              // G tiles per pass: chunk_pairs, or at least 2 nrb
+  int64_t max_passes;       // passes launched per chunk
   size_t g_bytes;           // bytes of one G tile (128 x 128 x sizeof(T))
   bool perm_ok;             // the sorted token order is available (N and tile count in range)
+  bool carry;               // the fp32 dE carry is reserved (more than one pass or chunk may run)
   // workspace byte offsets
-  size_t bits, counts, rb_start, slot_vt, slot_rb, vt_start, vt_slot, g_task, g_task_rb, own_rb, own_vt, dc_bin_start,
-      dc_bin_owner, gtile, colsum, de_acc;
+  size_t bits, counts, pinfo, rb_start, slot_vt, slot_rb, vt_start, vt_slot, g_task, g_task_rb, own_rb, own_vt,
+      dc_bin_start, dc_bin_owner, gtile, colsum, de_acc;
   size_t perm, sort_buf, rowbits, bits_p, t_perm, lse_perm, dnll_perm, e_perm;  // sorted order (perm_ok)
   size_t qrows;  // dequantized classifier rows of one chunk (quantized classifier only)
   size_t total_bytes;
@@ -110,10 +131,24 @@ struct BwdPlan {
 
 inline size_t plan_align(size_t x) { return (x + 255) & ~size_t(255); }
 
-// max_chunk_nvt > 0 caps the chunk width (a multiple of 32 tiles); quant reserves the
-// scratch of one chunk's dequantized classifier rows.
-inline BwdPlan make_bwd_plan(size_t esize, int64_t N, int64_t D, int64_t V, bool want_de, bool want_dc,
-                             bool want_db, int64_t max_chunk_nvt = 0, bool quant = false) {
+// Chunks of the vocabulary: the compaction's LDS limits; max_chunk_nvt > 0 caps the
+// width further (a multiple of 32 tiles: the quantized rows' chunks).
+inline int64_t plan_chunk_nvt(int64_t nvt, int64_t nrb, int64_t max_chunk_nvt) {
+  int64_t cw = nvt;
+  const int64_t by_lds = 32 * (kCompactMaxWords / nrb);
+  cw = cw < by_lds ? cw : by_lds;
+  cw = cw < kCompactMaxVt ? cw : kCompactMaxVt;
+  if (max_chunk_nvt > 0 && max_chunk_nvt < cw) cw = max_chunk_nvt;
+  if (cw < nvt) cw = cw / 32 * 32;
+  if (cw < 32) cw = nvt < 32 ? nvt : 32;
+  return cw;
+}
+
+// The plan for passes of at most `cap` G tiles (clamped to [min(2 nrb, chunk_pairs),
+// chunk_pairs]); perm: reserve the sorted token order when it is available; quant
+// reserves the scratch of one chunk's dequantized classifier rows.
+inline BwdPlan make_bwd_plan_cap(size_t esize, int64_t N, int64_t D, int64_t V, bool want_de, bool want_dc,
+                                 bool want_db, int64_t cap, bool perm, int64_t max_chunk_nvt, bool quant) {
   BwdPlan P{};
   P.nvt = (V + kBwdVocab - 1) / kBwdVocab;
   P.nrb = (N + kBwdTokens - 1) / kBwdTokens;
@@ -121,28 +156,17 @@ inline BwdPlan make_bwd_plan(size_t esize, int64_t N, int64_t D, int64_t V, bool
   P.nwords = (P.nvt + 31) / 32;
   P.g_bytes = (size_t)kBwdTokens * kBwdVocab * esize;
   const bool want_g = want_de || want_dc;
-  // Chunk width: bounded by the G scratch budget (a chunk may keep every pair),
-  // the compaction's LDS bitmap, and its per-tile counts; at least 32 tiles.
-  int64_t cw = P.nvt;
-  if (want_g) {
-    const int64_t by_budget = (int64_t)(kWScratchBudget / P.g_bytes) / P.nrb;
-    cw = cw < by_budget ? cw : by_budget;
-  }
-  const int64_t by_lds = 32 * (kCompactMaxWords / P.nrb);
-  cw = cw < by_lds ? cw : by_lds;
-  cw = cw < kCompactMaxVt ? cw : kCompactMaxVt;
-  if (max_chunk_nvt > 0 && max_chunk_nvt < cw) cw = max_chunk_nvt;
-  // Test hook: CCE_TEST_CHUNK_VT narrows the chunks (rounded down to a multiple of 32)
-  // so that the multi-chunk path runs at small sizes.
-  if (const char* env = std::getenv("CCE_TEST_CHUNK_VT")) {
-    const long long t = std::atoll(env);
-    if (t > 0 && t < cw) cw = t;
-  }
-  if (cw < P.nvt) cw = cw / 32 * 32;
-  if (cw < 32) cw = P.nvt < 32 ? P.nvt : 32;
+  const int64_t cw = plan_chunk_nvt(P.nvt, P.nrb, max_chunk_nvt);
   P.chunk_nvt = cw;
   P.n_chunks = (P.nvt + cw - 1) / cw;
-  P.cap = P.nrb * cw;
+  P.chunk_pairs = P.nrb * cw;
+  const int64_t cap_min = 2 * P.nrb < P.chunk_pairs ? 2 * P.nrb : P.chunk_pairs;
+  cap = cap < cap_min ? cap_min : cap;
+  cap = cap > P.chunk_pairs ? P.chunk_pairs : cap;
+  P.cap = cap;
+  // a chunk's tile v lies in pass floor(P[v] / (cap - nrb)), P[v] <= nrb (cw - 1)
+  P.max_passes = cap >= P.chunk_pairs ? 1 : (P.nrb * (cw - 1)) / (cap - P.nrb) + 1;
+  P.carry = want_de && (P.n_chunks > 1 || P.max_passes > 1);
   size_t off = 0;
   auto take = [&](size_t bytes) {
     const size_t o = off;
@@ -151,22 +175,23 @@ inline BwdPlan make_bwd_plan(size_t esize, int64_t N, int64_t D, int64_t V, bool
   };
   P.bits = take((size_t)P.nrb * P.nwords * 4);
   P.counts = take(16 * 4);
-  P.rb_start = take((size_t)(P.nrb + 1) * 4);
-  P.slot_vt = take((size_t)P.cap * 4);
-  P.slot_rb = take((size_t)P.cap * 4);
+  P.pinfo = take((size_t)P.max_passes * kPassInts * 4);
+  P.rb_start = take((size_t)(P.max_passes * P.nrb + 1) * 4);
+  P.slot_vt = take((size_t)P.chunk_pairs * 4);
+  P.slot_rb = take((size_t)P.chunk_pairs * 4);
   P.vt_start = take((size_t)(cw + 1) * 4);
-  P.vt_slot = take((size_t)P.cap * 4);
-  P.g_task = take((size_t)P.cap * 4);
-  P.g_task_rb = take((size_t)P.cap * 4);
-  P.own_rb = take((size_t)P.nrb * 4);
+  P.vt_slot = take((size_t)P.chunk_pairs * 4);
+  P.g_task = take((size_t)P.chunk_pairs * 4);
+  P.g_task_rb = take((size_t)P.chunk_pairs * 4);
+  P.own_rb = take((size_t)P.max_passes * P.nrb * 4);
   P.own_vt = take((size_t)cw * 4);
   P.dc_bin_start = take((size_t)(kMaxDcBins + 1) * 4);
   P.dc_bin_owner = take((size_t)cw * 4);
   P.gtile = want_g ? take((size_t)P.cap * P.g_bytes) : 0;
   P.colsum = want_db ? take((size_t)P.cap * kBwdVocab * sizeof(float)) : 0;
-  P.de_acc = (want_de && P.n_chunks > 1) ? take((size_t)N * (size_t)D * sizeof(float)) : 0;
+  P.de_acc = P.carry ? take((size_t)N * (size_t)D * sizeof(float)) : 0;
   // (dE rows are then written through the map with one buffer over all of dE: < 2^31 bytes)
-  P.perm_ok = N <= kPermMaxN && P.nvt + 1 <= kPermMaxKey && (want_g || want_db) &&
+  P.perm_ok = perm && N <= kPermMaxN && P.nvt + 1 <= kPermMaxKey && (want_g || want_db) &&
               (double)N * (double)D * (double)esize < 2147483648.0;
   if (P.perm_ok) {
     P.perm = take((size_t)N * 4);
@@ -180,6 +205,63 @@ inline BwdPlan make_bwd_plan(size_t esize, int64_t N, int64_t D, int64_t V, bool
   }
   P.qrows = quant ? take((size_t)P.chunk_nvt * kBwdVocab * (size_t)D * esize) : 0;
   P.total_bytes = off;
+  return P;
+}
+
+// G tiles of a pass in the default workspace: the budget, at least 2 per token block.
+inline int64_t default_cap(size_t esize, int64_t N) {
+  const int64_t nrb = (N + kBwdTokens - 1) / kBwdTokens;
+  const int64_t by_budget = (int64_t)(kGScratchBudget / ((size_t)kBwdTokens * kBwdVocab * esize));
+  return by_budget > 2 * nrb ? by_budget : 2 * nrb;
+}
+
+// The plan of the default workspace (max_g_tiles <= 0), or of passes of at most
+// max_g_tiles G tiles.
+inline BwdPlan make_bwd_plan(size_t esize, int64_t N, int64_t D, int64_t V, bool want_de, bool want_dc,
+                             bool want_db, int64_t max_chunk_nvt = 0, bool quant = false, int64_t max_g_tiles = 0) {
+  const int64_t dcap = default_cap(esize, N);
+  const int64_t cap = max_g_tiles > 0 && max_g_tiles < dcap ? max_g_tiles : dcap;
+  return make_bwd_plan_cap(esize, N, D, V, want_de, want_dc, want_db, cap, true, max_chunk_nvt, quant);
+}
+
+// The plan a workspace of ws_bytes runs: the default plan when it fits, else the
+// largest pass capacity that fits (the sorted token order is dropped when even the
+// smallest passes do not fit with it).  ok = false when nothing fits.
+inline BwdPlan plan_for_workspace(size_t esize, int64_t N, int64_t D, int64_t V, bool want_de, bool want_dc,
+                                  bool want_db, int64_t max_chunk_nvt, bool quant, size_t ws_bytes, bool& ok) {
+  BwdPlan P = make_bwd_plan(esize, N, D, V, want_de, want_dc, want_db, max_chunk_nvt, quant);
+  ok = P.total_bytes <= ws_bytes;
+  if (ok) return P;
+  const int64_t dcap = P.cap;
+  for (int perm = 1; perm >= 0; --perm) {
+    // Below one pass per chunk (cap < chunk_pairs) the size grows with cap: bisect.
+    int64_t lo = 1, hi = dcap < P.chunk_pairs ? dcap : P.chunk_pairs - 1;
+    BwdPlan best{};
+    bool found = false;
+    if (hi >= 1) {
+      BwdPlan m = make_bwd_plan_cap(esize, N, D, V, want_de, want_dc, want_db, lo, perm != 0, max_chunk_nvt, quant);
+      if (m.total_bytes <= ws_bytes) {
+        best = m;
+        found = true;
+        lo = m.cap;  // the clamped minimum
+        while (lo < hi) {
+          const int64_t mid = lo + (hi - lo + 1) / 2;
+          BwdPlan t = make_bwd_plan_cap(esize, N, D, V, want_de, want_dc, want_db, mid, perm != 0, max_chunk_nvt,
+                                        quant);
+          if (t.total_bytes <= ws_bytes) {
+            best = t;
+            lo = mid;
+          } else {
+            hi = mid - 1;
+          }
+        }
+      }
+    }
+    if (found) {
+      ok = true;
+      return best;
+    }
+  }
   return P;
 }
 
@@ -200,21 +282,22 @@ struct BwdArgs {
   void* dBias;  // output, dtype, or null
   // workspace (see BwdPlan); the lists are rebuilt for every chunk
   uint32_t* bits;     // [nrb][nwords] keep bitmap, bit b of word w = vocab tile 32 w + b
-  int* counts;        // [0] kept pairs, [1] G tasks, [2] tail item counter, [4] / [5] entries of own_rb / own_vt
-  int* rb_start;      // [nrb + 1] first slot of each token block
-  int* slot_vt;       // [cap] chunk-local vocab tile of each slot
-  int* slot_rb;       // [cap] token block of each slot
+  int* counts;        // [kPermFlag]: the sorted token order is in use
+  int* pinfo;         // [max_passes][kPassInts] pass table of the current chunk
+  int* rb_start;      // [max_passes * nrb + 1] first slot of (pass, token block), flattened
+  int* slot_vt;       // [chunk_pairs] chunk-local vocab tile of each slot
+  int* slot_rb;       // [chunk_pairs] token block of each slot
   int* vt_start;      // [chunk_nvt + 1] first entry of each vocab tile in vt_slot
-  int* vt_slot;       // [cap] slots grouped by vocab tile, token blocks ascending
-  int* g_task;        // [cap] first slot of each G task (up to 4 slots of one token block)
-  int* g_task_rb;     // [cap] token block of each G task
-  int* own_rb;        // [nrb] token blocks with kept tiles, most tiles first (dE owners)
-  int* own_vt;        // [chunk_nvt] chunk vocab tiles with kept tiles, most first (dC owners)
+  int* vt_slot;       // [chunk_pairs] slots grouped by vocab tile, token blocks ascending
+  int* g_task;        // [chunk_pairs] first slot of each G task (up to 4 slots of one token block)
+  int* g_task_rb;     // [chunk_pairs] token block of each G task
+  int* own_rb;        // [max_passes][nrb] token blocks with kept tiles in the pass, most tiles first (dE owners)
+  int* own_vt;        // [chunk_nvt] vocab tiles with kept tiles, by pass, most first (dC owners)
   int* dc_bin_start;  // [kMaxDcBins + 1] dC schedule: owners of bin m are dc_bin_owner[start[m] .. start[m + 1])
   int* dc_bin_owner;  // [chunk_nvt]
-  char* gtile;        // [cap][128 tokens][128 vocab] G tiles, token-major, dtype
+  char* gtile;        // [cap][128 tokens][128 vocab] G tiles of one pass, token-major, dtype
   float* colsum;      // [cap][128] per-slot column sums of G (dBias)
-  float* de_acc;      // [N, D] fp32, only when n_chunks > 1
+  float* de_acc;      // [N, D] fp32, only when the plan reserves the carry
   int64_t* tile_stats;  // [3] or null: kept pairs, all pairs, kept pairs of the input-order token blocks
   BwdPlan plan;
   int num_cus;
@@ -230,6 +313,8 @@ struct BwdArgs {
   float* dnll_perm;     // [N]
   void* e_perm;         // [N, D] dtype
   int perm_mode;        // 0: sorted order when it keeps >= 10% fewer tiles, 1: never, 2: always
+  int de_geo;           // dE sums geometry: 0 by size, 1 wide, 2 narrow
+  int dc_geo;           // dC sums geometry: 0 by the filter setting, 1 wide, 2 narrow
   int dc_zeroed;        // dC already holds zeros: only rows of vocab tiles with kept tiles are written
   QuantRows q;          // q.wq set: c is unused; every chunk first dequantizes its rows into q.scratch
 };

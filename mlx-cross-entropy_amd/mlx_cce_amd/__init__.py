@@ -13,7 +13,9 @@ requires grad; vocabulary tiles whose softmax is below 2^-12 for every row of a
 csrc/cce/cce.metal:191-204).
 
 API mirrors (reference file:line):
-    linear_cross_entropy   mlx_cce/__init__.py:79-107 (+ shift/return_lse of reference/__init__.py:22-85)
+    linear_cross_entropy   mlx_cce/__init__.py:79-107 (+ shift/return_lse/impl/compute_all_grads of
+                           reference/__init__.py:22-85)
+    linear_cross_entropy_reference  reference/_reference.py:5-48 (materialised logits, torch)
     cce_loss               mlx_cce/__init__.py:54-76
     cut_cross_entropy      csrc/bindings.cpp:15-56
     cce_forward_raw        csrc/bindings.cpp:58-69
@@ -32,6 +34,7 @@ import torch
 from . import _ext
 from ._ext import FILTER_LOG_EPS, cce_backward_raw, cce_forward_raw
 from .quant import QuantizedWeight, dequantize, quantize
+from .reference import linear_cross_entropy_reference
 
 __all__ = [
     "linear_cross_entropy",
@@ -40,6 +43,7 @@ __all__ = [
     "cce_forward_raw",
     "cce_backward_raw",
     "LinearCrossEntropy",
+    "linear_cross_entropy_reference",
     "FILTER_LOG_EPS",
     "last_tile_stats",
     "last_filter_stats",
@@ -49,6 +53,7 @@ __all__ = [
 ]
 
 _REDUCTIONS = ("none", "sum", "mean")
+_IMPLS = ("auto", "fused", "chunked", "reference")
 _last_stats = {}
 
 
@@ -150,26 +155,43 @@ def cce_loss(e, c, targets, bias=None, reduction="mean", ignore_index=-100, *, f
     return loss
 
 
-def linear_cross_entropy(e, c, targets, bias=None, reduction="mean", ignore_index=-100, *, shift=0,
-                         return_lse=False, filter_eps=FILTER_LOG_EPS):
+def linear_cross_entropy(e, c, targets, bias=None, reduction="mean", ignore_index=-100, shift=0, return_lse=False,
+                         impl="auto", compute_all_grads=None, *, filter_eps=FILTER_LOG_EPS):
     """Memory-efficient cross-entropy that never materializes [N, V] logits.
 
-    Reference mlx_cce/__init__.py:79-107; ``shift`` and ``return_lse`` follow the
-    research API reference/__init__.py:22-85 (reference/_ops.py:209-211,238-239).
+    Reference mlx_cce/__init__.py:79-107 (the installed API: e, c, targets, bias,
+    reduction, ignore_index) and the research API reference/__init__.py:22-85, whose
+    further arguments follow in the same order (shift, return_lse, impl,
+    compute_all_grads; reference/_ops.py:209-211,238-239).
 
     Args:
         e: hidden states [..., D] (flattened to [N, D])
-        c: classifier weights [V, D]
+        c: classifier weights [V, D], or a QuantizedWeight
         targets: target indices [...] (flattened to [N])
         bias: optional classifier bias [V]
         reduction: "mean", "sum" or "none"
         ignore_index: target value to mask (-100 default); None disables masking
         shift: drop the last `shift` positions of e and the first `shift` targets (causal LM)
         return_lse: also return the per-token logsumexp [N] (fp32, no gradient)
+        impl: "auto", "fused" or "chunked" run the HIP kernels (one path serves all
+            shapes, so the reference's choice between them has nothing to pick);
+            "reference" runs the materialised-logits restatement of
+            reference/_reference.py (linear_cross_entropy_reference)
+        compute_all_grads: True: gradients for c and bias as well as e; False: for e
+            only (LoRA / frozen head: c and bias get no gradient, where the
+            reference's VJP returns zeros, reference/_ops.py:31-45); None (default):
+            whatever autograd asks for -- dC / dBias exactly when c / bias require
+            grad.  The reference defaults to False because an MLX VJP cannot tell
+            which inputs are differentiated; torch's autograd can.
         filter_eps: backward tile-filter threshold (ln 2^-12); None disables filtering
     Returns:
         loss (fp32 scalar, or [...] for reduction="none"), optionally (loss, lse)
     """
+    if impl not in _IMPLS:
+        raise ValueError(f"Unknown impl: {impl!r} (expected one of {_IMPLS})")
+    if impl == "reference":
+        return linear_cross_entropy_reference(e, c, targets, bias=bias, reduction=reduction,
+                                              ignore_index=ignore_index, shift=shift, return_lse=return_lse)
     if shift:
         e = e[..., :-shift, :]
         targets = targets[..., shift:]
@@ -177,7 +199,8 @@ def linear_cross_entropy(e, c, targets, bias=None, reduction="mean", ignore_inde
     D = e.shape[-1]
     e_flat = e.reshape(-1, D)
     t_flat = targets.reshape(-1)
-    loss, lse = _cce(e_flat, c, t_flat, bias, reduction, ignore_index, filter_eps)
+    grads = True if compute_all_grads is None else bool(compute_all_grads)
+    loss, lse = _cce(e_flat, c, t_flat, bias, reduction, ignore_index, filter_eps, grad_c=grads, grad_bias=grads)
     if reduction == "none":
         loss = loss.reshape(orig_shape)
     if return_lse:
@@ -200,9 +223,14 @@ def cut_cross_entropy(e, c, targets, bias=None, reduction="mean", ignore_index=-
 
 
 class LinearCrossEntropy(torch.nn.Module):
-    """Drop-in module (reference/__init__.py:88-118)."""
+    """Drop-in module (reference/__init__.py:88-118): ``criterion(e, c, targets, bias=None)``.
 
-    def __init__(self, reduction="mean", ignore_index=-100, shift=0, compute_all_grads=True,
+    compute_all_grads defaults to None -- gradients for whatever requires grad -- where
+    the reference defaults to False (see linear_cross_entropy); pass False for the
+    reference's frozen-head behaviour whatever c.requires_grad says.
+    """
+
+    def __init__(self, reduction="mean", ignore_index=-100, shift=0, compute_all_grads=None,
                  filter_eps=FILTER_LOG_EPS):
         super().__init__()
         self.reduction = reduction
@@ -212,13 +240,6 @@ class LinearCrossEntropy(torch.nn.Module):
         self.filter_eps = filter_eps
 
     def forward(self, e, c, targets, bias=None):
-        if self.shift:
-            e = e[..., :-self.shift, :]
-            targets = targets[..., self.shift:]
-        orig_shape = targets.shape
-        e_flat = e.reshape(-1, e.shape[-1])
-        loss, _ = _cce(e_flat, c, targets.reshape(-1), bias, self.reduction, self.ignore_index, self.filter_eps,
-                       grad_c=self.compute_all_grads, grad_bias=self.compute_all_grads)
-        if self.reduction == "none":
-            loss = loss.reshape(orig_shape)
-        return loss
+        return linear_cross_entropy(e, c, targets, bias=bias, reduction=self.reduction,
+                                    ignore_index=self.ignore_index, shift=self.shift,
+                                    compute_all_grads=self.compute_all_grads, filter_eps=self.filter_eps)

@@ -7,6 +7,7 @@ There is no fallback: if the library is missing or the tensors are not on a
 ROCm device, the call raises.
 """
 
+import contextlib
 import ctypes
 import math
 import os
@@ -38,12 +39,13 @@ SIGNATURES = {
     "cce_num_vocab_tiles": (_I64, [_I64]),
     "cce_forward": (_INT, [_INT, _P, _P, _P, _P, _I64, _INT, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P]),
     "cce_backward_workspace_size": (ctypes.c_size_t, [_INT, _I64, _I64, _I64, _INT, _INT, _INT]),
+    "cce_backward_workspace_size_ex": (ctypes.c_size_t, [_INT, _I64, _I64, _I64, _INT, _INT, _INT, _I64, _I64]),
     "cce_backward": (_INT, [_INT, _P, _P, _P, _P, _I64, _INT, _I64, _I64, _I64, _P, _P, _P, ctypes.c_float,
                             _P, _P, _P, _P, ctypes.c_size_t, _P, _P]),
     "cce_forward_ex": (_INT, [_INT, _P, _P, _P, _P, _I64, _INT, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _I64,
                               _P]),
     "cce_backward_ex": (_INT, [_INT, _P, _P, _P, _P, _I64, _INT, _I64, _I64, _I64, _P, _P, _P, ctypes.c_float,
-                               _P, _P, _P, _P, ctypes.c_size_t, _P, _INT, _P]),
+                               _P, _P, _P, _P, ctypes.c_size_t, _P, _INT, _I64, _P]),
     "cce_dequantize": (_INT, [_INT, _P, _P, _P, _INT, _INT, _I64, _I64, _P, _P]),
     "cce_forward_q_scratch_size": (ctypes.c_size_t, [_INT, _I64, _I64, _I64]),
     "cce_forward_q": (_INT, [_INT, _P, _P, _P, _P, _INT, _INT, _P, _P, _I64, _INT, _I64, _I64, _I64, _P, _P, _P, _P,
@@ -51,9 +53,6 @@ SIGNATURES = {
     "cce_backward_q_workspace_size": (ctypes.c_size_t, [_INT, _I64, _I64, _I64, _INT, _INT, _I64]),
     "cce_backward_q": (_INT, [_INT, _P, _P, _P, _P, _INT, _INT, _P, _P, _I64, _INT, _I64, _I64, _I64, _P, _P, _P,
                               ctypes.c_float, _P, _P, _P, ctypes.c_size_t, _I64, _P, _P]),
-    "cce_forward_workspace_size": (ctypes.c_size_t, [_INT, _I64, _I64]),
-    "cce_forward_ws": (_INT, [_INT, _P, _P, _P, _P, _I64, _INT, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _I64,
-                              _P, ctypes.c_size_t, _P]),
     "cce_reduce_loss": (_INT, [_P, _P, _I64, _INT, _I64, _INT, _P, _P, _P]),
     "cce_broadcast_grad": (_INT, [_P, _P, _I64, _P, _P]),
 }
@@ -61,6 +60,37 @@ SIGNATURES = {
 CCE_REDUCE_SUM = 1
 CCE_REDUCE_MEAN = 2
 CCE_BWD_DC_ZEROED = 1
+CCE_BWD_TOKENS_INPUT = 2
+CCE_BWD_TOKENS_SORTED = 4
+CCE_BWD_DE_SUMS_WIDE = 8
+CCE_BWD_DE_SUMS_NARROW = 16
+CCE_BWD_DC_SUMS_WIDE = 32
+CCE_BWD_DC_SUMS_NARROW = 64
+
+# Overrides of choices the backward otherwise makes itself, for tests and tuning
+# (results agree to rounding either way).  They travel explicitly with every
+# cce_backward_ex call and its workspace-size query, so the two always agree.
+_bwd_opts = {"flags": 0, "max_g_tiles": 0, "max_chunk_tiles": 0}
+
+
+@contextlib.contextmanager
+def backward_options(token_order=None, de_sums=None, dc_sums=None, max_g_tiles=0, max_chunk_tiles=0):
+    """Within the block, backward() calls run with these overrides:
+    token_order "input" | "sorted" (128-row token blocks of the input order, or of the
+    rows grouped by target tile); de_sums / dc_sums "wide" | "narrow" (512- or
+    256-column sum tasks); max_g_tiles (passes of at most that many G tiles);
+    max_chunk_tiles (vocabulary chunks of at most that many tiles, a multiple of 32)."""
+    flags = 0
+    flags |= {None: 0, "input": CCE_BWD_TOKENS_INPUT, "sorted": CCE_BWD_TOKENS_SORTED}[token_order]
+    flags |= {None: 0, "wide": CCE_BWD_DE_SUMS_WIDE, "narrow": CCE_BWD_DE_SUMS_NARROW}[de_sums]
+    flags |= {None: 0, "wide": CCE_BWD_DC_SUMS_WIDE, "narrow": CCE_BWD_DC_SUMS_NARROW}[dc_sums]
+    saved = dict(_bwd_opts)
+    _bwd_opts.update(flags=flags, max_g_tiles=int(max_g_tiles), max_chunk_tiles=int(max_chunk_tiles))
+    try:
+        yield
+    finally:
+        _bwd_opts.clear()
+        _bwd_opts.update(saved)
 
 _lib = None
 
@@ -168,30 +198,13 @@ def _prep(e, c, targets, bias):
     return DTYPE_CODES[e.dtype]
 
 
-# Forward main loop: with a workspace (cce_forward_ws) the tile kernel reads E
-# fragments from a fragment-order copy straight into registers; without one both
-# operands go through the LDS.  Bit-identical results either way; a bias makes the
-# library use the LDS loop regardless.  The LDS loop is the default: at the
-# Llama-3-8B head (N=8192, D=4096, V=128256, bf16) it measured 6.42 ms against
-# 6.60 ms for the register-operand loop (copy included).
-_E_FRAG = False
-
-
-def set_forward_e_frag(on):
-    """Select the forward's main loop (True: fragment-order E in registers)."""
-    global _E_FRAG
-    _E_FRAG = bool(on)
-
-
-def forward(e, c, targets, bias=None, ignore_index=-100, zero_out=None, e_frag=None):
+def forward(e, c, targets, bias=None, ignore_index=-100, zero_out=None):
     """Run the fused forward.  Returns (tile_max, tile_sum_exp, neg_target_logit, lse, nll).
 
     tile_max / tile_sum_exp are [ceil(V/128), N] fp32 (vocab-tile major);
     nll is the per-token loss, 0 on rows whose target equals ignore_index.
     zero_out (optional, a contiguous device tensor of a multiple of 16 bytes) is
     filled with zeros by the forward's tile kernel (cce_forward_ex).
-    e_frag (default: set_forward_e_frag) passes a workspace for the fragment-order
-    copy of E (cce_forward_ws), taken from torch's caching allocator.
     """
     code = _prep(e, c, targets, bias)
     e = e.contiguous()
@@ -214,18 +227,9 @@ def forward(e, c, targets, bias=None, ignore_index=-100, zero_out=None, e_frag=N
         ev = _event_pair("forward")
         if ev:
             ev[0].record()
-        use_ws = (_E_FRAG if e_frag is None else bool(e_frag)) and bias is None
         if zero_out is not None and (not zero_out.is_contiguous() or zero_out.device != e.device):
             raise ValueError("[cce_forward] zero_out must be a contiguous tensor on the device of e")
-        if use_ws:
-            ws_bytes = int(lib().cce_forward_workspace_size(code, N, D))
-            ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=e.device)
-            zb = zero_out.numel() * zero_out.element_size() if zero_out is not None else 0
-            rc = lib().cce_forward_ws(code, _ptr(e), _ptr(c), _ptr(bias), _ptr(targets),
-                                      int(ignore_index) if has_ignore else 0, 1 if has_ignore else 0,
-                                      N, D, V, _ptr(tile_max), _ptr(tile_sum_exp), _ptr(neg_tl), _ptr(lse),
-                                      _ptr(nll), _ptr(zero_out), zb, _ptr(ws), ws_bytes, ctypes.c_void_p(stream))
-        elif zero_out is not None:
+        if zero_out is not None:
             rc = lib().cce_forward_ex(code, _ptr(e), _ptr(c), _ptr(bias), _ptr(targets),
                                       int(ignore_index) if has_ignore else 0, 1 if has_ignore else 0,
                                       N, D, V, _ptr(tile_max), _ptr(tile_sum_exp), _ptr(neg_tl), _ptr(lse),
@@ -243,11 +247,15 @@ def forward(e, c, targets, bias=None, ignore_index=-100, zero_out=None, e_frag=N
     return tile_max, tile_sum_exp, neg_tl, lse, nll
 
 
-def workspace_size(e, c, want_de, want_dc, want_db):
+def workspace_size(e, c, want_de, want_dc, want_db, max_g_tiles=None, max_chunk_tiles=None):
+    """Bytes of the backward's workspace (cce_backward_workspace_size_ex); the
+    backward_options in force unless given."""
     N, D = e.shape
     V = c.shape[0]
-    return int(lib().cce_backward_workspace_size(DTYPE_CODES.get(e.dtype, -1), N, D, V,
-                                                 int(want_de), int(want_dc), int(want_db)))
+    g = _bwd_opts["max_g_tiles"] if max_g_tiles is None else int(max_g_tiles)
+    ch = _bwd_opts["max_chunk_tiles"] if max_chunk_tiles is None else int(max_chunk_tiles)
+    return int(lib().cce_backward_workspace_size_ex(DTYPE_CODES.get(e.dtype, -1), N, D, V,
+                                                    int(want_de), int(want_dc), int(want_db), g, ch))
 
 
 def backward(e, c, targets, lse, tile_max, d_nll, bias=None, ignore_index=-100,
@@ -289,6 +297,7 @@ def backward(e, c, targets, lse, tile_max, d_nll, bias=None, ignore_index=-100,
     ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=e.device)
     eps = -math.inf if filter_eps is None else float(filter_eps)
     has_ignore = ignore_index is not None
+    flags = _bwd_opts["flags"] | (CCE_BWD_DC_ZEROED if dc_zeroed is not None else 0)
     with torch.cuda.device(e.device):
         stream = torch.cuda.current_stream(e.device).cuda_stream
         ev = _event_pair("backward")
@@ -298,8 +307,7 @@ def backward(e, c, targets, lse, tile_max, d_nll, bias=None, ignore_index=-100,
                                    int(ignore_index) if has_ignore else 0, 1 if has_ignore else 0,
                                    N, D, V, _ptr(lse), _ptr(tile_max), _ptr(d_nll), ctypes.c_float(eps),
                                    _ptr(dE), _ptr(dC), _ptr(dB), _ptr(ws), ctypes.c_size_t(ws_bytes),
-                                   _ptr(tile_stats), CCE_BWD_DC_ZEROED if dc_zeroed is not None else 0,
-                                   ctypes.c_void_p(stream))
+                                   _ptr(tile_stats), flags, _bwd_opts["max_chunk_tiles"], ctypes.c_void_p(stream))
         if ev:
             ev[1].record()
     if rc != CCE_OK:

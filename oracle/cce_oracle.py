@@ -24,6 +24,15 @@ below every tolerance it checks:
   (mlx_cce/__init__.py:61).
 * ``grads_filtered``: the gradients restricted to kept tiles (what a filtered
   backward computes).
+* ``round_bf16`` / ``round_f16``: round-to-nearest-even to the 16-bit types through
+  float32, the rounding of the library's 16-bit stores.  Pinned against torch's own
+  conversion on every kind of value (ties, subnormals, overflow) and by a planted
+  truncation that must fail.
+* ``grads_staged``: the gradients with G rounded to a 16-bit type before the two
+  products, as a backward that stores its G tiles in the input dtype computes them
+  (dBias from the unrounded G, as the column sums are taken before the store).
+  Pinned by reducing to ``grads`` with the identity as the rounding, and by a case
+  where the rounding of G provably moves dE.
 * ``dequantize``: affine group dequantization of quantized classifier rows, the
   layout of MLX's mx.quantize / mx.dequantize (mlx >= 0.22, absent here), which the
   reference's callers apply before the loss (README.md:84-95,136;
@@ -226,6 +235,36 @@ def grads_filtered(e, c, targets, keep, rows, cols, bias=None, d_nll=None, ignor
     G = np.where(mask, G, 0.0)
     dE = G @ _f64(c)
     dC = G.T @ _f64(e)
+    dB = G.sum(axis=0) if bias is not None else None
+    return dE, dC, dB
+
+
+def round_bf16(x):
+    """x rounded to the nearest bfloat16 (ties to even) through float32, as float64.
+    NaN and infinities pass through; values past the largest bfloat16 round to inf."""
+    x32 = np.asarray(x, dtype=np.float32)
+    b = x32.view(np.uint32).astype(np.uint64)
+    r = ((b + 0x7FFF + ((b >> 16) & 1)) & 0xFFFF0000).astype(np.uint32).view(np.float32)
+    return np.where(np.isnan(x32), x32, r).astype(np.float64)
+
+
+def round_f16(x):
+    """x rounded to the nearest float16 (ties to even) through float32, as float64."""
+    return np.asarray(x, dtype=np.float32).astype(np.float16).astype(np.float64)
+
+
+def grads_staged(e, c, targets, bias=None, reduction="mean", ignore_index=-100, grad_out=1.0, d_nll=None,
+                 stage=None):
+    """(dE, dC, dBias) with G passed through `stage` (a rounding, or None for none)
+    before dE = G C and dC = G^T E; dBias sums the unrounded G."""
+    t = np.asarray(targets).reshape(-1)
+    valid = valid_mask(t, ignore_index)
+    if d_nll is None:
+        d_nll = upstream(valid, reduction, grad_out)
+    G = grad_logits(e, c, t, bias, d_nll, ignore_index)
+    Gs = G if stage is None else stage(G)
+    dE = Gs @ _f64(c)
+    dC = Gs.T @ _f64(e)
     dB = G.sum(axis=0) if bias is not None else None
     return dE, dC, dB
 

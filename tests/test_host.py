@@ -55,17 +55,6 @@ def test_version_and_geometry(ext):
         assert lib.cce_num_vocab_tiles(V) == math.ceil(V / 128)
 
 
-def test_forward_workspace_size(ext):
-    """Fragment-order copy of E: whole 256-token tiles x row bytes rounded up to the
-    128-byte slice; zero for empty shapes and unknown dtypes."""
-    lib = ext.lib()
-    assert lib.cce_forward_workspace_size(2, 8192, 4096) == 8192 * 8192
-    assert lib.cce_forward_workspace_size(0, 300, 40) == 512 * 256  # fp32 rows of 160 B -> 2 slices
-    assert lib.cce_forward_workspace_size(1, 1, 8) == 256 * 128
-    assert lib.cce_forward_workspace_size(2, 0, 4096) == 0
-    assert lib.cce_forward_workspace_size(7, 8192, 4096) == 0
-
-
 def test_workspace_size_layout(ext):
     lib = ext.lib()
     N, D, V = 1000, 64, 3000
@@ -75,6 +64,49 @@ def test_workspace_size_layout(ext):
     full = lib.cce_backward_workspace_size(2, N, D, V, 1, 1, 1)
     assert full - base >= 4 * (N * D + V * D + V)
     assert lib.cce_backward_workspace_size(2, 0, D, V, 1, 1, 1) == 0
+
+
+G_BUDGET = 512 << 20  # default G-tile budget of one backward pass (CCE_G_SCRATCH_MIB)
+
+
+@pytest.mark.parametrize("N,D,V", [(8192, 4096, 128256), (32768, 8192, 128256), (65536, 4096, 128256),
+                                   (4096, 2304, 256000), (1 << 20, 4096, 128256)],
+                         ids=["c3", "c5", "N65536", "c4", "N1M"])
+def test_backward_workspace_is_bounded(ext, N, D, V):
+    """The backward's workspace is the G-tile budget + O(N*D + V) + per-pair lists of a
+    few bytes per 128 x 128 tile (bounded per chunk), never a logits-sized G scratch."""
+    lib = ext.lib()
+    nrb, nvt = -(-N // 128), -(-V // 128)
+    nwords = -(-nvt // 32)
+    chunk_pairs = min(nrb * nvt, nrb * 32 * (8192 // nrb))
+    for dtype, es in ((2, 2), (0, 4)):
+        ws = lib.cce_backward_workspace_size(dtype, N, D, V, 1, 1, 1)
+        g_slots = max(G_BUDGET // (128 * 128 * es), 2 * nrb)
+        bound = (g_slots * (128 * 128 * es + 512)  # G tiles + their column sums
+                 + N * D * (4 + es)                # fp32 dE carry + the sorted copy of E
+                 + N * nwords * 4 + 2 * nrb * nwords * 4  # keep bits per row / per block
+                 + 40 * chunk_pairs + 64 * N + (4 << 20))
+        print(f"N={N} D={D} V={V} dtype {dtype}: workspace {ws / 2**30:.3f} GiB (bound {bound / 2**30:.3f}, "
+              f"logits {N * V * es / 2**30:.2f})")
+        assert 0 < ws <= bound
+        assert ws < N * V * es / 2
+    # the same plan with the smallest passes is smaller still, and sizes grow with the pass size
+    sizes = [lib.cce_backward_workspace_size_ex(2, N, D, V, 1, 1, 1, k, 0) for k in (1, 4 * nrb, 16 * nrb)]
+    assert sizes == sorted(sizes) and sizes[-1] <= lib.cce_backward_workspace_size(2, N, D, V, 1, 1, 1)
+
+
+def test_backward_workspace_small_problems_fit_one_pass(ext):
+    """Below the budget the plan keeps every pair in one pass: no fp32 dE carry."""
+    lib = ext.lib()
+    N, D, V = 1000, 64, 3000
+    one = lib.cce_backward_workspace_size(2, N, D, V, 1, 1, 1)
+    assert one == lib.cce_backward_workspace_size_ex(2, N, D, V, 1, 1, 1, 0, 0)
+    tiles = math.ceil(N / 128) * math.ceil(V / 128)
+    assert one >= tiles * 128 * 128 * 2  # every pair's G tile
+    few = lib.cce_backward_workspace_size_ex(2, N, D, V, 1, 1, 1, 1, 0)  # smallest passes: carry + 16 tiles
+    assert few < one and few >= N * D * 4
+    assert lib.cce_backward_workspace_size_ex(2, N, D, V, 1, 1, 1, -1, 0) == 0
+    assert lib.cce_backward_workspace_size_ex(2, N, D, V, 1, 1, 1, 0, -32) == 0
 
 
 FAKE = 1 << 20  # 16-byte aligned, never dereferenced: validation fails first
@@ -103,14 +135,32 @@ def _bwd(lib, ext, ws=FAKE, ws_bytes=1 << 40, dbias=None, bias=None, eps=-8.3, d
                             FAKE, FAKE, dbias, ws, ctypes.c_size_t(ws_bytes), None, None)
 
 
+def _bwd_ex(lib, flags=0, chunk_tiles=0, ws_bytes=1 << 40):
+    return lib.cce_backward_ex(2, FAKE, FAKE, None, FAKE, -100, 1, 64, 64, 256, FAKE, FAKE, FAKE, ctypes.c_float(-8.3),
+                               FAKE, FAKE, None, FAKE, ctypes.c_size_t(ws_bytes), None, flags, chunk_tiles, None)
+
+
 def test_backward_validation_errors(ext):
     lib = ext.lib()
     assert _bwd(lib, ext, ws_bytes=16) == ext.CCE_ERR_WORKSPACE
-    assert b"workspace" in lib.cce_last_error()
+    assert b"workspace" in lib.cce_last_error() and b"at least" in lib.cce_last_error()
     assert _bwd(lib, ext, ws=None) == ext.CCE_ERR_WORKSPACE
     assert _bwd(lib, ext, dbias=FAKE) == ext.CCE_ERR_INVALID_ARGUMENT  # dBias without bias
     assert _bwd(lib, ext, eps=float("nan")) == ext.CCE_ERR_INVALID_ARGUMENT
     assert _bwd(lib, ext, dtype=3) == ext.CCE_ERR_UNSUPPORTED_DTYPE
+    assert _bwd_ex(lib, flags=1 << 10) == ext.CCE_ERR_INVALID_ARGUMENT
+    assert b"unknown flags" in lib.cce_last_error()
+    assert _bwd_ex(lib, flags=ext.CCE_BWD_TOKENS_INPUT | ext.CCE_BWD_TOKENS_SORTED) == ext.CCE_ERR_INVALID_ARGUMENT
+    assert _bwd_ex(lib, flags=ext.CCE_BWD_DE_SUMS_WIDE | ext.CCE_BWD_DE_SUMS_NARROW) == ext.CCE_ERR_INVALID_ARGUMENT
+    assert _bwd_ex(lib, chunk_tiles=48) == ext.CCE_ERR_INVALID_ARGUMENT
+    assert b"max_chunk_tiles" in lib.cce_last_error()
+    # the error names the least workspace; one byte less is refused
+    assert _bwd_ex(lib, ws_bytes=16) == ext.CCE_ERR_WORKSPACE
+    least = int(re.search(rb"at least (\d+)", lib.cce_last_error()).group(1))
+    assert 0 < least <= lib.cce_backward_workspace_size_ex(2, 64, 64, 256, 1, 1, 0, 1, 0)
+    assert _bwd_ex(lib, ws_bytes=least - 1) == ext.CCE_ERR_WORKSPACE
+    if not gpu_available():  # no device: the call passes the workspace check and stops at the device check
+        assert _bwd_ex(lib, ws_bytes=least) == ext.CCE_ERR_NO_DEVICE
 
 
 def test_reduction_helpers_validation_errors(ext):

@@ -332,3 +332,56 @@ def test_planted_mistakes_are_caught(kind):
     oE, oC = _mutant_grads(e, c, t, None, "none")
     np.testing.assert_allclose(oE, dE, rtol=1e-8, atol=1e-12)
     np.testing.assert_allclose(oC, dC, rtol=1e-8, atol=1e-12)
+
+
+# ------------------------------------------------------- 16-bit rounding points
+def _special_values():
+    rng = np.random.default_rng(3)
+    base = np.concatenate([rng.standard_normal(4000) * 10.0 ** rng.integers(-40, 38, 4000),
+                           [0.0, -0.0, 1.0, -1.0, 3.0e38, -3.4e38, 1e-40, -1e-45, np.inf, -np.inf, np.nan]])
+    # exact ties of bfloat16 (the dropped half is 0x8000) with odd and even kept parts
+    ties = (np.arange(1, 200, dtype=np.uint32) << 16 | 0x8000).view(np.float32)
+    return np.concatenate([base.astype(np.float32), ties, -ties])
+
+
+def test_round_bf16_matches_torch():
+    x = _special_values()
+    got = O.round_bf16(x)
+    ref = torch.tensor(x).to(torch.bfloat16).to(torch.float64).numpy()
+    same = (got == ref) | (np.isnan(got) & np.isnan(ref))
+    assert same.all(), x[~same][:8]
+
+
+def test_round_f16_matches_torch():
+    x = _special_values()
+    got = O.round_f16(x)
+    ref = torch.tensor(x).to(torch.float16).to(torch.float64).numpy()
+    same = (got == ref) | (np.isnan(got) & np.isnan(ref))
+    assert same.all()
+
+
+def test_planted_bf16_truncation_is_caught():
+    x = _special_values()
+    x = x[np.isfinite(x)]
+    trunc = (x.view(np.uint32) & 0xFFFF0000).view(np.float32).astype(np.float64)  # rounding towards zero
+    ref = torch.tensor(x).to(torch.bfloat16).to(torch.float64).numpy()
+    assert (trunc != ref).any()
+
+
+def test_grads_staged_reduces_to_grads_and_rounding_matters():
+    rng = np.random.default_rng(8)
+    e, c = rng.standard_normal((24, 16)), rng.standard_normal((300, 16)) * 0.3
+    b = rng.standard_normal(300) * 0.1
+    t = rng.integers(0, 300, 24)
+    t[3] = -100
+    for red in ("mean", "sum", "none"):
+        ref = O.grads(e, c, t, b, red)
+        same = O.grads_staged(e, c, t, b, red, stage=None)
+        for x, y in zip(same, ref):
+            np.testing.assert_array_equal(x, y)
+    dE, dC, dB = O.grads_staged(e, c, t, b, "sum", stage=O.round_bf16)
+    rE, rC, rB = O.grads(e, c, t, b, "sum")
+    np.testing.assert_array_equal(dB, rB)  # dBias sums the unrounded G
+    # rounding G to 8 significant bits moves dE by about its resolution, not more
+    assert 1e-4 < O.rel_fro(dE, rE) < 1e-2 and 1e-4 < O.rel_fro(dC, rC) < 1e-2
+

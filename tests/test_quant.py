@@ -235,11 +235,10 @@ def test_forward_q_equals_plain_forward(cuda, bias):
 @pytest.mark.gpu
 @pytest.mark.parametrize("bias", [False, True])
 @pytest.mark.parametrize("filtered", [False, True])
-def test_backward_q_equals_plain_backward(cuda, bias, filtered, monkeypatch):
+def test_backward_q_equals_plain_backward(cuda, bias, filtered):
     """dE and dBias bit for bit equal to the plain backward over the dequantized rows
     with the same vocabulary chunks (32 tiles = 4096 rows)."""
     import mlx_cce_amd as m
-    monkeypatch.setenv("CCE_TEST_CHUNK_VT", "32")
     e, qw, t, b = _peaked_q(cuda, 384, 256, 9000, torch.bfloat16, seed=22, bias=bias)
     t[::11] = -100
     cd = m.dequantize(qw)
@@ -248,7 +247,8 @@ def test_backward_q_equals_plain_backward(cuda, bias, filtered, monkeypatch):
     eps = m.FILTER_LOG_EPS if filtered else None
     st_p = torch.zeros(3, dtype=torch.int64, device=cuda)
     st_q = torch.zeros(3, dtype=torch.int64, device=cuda)
-    dE_p, _, dB_p = m._ext.backward(e, cd, t, lse, tm, d_nll, b, -100, eps, True, False, True, tile_stats=st_p)
+    with m._ext.backward_options(max_chunk_tiles=32):
+        dE_p, _, dB_p = m._ext.backward(e, cd, t, lse, tm, d_nll, b, -100, eps, True, False, True, tile_stats=st_p)
     dE_q, dB_q = m._ext.backward_q(e, qw, t, lse, tm, d_nll, b, -100, eps, True, True, tile_stats=st_q,
                                    chunk_rows=4096)
     torch.cuda.synchronize()
@@ -316,13 +316,12 @@ def test_quantized_rows_get_no_gradient(cuda):
 @pytest.mark.gpu
 @pytest.mark.parametrize("dtype,D,gs,bits", [(torch.bfloat16, 96, 32, 4), (torch.float16, 160, 32, 8),
                                                (torch.float32, 64, 32, 2)])
-def test_quantized_ragged_shapes_multi_chunk(cuda, dtype, D, gs, bits, monkeypatch):
+def test_quantized_ragged_shapes_multi_chunk(cuda, dtype, D, gs, bits):
     """Rows that are not a whole number of 128-byte slices (the zero-padded slice path),
     N not a multiple of the 128-row block, several chunks, ignore_index=None:
     the quantized passes equal the plain passes over the dequantized rows (forward to
     1e-5 across chunks, backward bit for bit with the same chunks)."""
     import mlx_cce_amd as m
-    monkeypatch.setenv("CCE_TEST_CHUNK_VT", "32")
     qw = _gpu_quant(cuda, 8500, D, gs, bits, dtype, seed=D + bits)
     g = torch.Generator(device=cuda).manual_seed(31)
     e = torch.randn((333, D), generator=g, device=cuda).to(dtype)
@@ -335,7 +334,8 @@ def test_quantized_ragged_shapes_multi_chunk(cuda, dtype, D, gs, bits, monkeypat
         torch.testing.assert_close(x, y, rtol=1e-5, atol=2e-5)
     tm, _, _, lse, _ = plain
     d_nll = torch.full((333,), 1.0 / 333, device=cuda)
-    dE_p, _, _ = m._ext.backward(e, cd, t, lse, tm, d_nll, None, None, m.FILTER_LOG_EPS, True, False, False)
+    with m._ext.backward_options(max_chunk_tiles=32):
+        dE_p, _, _ = m._ext.backward(e, cd, t, lse, tm, d_nll, None, None, m.FILTER_LOG_EPS, True, False, False)
     dE_q, _ = m._ext.backward_q(e, qw, t, lse, tm, d_nll, None, None, m.FILTER_LOG_EPS, True, False,
                                 chunk_rows=4096)
     torch.cuda.synchronize()
