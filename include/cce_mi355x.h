@@ -180,6 +180,32 @@ int cce_backward_ex(int dtype, const void* e, const void* c, const void* bias,
                     int64_t* tile_stats, int flags, int64_t max_chunk_tiles, void* hip_stream);
 
 /*
+ * Backward without any allocation -- no counterpart in the reference.  For callers
+ * that cannot call hipMalloc or take a caller-owned workspace: code under HIP graph
+ * capture, tight serving loops, harnesses that forbid allocation.  As cce_backward_ex
+ * (max_chunk_tiles 0), with the workspace taken from a static device array of
+ * CCE_NOALLOC_SCRATCH_BYTES (64 MiB) that every GPU the library runs on holds from
+ * its first call until the process ends.  The backward then runs in passes that fit
+ * the array; a problem whose least workspace (cce_backward_workspace_size_ex with
+ * max_g_tiles = 1) exceeds it is refused with CCE_ERR_WORKSPACE before any device
+ * work.  The caller still passes the inputs and the outputs.  Every call on one GPU
+ * shares that GPU's array: calls that overlap on one GPU (other streams, other
+ * threads) race and give wrong results; calls ordered on one stream are safe.
+ */
+#define CCE_NOALLOC_SCRATCH_BYTES (64ull << 20)
+
+/* Bytes of the static scratch cce_backward_noalloc uses (CCE_NOALLOC_SCRATCH_BYTES). */
+size_t cce_backward_noalloc_scratch_size(void);
+
+int cce_backward_noalloc(int dtype, const void* e, const void* c, const void* bias,
+                         const int64_t* targets, int64_t ignore_index, int has_ignore,
+                         int64_t N, int64_t D, int64_t V,
+                         const float* lse, const float* tile_max, const float* d_nll,
+                         float filter_log_eps,
+                         void* dE, void* dC, void* dBias,
+                         int64_t* tile_stats, int flags, void* hip_stream);
+
+/*
  * Quantized classifier rows.  The reference's callers pass an lm_head / tied
  * embedding stored with MLX's affine group quantization through mx.dequantize
  * before the loss (README.md:84-95,136; examples/mlx_lm_lora_test.py:16-21),

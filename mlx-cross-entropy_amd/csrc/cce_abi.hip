@@ -7,14 +7,20 @@
 // lifted: ragged N and V are masked inside the kernels.  Rows must be 16-byte
 // multiples (D % 8 == 0 for 16-bit dtypes, D % 4 == 0 for fp32); the reference
 // requires D % 8 == 0 for every dtype.
-#include <cstdlib>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 
 #include "cce_launch.h"
 #include "cce_mi355x.h"
+
+// Workspace of cce_backward_noalloc: one static array per GPU, held from the first
+// call on that GPU until the process ends.  Host code never uses this name as an
+// address (on the host it is a stand-in symbol); it uses the device address that
+// hipGetSymbolAddress returns for the current device.
+static __device__ __align__(256) char scratch[CCE_NOALLOC_SCRATCH_BYTES];
 
 namespace {
 
@@ -334,6 +340,77 @@ int cce_backward_ex(int dtype, const void* e, const void* c, const void* bias, c
   if (rc != CCE_OK) return rc;
   return backward_impl(dtype, e, c, bias, targets, ignore_index, has_ignore, N, D, V, lse, tile_max, d_nll,
                        filter_log_eps, dE, dC, dBias, workspace, workspace_bytes, tile_stats, flags, max_chunk_tiles,
+                       nullptr, hip_stream);
+}
+
+}  // extern "C"
+
+namespace {
+
+// Device address of `scratch` on each device, found once per device (with that
+// device current) and kept: every GPU holds its own copy at its own address.
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+int scratch_of_current_device(const char* fn, void** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0)
+    return fail(CCE_ERR_NO_DEVICE, "[%s] no HIP device is available", fn);
+  if (dev >= kMaxDevices) return fail(CCE_ERR_NO_DEVICE, "[%s] device %d is past the %d the library serves", fn, dev,
+                                      kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || p == nullptr)
+      return fail(CCE_ERR_NO_DEVICE, "[%s] hipGetSymbolAddress of the static scratch failed on device %d: %s", fn,
+                  dev, hipGetErrorString(err));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return CCE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t cce_backward_noalloc_scratch_size(void) { return (size_t)CCE_NOALLOC_SCRATCH_BYTES; }
+
+int cce_backward_noalloc(int dtype, const void* e, const void* c, const void* bias, const int64_t* targets,
+                         int64_t ignore_index, int has_ignore, int64_t N, int64_t D, int64_t V, const float* lse,
+                         const float* tile_max, const float* d_nll, float filter_log_eps, void* dE, void* dC,
+                         void* dBias, int64_t* tile_stats, int flags, void* hip_stream) {
+  g_err[0] = 0;
+  constexpr int kKnown = CCE_BWD_DC_ZEROED | CCE_BWD_TOKENS_INPUT | CCE_BWD_TOKENS_SORTED | CCE_BWD_DE_SUMS_WIDE |
+                         CCE_BWD_DE_SUMS_NARROW | CCE_BWD_DC_SUMS_WIDE | CCE_BWD_DC_SUMS_NARROW;
+  if (flags & ~kKnown)
+    return fail(CCE_ERR_INVALID_ARGUMENT, "[cce_backward_noalloc] unknown flags 0x%x", flags);
+  if (((flags & CCE_BWD_TOKENS_INPUT) && (flags & CCE_BWD_TOKENS_SORTED)) ||
+      ((flags & CCE_BWD_DE_SUMS_WIDE) && (flags & CCE_BWD_DE_SUMS_NARROW)) ||
+      ((flags & CCE_BWD_DC_SUMS_WIDE) && (flags & CCE_BWD_DC_SUMS_NARROW)))
+    return fail(CCE_ERR_INVALID_ARGUMENT, "[cce_backward_noalloc] a pair of flags excludes each other");
+  int rc = check_common("cce_backward_noalloc", dtype, e, c, targets, N, D, V);
+  if (rc != CCE_OK) return rc;
+  // Sizes beyond what the static scratch holds are refused before any device work.
+  const size_t es = elem_size(dtype);
+  bool fits = false;
+  cce::plan_for_workspace(es, N, D, V, dE != nullptr, dC != nullptr, dBias != nullptr, 0, false,
+                          (size_t)CCE_NOALLOC_SCRATCH_BYTES, fits);
+  if (!fits) {
+    const size_t least =
+        cce::make_bwd_plan_cap(es, N, D, V, dE != nullptr, dC != nullptr, dBias != nullptr, 1, false, 0, false)
+            .total_bytes;
+    return fail(CCE_ERR_WORKSPACE,
+                "[cce_backward_noalloc] N=%lld D=%lld V=%lld needs at least %zu bytes of workspace; the static scratch "
+                "holds %zu (call cce_backward with a workspace instead)",
+                (long long)N, (long long)D, (long long)V, least, (size_t)CCE_NOALLOC_SCRATCH_BYTES);
+  }
+  void* ws = nullptr;
+  if ((rc = scratch_of_current_device("cce_backward_noalloc", &ws)) != CCE_OK) return rc;
+  return backward_impl(dtype, e, c, bias, targets, ignore_index, has_ignore, N, D, V, lse, tile_max, d_nll,
+                       filter_log_eps, dE, dC, dBias, ws, (size_t)CCE_NOALLOC_SCRATCH_BYTES, tile_stats, flags, 0,
                        nullptr, hip_stream);
 }
 

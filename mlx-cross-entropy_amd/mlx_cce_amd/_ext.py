@@ -46,6 +46,9 @@ SIGNATURES = {
                               _P]),
     "cce_backward_ex": (_INT, [_INT, _P, _P, _P, _P, _I64, _INT, _I64, _I64, _I64, _P, _P, _P, ctypes.c_float,
                                _P, _P, _P, _P, ctypes.c_size_t, _P, _INT, _I64, _P]),
+    "cce_backward_noalloc_scratch_size": (ctypes.c_size_t, []),
+    "cce_backward_noalloc": (_INT, [_INT, _P, _P, _P, _P, _I64, _INT, _I64, _I64, _I64, _P, _P, _P, ctypes.c_float,
+                                    _P, _P, _P, _P, _INT, _P]),
     "cce_dequantize": (_INT, [_INT, _P, _P, _P, _INT, _INT, _I64, _I64, _P, _P]),
     "cce_forward_q_scratch_size": (ctypes.c_size_t, [_INT, _I64, _I64, _I64]),
     "cce_forward_q": (_INT, [_INT, _P, _P, _P, _P, _INT, _INT, _P, _P, _I64, _INT, _I64, _I64, _I64, _P, _P, _P, _P,
@@ -312,6 +315,44 @@ def backward(e, c, targets, lse, tile_max, d_nll, bias=None, ignore_index=-100,
             ev[1].record()
     if rc != CCE_OK:
         _raise(rc, "cce_backward")
+    return dE, dC, dB
+
+
+def backward_noalloc(e, c, targets, lse, tile_max, d_nll, bias=None, ignore_index=-100,
+                     filter_eps=FILTER_LOG_EPS, want_de=True, want_dc=True, want_db=True, tile_stats=None,
+                     dE=None, dC=None, dB=None):
+    """backward() through cce_backward_noalloc: the library takes no workspace and
+    allocates nothing (its static device scratch of cce_backward_noalloc_scratch_size()
+    bytes); the outputs are allocated here unless passed in.  Returns (dE, dC, dBias)."""
+    code = _prep(e, c, targets, bias)
+    for name, t in (("e", e), ("c", c), ("targets", targets), ("lse", lse), ("tile_max", tile_max),
+                    ("d_nll", d_nll)):
+        if not t.is_contiguous():
+            raise ValueError(f"[cce_backward_noalloc] {name} must be contiguous")
+    if d_nll.dtype != torch.float32 or lse.dtype != torch.float32 or targets.dtype != torch.int64:
+        raise TypeError("[cce_backward_noalloc] lse and d_nll must be float32, targets int64")
+    want_db = bool(want_db and bias is not None)
+    N, D = e.shape
+    if d_nll.shape != (N,) or lse.shape != (N,):
+        raise ValueError("[cce_backward_noalloc] lse and d_nll must be [N]")
+    if want_de and dE is None:
+        dE = torch.empty_like(e)
+    if want_dc and dC is None:
+        dC = torch.empty_like(c)
+    if want_db and dB is None:
+        dB = torch.empty_like(bias)
+    dE, dC, dB = (dE if want_de else None), (dC if want_dc else None), (dB if want_db else None)
+    eps = -math.inf if filter_eps is None else float(filter_eps)
+    has_ignore = ignore_index is not None
+    with torch.cuda.device(e.device):
+        stream = torch.cuda.current_stream(e.device).cuda_stream
+        rc = lib().cce_backward_noalloc(code, _ptr(e), _ptr(c), _ptr(bias), _ptr(targets),
+                                        int(ignore_index) if has_ignore else 0, 1 if has_ignore else 0,
+                                        N, D, c.shape[0], _ptr(lse), _ptr(tile_max), _ptr(d_nll), ctypes.c_float(eps),
+                                        _ptr(dE), _ptr(dC), _ptr(dB), _ptr(tile_stats), _bwd_opts["flags"],
+                                        ctypes.c_void_p(stream))
+    if rc != CCE_OK:
+        _raise(rc, "cce_backward_noalloc")
     return dE, dC, dB
 
 

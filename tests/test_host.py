@@ -163,6 +163,25 @@ def test_backward_validation_errors(ext):
         assert _bwd_ex(lib, ws_bytes=least) == ext.CCE_ERR_NO_DEVICE
 
 
+def _noalloc(lib, N=64, D=64, V=256, flags=0):
+    return lib.cce_backward_noalloc(2, FAKE, FAKE, None, FAKE, -100, 1, N, D, V, FAKE, FAKE, FAKE,
+                                    ctypes.c_float(-8.3), FAKE, FAKE, None, None, flags, None)
+
+
+def test_noalloc_validation(ext):
+    """cce_backward_noalloc refuses a problem past its static scratch before any device
+    work (the fp32 dE carry of N=8192, D=4096 alone is 128 MiB of its 64 MiB)."""
+    lib = ext.lib()
+    assert lib.cce_backward_noalloc_scratch_size() == 64 << 20
+    assert _noalloc(lib, N=8192, D=4096, V=128256) == ext.CCE_ERR_WORKSPACE
+    msg = lib.cce_last_error()
+    assert b"static scratch" in msg and b"N=8192" in msg
+    assert _noalloc(lib, flags=1 << 12) == ext.CCE_ERR_INVALID_ARGUMENT
+    assert _noalloc(lib, N=0) == ext.CCE_ERR_INVALID_ARGUMENT
+    if not gpu_available():  # fits: stops at the device lookup
+        assert _noalloc(lib) == ext.CCE_ERR_NO_DEVICE
+
+
 def test_reduction_helpers_validation_errors(ext):
     lib = ext.lib()
     assert lib.cce_reduce_loss(FAKE, FAKE, -100, 1, 0, ext.CCE_REDUCE_MEAN, FAKE, None, None) == ext.CCE_ERR_INVALID_ARGUMENT
