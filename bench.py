@@ -9,8 +9,11 @@ V=128256, bf16), the configuration the headline metric is quoted on.
 
 Prints one JSON line.  `value` is tokens/s of the whole job; `roofline` is the
 forward kernel pair (tile kernel + lse combine, timed with HIP events on the
-stream they run on) against the bf16 MFMA peak; `cpu_baseline` is the float32
-torch-CPU restatement of the reference's materialised-logits path timed on a
+stream they run on) against the bf16 MFMA peak; `step.mfma_frac` is the whole step
+against the peak for the MFMA work it performed (forward + the backward's three
+products over the tiles it computed); `dense` is the same step with the tile filter
+off (every tile: 8 N D V FLOPs), timed in the same run; `cpu_baseline` is the
+float32 torch-CPU restatement of the reference's materialised-logits path timed on a
 bounded slice of the same workload on this host.
 
 --quantize BITS (2, 4 or 8; not the default) stores the classifier rows in affine
@@ -73,6 +76,8 @@ def main():
     ap.add_argument("--cpu-baseline", default="on", choices=["on", "off"])
     ap.add_argument("--quantize", type=int, default=0, choices=[0, 2, 4, 8],
                     help="classifier rows in BITS-bit affine groups of 64 (frozen head: no dC)")
+    ap.add_argument("--dense-steps", type=int, default=3,
+                    help="steps of the filter-off (dense) leg timed after the main ones (0: skip it)")
     ap.add_argument("--cpu-rows", type=int, default=1024)
     ap.add_argument("--cpu-budget", type=float, default=12.0)
     ap.add_argument("--calib-copy-mib", type=int, default=0,
@@ -108,13 +113,14 @@ def main():
     feps = cce.FILTER_LOG_EPS if args.filter == "on" else None
     up = torch.ones(N, device=dev) if red == "none" else None
 
-    def step():
+    def step(filter_eps=feps):
         e.grad = None
         if qw is None:
             c.grad = None
         if b is not None:
             b.grad = None
-        loss = cce.linear_cross_entropy(e, c, t, b, reduction=red, ignore_index=w["ignore_index"], filter_eps=feps)
+        loss = cce.linear_cross_entropy(e, c, t, b, reduction=red, ignore_index=w["ignore_index"],
+                                        filter_eps=filter_eps)
         loss.backward(up)
         return loss
 
@@ -147,6 +153,27 @@ def main():
         step()
     tm["backward"] = _ext.timings_ms()["backward"]
     _ext.set_timing(False)
+    dense = None
+    if args.dense_steps > 0 and feps is not None:
+        # The conservative figure: every tile computed (filter off), same inputs.
+        _ext.set_timing(True)
+        step(None)
+        torch.cuda.synchronize()
+        _ext.set_timing(True)
+        td0 = time.perf_counter()
+        for i in range(args.dense_steps):
+            step(None)
+        torch.cuda.synchronize()
+        dense_ms = (time.perf_counter() - td0) * 1e3 / args.dense_steps
+        tmd = _ext.timings_ms()
+        _ext.set_timing(False)
+        dfl = workloads.flops(N, D, V, 0.0, qw is None)
+        dense = {"ms_per_step": dense_ms, "tokens_per_s": N / (dense_ms * 1e-3), "flops": dfl,
+                 "tflops": dfl / (dense_ms * 1e-3) / 1e12,
+                 "mfma_frac": dfl / (dense_ms * 1e-3) / 1e12 / PEAK_TFLOPS[dt],
+                 "fwd_ms": statistics.mean(tmd["forward"]), "bwd_ms": statistics.mean(tmd["backward"]),
+                 "steps": args.dense_steps, "note": "filter off: every 128x128 tile, 8NDV (6NDV without dC)"}
+        log(f"bench: dense leg {dense_ms:.2f} ms/step")
     if args.calib_copy_mib > 0:
         src = torch.empty(args.calib_copy_mib << 20, dtype=torch.uint8, device=dev)
         dst = torch.empty_like(src)
@@ -161,12 +188,14 @@ def main():
     peak = PEAK_TFLOPS[dt]
     fwd_flops = 2.0 * N * D * V
     achieved = fwd_flops / (fwd_ms * 1e-3) / 1e12
-    # Non-filtered FLOPs: the forward plus the backward's three GEMMs over the tiles the
-    # 2^-12 filter keeps with token blocks taken in input order; the backward may
-    # group the rows by target tile and then computes fewer tiles (performed_flops).
+    # MFMA work of the step as performed: the forward plus the backward's three GEMMs
+    # over the tiles it computed (the 2^-12 filter's kept tiles, with the rows grouped
+    # by target tile when that keeps fewer).  The non-filtered FLOPs of the metric's
+    # definition with token blocks in input order (more tiles kept, never computed
+    # when the rows are grouped) are reported beside it, labelled.
     want_dc = qw is None
-    step_flops = workloads.flops(N, D, V, skip_in, want_dc)
     performed_flops = workloads.flops(N, D, V, skip, want_dc)
+    input_order_flops = workloads.flops(N, D, V, skip_in, want_dc)
     dense_flops = workloads.flops(N, D, V, 0.0, want_dc)
 
     out = {
@@ -195,15 +224,16 @@ def main():
                      "achieved": achieved, "peak": peak, "unit": "TFLOP/s", "frac": achieved / peak,
                      "traffic": traffic_from_profiles(args.workload, args.filter) if qw is None else None,
                      "flops_per_launch": fwd_flops, "avg_launch_ms": fwd_ms},
-        "step": {"fwd_ms": fwd_ms, "bwd_ms": bwd_ms, "tile_skip_input_order": skip_in,
-                 "kept_tiles_input_order": kept_in, "total_tiles": total,
+        "step": {"fwd_ms": fwd_ms, "bwd_ms": bwd_ms, "total_tiles": total,
                  "rows_grouped_by_target": bool(fs["sorted_rows"]), "tile_skip": skip, "kept_tiles": kept,
-                 "algorithmic_flops": step_flops, "tflops": step_flops / (ms * 1e-3) / 1e12,
-                 "mfma_frac": step_flops / (ms * 1e-3) / 1e12 / peak,
-                 "performed_flops": performed_flops,
-                 "mfma_frac_performed": performed_flops / (ms * 1e-3) / 1e12 / peak,
+                 "performed_flops": performed_flops, "tflops": performed_flops / (ms * 1e-3) / 1e12,
+                 "mfma_frac": performed_flops / (ms * 1e-3) / 1e12 / peak,
+                 "kept_tiles_input_order": kept_in, "tile_skip_input_order": skip_in,
+                 "input_order_flops": input_order_flops,
+                 "mfma_frac_input_order_flops": input_order_flops / (ms * 1e-3) / 1e12 / peak,
                  "dense_flops": dense_flops,
                  "peak_mem_gb": peak_mem / 2 ** 30, "logits_bytes_if_materialised": 4.0 * N * V},
+        "dense": dense,
         "cpu_baseline": None,
     }
     if args.cpu_baseline == "on":
