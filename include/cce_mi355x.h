@@ -66,6 +66,10 @@ void cce_tile_config(int* fwd_tokens, int* fwd_vocab, int* stat_tile, int* bwd_t
 /* Number of vocabulary statistic tiles: ceil(V / CCE_STAT_TILE). */
 int64_t cce_num_vocab_tiles(int64_t V);
 
+/* The reference's statistic tile (32 columns) and the number of them: ceil(V / 32). */
+#define CCE_REF_STAT_TILE 32
+int64_t cce_num_ref_tiles(int64_t V);
+
 /*
  * Forward pass.  Replaces cce_forward_raw (csrc/bindings.cpp:58-69, cce.cpp:123-145)
  * and CutCrossEntropy::eval_gpu (cce.cpp:207-277): one fused tiled-MFMA kernel that
@@ -98,6 +102,20 @@ int cce_forward_ex(int dtype, const void* e, const void* c, const void* bias,
                    int64_t N, int64_t D, int64_t V,
                    float* tile_max, float* tile_sum_exp, float* neg_target_logit,
                    float* lse, float* nll, void* zero_buf, int64_t zero_bytes, void* hip_stream);
+
+/*
+ * As cce_forward, with tile_max and tile_sum_exp in the reference's layout: per 32
+ * vocabulary columns, flat [N * ceil(V/32)], row major per row of e -- what
+ * cce_forward_raw returns in the reference (csrc/bindings.cpp:58-69, cce.cpp:123-145)
+ * and its glue reshapes to (B, (V + 31) // 32) (mlx_cce/__init__.py:25-30).  lse and
+ * nll are merged from those tiles (reference reduce_tile_to_lse, cce.metal:332-355).
+ * A later cce_backward_ex(..., CCE_BWD_REF_STATS) takes this tile_max as it is.
+ */
+int cce_forward_ref(int dtype, const void* e, const void* c, const void* bias,
+                    const int64_t* targets, int64_t ignore_index, int has_ignore,
+                    int64_t N, int64_t D, int64_t V,
+                    float* tile_max, float* tile_sum_exp, float* neg_target_logit,
+                    float* lse, float* nll, void* hip_stream);
 
 /*
  * Bytes of the default device workspace of cce_backward for these sizes and outputs.
@@ -165,6 +183,9 @@ int cce_backward(int dtype, const void* e, const void* c, const void* bias,
 #define CCE_BWD_DE_SUMS_NARROW 16 /* dE sums in 256-column tasks */
 #define CCE_BWD_DC_SUMS_WIDE 32   /* dC sums in 512-column tasks */
 #define CCE_BWD_DC_SUMS_NARROW 64 /* dC sums in 256-column tasks */
+/* tile_max is in the reference's layout (cce_forward_ref: per 32 columns, [N][ceil(V/32)]);
+ * the filter takes each 128-column tile's max as the max of its four 32-column maxima. */
+#define CCE_BWD_REF_STATS 128
 
 /* As cce_backward, with flags (CCE_BWD_*) and vocabulary chunks of at most
  * max_chunk_tiles tiles (0: the library's choice; else a multiple of 32; the workspace

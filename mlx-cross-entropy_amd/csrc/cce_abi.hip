@@ -120,6 +120,49 @@ int check_chunk_rows(const char* fn, int64_t chunk_rows) {
   return CCE_OK;
 }
 
+// cce_forward_ex / cce_forward_ref: stats32 selects the statistics' layout.
+int forward_impl(const char* fn, int dtype, const void* e, const void* c, const void* bias, const int64_t* targets,
+                 int64_t ignore_index, int has_ignore, int64_t N, int64_t D, int64_t V, float* tile_max,
+                 float* tile_sum_exp, float* neg_target_logit, float* lse, float* nll, void* zero_buf,
+                 int64_t zero_bytes, int stats32, void* hip_stream) {
+  g_err[0] = 0;
+  int rc = check_common(fn, dtype, e, c, targets, N, D, V);
+  if (rc != CCE_OK) return rc;
+  if (!tile_max || !tile_sum_exp || !neg_target_logit || !lse || !nll)
+    return fail(CCE_ERR_INVALID_ARGUMENT, "[%s] tile_max, tile_sum_exp, neg_target_logit, lse and nll must be non-null",
+                fn);
+  if (bias && !aligned(bias, elem_size(dtype)))
+    return fail(CCE_ERR_INVALID_ARGUMENT, "[%s] bias is not aligned to its element size", fn);
+  if (zero_bytes < 0 || zero_bytes % 16 != 0 || (zero_bytes > 0 && (!zero_buf || !aligned(zero_buf, 16))))
+    return fail(CCE_ERR_INVALID_ARGUMENT,
+                "[%s] zero_buf must be 16-byte aligned and zero_bytes a non-negative multiple of 16", fn);
+  const int cus = num_cus_current();
+  if (cus <= 0) return fail(CCE_ERR_NO_DEVICE, "[%s] no HIP device is available", fn);
+  cce::FwdArgs a{};
+  a.e = e;
+  a.c = c;
+  a.bias = bias;
+  a.targets = targets;
+  a.ignore_index = ignore_index;
+  a.has_ignore = has_ignore ? 1 : 0;
+  a.N = N;
+  a.D = D;
+  a.V = V;
+  a.tile_max = tile_max;
+  a.tile_sum_exp = tile_sum_exp;
+  a.neg_target_logit = neg_target_logit;
+  a.lse = lse;
+  a.nll = nll;
+  a.num_cus = cus;
+  a.zero_buf = zero_bytes > 0 ? zero_buf : nullptr;
+  a.zero_units = zero_bytes / 16;
+  a.stats32 = stats32;
+  hipError_t err = cce::launch_forward(dtype, a, reinterpret_cast<hipStream_t>(hip_stream));
+  if (err != hipSuccess)
+    return fail(CCE_ERR_LAUNCH, "[%s] kernel launch failed: %s", fn, hipGetErrorString(err));
+  return CCE_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -145,46 +188,21 @@ int cce_forward(int dtype, const void* e, const void* c, const void* bias, const
                         neg_target_logit, lse, nll, nullptr, 0, hip_stream);
 }
 
+int64_t cce_num_ref_tiles(int64_t V) { return V <= 0 ? 0 : (V + cce::kRefStatTile - 1) / cce::kRefStatTile; }
+
 int cce_forward_ex(int dtype, const void* e, const void* c, const void* bias, const int64_t* targets,
                    int64_t ignore_index, int has_ignore, int64_t N, int64_t D, int64_t V, float* tile_max,
                    float* tile_sum_exp, float* neg_target_logit, float* lse, float* nll, void* zero_buf,
                    int64_t zero_bytes, void* hip_stream) {
-  g_err[0] = 0;
-  int rc = check_common("cce_forward", dtype, e, c, targets, N, D, V);
-  if (rc != CCE_OK) return rc;
-  if (!tile_max || !tile_sum_exp || !neg_target_logit || !lse || !nll)
-    return fail(CCE_ERR_INVALID_ARGUMENT,
-                "[cce_forward] tile_max, tile_sum_exp, neg_target_logit, lse and nll must be non-null");
-  if (bias && !aligned(bias, elem_size(dtype)))
-    return fail(CCE_ERR_INVALID_ARGUMENT, "[cce_forward] bias is not aligned to its element size");
-  if (zero_bytes < 0 || zero_bytes % 16 != 0 || (zero_bytes > 0 && (!zero_buf || !aligned(zero_buf, 16))))
-    return fail(CCE_ERR_INVALID_ARGUMENT,
-                "[cce_forward] zero_buf must be 16-byte aligned and zero_bytes a non-negative multiple of 16");
-  const int cus = num_cus_current();
-  if (cus <= 0) return fail(CCE_ERR_NO_DEVICE, "[cce_forward] no HIP device is available");
+  return forward_impl("cce_forward", dtype, e, c, bias, targets, ignore_index, has_ignore, N, D, V, tile_max,
+                      tile_sum_exp, neg_target_logit, lse, nll, zero_buf, zero_bytes, 0, hip_stream);
+}
 
-  cce::FwdArgs a{};
-  a.e = e;
-  a.c = c;
-  a.bias = bias;
-  a.targets = targets;
-  a.ignore_index = ignore_index;
-  a.has_ignore = has_ignore ? 1 : 0;
-  a.N = N;
-  a.D = D;
-  a.V = V;
-  a.tile_max = tile_max;
-  a.tile_sum_exp = tile_sum_exp;
-  a.neg_target_logit = neg_target_logit;
-  a.lse = lse;
-  a.nll = nll;
-  a.num_cus = cus;
-  a.zero_buf = zero_bytes > 0 ? zero_buf : nullptr;
-  a.zero_units = zero_bytes / 16;
-  hipError_t err = cce::launch_forward(dtype, a, reinterpret_cast<hipStream_t>(hip_stream));
-  if (err != hipSuccess)
-    return fail(CCE_ERR_LAUNCH, "[cce_forward] kernel launch failed: %s", hipGetErrorString(err));
-  return CCE_OK;
+int cce_forward_ref(int dtype, const void* e, const void* c, const void* bias, const int64_t* targets,
+                    int64_t ignore_index, int has_ignore, int64_t N, int64_t D, int64_t V, float* tile_max,
+                    float* tile_sum_exp, float* neg_target_logit, float* lse, float* nll, void* hip_stream) {
+  return forward_impl("cce_forward_ref", dtype, e, c, bias, targets, ignore_index, has_ignore, N, D, V, tile_max,
+                      tile_sum_exp, neg_target_logit, lse, nll, nullptr, 0, 1, hip_stream);
 }
 
 size_t cce_backward_workspace_size(int dtype, int64_t N, int64_t D, int64_t V, int want_dE, int want_dC,
@@ -302,6 +320,7 @@ int backward_impl(int dtype, const void* e, const void* c, const void* bias, con
   a.dc_geo = (flags & CCE_BWD_DC_SUMS_WIDE) ? 1 : (flags & CCE_BWD_DC_SUMS_NARROW) ? 2 : 0;
   a.tile_stats = tile_stats;
   a.dc_zeroed = (flags & CCE_BWD_DC_ZEROED) ? 1 : 0;
+  a.stats32 = (flags & CCE_BWD_REF_STATS) ? 1 : 0;
   a.plan = P;
   a.num_cus = cus;
   if (q) {
@@ -326,7 +345,8 @@ int cce_backward_ex(int dtype, const void* e, const void* c, const void* bias, c
                     int64_t max_chunk_tiles, void* hip_stream) {
   g_err[0] = 0;
   constexpr int kKnown = CCE_BWD_DC_ZEROED | CCE_BWD_TOKENS_INPUT | CCE_BWD_TOKENS_SORTED | CCE_BWD_DE_SUMS_WIDE |
-                         CCE_BWD_DE_SUMS_NARROW | CCE_BWD_DC_SUMS_WIDE | CCE_BWD_DC_SUMS_NARROW;
+                         CCE_BWD_DE_SUMS_NARROW | CCE_BWD_DC_SUMS_WIDE | CCE_BWD_DC_SUMS_NARROW |
+                         CCE_BWD_REF_STATS;
   if (flags & ~kKnown) return fail(CCE_ERR_INVALID_ARGUMENT, "[cce_backward] unknown flags 0x%x", flags);
   if ((flags & CCE_BWD_TOKENS_INPUT) && (flags & CCE_BWD_TOKENS_SORTED))
     return fail(CCE_ERR_INVALID_ARGUMENT, "[cce_backward] CCE_BWD_TOKENS_INPUT and CCE_BWD_TOKENS_SORTED exclude each other");
@@ -384,7 +404,8 @@ int cce_backward_noalloc(int dtype, const void* e, const void* c, const void* bi
                          void* dBias, int64_t* tile_stats, int flags, void* hip_stream) {
   g_err[0] = 0;
   constexpr int kKnown = CCE_BWD_DC_ZEROED | CCE_BWD_TOKENS_INPUT | CCE_BWD_TOKENS_SORTED | CCE_BWD_DE_SUMS_WIDE |
-                         CCE_BWD_DE_SUMS_NARROW | CCE_BWD_DC_SUMS_WIDE | CCE_BWD_DC_SUMS_NARROW;
+                         CCE_BWD_DE_SUMS_NARROW | CCE_BWD_DC_SUMS_WIDE | CCE_BWD_DC_SUMS_NARROW |
+                         CCE_BWD_REF_STATS;
   if (flags & ~kKnown)
     return fail(CCE_ERR_INVALID_ARGUMENT, "[cce_backward_noalloc] unknown flags 0x%x", flags);
   if (((flags & CCE_BWD_TOKENS_INPUT) && (flags & CCE_BWD_TOKENS_SORTED)) ||

@@ -97,8 +97,20 @@ __device__ __forceinline__ void filter_item(const BwdArgs& a, int item) {
     for (int u = 0; u < 8; ++u) {
       const int vt = vt0 + b0 + u;
 #pragma unroll
-      for (int k = 0; k < 2; ++k)
-        tm[u][k] = (vt < nvt && act[k]) ? a.tile_max[(size_t)vt * a.N + row[k]] : -INFINITY;
+      for (int k = 0; k < 2; ++k) {
+        tm[u][k] = -INFINITY;
+        if (vt < nvt && act[k]) {
+          if (a.stats32) {  // the reference's layout: the max of the tile's four 32-column maxima
+            const int64_t nt = (a.V + kRefStatTile - 1) / kRefStatTile;
+            const float* p = a.tile_max + row[k] * nt;
+#pragma unroll
+            for (int q = 0; q < kStatTile / kRefStatTile; ++q)
+              if (vt * (kStatTile / kRefStatTile) + q < nt) tm[u][k] = fmaxf(tm[u][k], p[vt * (kStatTile / kRefStatTile) + q]);
+          } else {
+            tm[u][k] = a.tile_max[(size_t)vt * a.N + row[k]];
+          }
+        }
+      }
     }
 #pragma unroll
     for (int u = 0; u < 8; ++u) {

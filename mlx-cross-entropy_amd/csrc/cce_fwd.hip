@@ -54,7 +54,9 @@ struct FwdSched {
 // and 128-column tile the max and sum of exp(logit - max), and the target gather.
 // acc[i][j][r] holds logit(vocab = vbase + 32i + 8(r/4) + 4h + r%4,
 //                          token = tbase + 32j + n)   with n = lane%32, h = lane/32.
-template <typename T, bool HAS_BIAS, int TI, int TJ>
+// S32: the statistics per 32 columns (the four 32-row blocks i of the wave's tile)
+// in the reference's layout, [N][ceil(V/32)], instead of per 128 columns.
+template <typename T, bool HAS_BIAS, bool S32, int TI, int TJ>
 __device__ __forceinline__ void fwd_epilogue(const FwdArgs& a, int nvt, f32x16 (&acc)[TI][TJ], int tb, int vb,
                                              const int64_t (&tg)[TJ]) {
   static_assert(TI == 4, "a wave covers one 128-column statistic tile");
@@ -97,6 +99,26 @@ __device__ __forceinline__ void fwd_epilogue(const FwdArgs& a, int nvt, f32x16 (
   for (int j = 0; j < TJ; ++j) {
     const int64_t tok = tbase + j * 32 + n;
 
+    if constexpr (S32) {
+      const int64_t nt = (a.V + kRefStatTile - 1) / kRefStatTile;
+      const int64_t g0 = vbase / kRefStatTile;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float m = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) m = fmaxf(m, acc[i][j][r]);
+        m = fmaxf(m, __shfl_xor(m, 32));
+        const float mb = (m == -INFINITY) ? 0.f : m * kLog2e;
+        float s = 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s += __builtin_amdgcn_exp2f(fmaf(acc[i][j][r], kLog2e, -mb));
+        s += __shfl_xor(s, 32);
+        if (h == 0 && tok < a.N && g0 + i < nt) {
+          a.tile_max[tok * nt + g0 + i] = m;
+          a.tile_sum_exp[tok * nt + g0 + i] = s;
+        }
+      }
+    } else {
     float m = -INFINITY;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -114,6 +136,7 @@ __device__ __forceinline__ void fwd_epilogue(const FwdArgs& a, int nvt, f32x16 (
     if (h == 0 && tok < a.N && tile < nvt) {
       a.tile_max[(size_t)tile * a.N + tok] = m;
       a.tile_sum_exp[(size_t)tile * a.N + tok] = s;
+    }
     }
 
     // Target gather: the lane holding (target, token) writes -(logit + bias).
@@ -135,7 +158,7 @@ __device__ __forceinline__ void fwd_epilogue(const FwdArgs& a, int nvt, f32x16 (
   }
 }
 
-template <typename T, bool HAS_BIAS, bool RAGGED>
+template <typename T, bool HAS_BIAS, bool RAGGED, bool S32>
 __global__ __launch_bounds__(FwdLoop<T>::NTHREADS, 1) void fwd_tile_kernel(FwdArgs a, FwdSched sc) {
   using Loop = FwdLoop<T>;
   constexpr int TI = Loop::TI, TJ = Loop::TJ;
@@ -216,7 +239,7 @@ __global__ __launch_bounds__(FwdLoop<T>::NTHREADS, 1) void fwd_tile_kernel(FwdAr
       Loop::template prefetch<RAGGED>(src, smem);
       targets(tbn, tgn);
     }
-    fwd_epilogue<T, HAS_BIAS>(a, sc.nvt, acc, tb, vb, tg);
+    fwd_epilogue<T, HAS_BIAS, S32>(a, sc.nvt, acc, tb, vb, tg);
     zero_upto(min(zc + zpiece, z1));
     if (rn >= r_end) break;
     r = rn;
@@ -236,6 +259,21 @@ __device__ __forceinline__ void lse_merge(float& M, float& S, float m, float s) 
   } else {
     S += s * __expf(m - M);
   }
+}
+
+// lse[tok] = l and the masked per-token loss (mlx_cce/__init__.py:59-70).
+__device__ __forceinline__ void nll_of(const FwdArgs& a, int64_t tok, float l) {
+  a.lse[tok] = l;
+  const int64_t tg = a.targets[tok];
+  float out;
+  if (a.has_ignore && tg == a.ignore_index) {
+    out = 0.f;
+  } else if (tg < 0 || tg >= a.V) {
+    out = __builtin_nanf("");
+  } else {
+    out = l + a.neg_target_logit[tok];
+  }
+  a.nll[tok] = out;
 }
 
 // 64 tokens per workgroup (one per lane, coalesced 256-byte rows); the 16 waves
@@ -270,35 +308,47 @@ __global__ __launch_bounds__(64 * kLseSplits) void lse_kernel(FwdArgs a, int nvt
   if (split == 0 && tok < a.N) {
 #pragma unroll
     for (int k = 1; k < kLseSplits; ++k) lse_merge(M, S, sm[k][lane], ss[k][lane]);
-    const float l = M + __logf(S);
-    a.lse[tok] = l;
-    const int64_t tg = a.targets[tok];
-    float out;
-    if (a.has_ignore && tg == a.ignore_index) {
-      out = 0.f;
-    } else if (tg < 0 || tg >= a.V) {
-      out = __builtin_nanf("");
-    } else {
-      out = l + a.neg_target_logit[tok];
-    }
-    a.nll[tok] = out;
+    nll_of(a, tok, M + __logf(S));
   }
+}
+
+// lse / nll from statistics in the reference's layout ([N][nt], a token's tiles
+// contiguous): one wave per token, each lane merging a strided share of the row
+// (coalesced), then the lanes' pairs in a fixed butterfly; lane 0's result is kept.
+// Reference: reduce_tile_to_lse, csrc/cce/cce.metal:332-355.
+__global__ __launch_bounds__(256) void lse_rows_kernel(FwdArgs a, int64_t nt) {
+  const int lane = threadIdx.x & 63;
+  const int64_t tok = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (tok >= a.N) return;  // uniform per wave
+  const float* tm = a.tile_max + tok * nt;
+  const float* ts = a.tile_sum_exp + tok * nt;
+  float M = -INFINITY, S = 0.f;
+  for (int64_t t = lane; t < nt; t += 64) lse_merge(M, S, tm[t], ts[t]);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const float m2 = __shfl_xor(M, off), s2 = __shfl_xor(S, off);
+    lse_merge(M, S, m2, s2);
+  }
+  if (lane == 0) nll_of(a, tok, M + __logf(S));
 }
 
 template <typename T>
 static void launch_tile_variant(const FwdArgs& a, const FwdSched& sc, bool bias, bool ragged, dim3 grid, dim3 block,
                                 hipStream_t s) {
-  if (bias) {
-    if (ragged)
-      hipLaunchKernelGGL((fwd_tile_kernel<T, true, true>), grid, block, 0, s, a, sc);
-    else
-      hipLaunchKernelGGL((fwd_tile_kernel<T, true, false>), grid, block, 0, s, a, sc);
-  } else {
-    if (ragged)
-      hipLaunchKernelGGL((fwd_tile_kernel<T, false, true>), grid, block, 0, s, a, sc);
-    else
-      hipLaunchKernelGGL((fwd_tile_kernel<T, false, false>), grid, block, 0, s, a, sc);
+#define CCE_T(B, R, S)                                                                   \
+  if (bias == B && ragged == R && (a.stats32 != 0) == S) {                               \
+    hipLaunchKernelGGL((fwd_tile_kernel<T, B, R, S>), grid, block, 0, s, a, sc);         \
+    return;                                                                              \
   }
+  CCE_T(false, false, false)
+  CCE_T(false, true, false)
+  CCE_T(true, false, false)
+  CCE_T(true, true, false)
+  CCE_T(false, false, true)
+  CCE_T(false, true, true)
+  CCE_T(true, false, true)
+  CCE_T(true, true, true)
+#undef CCE_T
 }
 
 // The tile kernel over vocabulary blocks [vb0, vb0 + nvb): a.c must address the
@@ -327,6 +377,11 @@ static hipError_t launch_tiles(const FwdArgs& a, int vb0, int nvb, hipStream_t s
 
 template <typename T>
 static hipError_t launch_lse(const FwdArgs& a, hipStream_t s) {
+  if (a.stats32) {
+    hipLaunchKernelGGL(lse_rows_kernel, dim3((unsigned)((a.N + 3) / 4)), dim3(256), 0, s, a,
+                       (a.V + kRefStatTile - 1) / kRefStatTile);
+    return hipGetLastError();
+  }
   const int nvt = (int)((a.V + kStatTile - 1) / kStatTile);
   hipLaunchKernelGGL(lse_kernel, dim3((unsigned)((a.N + 63) / 64)), dim3(64 * kLseSplits), 0, s, a, nvt);
   return hipGetLastError();

@@ -13,6 +13,9 @@ constexpr int kFwdTokens = 256;
 constexpr int kFwdVocab = 256;
 // Statistic / filter tile: 128 vocabulary columns (one wave's share of a forward tile).
 constexpr int kStatTile = 128;
+// The reference's statistic tile (cce.metal: 32 columns), for its layout of the raw
+// statistics: [N][ceil(V / 32)], row major per token (mlx_cce/__init__.py:25-30).
+constexpr int kRefStatTile = 32;
 // Backward tile: 128 tokens x 128 vocabulary rows.
 constexpr int kBwdTokens = 128;
 constexpr int kBwdVocab = 128;
@@ -33,6 +36,8 @@ struct FwdArgs {
   int num_cus;  // compute units of the device (the persistent forward runs one workgroup per CU)
   void* zero_buf;       // filled with zeros alongside the tiles (null: none)
   int64_t zero_units;   // 16-byte units of zero_buf
+  int stats32;          // tile_max / tile_sum_exp per 32 columns in the reference's layout [N][ceil(V/32)]
+                        // (else per 128 columns, [ceil(V/128)][N])
 };
 
 // Classifier rows stored with affine group quantization (the layout of MLX's
@@ -316,6 +321,7 @@ struct BwdArgs {
   int de_geo;           // dE sums geometry: 0 by size, 1 wide, 2 narrow
   int dc_geo;           // dC sums geometry: 0 by the filter setting, 1 wide, 2 narrow
   int dc_zeroed;        // dC already holds zeros: only rows of vocab tiles with kept tiles are written
+  int stats32;          // tile_max per 32 columns in the reference's layout [N][ceil(V/32)] (else [nvt][N])
   QuantRows q;          // q.wq set: c is unused; every chunk first dequantizes its rows into q.scratch
 };
 

@@ -37,6 +37,8 @@ SIGNATURES = {
     "cce_version": (ctypes.c_char_p, []),
     "cce_tile_config": (None, [_P, _P, _P, _P, _P]),
     "cce_num_vocab_tiles": (_I64, [_I64]),
+    "cce_num_ref_tiles": (_I64, [_I64]),
+    "cce_forward_ref": (_INT, [_INT, _P, _P, _P, _P, _I64, _INT, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P]),
     "cce_forward": (_INT, [_INT, _P, _P, _P, _P, _I64, _INT, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P]),
     "cce_backward_workspace_size": (ctypes.c_size_t, [_INT, _I64, _I64, _I64, _INT, _INT, _INT]),
     "cce_backward_workspace_size_ex": (ctypes.c_size_t, [_INT, _I64, _I64, _I64, _INT, _INT, _INT, _I64, _I64]),
@@ -69,6 +71,8 @@ CCE_BWD_DE_SUMS_WIDE = 8
 CCE_BWD_DE_SUMS_NARROW = 16
 CCE_BWD_DC_SUMS_WIDE = 32
 CCE_BWD_DC_SUMS_NARROW = 64
+CCE_BWD_REF_STATS = 128
+REF_STAT_TILE = 32
 
 # Overrides of choices the backward otherwise makes itself, for tests and tuning
 # (results agree to rounding either way).  They travel explicitly with every
@@ -201,13 +205,14 @@ def _prep(e, c, targets, bias):
     return DTYPE_CODES[e.dtype]
 
 
-def forward(e, c, targets, bias=None, ignore_index=-100, zero_out=None):
+def forward(e, c, targets, bias=None, ignore_index=-100, zero_out=None, ref_stats=False):
     """Run the fused forward.  Returns (tile_max, tile_sum_exp, neg_target_logit, lse, nll).
 
-    tile_max / tile_sum_exp are [ceil(V/128), N] fp32 (vocab-tile major);
-    nll is the per-token loss, 0 on rows whose target equals ignore_index.
-    zero_out (optional, a contiguous device tensor of a multiple of 16 bytes) is
-    filled with zeros by the forward's tile kernel (cce_forward_ex).
+    tile_max / tile_sum_exp are [ceil(V/128), N] fp32 (vocab-tile major), or with
+    ref_stats=True per 32 columns, flat [N * ceil(V/32)] (the reference's layout,
+    cce_forward_ref); nll is the per-token loss, 0 on rows whose target equals
+    ignore_index.  zero_out (optional, a contiguous device tensor of a multiple of 16
+    bytes) is filled with zeros by the forward's tile kernel (cce_forward_ex).
     """
     code = _prep(e, c, targets, bias)
     e = e.contiguous()
@@ -219,8 +224,9 @@ def forward(e, c, targets, bias=None, ignore_index=-100, zero_out=None):
     V = c.shape[0]
     nvt = (V + STAT_TILE - 1) // STAT_TILE
     f32 = dict(dtype=torch.float32, device=e.device)
-    tile_max = torch.empty((nvt, N), **f32)
-    tile_sum_exp = torch.empty((nvt, N), **f32)
+    shape = (N * ((V + REF_STAT_TILE - 1) // REF_STAT_TILE),) if ref_stats else (nvt, N)
+    tile_max = torch.empty(shape, **f32)
+    tile_sum_exp = torch.empty(shape, **f32)
     neg_tl = torch.empty((N,), **f32)
     lse = torch.empty((N,), **f32)
     nll = torch.empty((N,), **f32)
@@ -232,7 +238,14 @@ def forward(e, c, targets, bias=None, ignore_index=-100, zero_out=None):
             ev[0].record()
         if zero_out is not None and (not zero_out.is_contiguous() or zero_out.device != e.device):
             raise ValueError("[cce_forward] zero_out must be a contiguous tensor on the device of e")
-        if zero_out is not None:
+        if ref_stats and zero_out is not None:
+            raise ValueError("[cce_forward_ref] takes no zero_out")
+        if ref_stats:
+            rc = lib().cce_forward_ref(code, _ptr(e), _ptr(c), _ptr(bias), _ptr(targets),
+                                       int(ignore_index) if has_ignore else 0, 1 if has_ignore else 0,
+                                       N, D, V, _ptr(tile_max), _ptr(tile_sum_exp), _ptr(neg_tl), _ptr(lse),
+                                       _ptr(nll), ctypes.c_void_p(stream))
+        elif zero_out is not None:
             rc = lib().cce_forward_ex(code, _ptr(e), _ptr(c), _ptr(bias), _ptr(targets),
                                       int(ignore_index) if has_ignore else 0, 1 if has_ignore else 0,
                                       N, D, V, _ptr(tile_max), _ptr(tile_sum_exp), _ptr(neg_tl), _ptr(lse),
@@ -261,17 +274,30 @@ def workspace_size(e, c, want_de, want_dc, want_db, max_g_tiles=None, max_chunk_
                                                     int(want_de), int(want_dc), int(want_db), g, ch))
 
 
+def _ref_stats_layout(tile_max, N, V, fn):
+    """True when tile_max is in the reference's layout (flat [N * ceil(V/32)]), False
+    for [ceil(V/128), N]; raises for any other shape."""
+    nt = (V + REF_STAT_TILE - 1) // REF_STAT_TILE
+    if tile_max.dim() == 1 and tile_max.numel() == N * nt:
+        return True
+    if tile_max.dim() == 2 and tuple(tile_max.shape) == ((V + STAT_TILE - 1) // STAT_TILE, N):
+        return False
+    raise ValueError(f"[{fn}] tile_max must be flat [N * ceil(V/32)] (reference layout) or "
+                     f"[ceil(V/128), N], got {tuple(tile_max.shape)}")
+
+
 def backward(e, c, targets, lse, tile_max, d_nll, bias=None, ignore_index=-100,
              filter_eps=FILTER_LOG_EPS, want_de=True, want_dc=True, want_db=True, tile_stats=None,
              dc_zeroed=None):
     """Run the filtered backward.  Returns (dE, dC, dBias), each None when not wanted.
 
-    d_nll is the fp32 cotangent of the per-token loss [N].  filter_eps=None or
-    -inf disables the 2^-12 tile filter.  tile_stats, if given, is a device
-    int64[3] tensor that receives (kept tiles, total tiles, kept tiles of the
-    input-order token blocks).  dc_zeroed, if given, is a tensor like c that
-    already holds zeros (from forward(..., zero_out=)): it becomes dC, and only its
-    rows of vocabulary tiles with kept tiles are written (cce_backward_ex).
+    d_nll is the fp32 cotangent of the per-token loss [N].  tile_max is forward()'s,
+    in either layout (the flat reference layout runs with CCE_BWD_REF_STATS).
+    filter_eps=None or -inf disables the 2^-12 tile filter.  tile_stats, if given, is
+    a device int64[3] tensor that receives (kept tiles, total tiles, kept tiles of the
+    input-order token blocks).  dc_zeroed, if given, is a tensor like c that already
+    holds zeros (from forward(..., zero_out=)): it becomes dC, and only its rows of
+    vocabulary tiles with kept tiles are written (cce_backward_ex).
     """
     code = _prep(e, c, targets, bias)
     e = e.contiguous()
@@ -284,6 +310,7 @@ def backward(e, c, targets, lse, tile_max, d_nll, bias=None, ignore_index=-100,
     V = c.shape[0]
     lse = lse.contiguous()
     tile_max = tile_max.contiguous()
+    ref = _ref_stats_layout(tile_max, N, V, "cce_backward")
     d_nll = d_nll.to(torch.float32).contiguous()
     if d_nll.shape != (N,) or lse.shape != (N,):
         raise ValueError("[cce_backward] lse and d_nll must be [N]")
@@ -300,7 +327,7 @@ def backward(e, c, targets, lse, tile_max, d_nll, bias=None, ignore_index=-100,
     ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=e.device)
     eps = -math.inf if filter_eps is None else float(filter_eps)
     has_ignore = ignore_index is not None
-    flags = _bwd_opts["flags"] | (CCE_BWD_DC_ZEROED if dc_zeroed is not None else 0)
+    flags = _bwd_opts["flags"] | (CCE_BWD_DC_ZEROED if dc_zeroed is not None else 0) | (CCE_BWD_REF_STATS if ref else 0)
     with torch.cuda.device(e.device):
         stream = torch.cuda.current_stream(e.device).cuda_stream
         ev = _event_pair("backward")
@@ -335,6 +362,7 @@ def backward_noalloc(e, c, targets, lse, tile_max, d_nll, bias=None, ignore_inde
     N, D = e.shape
     if d_nll.shape != (N,) or lse.shape != (N,):
         raise ValueError("[cce_backward_noalloc] lse and d_nll must be [N]")
+    ref = _ref_stats_layout(tile_max, N, c.shape[0], "cce_backward_noalloc")
     if want_de and dE is None:
         dE = torch.empty_like(e)
     if want_dc and dC is None:
@@ -349,7 +377,8 @@ def backward_noalloc(e, c, targets, lse, tile_max, d_nll, bias=None, ignore_inde
         rc = lib().cce_backward_noalloc(code, _ptr(e), _ptr(c), _ptr(bias), _ptr(targets),
                                         int(ignore_index) if has_ignore else 0, 1 if has_ignore else 0,
                                         N, D, c.shape[0], _ptr(lse), _ptr(tile_max), _ptr(d_nll), ctypes.c_float(eps),
-                                        _ptr(dE), _ptr(dC), _ptr(dB), _ptr(tile_stats), _bwd_opts["flags"],
+                                        _ptr(dE), _ptr(dC), _ptr(dB), _ptr(tile_stats),
+                                        _bwd_opts["flags"] | (CCE_BWD_REF_STATS if ref else 0),
                                         ctypes.c_void_p(stream))
     if rc != CCE_OK:
         _raise(rc, "cce_backward_noalloc")
@@ -489,15 +518,20 @@ def backward_q(e, qw, targets, lse, tile_max, d_nll, bias=None, ignore_index=-10
 # --------------------------------------------------------------------------
 # Mirrors of the reference's native entry points (csrc/bindings.cpp:58-86).
 
-def cce_forward_raw(e, c, targets, bias=None, *, ignore_index=None, stream=None):
+def cce_forward_raw(e, c, targets, bias=None, *, ignore_index=None, stream=None, layout="reference"):
     """Reference csrc/bindings.cpp:58-69: returns [tile_max, tile_sum_exp, neg_target_logit, lse].
 
-    Differences: statistics are per 128-column tile and laid out [num_vocab_tiles, N]
-    (the reference uses 32-column tiles, row major); targets may be any integer dtype.
+    layout "reference" (default): the statistics per 32 columns, flat [N * ceil(V/32)],
+    row major per row of e -- the reference's own layout, which its glue reshapes to
+    (B, (V + 31) // 32) (mlx_cce/__init__.py:25-30).  layout "tiles128": per 128
+    columns, [ceil(V/128), N] (the layout the fused path keeps internally).  targets
+    may be any integer dtype.
     """
+    if layout not in ("reference", "tiles128"):
+        raise ValueError(f"[cce_forward_raw] layout must be 'reference' or 'tiles128', got {layout!r}")
     ctx = torch.cuda.stream(stream) if stream is not None else _nullctx()
     with ctx:
-        tm, ts, ntl, lse, _ = forward(e, c, targets, bias, ignore_index)
+        tm, ts, ntl, lse, _ = forward(e, c, targets, bias, ignore_index, ref_stats=layout == "reference")
     return [tm, ts, ntl, lse]
 
 
@@ -505,8 +539,10 @@ def cce_backward_raw(e, c, lse, targets, d_nll, tile_max, bias=None, *, ignore_i
                      filter_eps=FILTER_LOG_EPS, compute_all_grads=False, stream=None):
     """Reference csrc/bindings.cpp:71-86: returns dE (in e.dtype).
 
-    With compute_all_grads=True returns (dE, dC, dBias) — the semantics of the
-    reference's full-gradient kernel, reference/_fused_backward.py:1618-1655.
+    tile_max is cce_forward_raw's in either layout: the reference's flat
+    [N * ceil(V/32)] (as its glue passes it back, tile_max.reshape(-1)) or
+    [ceil(V/128), N].  With compute_all_grads=True returns (dE, dC, dBias) — the
+    semantics of the reference's full-gradient kernel, reference/_fused_backward.py:1618-1655.
     """
     ctx = torch.cuda.stream(stream) if stream is not None else _nullctx()
     with ctx:

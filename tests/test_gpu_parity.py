@@ -134,15 +134,19 @@ def test_integer_inputs_exact(m, cuda):
         b = torch.tensor(z["bias"], device=cuda).to(dtype)
         t = torch.tensor(z["targets"], device=cuda)
         t[::7] = -100
-        tm, ts, ntl, lse = m.cce_forward_raw(e, c, t, b, ignore_index=-100)
+        tm, ts, ntl, lse = m.cce_forward_raw(e, c, t, b, ignore_index=-100)  # the reference's layout
+        tm128, _, ntl128, _ = m.cce_forward_raw(e, c, t, b, ignore_index=-100, layout="tiles128")
         torch.cuda.synchronize()
         S = z["e"].astype(np.float64) @ z["c"].astype(np.float64).T + z["bias"]
         tt = t.cpu().numpy()
         valid = tt != -100
         rows = np.nonzero(valid)[0]
         np.testing.assert_array_equal(f64(ntl)[rows], -S[rows, tt[rows]])
+        np.testing.assert_array_equal(f64(ntl128)[rows], -S[rows, tt[rows]])  # masked rows are not written
         tm_ref, _ = O.tile_stats(z["e"], z["c"], z["bias"])
-        np.testing.assert_array_equal(f64(tm), tm_ref)
+        np.testing.assert_array_equal(f64(tm128), tm_ref)
+        tm32_ref, _ = O.tile_stats(z["e"], z["c"], z["bias"], tile=32)  # V = 260: a ragged last tile
+        np.testing.assert_array_equal(f64(tm), tm32_ref.T.reshape(-1))
         _, _, _, _, nll = m._ext.forward(e, c, t, b, -100)
         nll = f64(nll)
         assert (nll[~valid] == 0.0).all()
@@ -816,6 +820,49 @@ def test_train_validation_call_pattern(m, cuda):
     ref.backward()
     assert abs(float(loss) - float(ref)) <= 1e-5 * abs(float(ref))
     assert O.rel_fro(f64(gx), f64(x.grad)) < 2e-2 and O.rel_fro(f64(gw), f64(head.weight.grad)) < 2e-2
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_reference_layout_statistics_and_glue(m, cuda, dtype):
+    """cce_forward_raw's default layout is the reference's: per 32 columns, flat
+    [N * ceil(V/32)], row major per row (cce.cpp:123-145), which the reference's glue
+    reshapes to (B, (V + 31) // 32) and flattens back into cce_backward_raw
+    (mlx_cce/__init__.py:22-49).  tile_max / tile_sum_exp against the oracle's 32-column
+    statistics; lse, nll and the target logit against the 128-column forward; the glue's
+    round trip gives the same dE, bit for bit, as the 128-column statistics with the same
+    lse (the filter takes a 128-column tile's max as the max of its four 32-column maxima:
+    the same fp32 logits, so the same kept tiles)."""
+    N, D, V = 200, 96, 3000  # V % 32 != 0 and V % 128 != 0: ragged last tiles of both widths
+    e, c, t = normal_case(N, D, V, dtype, cuda, seed=51, std=0.2)
+    b = (torch.randn(V, device=cuda) * 0.5).to(dtype)
+    t[::11] = -100
+    tm, ts, ntl, lse = m.cce_forward_raw(e, c, t, b, ignore_index=-100)
+    tm128, ts128, ntl128, lse128 = m.cce_forward_raw(e, c, t, b, ignore_index=-100, layout="tiles128")
+    _, _, _, _, nll = m._ext.forward(e, c, t, b, -100, ref_stats=True)
+    _, _, _, _, nll128 = m._ext.forward(e, c, t, b, -100)
+    torch.cuda.synchronize()
+    nt = (V + 31) // 32
+    assert tm.shape == (N * nt,) and ts.shape == (N * nt,)
+    tm_o, ts_o = O.tile_stats(f64(e), f64(c), f64(b), tile=32)
+    np.testing.assert_allclose(f64(tm), tm_o.T.reshape(-1), rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(f64(ts), ts_o.T.reshape(-1), rtol=1e-5)
+    rows = (t != -100).nonzero().flatten()  # neg_target_logit of masked rows is not written
+    assert torch.equal(ntl[rows], ntl128[rows])
+    np.testing.assert_allclose(f64(lse), f64(lse128), rtol=1e-6)
+    np.testing.assert_allclose(f64(nll), f64(nll128), rtol=1e-5, atol=1e-6)
+    # the 128-column maxima are the maxima of the 32-column ones, exactly
+    t32 = tm.reshape(N, nt)
+    pad = torch.full((N, 4 * ((V + 127) // 128) - nt), -float("inf"), device=cuda)
+    assert torch.equal(torch.cat([t32, pad], 1).reshape(N, -1, 4).amax(-1).T.contiguous(), tm128)
+    # the reference glue: reshape(B, num_v_tiles), then reshape(-1) back into the backward
+    tile_max_2d = tm.reshape(N, nt)
+    d_nll = torch.linspace(0.5, 1.5, N, device=cuda)
+    dE = m.cce_backward_raw(e, c, lse, t, d_nll, tile_max_2d.reshape(-1), b, ignore_index=-100)
+    dE128 = m.cce_backward_raw(e, c, lse, t, d_nll, tm128, b, ignore_index=-100)
+    torch.cuda.synchronize()
+    assert torch.equal(dE, dE128)
+    with pytest.raises(ValueError, match="tile_max must be"):
+        m.cce_backward_raw(e, c, lse, t, d_nll, tile_max_2d, b, ignore_index=-100)
 
 
 def test_raw_forward_then_raw_backward(m, cuda):

@@ -168,6 +168,13 @@ def _noalloc(lib, N=64, D=64, V=256, flags=0):
                                     ctypes.c_float(-8.3), FAKE, FAKE, None, None, flags, None)
 
 
+def test_reference_statistic_tiles(ext):
+    """The reference's statistic tile is 32 columns: ceil(V / 32) of them."""
+    lib = ext.lib()
+    assert [lib.cce_num_ref_tiles(v) for v in (0, 1, 32, 33, 260, 128256)] == [0, 1, 1, 2, 9, 4008]
+    assert ext.REF_STAT_TILE == 32 and ext.CCE_BWD_REF_STATS == 128
+
+
 def test_noalloc_validation(ext):
     """cce_backward_noalloc refuses a problem past its static scratch before any device
     work (the fp32 dE carry of N=8192, D=4096 alone is 128 MiB of its 64 MiB)."""
