@@ -696,38 +696,50 @@ __global__ __launch_bounds__(1024) void bwd_compact_kernel(BwdArgs a, int chunk)
   };
   int ntask;
   {
-    const int pj = (J + 1023) >> 10;
-    const int j0 = min(J, tid * pj), j1 = min(J, j0 + pj);
+    // (item, token block) pairs in task order, a contiguous run of them per thread:
+    // pair f = j nrb + rb holds a task when block rb keeps more than 4 k tiles in the
+    // item's pass (k its run index).
+    const int P = J * nrb;
+    const int per = (P + 1023) >> 10;
+    const int f0 = min(P, tid * per), f1 = min(P, f0 + per);
     int cnt = 0;
-    for (int j = j0; j < j1; ++j) {
-      const int p = item_pass(j), k4 = 4 * (j - kbp[p]);
-      int prev = rbs(p * nrb);
-      for (int rb = 0; rb < nrb; ++rb) {
-        const int next = rbs(p * nrb + rb + 1);
-        cnt += next - prev > k4 ? 1 : 0;
-        prev = next;
+    {
+      int jc = -1, p = 0, k4 = 0;
+      for (int f = f0; f < f1; ++f) {
+        const int j = f / nrb, rb = f - j * nrb;
+        if (j != jc) {
+          jc = j;
+          p = item_pass(j);
+          k4 = 4 * (j - kbp[p]);
+        }
+        cnt += rbs(p * nrb + rb + 1) - rbs(p * nrb + rb) > k4 ? 1 : 0;
       }
     }
     int tb = block_excl_scan(cnt, wsum, ntask);
-    for (int j = j0; j < j1; ++j) {
-      const int p = item_pass(j), k4 = 4 * (j - kbp[p]);
-      if (k4 == 0) {  // the pass's first item: its tasks start here
+    int jc = -1, p = 0, k4 = 0;
+    for (int f = f0; f < f1; ++f) {
+      const int j = f / nrb, rb = f - j * nrb;
+      if (j != jc) {
+        jc = j;
+        p = item_pass(j);
+        k4 = 4 * (j - kbp[p]);
+      }
+      if (k4 == 0 && rb == 0) {  // the pass's first pair: its tasks start here
         a.pinfo[p * kPassInts + kPiTask0] = tb;
         if (p > 0) a.pinfo[(p - 1) * kPassInts + kPiTask1] = tb;
       }
-      int prev = rbs(p * nrb);
-      for (int rb = 0; rb < nrb; ++rb) {
-        const int next = rbs(p * nrb + rb + 1);
-        if (next - prev > k4) {
-          a.g_task[tb] = prev + k4;
-          a.g_task_rb[tb] = rb;
-          ++tb;
-        }
-        prev = next;
+      const int b0 = rbs(p * nrb + rb);
+      if (rbs(p * nrb + rb + 1) - b0 > k4) {
+        a.g_task[tb] = b0 + k4;
+        a.g_task_rb[tb] = rb;
+        ++tb;
       }
     }
   }
   if (tid == 0) a.pinfo[(npass - 1) * kPassInts + kPiTask1] = ntask;
+  // kbp lives in hist, which order_by_size clears first thing: every thread must be
+  // done with the task lists before any thread starts on the owners.
+  __syncthreads();
 
   // the owners of every pass's sums, most kept tiles first
   for (int p = 0; p < npass; ++p) {
