@@ -958,6 +958,115 @@ template <typename T>
 using GLoop = NTMainLoop<T, 4 * kBwdVocab, kBwdTokens, 4, 2, kGSlice, kGStages>;  // A = 4 x 128 C rows, B = 128 E rows
 constexpr int kGThreads = GLoop<__bf16>::NTHREADS;
 
+// G of one wave's 128 x 64 block of a tile from its logits w: w[i][j][r] is the logit
+// of vocabulary v0 + 32 i + 8 (r/4) + 4 h + r%4 and token tok0 + 32 j + n.  Stored
+// token-major (rows of 128 columns) into the slot's G tile gtile at rows
+// row0 + 32 j + n, in the input dtype; with WANT_DB the block's column sums over its 64
+// tokens go to red[0, 128).  Per token: g (0 for masked / out-of-range rows), lz =
+// lse log2(e), or +inf when g == 0 so that p = 0 and G = 0 without a select, and the
+// target's place in the tile as tl - 4 h, which register (i, r) holds iff it equals
+// 32 i + 8 (r/4) + r%4 (a compile-time constant).  Columns past V (last vocabulary
+// tile) keep finite values: the dE sums read zeros for C rows past V, and dC / dBias
+// are never written there.
+template <typename T, bool HAS_BIAS, bool WANT_G, bool WANT_DB>
+__device__ __forceinline__ void g_block_epilogue(const BwdArgs& a, const RowData& rd, const f32x16 (&w)[4][2],
+                                                 int64_t v0, int64_t tok0, int row0, char* gtile, float* red) {
+  constexpr int TI = 4, TJ = 2, ES = sizeof(T);
+  const int lane = threadIdx.x & 63;
+  const int n = lane & 31, h = lane >> 5;
+  const T* bias = reinterpret_cast<const T*>(a.bias);
+  float g[TJ], lz[TJ];
+  int tl[TJ];
+#pragma unroll
+  for (int j = 0; j < TJ; ++j) {
+    const int64_t tok = tok0 + j * 32 + n;
+    g[j] = 0.f;
+    lz[j] = INFINITY;
+    tl[j] = -4096;
+    if (tok < a.N) {
+      const int64_t tg = rd.targets[tok];
+      g[j] = (a.has_ignore && tg == a.ignore_index) ? 0.f : rd.d_nll[tok];
+      if (g[j] != 0.f) lz[j] = rd.lse[tok] * kLog2e;
+      const int64_t loc = tg - v0;
+      if (loc >= 0 && loc < kBwdVocab) tl[j] = (int)loc - 4 * h;
+    }
+  }
+  // One 32-column block i at a time: form its 32 G values per lane, store them
+  // token-major (4 consecutive vocab columns per store), add their column sums.
+  const __amdgpu_buffer_rsrc_t grs =
+      __builtin_amdgcn_make_buffer_rsrc(gtile, (short)0, (int)a.plan.g_bytes, 0x00020000);
+#pragma unroll
+  for (int i = 0; i < TI; ++i) {
+    float gv[TJ][16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int c = i * 32 + (r >> 2) * 8 + (r & 3);
+      float add = 0.f;
+      if (HAS_BIAS) {
+        const int64_t v = v0 + c + 4 * h;
+        add = v < a.V ? to_f32(bias[v]) * kLog2e : 0.f;
+      }
+#pragma unroll
+      for (int j = 0; j < TJ; ++j) {
+        const float p = __builtin_amdgcn_exp2f(fmaf(w[i][j][r], kLog2e, add - lz[j]));
+        gv[j][r] = g[j] * p - (tl[j] == c ? g[j] : 0.f);
+      }
+    }
+    if constexpr (WANT_G) {
+      // Buffer stores at 32-bit offsets within the 128 x 128 tile: row (token)
+      // row0 + 32 j + n of 128 ES bytes.  Lane (n, h) holds columns 32 i + 8 q +
+      // 4 h + 0..3; for 16-bit types one lane swap per q pair gives every lane the 8
+      // consecutive columns 32 i + 16 p + 8 h + 0..7 of the pair (2 p, 2 p + 1).
+      if constexpr (ES == 4) {
+        const uint32_t lane_off = (uint32_t)((row0 + n) * kBwdVocab * ES + h * 4 * ES);
+#pragma unroll
+        for (int j = 0; j < TJ; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const f32x4 v{gv[j][q * 4], gv[j][q * 4 + 1], gv[j][q * 4 + 2], gv[j][q * 4 + 3]};
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), grs,
+                                                   lane_off + (uint32_t)((j * 32 * kBwdVocab + i * 32 + q * 8) * ES), 0, 0);
+          }
+      } else {
+        const uint32_t lane_off = (uint32_t)((row0 + n) * kBwdVocab * ES + h * 8 * ES);
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) {
+          uint32_t pk[4][2];
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int k = 0; k < 2; ++k) pk[q][k] = pack2<T>(gv[j][4 * q + 2 * k], gv[j][4 * q + 2 * k + 1]);
+#pragma unroll
+          for (int pq = 0; pq < 2; ++pq) {
+            u32x4 v;
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+              const auto sw = __builtin_amdgcn_permlane32_swap(pk[2 * pq][k], pk[2 * pq + 1][k], false, false);
+              v[k] = sw[0];
+              v[2 + k] = sw[1];
+            }
+            __builtin_amdgcn_raw_buffer_store_b128(v, grs,
+                                                   lane_off + (uint32_t)((j * 32 * kBwdVocab + i * 32 + pq * 16) * ES), 0, 0);
+          }
+        }
+      }
+    }
+    if constexpr (WANT_DB) {
+      // column sums over this wave's 64 tokens; lanes n == 0 of each half hold them
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float sm = gv[0][r] + gv[1][r];
+        sm += __shfl_xor(sm, 1);
+        sm += __shfl_xor(sm, 2);
+        sm += __shfl_xor(sm, 4);
+        sm += __shfl_xor(sm, 8);
+        sm += __shfl_xor(sm, 16);
+        if (n == 0) red[i * 32 + (r >> 2) * 8 + h * 4 + (r & 3)] = sm;
+      }
+    }
+  }
+}
+
 template <typename T, bool HAS_BIAS, bool WANT_G, bool WANT_DB, bool RAGGED>
 __global__ __launch_bounds__(kGThreads, 1) void bwd_g_kernel(BwdArgs a, int chunk, int pass) {
   using Loop = GLoop<T>;
@@ -1067,100 +1176,10 @@ __global__ __launch_bounds__(kGThreads, 1) void bwd_g_kernel(BwdArgs a, int chun
     const int64_t t0 = (int64_t)cur.rb * kBwdTokens;
     float* red = reinterpret_cast<float*>(smem + (Loop::SMEM_BYTES - Loop::STAGE_BYTES));  // [2 wb][4 wa][128] column sums
     static_assert(8 * kBwdVocab * sizeof(float) <= Loop::STAGE_BYTES, "column sums fit one stage");
-    if (active) {
-      float g[TJ], lz[TJ];
-      int tl[TJ];
-#pragma unroll
-      for (int j = 0; j < TJ; ++j) {
-        const int64_t tok = t0 + wb * 64 + j * 32 + n;
-        g[j] = 0.f;
-        lz[j] = INFINITY;
-        tl[j] = -4096;
-        if (tok < a.N) {
-          const int64_t tg = rd.targets[tok];
-          g[j] = (a.has_ignore && tg == a.ignore_index) ? 0.f : rd.d_nll[tok];
-          if (g[j] != 0.f) lz[j] = rd.lse[tok] * kLog2e;
-          const int64_t loc = tg - v0;
-          if (loc >= 0 && loc < kBwdVocab) tl[j] = (int)loc - 4 * h;
-        }
-      }
-      // Columns past V (last vocabulary tile) keep finite values: the dE sums read
-      // zeros for C rows past V, and dC / dBias are never written there.  One
-      // 32-column block i at a time: form its 32 G values per lane, store them
-      // token-major (4 consecutive vocab columns per store), add their column sums.
-      const __amdgpu_buffer_rsrc_t grs = __builtin_amdgcn_make_buffer_rsrc(
-          a.gtile + (size_t)(slot - s0) * a.plan.g_bytes, (short)0, (int)a.plan.g_bytes, 0x00020000);
-#pragma unroll
-      for (int i = 0; i < TI; ++i) {
-        float gv[TJ][16];
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int c = i * 32 + (r >> 2) * 8 + (r & 3);
-          float add = 0.f;
-          if (HAS_BIAS) {
-            const int64_t v = v0 + c + 4 * h;
-            add = v < a.V ? to_f32(bias[v]) * kLog2e : 0.f;
-          }
-#pragma unroll
-          for (int j = 0; j < TJ; ++j) {
-            const float p = __builtin_amdgcn_exp2f(fmaf(w[i][j][r], kLog2e, add - lz[j]));
-            gv[j][r] = g[j] * p - (tl[j] == c ? g[j] : 0.f);
-          }
-        }
-        if constexpr (WANT_G) {
-          // Buffer stores at 32-bit offsets within the 128 x 128 tile: row (token)
-          // 64 wb + 32 j + n of 128 ES bytes.  Lane (n, h) holds columns 32 i + 8 q +
-          // 4 h + 0..3; for 16-bit types one lane swap per q pair gives every lane the 8
-          // consecutive columns 32 i + 16 p + 8 h + 0..7 of the pair (2 p, 2 p + 1).
-          if constexpr (ES == 4) {
-            const uint32_t lane_off = (uint32_t)((wb * 64 + n) * kBwdVocab * ES + h * 4 * ES);
-#pragma unroll
-            for (int j = 0; j < TJ; ++j)
-#pragma unroll
-              for (int q = 0; q < 4; ++q) {
-                const f32x4 v{gv[j][q * 4], gv[j][q * 4 + 1], gv[j][q * 4 + 2], gv[j][q * 4 + 3]};
-                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), grs,
-                                                       lane_off + (uint32_t)((j * 32 * kBwdVocab + i * 32 + q * 8) * ES), 0, 0);
-              }
-          } else {
-            const uint32_t lane_off = (uint32_t)((wb * 64 + n) * kBwdVocab * ES + h * 8 * ES);
-#pragma unroll
-            for (int j = 0; j < TJ; ++j) {
-              uint32_t pk[4][2];
-#pragma unroll
-              for (int q = 0; q < 4; ++q)
-#pragma unroll
-                for (int k = 0; k < 2; ++k) pk[q][k] = pack2<T>(gv[j][4 * q + 2 * k], gv[j][4 * q + 2 * k + 1]);
-#pragma unroll
-              for (int pq = 0; pq < 2; ++pq) {
-                u32x4 v;
-#pragma unroll
-                for (int k = 0; k < 2; ++k) {
-                  const auto sw = __builtin_amdgcn_permlane32_swap(pk[2 * pq][k], pk[2 * pq + 1][k], false, false);
-                  v[k] = sw[0];
-                  v[2 + k] = sw[1];
-                }
-                __builtin_amdgcn_raw_buffer_store_b128(v, grs,
-                                                       lane_off + (uint32_t)((j * 32 * kBwdVocab + i * 32 + pq * 16) * ES), 0, 0);
-              }
-            }
-          }
-        }
-        if constexpr (WANT_DB) {
-          // column sums over this wave's 64 tokens; lanes n == 0 of each half hold them
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            float sm = gv[0][r] + gv[1][r];
-            sm += __shfl_xor(sm, 1);
-            sm += __shfl_xor(sm, 2);
-            sm += __shfl_xor(sm, 4);
-            sm += __shfl_xor(sm, 8);
-            sm += __shfl_xor(sm, 16);
-            if (n == 0) red[(wb * 4 + wa) * kBwdVocab + i * 32 + (r >> 2) * 8 + h * 4 + (r & 3)] = sm;
-          }
-        }
-      }
-    }
+    if (active)
+      g_block_epilogue<T, HAS_BIAS, WANT_G, WANT_DB>(a, rd, w, v0, t0 + 64 * wb, 64 * wb,
+                                                     a.gtile + (size_t)(slot - s0) * a.plan.g_bytes,
+                                                     red + (wb * 4 + wa) * kBwdVocab);
     if constexpr (WANT_DB) {
       // the two token halves' column sums meet in LDS (the last stage, which no DMA
       // fills until the next task's main loop has passed its first barrier)
@@ -1176,6 +1195,138 @@ __global__ __launch_bounds__(kGThreads, 1) void bwd_g_kernel(BwdArgs a, int chun
     cur = nxt;
   }
   tail();
+}
+
+// ---------------------------------------------------------------- 4b. G tiles, filter off
+// With the filter off a token block keeps every tile of the pass or none, so the kept
+// pairs form the pass's whole [token blocks x vocabulary tiles] block: one GEMM's
+// worth of logits, computed here with the forward tile kernel's geometry (256 x 256
+// workgroup tiles, 8 waves of 128 vocabulary x 64 tokens, rounds of gt token blocks x
+// gv vocabulary blocks per XCD that share their rows in that XCD's L2) instead of the
+// task list's runs of 512 x 128.  A wave's block is half of one (token block,
+// vocabulary tile) G tile; its slot is the block's first slot of the pass plus the
+// block's kept tiles before this one (a popcount over the filter's bitmap), and a tile
+// the bitmap does not keep is not stored: the kernel is right for any kept set, and
+// fast for the full one.  Owners without kept tiles take the tail, as in bwd_g_kernel
+// (no dC schedule: the wide dC sums run with it).
+template <typename T>
+using GDLoop = NTMainLoop<T, 2 * kBwdVocab, 2 * kBwdTokens, 2, 4>;  // A = 256 C rows, B = 256 E rows
+constexpr int kGDThreads = GDLoop<__bf16>::NTHREADS;
+
+template <typename T, bool HAS_BIAS, bool WANT_G, bool WANT_DB, bool RAGGED>
+__global__ __launch_bounds__(kGDThreads, 1) void bwd_g_dense_kernel(BwdArgs a, int chunk, int pass) {
+  using Loop = GDLoop<T>;
+  static_assert(Loop::NTHREADS == kGDThreads && Loop::TI == 4 && Loop::TJ == 2, "wave block: 128 vocabulary x 64 tokens");
+  __shared__ __attribute__((aligned(16))) char smem[Loop::SMEM_BYTES];
+  const int* pi = a.pinfo + pass * kPassInts;
+  if (ldu(pi, kPiDeMode) < 0) return;  // past the passes the data needs
+  const int nrb = (int)a.plan.nrb, nw = (int)a.plan.nwords;
+  const int vt0 = ldu(pi, kPiVt0), vt1 = ldu(pi, kPiVt1);
+  const int s0 = ldu(pi, kPiS0);  // the G scratch holds slot s at s - s0
+  const int* rb_start = a.rb_start + pass * nrb;
+  const int vlo = chunk * (int)a.plan.chunk_nvt;
+  const RowData rd = row_data(a);
+  const uint32_t* bits = rd.map ? a.bits_p : a.bits;  // the token blocks the compaction used
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int wv = wave & 1, wt = wave >> 1;  // NTMainLoop: wa = wave % 2 (vocabulary), wb = wave / 2 (tokens)
+
+  // rounds of gt token blocks (256 rows) x gv vocabulary blocks (2 tiles) per XCD
+  const int ntb = (nrb + 1) / 2, nvb = (vt1 - vt0 + 1) / 2;
+  const int cpx = (int)(gridDim.x >> 3);
+  const int gt = (ntb >= 4 && cpx % 4 == 0) ? 4 : (ntb >= 2 && cpx % 2 == 0) ? 2 : 1;
+  const int gv = cpx / gt;
+  const int ngv = (nvb + gv - 1) / gv;
+  const int rounds = ((ntb + gt - 1) / gt) * ngv;
+  const int xcd = (int)(blockIdx.x & 7), member = (int)(blockIdx.x >> 3);
+  const int st = member % gt, sv = member / gt;
+  const int r_end = (int)((int64_t)(xcd + 1) * rounds / 8);
+  auto next_round = [&](int r, int& tb, int& vb) {
+    for (; r < r_end; ++r) {
+      tb = (r / ngv) * gt + st;
+      vb = (r % ngv) * gv + sv;
+      if (tb < ntb && vb < nvb) break;
+    }
+    return r;
+  };
+  const int64_t pitch = a.D * (int64_t)sizeof(T);
+  const char* C = reinterpret_cast<const char*>(a.c);
+  auto sources = [&](int tb, int vb) {
+    const int64_t seg[1] = {(int64_t)(vlo + vt0 + 2 * vb) * kBwdVocab};
+    return Loop::template make_src<2 * kBwdVocab>(C, a.V, seg, rd.e, a.N, (int64_t)tb * 2 * kBwdTokens, pitch, pitch,
+                                                  xcd);
+  };
+  // slot of (token block rb, chunk-local tile vt) of the pass, or -1 when not kept
+  auto slot_of = [&](int rb, int vt) {
+    const uint32_t* row = bits + (size_t)rb * nw + (vlo >> 5);
+    const int* rowi = reinterpret_cast<const int*>(row);
+    if (!(((uint32_t)ldu(rowi, vt >> 5) >> (vt & 31)) & 1u)) return -1;
+    int cnt = 0;
+    for (int w = vt0 >> 5; w <= (vt >> 5); ++w) {
+      uint32_t x = (uint32_t)ldu(rowi, w);
+      if (w == (vt0 >> 5)) x &= ~((1u << (vt0 & 31)) - 1u);
+      if (w == (vt >> 5)) x &= (1u << (vt & 31)) - 1u;
+      cnt += __builtin_popcount(x);
+    }
+    return ldu(rb_start, rb) + cnt;
+  };
+
+  int tb = 0, vb = 0;
+  int r = next_round((int)((int64_t)xcd * rounds / 8), tb, vb);
+  if (r < r_end) {
+    auto src = sources(tb, vb);
+    Loop::template prefetch<RAGGED>(src, smem);
+    float* red = reinterpret_cast<float*>(smem + (Loop::SMEM_BYTES - Loop::STAGE_BYTES));  // [8 waves][128] column sums
+    static_assert(8 * kBwdVocab * sizeof(float) <= Loop::STAGE_BYTES, "column sums fit one stage");
+    for (;;) {
+      f32x16 w[4][2];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) w[i][j] = zero16();
+      Loop::template consume<RAGGED>(src, smem, w);
+      int tbn = tb, vbn = vb;
+      const int rn = next_round(r + 1, tbn, vbn);
+      if (rn < r_end) {
+        src = sources(tbn, vbn);
+        Loop::template prefetch<RAGGED>(src, smem);  // all stages but the last; red uses the last one's bytes
+      }
+      const int vt = vt0 + 2 * vb + wv;  // this wave's chunk-local vocabulary tile
+      const int rb = 2 * tb + (wt >> 1), half = wt & 1;
+      const int slot = (vt < vt1 && rb < nrb) ? slot_of(rb, vt) : -1;  // uniform per wave
+      if (slot >= 0)
+        g_block_epilogue<T, HAS_BIAS, WANT_G, WANT_DB>(a, rd, w, (int64_t)(vlo + vt) * kBwdVocab,
+                                                       (int64_t)rb * kBwdTokens + half * 64, half * 64,
+                                                       a.gtile + (size_t)(slot - s0) * a.plan.g_bytes,
+                                                       red + wave * kBwdVocab);
+      if constexpr (WANT_DB) {
+        // the two token halves of a tile are waves wave and wave + 2
+        __syncthreads();
+        if (slot >= 0 && half == 0) {
+          float* cs = a.colsum + (size_t)(slot - s0) * kBwdVocab;
+          for (int c = lane; c < kBwdVocab; c += 64) cs[c] = red[wave * kBwdVocab + c] + red[(wave + 2) * kBwdVocab + c];
+        }
+        __syncthreads();
+      }
+      if (rn >= r_end) break;
+      r = rn;
+      tb = tbn;
+      vb = vbn;
+    }
+  }
+  // owners without kept tiles in the pass: dE rows, and dC rows unless dC came zeroed
+  if constexpr (WANT_G) {
+    const int nitems = nrb + (a.dc_zeroed ? 0 : vt1 - vt0);
+    int* box = reinterpret_cast<int*>(smem);
+    for (;;) {
+      __syncthreads();  // box (and smem) free
+      if (threadIdx.x == 0) box[0] = atomicAdd(&a.pinfo[pass * kPassInts + kPiTail], 1);
+      __syncthreads();
+      const int o = box[0];
+      if (o >= nitems) break;
+      empty_owner<T, kGDThreads>(a, chunk, pass, o);
+    }
+  }
 }
 
 // ---------------------------------------------------------------- 5. sums of G_j . X_j
@@ -2027,6 +2178,24 @@ static void launch_g(const BwdArgs& a, int chunk, int pass, dim3 grid, hipStream
 #undef CCE_G
 }
 
+template <typename T, bool HB>
+static void launch_g_dense(const BwdArgs& a, int chunk, int pass, dim3 grid, hipStream_t s) {
+  const bool g = a.dE != nullptr || a.dC != nullptr, db = a.dBias != nullptr;
+  const bool rg = (a.D * (int64_t)sizeof(T)) % kSliceBytes != 0;
+#define CCE_GD(G, DB, RG)                                                                                          \
+  if (g == G && db == DB && rg == RG) {                                                                            \
+    hipLaunchKernelGGL((bwd_g_dense_kernel<T, HB, G, DB, RG>), grid, dim3(kGDThreads), 0, s, a, chunk, pass);      \
+    return;                                                                                                        \
+  }
+  CCE_GD(true, true, false)
+  CCE_GD(true, false, false)
+  CCE_GD(false, true, false)
+  CCE_GD(true, true, true)
+  CCE_GD(true, false, true)
+  CCE_GD(false, true, true)
+#undef CCE_GD
+}
+
 // dE sums: the wide geometry (512 columns per task, measured 0.85x the time of two
 // narrow tasks) unless it leaves so few tasks that the narrow one finishes in fewer
 // rounds of equal tasks over the persistent grid.  a.de_geo forces one (1 wide, 2 narrow).
@@ -2076,6 +2245,9 @@ static hipError_t backward_typed(const BwdArgs& a, hipStream_t s) {
   const int gp = (cus + 7) / 8 * 8;  // persistent grids: a multiple of the 8 XCDs
   const int dtype = sizeof(T) == 4 ? 0 : (std::is_same<T, _Float16>::value ? 1 : 2);
   const bool wide_de = use_wide_de_sums(a, gp), wide_dc = use_wide_dc_sums(a);
+  // With the filter off the G tiles are one dense block per pass: the forward's tiling
+  // (the narrow dC sums need the G kernel's dC schedule, so they keep that kernel).
+  const bool dense_g = !(a.filter_log_eps > -INFINITY) && (!want_dc || wide_dc);
   for (int chunk = 0; chunk < (int)P.n_chunks; ++chunk) {
     const int vlo = chunk * (int)P.chunk_nvt;
     const int nv = (int)(P.nvt - vlo < P.chunk_nvt ? P.nvt - vlo : P.chunk_nvt);
@@ -2096,7 +2268,11 @@ static hipError_t backward_typed(const BwdArgs& a, hipStream_t s) {
     if (!(want_de || want_dc || want_db)) continue;
     // Every pass the chunk may need; passes past the data's last return at once.
     for (int pass = 0; pass < (int)P.max_passes; ++pass) {
-      if (a.bias)
+      if (dense_g && a.bias)
+        launch_g_dense<T, true>(ac, chunk, pass, dim3(gp), s);
+      else if (dense_g)
+        launch_g_dense<T, false>(ac, chunk, pass, dim3(gp), s);
+      else if (a.bias)
         launch_g<T, true>(ac, chunk, pass, dim3(gp), s);
       else
         launch_g<T, false>(ac, chunk, pass, dim3(gp), s);
