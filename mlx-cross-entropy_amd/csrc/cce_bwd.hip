@@ -858,13 +858,31 @@ __host__ __device__ inline int dc_bins(int nwg, int nds) {
 }
 
 // Longest-processing-time-first dealing of the dC owners of a pass (own_vt: most kept
-// blocks first) to nbins bins: each owner goes to the bin with the least work so far.
-// Owners of equal size form a batch: the bins are ranked once by (work, index) and
-// owner t of the batch goes to the bin of rank t % nbins -- what dealing them one
-// at a time does, since equal additions keep the ranking.  A bin lists its owners
-// in dealing order.  Run by one workgroup of NT threads; smem holds its tables.
+// blocks first) to nbins bins: each owner goes to the bin with the least work so far
+// (ties: lowest bin).  An owner's work is its pipeline steps (spt per kept block) plus
+// kDcOwnerCost for its epilogue and pipeline restart.  Owners of equal size form a
+// batch, dealt at once by water-filling: bin b offers the work levels W_b, W_b + w,
+// W_b + 2w, ... (w = the owners' work) and dealing one at a time takes the c lowest
+// levels, ties to the lower bin; so the smallest level L at which c levels are
+// available is found by bisection, every bin takes its levels below L, and the rest
+// go to the bins with a level exactly at L in bin order.  A bin lists its owners in
+// dealing order.  Run by one workgroup of NT threads (the bisection by wave 0);
+// smem holds its tables.
+constexpr int kDcOwnerCost = 3;  // a task's epilogue and restart, in pipeline steps (measured at c3)
+
+__device__ __forceinline__ int wave_sum(int v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+__device__ __forceinline__ int wave_min(int v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = min(v, __shfl_xor(v, o));
+  return v;
+}
+
 template <int NT>
-__device__ void dc_schedule(const BwdArgs& a, int pass, int nbins, char* smem) {
+__device__ void dc_schedule(const BwdArgs& a, int pass, int nbins, int spt, char* smem) {
   constexpr int NW = NT / 64;
   const int tid = threadIdx.x;
   const int* pi = a.pinfo + pass * kPassInts;
@@ -876,8 +894,9 @@ __device__ void dc_schedule(const BwdArgs& a, int pass, int nbins, char* smem) {
   int* pos = bin + kCompactMaxVt;          // [n] place of owner i in its bin
   int* work = pos + kCompactMaxVt;         // [nbins] work dealt so far, then bin starts
   int* cnt = work + kMaxDcBins;            // [nbins] owners dealt so far
-  int* byrank = cnt + kMaxDcBins;          // [nbins] bin of each rank
-  int* wsum = byrank + kMaxDcBins;         // [NW]
+  int* take = cnt + kMaxDcBins;            // [nbins] owners of the current batch per bin
+  int* pre = take + kMaxDcBins;            // [nbins] first owner of the batch per bin
+  int* wsum = pre + kMaxDcBins;            // [NW]
   for (int i = tid; i < n; i += NT) {
     const int v = own_vt[i];
     sz[i] = a.vt_start[v + 1] - a.vt_start[v];
@@ -898,29 +917,69 @@ __device__ void dc_schedule(const BwdArgs& a, int pass, int nbins, char* smem) {
   if (tid == 0) bst[nb] = n;
   __syncthreads();
   for (int bt = 0; bt < nb; ++bt) {
-    const int b0 = bst[bt], c = bst[bt + 1] - b0, s = sz[b0];
-    for (int b = tid; b < nbins; b += NT) {
-      const int wb = work[b];
-      int r = 0;
-      for (int b2 = 0; b2 < nbins; ++b2) {
-        const int w2 = work[b2];
-        r += (w2 < wb || (w2 == wb && b2 < b)) ? 1 : 0;
+    const int b0 = bst[bt], c = bst[bt + 1] - b0;
+    const int w = spt * sz[b0] + kDcOwnerCost;
+    if (tid < 64) {
+      const int lane = tid;
+      int wmin = INT_MAX;
+      for (int b = lane; b < nbins; b += 64) wmin = min(wmin, work[b]);
+      wmin = wave_min(wmin);
+      // levels at or below L over all bins
+      auto levels = [&](int L) {
+        int k = 0;
+        for (int b = lane; b < nbins; b += 64) {
+          const int wb = work[b];
+          k += L >= wb ? (L - wb) / w + 1 : 0;
+        }
+        return wave_sum(k);
+      };
+      int lo = wmin, hi = wmin + (c - 1) * w;  // the least loaded bin alone has c levels up to hi
+      while (lo < hi) {
+        const int mid = lo + (hi - lo) / 2;
+        if (levels(mid) >= c)
+          hi = mid;
+        else
+          lo = mid + 1;
       }
-      byrank[r] = b;
+      const int L = lo;
+      int below = 0;
+      for (int b = lane; b < nbins; b += 64) {
+        const int wb = work[b];
+        const int k = L > wb ? (L - 1 - wb) / w + 1 : 0;
+        take[b] = k;
+        below += k;
+      }
+      int rest = c - wave_sum(below);  // 1 .. the bins with a level at L
+      int carry = 0;
+      for (int base = 0; base < nbins; base += 64) {
+        const int b = base + lane;
+        const int at = (b < nbins && rest > 0 && L >= work[b] && (L - work[b]) % w == 0) ? 1 : 0;
+        const int r = wave_incl_scan(at);
+        if (at && r <= rest) take[b] += 1;
+        rest -= min(rest, __shfl(r, 63));
+        const int v = b < nbins ? take[b] : 0;
+        const int incl = wave_incl_scan(v);
+        if (b < nbins) pre[b] = carry + incl - v;
+        carry += __shfl(incl, 63);
+      }
     }
     __syncthreads();
-    for (int t = tid; t < c; t += NT) {
-      const int b = byrank[t % nbins];
-      bin[b0 + t] = b;
-      pos[b0 + t] = cnt[b] + t / nbins;
+    for (int t = tid; t < c; t += NT) {  // owner t goes to the last bin whose first owner is at or before it
+      int lo = 0, hi = nbins - 1;
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (pre[mid] <= t)
+          lo = mid;
+        else
+          hi = mid - 1;
+      }
+      bin[b0 + t] = lo;
+      pos[b0 + t] = cnt[lo] + t - pre[lo];
     }
     __syncthreads();
-    const int full = c / nbins, rem = c - full * nbins;
-    for (int r = tid; r < nbins; r += NT) {
-      const int b = byrank[r];
-      const int add = full + (r < rem ? 1 : 0);
-      work[b] += add * s;
-      cnt[b] += add;
+    for (int b = tid; b < nbins; b += NT) {
+      work[b] += take[b] * w;
+      cnt[b] += take[b];
     }
     __syncthreads();
   }
@@ -1129,7 +1188,8 @@ __global__ __launch_bounds__(kGThreads, 1) void bwd_g_kernel(BwdArgs a, int chun
         if (o < sched) {
           const int nds = (int)((a.D + kDcSliceCols - 1) / kDcSliceCols);
           const int nb = dc_bins((int)gridDim.x, nds);
-          dc_schedule<kGThreads>(a, pass, nb > 0 ? nb : 1, smem + 256);  // its tables start past box
+          dc_schedule<kGThreads>(a, pass, nb > 0 ? nb : 1, kBwdTokens * (int)sizeof(T) / 128,
+                                 smem + 256);  // its tables start past box
         } else {
           empty_owner<T, kGThreads>(a, chunk, pass, o - sched);
         }
