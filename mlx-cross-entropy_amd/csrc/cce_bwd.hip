@@ -613,6 +613,8 @@ __global__ __launch_bounds__(1024) void bwd_compact_kernel(BwdArgs a, int chunk)
   // the most kept tiles of one block in each pass (hist, before it holds kbp).
   const int I = npass * nrb;
   for (int p = tid; p < npass; p += 1024) hist[p] = 0;
+  __shared__ int ntr[4];  // G tasks with runs of at most 1, 2, 3, 4 slots
+  if (tid < 4) ntr[tid] = 0;
   {
     const int per = (I + 1023) >> 10;
     const int i0 = min(I, tid * per), i1 = min(I, i0 + per);
@@ -620,13 +622,19 @@ __global__ __launch_bounds__(1024) void bwd_compact_kernel(BwdArgs a, int chunk)
     for (int i = i0; i < i1; ++i) sum += pcnt(i / nrb, i % nrb);
     int tot;
     int pos = block_excl_scan(sum, wsum, tot);  // its barriers order the zeroing of hist before the maxima
+    int tr[4] = {0, 0, 0, 0};
     for (int i = i0; i < i1; ++i) {
       const int c = pcnt(i / nrb, i % nrb);
       a.rb_start[i] = pos;
       if (I <= kRbsLds) rbs_l[i] = pos;
       atomicMax(&hist[i / nrb], c);
       pos += c;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) tr[r] += (c + r) / (r + 1);
     }
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      if (tr[r] > 0) atomicAdd(&ntr[r], tr[r]);
   }
   for (int i = I + tid; i <= maxp * nrb; i += 1024) a.rb_start[i] = kept;
   if (tid == 0 && I <= kRbsLds) rbs_l[I] = kept;
@@ -658,13 +666,17 @@ __global__ __launch_bounds__(1024) void bwd_compact_kernel(BwdArgs a, int chunk)
   }
   if (tid == 0) a.vt_start[nv] = kept;
 
-  // G tasks: runs of at most 4 consecutive slots of one (pass, token block), ordered by
+  // G tasks: runs of at most R consecutive slots of one (pass, token block), ordered by
   // pass, then run index, then token block.  Tasks that run at the same time then read
   // the same vocabulary tiles when the lists are dense, and every block's first run
-  // (its lowest, most shared tiles) is taken early.  Item (p, k) -- run index k of
-  // pass p, k < ceil(most kept tiles of a block in the pass / 4), at least one item
-  // per pass -- counts the blocks with more than k runs; the counts are scanned and
-  // every item writes its column.
+  // (its lowest, most shared tiles) is taken early.  R is the shortest run (1 to 4)
+  // whose tasks all fit one round of the G kernel's persistent grid, else 4: a task
+  // streams only its own tiles' rows, and the task's time is the kernel's.  Item
+  // (p, k) -- run index k of pass p, k < ceil(most kept tiles of a block in the pass /
+  // R), at least one item per pass -- counts the blocks with more than k runs; the
+  // counts are scanned and every item writes its column.
+  const int gwg = (a.num_cus > 0 ? a.num_cus + 7 : 256 + 7) / 8 * 8;  // the G kernel's grid
+  const int R = ntr[0] <= gwg ? 1 : ntr[1] <= gwg ? 2 : ntr[2] <= gwg ? 3 : 4;
   {
     const int pp = (npass + 1023) >> 10;
     const int p0 = min(npass, tid * pp), p1 = min(npass, p0 + pp);
@@ -672,7 +684,7 @@ __global__ __launch_bounds__(1024) void bwd_compact_kernel(BwdArgs a, int chunk)
     int sum = 0;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      kb[q] = p0 + q < p1 ? max(1, (hist[p0 + q] + 3) >> 2) : 0;
+      kb[q] = p0 + q < p1 ? max(1, (hist[p0 + q] + R - 1) / R) : 0;
       sum += kb[q];
     }
     int J;
@@ -697,7 +709,7 @@ __global__ __launch_bounds__(1024) void bwd_compact_kernel(BwdArgs a, int chunk)
   int ntask;
   {
     // (item, token block) pairs in task order, a contiguous run of them per thread:
-    // pair f = j nrb + rb holds a task when block rb keeps more than 4 k tiles in the
+    // pair f = j nrb + rb holds a task when block rb keeps more than R k tiles in the
     // item's pass (k its run index).
     const int P = J * nrb;
     const int per = (P + 1023) >> 10;
@@ -710,7 +722,7 @@ __global__ __launch_bounds__(1024) void bwd_compact_kernel(BwdArgs a, int chunk)
         if (j != jc) {
           jc = j;
           p = item_pass(j);
-          k4 = 4 * (j - kbp[p]);
+          k4 = R * (j - kbp[p]);
         }
         cnt += rbs(p * nrb + rb + 1) - rbs(p * nrb + rb) > k4 ? 1 : 0;
       }
@@ -722,10 +734,11 @@ __global__ __launch_bounds__(1024) void bwd_compact_kernel(BwdArgs a, int chunk)
       if (j != jc) {
         jc = j;
         p = item_pass(j);
-        k4 = 4 * (j - kbp[p]);
+        k4 = R * (j - kbp[p]);
       }
       if (k4 == 0 && rb == 0) {  // the pass's first pair: its tasks start here
         a.pinfo[p * kPassInts + kPiTask0] = tb;
+        a.pinfo[p * kPassInts + kPiRun] = R;
         if (p > 0) a.pinfo[(p - 1) * kPassInts + kPiTask1] = tb;
       }
       const int b0 = rbs(p * nrb + rb);
@@ -1160,12 +1173,18 @@ __global__ __launch_bounds__(kGThreads, 1) void bwd_g_kernel(BwdArgs a, int chun
   auto load_task = [&](int t, Task& k) {
     k.s0 = ldu(a.g_task, task0 + t);
     k.rb = ldu(a.g_task_rb, task0 + t);
-    k.cnt = min(4, ldu(rb_start, k.rb + 1) - k.s0);
+    k.cnt = min(ldu(pi, kPiRun), ldu(rb_start, k.rb + 1) - k.s0);
 #pragma unroll
     for (int i = 0; i < 4; ++i) k.seg[i] = (int64_t)(vlo + ldu(a.slot_vt, k.s0 + (i < k.cnt ? i : k.cnt - 1))) * kBwdVocab;
   };
+  // the C rows of vocabulary tiles past the task's count are not loaded (their waves
+  // compute on stale bytes and store nothing)
+  static_assert(Loop::RPL * Loop::NW * 2 == kBwdVocab, "two load rounds per vocabulary tile");
+  static_assert(kGStages == 2, "skipped loads rely on the vmcnt(0) stage waits of two stages");
   auto sources = [&](const Task& k) {
-    return Loop::template make_src<kBwdVocab>(C, a.V, k.seg, E, a.N, (int64_t)k.rb * kBwdTokens, pitch, pitch, xcd);
+    auto src = Loop::template make_src<kBwdVocab>(C, a.V, k.seg, E, a.N, (int64_t)k.rb * kBwdTokens, pitch, pitch, xcd);
+    src.skip = (0xffu << (2 * k.cnt)) & 0xffu;
+    return src;
   };
   auto prefetch = [&](const typename Loop::template Src<4>& src) { Loop::template prefetch<RAGGED>(src, smem); };
 

@@ -232,6 +232,7 @@ struct NTMainLoop {
     uint32_t qb[LPW];
     int64_t kbytes;
     int KT, kskew;
+    uint32_t skip;  // wave-uniform: load j is not issued when bit j is set
   };
 
   // Sources for A_blk gathered from ROWS_A / A_SEG segments (rows [s * A_SEG,
@@ -274,6 +275,7 @@ struct NTMainLoop {
       }
     }
     src.kbytes = kbytes;
+    src.skip = 0;
     src.KT = (int)((kbytes + SLICE - 1) / SLICE);
     src.kskew = (int)(((int64_t)(phase8 & 7) * src.KT) >> 3);
     return src;
@@ -296,6 +298,7 @@ struct NTMainLoop {
     const int64_t k0 = (int64_t)kr * SLICE;
 #pragma unroll
     for (int j = 0; j < LPW; ++j) {
+      if ((src.skip >> j) & 1u) continue;
       const int sg = j * NW * RPL < ROWS_A ? (j * NW * RPL) / (ROWS_A / NSEG) : NSEG;
       const uint32_t lds = __builtin_amdgcn_readfirstlane(lds_addr(st + lds_w + j * NW * RPL * SLICE));
       if constexpr (RAGGED) {
