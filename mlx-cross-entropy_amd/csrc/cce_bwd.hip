@@ -642,27 +642,76 @@ __global__ __launch_bounds__(1024) void bwd_compact_kernel(BwdArgs a, int chunk)
   auto rbs = [&](int i) { return I <= kRbsLds ? rbs_l[i] : a.rb_start[i]; };  // i <= I
   auto slot_of = [&](int p, int rb, int v) { return rbs(p * nrb + rb) + rowpre(rb, v) - rowpre(rb, pvt[p]); };
 
-  // slot lists
+  // slot lists: a row's kept tiles of one pass hold consecutive slots, so each word
+  // looks its first slot up and counts on, again after a pass boundary
+  typedef __attribute__((address_space(1))) int gint;
+  gint* slot_vt = (gint*)a.slot_vt;
+  gint* slot_rb = (gint*)a.slot_rb;
   for (int e = tid; e < E; e += 1024) {
     uint32_t x = bm[e];
+    if (!x) continue;
     const int rb = e / cwd;
     const int vb = (e - rb * cwd) * 32;
-    while (x) {
-      const int v = vb + __builtin_ctz(x);
+    int v = vb + __builtin_ctz(x);
+    int p = pass_of(v);
+    int pend = pvt[p + 1];
+    int sl = slot_of(p, rb, v);
+    for (;;) {
+      slot_vt[sl] = v;
+      slot_rb[sl] = rb;
       x &= x - 1u;
-      const int sl = slot_of(pass_of(v), rb, v);
-      a.slot_vt[sl] = v;
-      a.slot_rb[sl] = rb;
+      if (!x) break;
+      v = vb + __builtin_ctz(x);
+      if (v >= pend) {
+        p = pass_of(v);
+        pend = pvt[p + 1];
+        sl = slot_of(p, rb, v);
+      } else {
+        ++sl;
+      }
     }
   }
-  // per vocab tile: its kept token blocks, ascending, as slots
-  for (int v = tid; v < nv; v += 1024) {
-    a.vt_start[v] = vpre[v];
-    const int p = pass_of(v);
-    const int wl = v >> 5, bit = v & 31;
-    int q = vpre[v];
-    for (int rb = 0; rb < nrb; ++rb)
-      if ((bm[rb * cwd + wl] >> bit) & 1u) a.vt_slot[q++] = slot_of(p, rb, v);
+  // per vocab tile: its kept token blocks, ascending, as slots.  A tile with few kept
+  // blocks takes one thread; one with many (a popular target's tile) takes a wave, a
+  // lane per token block, so that no thread walks a long list alone.
+  {
+    // the lists in global memory, through global-space pointers: the compiler then
+    // knows that their stores do not alias the LDS tables it reads next
+    gint* vt_slot = (gint*)a.vt_slot;
+    gint* vt_start = (gint*)a.vt_start;
+    constexpr int kVtWave = 8;
+    for (int v = tid; v < nv; v += 1024) {
+      vt_start[v] = vpre[v];
+      if (vpre[v + 1] - vpre[v] > kVtWave) continue;
+      const int p = pass_of(v);
+      const int wl = v >> 5, bit = v & 31;
+      int q = vpre[v];
+      for (int r0 = 0; r0 < nrb; r0 += 64) {  // the tile's column of the bitmap, 64 blocks at a time
+        const int nr = min(64, nrb - r0);
+        uint64_t col = 0;
+        for (int r = 0; r < nr; ++r) col |= (uint64_t)((bm[(r0 + r) * cwd + wl] >> bit) & 1u) << r;
+        while (col) {
+          const int rb = r0 + __builtin_ctzll(col);
+          col &= col - 1ull;
+          vt_slot[q++] = slot_of(p, rb, v);
+        }
+      }
+    }
+    const int lane = tid & 63, wv = tid >> 6;
+    const uint64_t below = (1ull << lane) - 1ull;
+    for (int v = wv; v < nv; v += 16) {
+      if (vpre[v + 1] - vpre[v] <= kVtWave) continue;
+      const int p = pass_of(v);
+      const int wl = v >> 5, bit = v & 31;
+      int q = vpre[v];
+      for (int r0 = 0; r0 < nrb; r0 += 64) {
+        const int rb = r0 + lane;
+        const bool k = rb < nrb && ((bm[rb * cwd + wl] >> bit) & 1u);
+        const uint64_t m = __ballot(k);
+        if (k) vt_slot[q + __builtin_popcountll(m & below)] = slot_of(p, rb, v);
+        q += __builtin_popcountll(m);
+      }
+    }
   }
   if (tid == 0) a.vt_start[nv] = kept;
 
