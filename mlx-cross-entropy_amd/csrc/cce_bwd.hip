@@ -642,47 +642,72 @@ __global__ __launch_bounds__(1024) void bwd_compact_kernel(BwdArgs a, int chunk)
   auto rbs = [&](int i) { return I <= kRbsLds ? rbs_l[i] : a.rb_start[i]; };  // i <= I
   auto slot_of = [&](int p, int rb, int v) { return rbs(p * nrb + rb) + rowpre(rb, v) - rowpre(rb, pvt[p]); };
 
-  // slot lists: a row's kept tiles of one pass hold consecutive slots, so each word
-  // looks its first slot up and counts on, again after a pass boundary
+  // slot lists.  Dense bitmaps (16+ kept tiles per word on average): a wave takes two
+  // words at a time, a lane per bit, so the lanes of a row's kept tiles store
+  // consecutive slots (the table reads are the same word per half-wave: broadcasts).
+  // Sparse ones: a thread per word; a row's kept tiles of one pass hold consecutive
+  // slots, so it looks its first slot up and counts on, again after a pass boundary.
   typedef __attribute__((address_space(1))) int gint;
   gint* slot_vt = (gint*)a.slot_vt;
   gint* slot_rb = (gint*)a.slot_rb;
-  for (int e = tid; e < E; e += 1024) {
-    uint32_t x = bm[e];
-    if (!x) continue;
-    const int rb = e / cwd;
-    const int vb = (e - rb * cwd) * 32;
-    int v = vb + __builtin_ctz(x);
-    int p = pass_of(v);
-    int pend = pvt[p + 1];
-    int sl = slot_of(p, rb, v);
-    for (;;) {
+  if (kept >= 16 * E) {
+    const int half = (tid >> 5) & 1, bitl = tid & 31;
+    for (int e = 2 * (tid >> 6) + half; e < E; e += 32) {
+      if (!((bm[e] >> bitl) & 1u)) continue;
+      const int rb = e / cwd;
+      const int v = (e - rb * cwd) * 32 + bitl;
+      const int sl = slot_of(pass_of(v), rb, v);
       slot_vt[sl] = v;
       slot_rb[sl] = rb;
-      x &= x - 1u;
-      if (!x) break;
-      v = vb + __builtin_ctz(x);
-      if (v >= pend) {
-        p = pass_of(v);
-        pend = pvt[p + 1];
-        sl = slot_of(p, rb, v);
-      } else {
-        ++sl;
+    }
+  } else {
+    for (int e = tid; e < E; e += 1024) {
+      uint32_t x = bm[e];
+      if (!x) continue;
+      const int rb = e / cwd;
+      const int vb = (e - rb * cwd) * 32;
+      int v = vb + __builtin_ctz(x);
+      int p = pass_of(v);
+      int pend = pvt[p + 1];
+      int sl = slot_of(p, rb, v);
+      for (;;) {
+        slot_vt[sl] = v;
+        slot_rb[sl] = rb;
+        x &= x - 1u;
+        if (!x) break;
+        v = vb + __builtin_ctz(x);
+        if (v >= pend) {
+          p = pass_of(v);
+          pend = pvt[p + 1];
+          sl = slot_of(p, rb, v);
+        } else {
+          ++sl;
+        }
       }
     }
   }
   // per vocab tile: its kept token blocks, ascending, as slots.  A tile with few kept
-  // blocks takes one thread; one with many (a popular target's tile) takes a wave, a
-  // lane per token block, so that no thread walks a long list alone.
+  // blocks takes one thread; when only a few tiles keep many (the tiles of popular
+  // targets), each of those takes a wave, a lane per token block, so that no thread
+  // walks a long list alone.  (With many such tiles -- the filter off -- threads keep
+  // them all: a wave's lanes would read the bitmap a row apart, in one LDS bank.)
   {
     // the lists in global memory, through global-space pointers: the compiler then
     // knows that their stores do not alias the LDS tables it reads next
     gint* vt_slot = (gint*)a.vt_slot;
     gint* vt_start = (gint*)a.vt_start;
-    constexpr int kVtWave = 8;
+    constexpr int kVtWave = 8, kVtWaveTiles = 64;
+    __shared__ int nheavy;
+    if (tid == 0) nheavy = 0;
+    __syncthreads();
+    int h = 0;
+    for (int v = tid; v < nv; v += 1024) h += vpre[v + 1] - vpre[v] > kVtWave ? 1 : 0;
+    if (h) atomicAdd(&nheavy, h);
+    __syncthreads();
+    const int wave_min = nheavy <= kVtWaveTiles ? kVtWave : 0x7fffffff;  // kept blocks that make a wave's tile
     for (int v = tid; v < nv; v += 1024) {
       vt_start[v] = vpre[v];
-      if (vpre[v + 1] - vpre[v] > kVtWave) continue;
+      if (vpre[v + 1] - vpre[v] > wave_min) continue;
       const int p = pass_of(v);
       const int wl = v >> 5, bit = v & 31;
       int q = vpre[v];
@@ -700,7 +725,7 @@ __global__ __launch_bounds__(1024) void bwd_compact_kernel(BwdArgs a, int chunk)
     const int lane = tid & 63, wv = tid >> 6;
     const uint64_t below = (1ull << lane) - 1ull;
     for (int v = wv; v < nv; v += 16) {
-      if (vpre[v + 1] - vpre[v] <= kVtWave) continue;
+      if (vpre[v + 1] - vpre[v] <= wave_min) continue;
       const int p = pass_of(v);
       const int wl = v >> 5, bit = v & 31;
       int q = vpre[v];
