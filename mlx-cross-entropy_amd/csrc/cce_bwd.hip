@@ -2351,9 +2351,14 @@ static void launch_g_dense(const BwdArgs& a, int chunk, int pass, dim3 grid, hip
 
 // dE sums: the wide geometry (512 columns per task, measured 0.85x the time of two
 // narrow tasks) unless it leaves so few tasks that the narrow one finishes in fewer
-// rounds of equal tasks over the persistent grid.  a.de_geo forces one (1 wide, 2 narrow).
+// rounds of equal tasks over the persistent grid.  With the filter on the owners' kept
+// counts differ, and two or four wide tasks per workgroup balance worse than twice as
+// many narrow ones (c3: the wide tasks' 18 to 28 kept tiles per workgroup; narrow
+// measured 10-13 us faster at c3 and c4), so the filter on takes the narrow one.
+// a.de_geo forces one (1 wide, 2 narrow).
 static bool use_wide_de_sums(const BwdArgs& a, int grid) {
   if (a.de_geo != 0) return a.de_geo == 1;
+  if (a.filter_log_eps > -INFINITY) return false;
   const BwdPlan& P = a.plan;
   const int64_t tw = P.nrb * ((a.D + 511) / 512), tn = P.nrb * ((a.D + 255) / 256);
   const int64_t rw = (tw + grid - 1) / grid, rn = (tn + grid - 1) / grid;
