@@ -835,10 +835,24 @@ __global__ __launch_bounds__(1024) void bwd_compact_kernel(BwdArgs a, int chunk)
     const int vt0 = pvt[p];
     const int n_vt = order_by_size(pvt[p + 1] - vt0, [&](int i) { return vpre[vt0 + i + 1] - vpre[vt0 + i]; },
                                    a.own_vt + vt0, vt0, hist, wsum);
+    // dC geometry of the pass: the wide one (512 columns, 8 waves) unless its largest
+    // owner's tasks alone outlast a workgroup's average share (a popular target's tile
+    // keeping many blocks), which the narrow one spreads over twice as many workgroups
+    int mk = 0;
+    for (int i = tid; i < pvt[p + 1] - vt0; i += 1024) mk = max(mk, vpre[vt0 + i + 1] - vpre[vt0 + i]);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) mk = max(mk, __shfl_xor(mk, o));
+    if ((tid & 63) == 0) wsum[tid >> 6] = mk;
+    __syncthreads();
     if (tid == 0) {
+      for (int w = 1; w < 16; ++w) mk = max(mk, wsum[w]);
+      const int64_t kept_p = rbs((p + 1) * nrb) - rbs(p * nrb);
+      const int64_t nds_w = (a.D + 511) / 512;
       a.pinfo[p * kPassInts + kPiOwnRb] = n_rb;
       a.pinfo[p * kPassInts + kPiOwnVt] = n_vt;
+      a.pinfo[p * kPassInts + kPiDcWide] = (int64_t)mk * gwg <= kept_p * nds_w ? 1 : 0;
     }
+    __syncthreads();  // wsum is the next scan's
   }
   // the rest of the pass table
   const bool multi = a.plan.n_chunks > 1 || npass > 1;
@@ -1639,6 +1653,8 @@ __global__ __launch_bounds__(SumGeo<T>::NT, 1) void bwd_sum_kernel(BwdArgs a, in
   const int* pi = a.pinfo + pass * kPassInts;
   const int pmode = ldu(pi, kPiDeMode);
   if (pmode < 0) return;  // past the passes the data needs
+  // the filtered backward launches both dC geometries; the compaction picked one per pass
+  if (PHASE == 1 && a.dc_geo == 0 && a.filter_log_eps > -INFINITY && ldu(pi, kPiDcWide) != 1) return;
   const int s0 = ldu(pi, kPiS0);  // the G scratch holds slot s at s - s0
   const int ntasks = ldu(pi, PHASE == 0 ? kPiOwnRb : kPiOwnVt) * nds;
   const int* own = PHASE == 0 ? a.own_rb + pass * nrb : a.own_vt + ldu(pi, kPiVt0);
@@ -1967,6 +1983,8 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_narrow_kernel(BwdArgs a, 
   const int* pi = a.pinfo + pass * kPassInts;
   const int pmode = ldu(pi, kPiDeMode);
   if (pmode < 0) return;  // past the passes the data needs
+  // the filtered backward launches both dC geometries; the compaction picked one per pass
+  if (PHASE == 1 && a.dc_geo == 0 && a.filter_log_eps > -INFINITY && ldu(pi, kPiDcWide) != 0) return;
   const int s0 = ldu(pi, kPiS0);  // the G scratch holds slot s at s - s0
   const int ntasks = ldu(pi, PHASE == 0 ? kPiOwnRb : kPiOwnVt) * nds;
   const int* own = PHASE == 0 ? a.own_rb + pass * nrb : a.own_vt + ldu(pi, kPiVt0);
@@ -2365,10 +2383,14 @@ static bool use_wide_de_sums(const BwdArgs& a, int grid) {
   return rw * 512 * 85 < rn * 256 * 100;
 }
 
-// dC sums: the narrow geometry suits the filtered backward (owners keep one or two
-// token blocks, so tasks are short); with the filter off every owner keeps all of its
-// token blocks and the wide geometry runs ~35% faster.  The kept counts are not known
-// on the host, so the choice follows the filter setting.  a.dc_geo forces one.
+// dC sums: with the filter off every owner keeps all of its token blocks and the wide
+// geometry runs ~35% faster.  With the filter on the compaction picks one per pass
+// (kPiDcWide): narrow when one owner keeps so many blocks that its tasks outlast a
+// workgroup's average share (skewed targets, c3), else wide (c2, c4: 50-55 us faster).
+// The host then launches both kernels and the one not picked returns at once: one
+// kernel holding both bodies spilled the narrow one's registers (measured 50-90 us
+// slower).  This function decides the dense G kernel and the forced choices; a.dc_geo
+// forces one (1 wide, 2 narrow).
 static bool use_wide_dc_sums(const BwdArgs& a) {
   if (a.dc_geo != 0) return a.dc_geo == 1;
   return !(a.filter_log_eps > -INFINITY);
@@ -2406,6 +2428,8 @@ static hipError_t backward_typed(const BwdArgs& a, hipStream_t s) {
   // With the filter off the G tiles are one dense block per pass: the forward's tiling
   // (the narrow dC sums need the G kernel's dC schedule, so they keep that kernel).
   const bool dense_g = !(a.filter_log_eps > -INFINITY) && (!want_dc || wide_dc);
+  // the filtered backward's dC geometry: the compaction's choice per pass
+  const bool auto_dc = a.dc_geo == 0 && a.filter_log_eps > -INFINITY;
   for (int chunk = 0; chunk < (int)P.n_chunks; ++chunk) {
     const int vlo = chunk * (int)P.chunk_nvt;
     const int nv = (int)(P.nvt - vlo < P.chunk_nvt ? P.nvt - vlo : P.chunk_nvt);
@@ -2444,7 +2468,10 @@ static hipError_t backward_typed(const BwdArgs& a, hipStream_t s) {
         if ((err = hipGetLastError()) != hipSuccess) return err;
       }
       if (want_dc) {
-        if (wide_dc)
+        if (auto_dc) {
+          hipLaunchKernelGGL((bwd_sum_narrow_kernel<T, 1>), dim3(gp), dim3(SumGeoNarrow<T>::NT), 0, s, a, chunk, pass);
+          hipLaunchKernelGGL((bwd_sum_kernel<T, 1>), dim3(gp), dim3(SumGeo<T>::NT), 0, s, a, chunk, pass);
+        } else if (wide_dc)
           hipLaunchKernelGGL((bwd_sum_kernel<T, 1>), dim3(gp), dim3(SumGeo<T>::NT), 0, s, a, chunk, pass);
         else
           hipLaunchKernelGGL((bwd_sum_narrow_kernel<T, 1>), dim3(gp), dim3(SumGeoNarrow<T>::NT), 0, s, a, chunk, pass);

@@ -110,6 +110,7 @@ enum PassField {
   kPiTail = 8,     // item counter of the G kernel's tail (zeroed by the compaction)
   kPiDeMode = 9,   // -1: no work (past the passes the data needs); else a dE write mode (WriteMode)
   kPiRun = 10,     // G tasks are runs of at most this many slots of one token block
+  kPiDcWide = 11,  // filter on: 1 if the dC sums of the pass run in the wide geometry, 0 narrow
 };
 // dE write mode of a pass: one pass over everything writes dE directly; with more
 // passes (or chunks) dE is summed in an fp32 carry: the first pass stores it, the

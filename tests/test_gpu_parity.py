@@ -538,6 +538,37 @@ def test_vocabulary_chunks(m, cuda, dtype, filtered, de_sums, split):
         assert err < tol, (name, err)
 
 
+@pytest.mark.parametrize("case", ["skewed", "uniform"])
+def test_dc_geometry_chosen_per_pass(m, cuda, case):
+    """With the filter on the compaction picks the dC sums' geometry per pass: narrow
+    when the largest owner's kept blocks times the grid exceed the pass's kept tiles
+    times the 512-column slices (Zipf targets: vocabulary tile 0 keeps every token
+    block), else wide (uniform targets with a peaked softmax: each tile keeps at most
+    a few blocks).  The default run equals both forced geometries bit for bit."""
+    if case == "skewed":
+        e, c, t = _peaked(cuda, N=4096, D=512, V=16000, seed=21)
+    else:
+        N, D, V = 1024, 2048, 32000
+        g = torch.Generator(device=cuda).manual_seed(22)
+        c = (torch.randn((V, D), generator=g, device=cuda) * 0.02).to(torch.bfloat16)
+        t = torch.randint(0, V, (N,), generator=g, device=cuda)
+        ct = c.float()[t]
+        e = (0.5 * torch.randn((N, D), generator=g, device=cuda) + 12.0 * ct / ct.pow(2).sum(1, keepdim=True)).to(
+            torch.bfloat16)
+    N = e.shape[0]
+    tm, _, _, lse, _ = m._ext.forward(e, c, t, None, -100)
+    d_nll = torch.full((N,), 1.0 / N, device=cuda)
+    outs = {}
+    for geo in (None, "wide", "narrow"):
+        with m._ext.backward_options(dc_sums=geo):
+            outs[geo] = m._ext.backward(e, c, t, lse, tm, d_nll, None, -100, m.FILTER_LOG_EPS, True, True, False)
+    torch.cuda.synchronize()
+    for geo in ("wide", "narrow"):
+        assert torch.equal(outs[None][0].view(torch.int16), outs[geo][0].view(torch.int16)), ("dE", geo)
+        assert torch.equal(outs[None][1].view(torch.int16), outs[geo][1].view(torch.int16)), ("dC", geo)
+    assert float(outs[None][1].float().abs().sum()) > 0
+
+
 def test_many_passes_pass_table_in_global_memory(m, cuda):
     """The smallest G scratch (2 tiles per 128-row block) on a dense problem runs one pass
     per vocabulary tile: 157 passes of 64 token blocks, more (pass, block) slot starts
