@@ -2433,21 +2433,22 @@ static hipError_t backward_typed(const BwdArgs& a, hipStream_t s) {
   for (int chunk = 0; chunk < (int)P.n_chunks; ++chunk) {
     const int vlo = chunk * (int)P.chunk_nvt;
     const int nv = (int)(P.nvt - vlo < P.chunk_nvt ? P.nvt - vlo : P.chunk_nvt);
-    // Quantized classifier rows: dequantize this chunk's rows into the scratch and
-    // let c address it at global row numbers (only the G kernel and the dE sums read c).
-    BwdArgs ac = a;
-    if (a.q.wq != nullptr && (want_de || want_db)) {
-      const int64_t r0 = (int64_t)vlo * kBwdVocab;
-      const int64_t r1 = (int64_t)(vlo + nv) * kBwdVocab < a.V ? (int64_t)(vlo + nv) * kBwdVocab : a.V;
-      err = launch_dequantize(dtype, a.q, r0, r1 - r0, a.D, a.q.scratch, s);
-      if (err != hipSuccess) return err;
-      ac.c = reinterpret_cast<const char*>(a.q.scratch) - r0 * a.D * (int64_t)sizeof(T);
-    }
     // chunk 0 also copies the rows into the sorted order (extra workgroups)
     const unsigned cg = 1 + (chunk == 0 && sorted_ok ? (unsigned)((a.N + 15) / 16) : 0u);
     hipLaunchKernelGGL(bwd_compact_kernel, dim3(cg), dim3(1024), 0, s, a, chunk);
     if ((err = hipGetLastError()) != hipSuccess) return err;
     if (!(want_de || want_dc || want_db)) continue;
+    // Quantized classifier rows: dequantize the rows of this chunk's tiles that keep
+    // pairs (the compaction's vt_start) into the scratch and let c address it at global
+    // row numbers (only the G kernel and the dE sums read c, and only kept tiles' rows).
+    BwdArgs ac = a;
+    if (a.q.wq != nullptr) {
+      const int64_t r0 = (int64_t)vlo * kBwdVocab;
+      const int64_t r1 = (int64_t)(vlo + nv) * kBwdVocab < a.V ? (int64_t)(vlo + nv) * kBwdVocab : a.V;
+      err = launch_dequantize(dtype, a.q, r0, r1 - r0, a.D, a.q.scratch, s, a.vt_start);
+      if (err != hipSuccess) return err;
+      ac.c = reinterpret_cast<const char*>(a.q.scratch) - r0 * a.D * (int64_t)sizeof(T);
+    }
     // Every pass the chunk may need; passes past the data's last return at once.
     for (int pass = 0; pass < (int)P.max_passes; ++pass) {
       if (dense_g && a.bias)

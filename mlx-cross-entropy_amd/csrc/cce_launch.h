@@ -331,9 +331,11 @@ struct BwdArgs {
 hipError_t launch_forward(int dtype, const FwdArgs& a, hipStream_t s);
 // As launch_forward with the classifier rows in q (a.c unused).
 hipError_t launch_forward_q(int dtype, const FwdArgs& a, const QuantRows& q, hipStream_t s);
-// Rows [row0, row0 + rows) of q dequantized into out ([rows, D], dtype).
+// Rows [row0, row0 + rows) of q dequantized into out ([rows, D], dtype); with keep (a
+// per-128-row-tile table, entries t and t + 1 equal = tile t not needed) only the
+// rows of the tiles needed.
 hipError_t launch_dequantize(int dtype, const QuantRows& q, int64_t row0, int64_t rows, int64_t D, void* out,
-                             hipStream_t s);
+                             hipStream_t s, const int* keep = nullptr);
 hipError_t launch_backward(int dtype, const BwdArgs& a, hipStream_t s);
 hipError_t launch_reduce_loss(const float* nll, const int64_t* targets, int64_t ignore_index, int has_ignore,
                               int64_t N, int mode, float* loss, float* scale, hipStream_t s);

@@ -33,16 +33,19 @@ __device__ __forceinline__ float affine(float s, float q, float b) {
 
 // Rows are blockIdx.x (chunk-local); words of a row are split over blockIdx.y.  W
 // (words per row) and G (groups per row) come from the host and group_size is a power
-// of two, so the indexing needs no 64-bit division.
+// of two, so the indexing needs no 64-bit division.  keep (or null: every row): the
+// backward's per-tile table of the chunk (vt_start), rows of 128-row tiles without kept
+// pairs are skipped -- nothing reads them.
 template <typename T, int BITS>
 __global__ __launch_bounds__(256) void dequant_kernel(const uint32_t* __restrict__ wq, const T* __restrict__ scales,
                                                       const T* __restrict__ biases, int W, int G, int gshift,
-                                                      int64_t D, T* __restrict__ out) {
+                                                      int64_t D, T* __restrict__ out, const int* __restrict__ keep) {
   constexpr int EPW = 32 / BITS;  // codes per word
   typedef T vec_t __attribute__((ext_vector_type(EPW)));
   const int w = (int)blockIdx.y * 256 + (int)threadIdx.x;
   if (w >= W) return;
   const int64_t r = blockIdx.x;
+  if (keep != nullptr && ldu(keep, (int)(r >> 7) + 1) == ldu(keep, (int)(r >> 7))) return;
   const uint32_t word = wq[r * W + w];
   const int d0 = w * EPW;
   const float s = to_f32(scales[r * G + (d0 >> gshift)]);
@@ -58,7 +61,7 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint32_t* __restrict
 
 template <typename T>
 static hipError_t dequantize_typed(const QuantRows& q, int64_t row0, int64_t rows, int64_t D, void* out,
-                                   hipStream_t s) {
+                                   const int* keep, hipStream_t s) {
   if (rows <= 0) return hipSuccess;
   const int64_t words = D * q.bits / 32;  // D < 2^22 elements (8 MiB rows): fits int
   const dim3 grid((unsigned)rows, (unsigned)((words + 255) / 256));
@@ -71,13 +74,13 @@ static hipError_t dequantize_typed(const QuantRows& q, int64_t row0, int64_t row
   const int W = (int)words, G = (int)g;
   switch (q.bits) {
     case 2:
-      hipLaunchKernelGGL((dequant_kernel<T, 2>), grid, dim3(256), 0, s, wq, sc, bi, W, G, gshift, D, o);
+      hipLaunchKernelGGL((dequant_kernel<T, 2>), grid, dim3(256), 0, s, wq, sc, bi, W, G, gshift, D, o, keep);
       break;
     case 4:
-      hipLaunchKernelGGL((dequant_kernel<T, 4>), grid, dim3(256), 0, s, wq, sc, bi, W, G, gshift, D, o);
+      hipLaunchKernelGGL((dequant_kernel<T, 4>), grid, dim3(256), 0, s, wq, sc, bi, W, G, gshift, D, o, keep);
       break;
     case 8:
-      hipLaunchKernelGGL((dequant_kernel<T, 8>), grid, dim3(256), 0, s, wq, sc, bi, W, G, gshift, D, o);
+      hipLaunchKernelGGL((dequant_kernel<T, 8>), grid, dim3(256), 0, s, wq, sc, bi, W, G, gshift, D, o, keep);
       break;
     default:
       return hipErrorInvalidValue;
@@ -86,14 +89,14 @@ static hipError_t dequantize_typed(const QuantRows& q, int64_t row0, int64_t row
 }
 
 hipError_t launch_dequantize(int dtype, const QuantRows& q, int64_t row0, int64_t rows, int64_t D, void* out,
-                             hipStream_t s) {
+                             hipStream_t s, const int* keep) {
   switch (dtype) {
     case 0:
-      return dequantize_typed<float>(q, row0, rows, D, out, s);
+      return dequantize_typed<float>(q, row0, rows, D, out, keep, s);
     case 1:
-      return dequantize_typed<_Float16>(q, row0, rows, D, out, s);
+      return dequantize_typed<_Float16>(q, row0, rows, D, out, keep, s);
     default:
-      return dequantize_typed<__bf16>(q, row0, rows, D, out, s);
+      return dequantize_typed<__bf16>(q, row0, rows, D, out, keep, s);
   }
 }
 
