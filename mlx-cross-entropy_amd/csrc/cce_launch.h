@@ -320,8 +320,8 @@ struct BwdArgs {
   float* dnll_perm;     // [N]
   void* e_perm;         // [N, D] dtype
   int perm_mode;        // 0: sorted order when it keeps >= 10% fewer tiles, 1: never, 2: always
-  int de_geo;           // dE sums geometry: 0 by size, 1 wide, 2 narrow
-  int dc_geo;           // dC sums geometry: 0 by the filter setting, 1 wide, 2 narrow
+  int de_geo;           // dE sums geometry: 0 the backward's choice (filter off: by size; on: narrow), 1 wide, 2 narrow
+  int dc_geo;           // dC sums geometry: 0 the backward's choice (filter off: wide; on: per pass), 1 wide, 2 narrow
   int dc_zeroed;        // dC already holds zeros: only rows of vocab tiles with kept tiles are written
   int stats32;          // tile_max per 32 columns in the reference's layout [N][ceil(V/32)] (else [nvt][N])
   QuantRows q;          // q.wq set: c is unused; every chunk first dequantizes its rows into q.scratch
