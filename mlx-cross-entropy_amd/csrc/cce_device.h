@@ -338,8 +338,14 @@ struct NTMainLoop {
   // compiler cannot tell the DMA's LDS writes from the reads, so reads that
   // follow the DMA in program order are held behind all of it, and the MFMAs of
   // step 1 would then wait on their own operands.
-  template <bool RAGGED, int NSEG>
-  static __device__ __forceinline__ void consume(const Src<NSEG>& src, char* smem, f32x16 (&acc)[TI][TJ]) {
+  // consume() calls hook() once, right after its first stage barrier (the caller's
+  // deferred stores then drain while the first slice computes).
+  struct NoHook {
+    __device__ void operator()() const {}
+  };
+  template <bool RAGGED, int NSEG, typename Hook = NoHook>
+  static __device__ __forceinline__ void consume(const Src<NSEG>& src, char* smem, f32x16 (&acc)[TI][TJ],
+                                                 Hook hook = Hook()) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wa = wave % WA;
@@ -366,6 +372,7 @@ struct NTMainLoop {
     constexpr int INFLIGHT = (STAGES - 2) * LPW;  // loads allowed in flight at the barrier
 
     stage_barrier<INFLIGHT>();
+    hook();  // stores deferred from the caller's previous tile: they drain during this slice
     u32x4 fa0[TI], fb0[TJ], fa1[TI], fb1[TJ];
     frags(smem, 0, fa0, fb0);
     for (int it = 0; it < KT; ++it) {

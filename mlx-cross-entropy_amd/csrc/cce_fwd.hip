@@ -56,9 +56,41 @@ struct FwdSched {
 //                          token = tbase + 32j + n)   with n = lane%32, h = lane/32.
 // S32: the statistics per 32 columns (the four 32-row blocks i of the wave's tile)
 // in the reference's layout, [N][ceil(V/32)], instead of per 128 columns.
+// The epilogue's stores of a tile (per token the statistics of its 128-column tile, and
+// the target logit) go out right after the next tile's first stage barrier instead of
+// just before it: every stage barrier waits for all of a wave's memory operations, so
+// stores issued at the end of the epilogue held the next tile's first slice for their
+// write latency (≈0.5% of the forward at c3).  The last tile stores at once.
+template <int TJ>
+struct FwdPending {
+  float m[TJ], s[TJ], tv[TJ];
+  uint32_t flags;  // bit j: statistics of column j; bit 8 + j: its target logit
+};
+
+// The stores fwd_epilogue deferred: tile (tb, vb)'s statistics and target logits.
+template <int TJ>
+__device__ __forceinline__ void fwd_store_pending(const FwdArgs& a, const FwdPending<TJ>& p, int tb, int vb) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int wv = wave & 1, wt = wave >> 1;
+  const int64_t vbase = (int64_t)vb * kFwdVocab + wv * 128;
+  const int64_t tbase = (int64_t)tb * kFwdTokens + wt * (kFwdTokens / kFwdWB);
+  const int tile = (int)(vbase / kStatTile);
+#pragma unroll
+  for (int j = 0; j < TJ; ++j) {
+    const int64_t tok = tbase + j * 32 + (lane & 31);
+    if (p.flags & (1u << j)) {
+      a.tile_max[(size_t)tile * a.N + tok] = p.m[j];
+      a.tile_sum_exp[(size_t)tile * a.N + tok] = p.s[j];
+    }
+    if (p.flags & (1u << (8 + j))) a.neg_target_logit[tok] = p.tv[j];
+  }
+}
+
 template <typename T, bool HAS_BIAS, bool S32, int TI, int TJ>
 __device__ __forceinline__ void fwd_epilogue(const FwdArgs& a, int nvt, f32x16 (&acc)[TI][TJ], int tb, int vb,
-                                             const int64_t (&tg)[TJ]) {
+                                             const int64_t (&tg)[TJ], FwdPending<TJ>* pend = nullptr) {
+  if (pend) pend->flags = 0;
   static_assert(TI == 4, "a wave covers one 128-column statistic tile");
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -133,7 +165,11 @@ __device__ __forceinline__ void fwd_epilogue(const FwdArgs& a, int nvt, f32x16 (
       for (int r = 0; r < 16; ++r) s += __builtin_amdgcn_exp2f(fmaf(acc[i][j][r], kLog2e, -mb));
     s += __shfl_xor(s, 32);
 
-    if (h == 0 && tok < a.N && tile < nvt) {
+    if (pend) {
+      pend->m[j] = m;
+      pend->s[j] = s;
+      if (h == 0 && tok < a.N && tile < nvt) pend->flags |= 1u << j;
+    } else if (h == 0 && tok < a.N && tile < nvt) {
       a.tile_max[(size_t)tile * a.N + tok] = m;
       a.tile_sum_exp[(size_t)tile * a.N + tok] = s;
     }
@@ -153,7 +189,12 @@ __device__ __forceinline__ void fwd_epilogue(const FwdArgs& a, int nvt, f32x16 (
       for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int r = 0; r < 16; ++r) val = (i == ti && r == rt) ? acc[i][j][r] : val;
-      if (hit && h == ht) a.neg_target_logit[tok] = -val;
+      if (pend) {
+        pend->tv[j] = -val;
+        if (hit && h == ht) pend->flags |= 1u << (8 + j);
+      } else if (hit && h == ht) {
+        a.neg_target_logit[tok] = -val;
+      }
     }
   }
 }
@@ -221,13 +262,20 @@ __global__ __launch_bounds__(FwdLoop<T>::NTHREADS, 1) void fwd_tile_kernel(FwdAr
   int64_t tg[TJ];
   targets(tb, tg);
 
+  FwdPending<TJ> pend;
+  pend.flags = 0;
+  int ptb = 0, pvb = 0;  // the tile whose stores are pending
   for (;;) {
     f32x16 acc[TI][TJ];
 #pragma unroll
     for (int i = 0; i < TI; ++i)
 #pragma unroll
       for (int j = 0; j < TJ; ++j) acc[i][j] = zero16();
-    Loop::template consume<RAGGED>(src, smem, acc);
+    if constexpr (S32) {
+      Loop::template consume<RAGGED>(src, smem, acc);
+    } else {
+      Loop::template consume<RAGGED>(src, smem, acc, [&]() { fwd_store_pending(a, pend, ptb, pvb); });
+    }
 
     // Start the next tile's pipeline fill and target reads, then reduce this
     // tile from registers while they are in flight.
@@ -239,7 +287,14 @@ __global__ __launch_bounds__(FwdLoop<T>::NTHREADS, 1) void fwd_tile_kernel(FwdAr
       Loop::template prefetch<RAGGED>(src, smem);
       targets(tbn, tgn);
     }
-    fwd_epilogue<T, HAS_BIAS, S32>(a, sc.nvt, acc, tb, vb, tg);
+    if constexpr (S32) {
+      fwd_epilogue<T, HAS_BIAS, S32>(a, sc.nvt, acc, tb, vb, tg);
+    } else {
+      fwd_epilogue<T, HAS_BIAS, S32>(a, sc.nvt, acc, tb, vb, tg, &pend);
+      ptb = tb;
+      pvb = vb;
+      if (rn >= r_end) fwd_store_pending(a, pend, ptb, pvb);  // no next tile to carry them
+    }
     zero_upto(min(zc + zpiece, z1));
     if (rn >= r_end) break;
     r = rn;
