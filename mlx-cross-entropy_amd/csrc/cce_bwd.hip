@@ -1128,15 +1128,38 @@ constexpr int kGThreads = GLoop<__bf16>::NTHREADS;
 // 32 i + 8 (r/4) + r%4 (a compile-time constant).  Columns past V (last vocabulary
 // tile) keep finite values: the dE sums read zeros for C rows past V, and dC / dBias
 // are never written there.
+// A G block's per-token inputs (target, cotangent, lse) for the lane's two token
+// columns, loaded together (tokens past N read nothing).
+struct GRows {
+  int64_t tg[2];
+  float dn[2], lse[2];
+};
+__device__ __forceinline__ GRows g_rows_load(const BwdArgs& a, const RowData& rd, int64_t tok0) {
+  GRows r;
+  const int n = threadIdx.x & 31;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int64_t tok = tok0 + j * 32 + n;
+    const bool ok = tok < a.N;
+    r.tg[j] = ok ? rd.targets[tok] : 0;
+    r.dn[j] = ok ? rd.d_nll[tok] : 0.f;
+    r.lse[j] = ok ? rd.lse[tok] : 0.f;
+  }
+  return r;
+}
+
 template <typename T, bool HAS_BIAS, bool WANT_G, bool WANT_DB>
 __device__ __forceinline__ void g_block_epilogue(const BwdArgs& a, const RowData& rd, const f32x16 (&w)[4][2],
-                                                 int64_t v0, int64_t tok0, int row0, char* gtile, float* red) {
+                                                 int64_t v0, int64_t tok0, int row0, char* gtile, float* red,
+                                                 const GRows* pre = nullptr) {
   constexpr int TI = 4, TJ = 2, ES = sizeof(T);
   const int lane = threadIdx.x & 63;
   const int n = lane & 31, h = lane >> 5;
   const T* bias = reinterpret_cast<const T*>(a.bias);
   float g[TJ], lz[TJ];
   int tl[TJ];
+  GRows gr;
+  if (pre != nullptr) gr = *pre; else gr = g_rows_load(a, rd, tok0);
 #pragma unroll
   for (int j = 0; j < TJ; ++j) {
     const int64_t tok = tok0 + j * 32 + n;
@@ -1144,9 +1167,9 @@ __device__ __forceinline__ void g_block_epilogue(const BwdArgs& a, const RowData
     lz[j] = INFINITY;
     tl[j] = -4096;
     if (tok < a.N) {
-      const int64_t tg = rd.targets[tok];
-      g[j] = (a.has_ignore && tg == a.ignore_index) ? 0.f : rd.d_nll[tok];
-      if (g[j] != 0.f) lz[j] = rd.lse[tok] * kLog2e;
+      const int64_t tg = gr.tg[j];
+      g[j] = (a.has_ignore && tg == a.ignore_index) ? 0.f : gr.dn[j];
+      if (g[j] != 0.f) lz[j] = gr.lse[j] * kLog2e;
       const int64_t loc = tg - v0;
       if (loc >= 0 && loc < kBwdVocab) tl[j] = (int)loc - 4 * h;
     }
@@ -1378,6 +1401,12 @@ __global__ __launch_bounds__(kGThreads, 1) void bwd_g_kernel(BwdArgs a, int chun
 // (no dC schedule: the wide dC sums run with it).
 template <typename T>
 using GDLoop = NTMainLoop<T, 2 * kBwdVocab, 2 * kBwdTokens, 2, 4>;  // A = 256 C rows, B = 256 E rows
+// Buffer stores one wave's G block epilogue issues (WANT_G, every one unconditional):
+// 4 column blocks x 2 token blocks x (2 for 16-bit types, 4 for fp32).  The dense
+// kernel's next first stage barrier lets exactly these stay in flight; the count must
+// follow g_block_epilogue's store loops (fewer stores would let prefetch loads through).
+template <typename T>
+constexpr int kGStoresPerWave = sizeof(T) == 4 ? 32 : 16;
 constexpr int kGDThreads = GDLoop<__bf16>::NTHREADS;
 
 template <typename T, bool HAS_BIAS, bool WANT_G, bool WANT_DB, bool RAGGED>
@@ -1444,6 +1473,7 @@ __global__ __launch_bounds__(kGDThreads, 1) void bwd_g_dense_kernel(BwdArgs a, i
     auto src = sources(tb, vb);
     Loop::template prefetch<RAGGED>(src, smem);
     float* red = reinterpret_cast<float*>(smem + (Loop::SMEM_BYTES - Loop::STAGE_BYTES));  // [8 waves][128] column sums
+    bool stored = false;  // this wave's previous G block stores may still be in flight
     static_assert(8 * kBwdVocab * sizeof(float) <= Loop::STAGE_BYTES, "column sums fit one stage");
     for (;;) {
       f32x16 w[4][2];
@@ -1451,21 +1481,30 @@ __global__ __launch_bounds__(kGDThreads, 1) void bwd_g_dense_kernel(BwdArgs a, i
       for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j) w[i][j] = zero16();
-      Loop::template consume<RAGGED>(src, smem, w);
+      Loop::template consume<RAGGED, 1, typename Loop::NoHook, kGStoresPerWave<T>>(src, smem, w, typename Loop::NoHook(),
+                                                                                     stored);
       int tbn = tb, vbn = vb;
       const int rn = next_round(r + 1, tbn, vbn);
+      const int vt = vt0 + 2 * vb + wv;  // this wave's chunk-local vocabulary tile
+      const int rb = 2 * tb + (wt >> 1), half = wt & 1;
+      const int slot = (vt < vt1 && rb < nrb) ? slot_of(rb, vt) : -1;  // uniform per wave
+      // the block's row inputs before the next tile's loads: their wait then does not
+      // include the DMA
+      GRows gr;
+      if (slot >= 0) {
+        gr = g_rows_load(a, rd, (int64_t)rb * kBwdTokens + half * 64);
+        wait_vmcnt<0>();
+      }
       if (rn < r_end) {
         src = sources(tbn, vbn);
         Loop::template prefetch<RAGGED>(src, smem);  // all stages but the last; red uses the last one's bytes
       }
-      const int vt = vt0 + 2 * vb + wv;  // this wave's chunk-local vocabulary tile
-      const int rb = 2 * tb + (wt >> 1), half = wt & 1;
-      const int slot = (vt < vt1 && rb < nrb) ? slot_of(rb, vt) : -1;  // uniform per wave
       if (slot >= 0)
         g_block_epilogue<T, HAS_BIAS, WANT_G, WANT_DB>(a, rd, w, (int64_t)(vlo + vt) * kBwdVocab,
                                                        (int64_t)rb * kBwdTokens + half * 64, half * 64,
                                                        a.gtile + (size_t)(slot - s0) * a.plan.g_bytes,
-                                                       red + wave * kBwdVocab);
+                                                       red + wave * kBwdVocab, &gr);
+      stored = WANT_G && !WANT_DB && slot >= 0;
       if constexpr (WANT_DB) {
         // the two token halves of a tile are waves wave and wave + 2
         __syncthreads();

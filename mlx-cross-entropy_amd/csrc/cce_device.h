@@ -343,9 +343,9 @@ struct NTMainLoop {
   struct NoHook {
     __device__ void operator()() const {}
   };
-  template <bool RAGGED, int NSEG, typename Hook = NoHook>
+  template <bool RAGGED, int NSEG, typename Hook = NoHook, int FIRST_STORES = 0>
   static __device__ __forceinline__ void consume(const Src<NSEG>& src, char* smem, f32x16 (&acc)[TI][TJ],
-                                                 Hook hook = Hook()) {
+                                                 Hook hook = Hook(), bool stores_pending = false) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wa = wave % WA;
@@ -371,7 +371,12 @@ struct NTMainLoop {
     constexpr int NR = TI + TJ;
     constexpr int INFLIGHT = (STAGES - 2) * LPW;  // loads allowed in flight at the barrier
 
-    stage_barrier<INFLIGHT>();
+    // FIRST_STORES: the caller issued that many stores after this block pair's prefetch
+    // (vmcnt counts in issue order, so waiting down to them leaves the loads landed)
+    if (FIRST_STORES > 0 && stores_pending)
+      stage_barrier<INFLIGHT + FIRST_STORES>();
+    else
+      stage_barrier<INFLIGHT>();
     hook();  // stores deferred from the caller's previous tile: they drain during this slice
     u32x4 fa0[TI], fb0[TJ], fa1[TI], fb1[TJ];
     frags(smem, 0, fa0, fb0);
