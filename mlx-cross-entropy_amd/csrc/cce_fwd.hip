@@ -50,7 +50,7 @@ struct FwdSched {
   int vb0;          // first vocabulary block (a chunk of dequantized rows; 0 otherwise)
 };
 
-// Epilogue of one tile, registers only: bias, ragged-vocabulary mask, per token
+// Epilogue of one tile (its bias already added), registers only: ragged-vocabulary mask, per token
 // and 128-column tile the max and sum of exp(logit - max), and the target gather.
 // acc[i][j][r] holds logit(vocab = vbase + 32i + 8(r/4) + 4h + r%4,
 //                          token = tbase + 32j + n)   with n = lane%32, h = lane/32.
@@ -87,7 +87,29 @@ __device__ __forceinline__ void fwd_store_pending(const FwdArgs& a, const FwdPen
   }
 }
 
-template <typename T, bool HAS_BIAS, bool S32, int TI, int TJ>
+// The bias of the wave's 128 vocabulary rows added to a tile's logits.  The tile
+// kernel does this before it issues the next tile's pipeline fill: waiting for the
+// bias loads after it would wait for the fill's DMA as well (vmcnt counts in order).
+template <typename T, int TI, int TJ>
+__device__ __forceinline__ void fwd_add_bias(const FwdArgs& a, f32x16 (&acc)[TI][TJ], int vb) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int h = lane >> 5;
+  const int64_t vbase = (int64_t)vb * kFwdVocab + (wave & 1) * 128;
+  const T* bias = reinterpret_cast<const T*>(a.bias);
+#pragma unroll
+  for (int i = 0; i < TI; ++i) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int64_t v = vbase + i * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
+      const float add = v < a.V ? to_f32(bias[v]) : 0.f;
+#pragma unroll
+      for (int j = 0; j < TJ; ++j) acc[i][j][r] += add;
+    }
+  }
+}
+
+template <typename T, bool S32, int TI, int TJ>
 __device__ __forceinline__ void fwd_epilogue(const FwdArgs& a, int nvt, f32x16 (&acc)[TI][TJ], int tb, int vb,
                                              const int64_t (&tg)[TJ], FwdPending<TJ>* pend = nullptr) {
   if (pend) pend->flags = 0;
@@ -101,19 +123,6 @@ __device__ __forceinline__ void fwd_epilogue(const FwdArgs& a, int nvt, f32x16 (
   const int64_t vbase = (int64_t)vb * kFwdVocab + wv * 128;
   const int64_t tbase = (int64_t)tb * kFwdTokens + wt * (kFwdTokens / kFwdWB);
 
-  if constexpr (HAS_BIAS) {
-    const T* bias = reinterpret_cast<const T*>(a.bias);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t v = vbase + i * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
-        const float add = v < a.V ? to_f32(bias[v]) : 0.f;
-#pragma unroll
-        for (int j = 0; j < TJ; ++j) acc[i][j][r] += add;
-      }
-    }
-  }
   if (vbase + 128 > a.V) {  // last vocabulary block only (uniform per wave)
     const int lim = (int)(a.V - vbase) - 4 * h;
 #pragma unroll
@@ -282,15 +291,16 @@ __global__ __launch_bounds__(FwdLoop<T>::NTHREADS, 1) void fwd_tile_kernel(FwdAr
     int tbn = tb, vbn = vb;
     const int rn = next_round(r + 1, tbn, vbn);
     int64_t tgn[TJ];
+    if constexpr (HAS_BIAS) fwd_add_bias<T>(a, acc, vb);
     if (rn < r_end) {
       src = sources(tbn, vbn);
       Loop::template prefetch<RAGGED>(src, smem);
       targets(tbn, tgn);
     }
     if constexpr (S32) {
-      fwd_epilogue<T, HAS_BIAS, S32>(a, sc.nvt, acc, tb, vb, tg);
+      fwd_epilogue<T, S32>(a, sc.nvt, acc, tb, vb, tg);
     } else {
-      fwd_epilogue<T, HAS_BIAS, S32>(a, sc.nvt, acc, tb, vb, tg, &pend);
+      fwd_epilogue<T, S32>(a, sc.nvt, acc, tb, vb, tg, &pend);
       ptb = tb;
       pvb = vb;
       if (rn >= r_end) fwd_store_pending(a, pend, ptb, pvb);  // no next tile to carry them
