@@ -321,6 +321,7 @@ int backward_impl(int dtype, const void* e, const void* c, const void* bias, con
   a.tile_stats = tile_stats;
   a.dc_zeroed = (flags & CCE_BWD_DC_ZEROED) ? 1 : 0;
   a.stats32 = (flags & CCE_BWD_REF_STATS) ? 1 : 0;
+  a.g_scaled = dtype == CCE_DTYPE_F16 ? 1 : 0;  // fp16 G tiles are scaled into fp16's normal range
   a.plan = P;
   a.num_cus = cus;
   if (q) {

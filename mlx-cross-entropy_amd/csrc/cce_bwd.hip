@@ -500,7 +500,7 @@ __global__ __launch_bounds__(1024) void bwd_compact_kernel(BwdArgs a, int chunk)
   // per wave) while the first compacts: the copy does not wait for the choice of
   // order, and is only read if the sorted order is chosen.
   if (blockIdx.x > 0) {
-    permute_row(a, (int64_t)(blockIdx.x - 1) * 16 + (threadIdx.x >> 6), a.D * (int64_t)(a.plan.g_bytes >> 14));
+    permute_row(a, (int64_t)(blockIdx.x - 1) * 16 + (threadIdx.x >> 6), a.D * (int64_t)a.plan.esize);
     return;
   }
   __shared__ uint32_t bm[kCompactMaxWords];
@@ -551,6 +551,26 @@ __global__ __launch_bounds__(1024) void bwd_compact_kernel(BwdArgs a, int chunk)
   }
   __syncthreads();
   const uint32_t* bsrc = sorted ? a.bits_p : a.bits;
+  if (chunk == 0 && a.g_scaled) {
+    // fp16 G tiles: s with max |d_nll| 2^s in [2^13, 2^14) (|G| <= |d_nll|), so G * 2^s
+    // neither overflows fp16 nor meets its subnormals above 2^-10 of the largest
+    // value; 0 when every d_nll is 0 or one is not finite.
+    uint32_t mb = 0u;
+    for (int64_t r = tid; r < a.N; r += 1024) mb = max(mb, __float_as_uint(a.d_nll[r]) & 0x7fffffffu);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) mb = max(mb, (uint32_t)__shfl_xor((int)mb, o));
+    if ((tid & 63) == 0) wsum[tid >> 6] = (int)mb;
+    __syncthreads();
+    if (tid == 0) {
+      for (int w = 1; w < 16; ++w) mb = max(mb, (uint32_t)wsum[w]);
+      int se = 0;
+      if (mb >= 0x7f800000u || mb == 0u) se = 0;
+      else if (mb < 0x00800000u) se = 120;  // subnormal
+      else se = min(120, 14 - ((int)(mb >> 23) - 126));
+      a.counts[kGScaleExp] = se;
+    }
+    __syncthreads();
+  }
 
   for (int e = tid; e < E; e += 1024) {
     const int rb = e / cwd, wl = e - rb * cwd;
@@ -970,6 +990,7 @@ __host__ __device__ inline int dc_bins(int nwg, int nds) {
 // dealing order.  Run by one workgroup of NT threads (the bisection by wave 0);
 // smem holds its tables.
 constexpr int kDcOwnerCost = 3;  // a task's epilogue and restart, in pipeline steps (measured at c3)
+constexpr int kDcStepsPerTile = 4;  // pipeline steps of the narrow dC sums per kept tile (32-deep slices)
 
 __device__ __forceinline__ int wave_sum(int v) {
 #pragma unroll
@@ -1120,9 +1141,9 @@ constexpr int kGThreads = GLoop<__bf16>::NTHREADS;
 
 // G of one wave's 128 x 64 block of a tile from its logits w: w[i][j][r] is the logit
 // of vocabulary v0 + 32 i + 8 (r/4) + 4 h + r%4 and token tok0 + 32 j + n.  Stored
-// token-major (rows of 128 columns) into the slot's G tile gtile at rows
-// row0 + 32 j + n, in the input dtype; with WANT_DB the block's column sums over its 64
-// tokens go to red[0, 128).  Per token: g (0 for masked / out-of-range rows), lz =
+// token-major into the slot's G tile gtile at rows row0 + 32 j + n: fp32 as it is,
+// 16-bit types as the hi / lo pair of g_tile_bytes's layout (fp16 scaled by 2^gexp);
+// with WANT_DB the block's (unscaled) column sums over its 64 tokens go to red[0, 128).  Per token: g (0 for masked / out-of-range rows), lz =
 // lse log2(e), or +inf when g == 0 so that p = 0 and G = 0 without a select, and the
 // target's place in the tile as tl - 4 h, which register (i, r) holds iff it equals
 // 32 i + 8 (r/4) + r%4 (a compile-time constant).  Columns past V (last vocabulary
@@ -1148,6 +1169,9 @@ __device__ __forceinline__ GRows g_rows_load(const BwdArgs& a, const RowData& rd
   return r;
 }
 
+// The exponent s of the fp16 G tiles' scale 2^s (0 unless a.g_scaled).
+__device__ __forceinline__ int g_scale_exp(const BwdArgs& a) { return a.g_scaled ? ldu(a.counts, kGScaleExp) : 0; }
+
 template <typename T, bool HAS_BIAS, bool WANT_G, bool WANT_DB>
 __device__ __forceinline__ void g_block_epilogue(const BwdArgs& a, const RowData& rd, const f32x16 (&w)[4][2],
                                                  int64_t v0, int64_t tok0, int row0, char* gtile, float* red,
@@ -1156,6 +1180,10 @@ __device__ __forceinline__ void g_block_epilogue(const BwdArgs& a, const RowData
   const int lane = threadIdx.x & 63;
   const int n = lane & 31, h = lane >> 5;
   const T* bias = reinterpret_cast<const T*>(a.bias);
+  // fp16: G is formed as (d_nll 2^s) (p - onehot), exact scaling by a power of two;
+  // the column sums take it back out
+  const int gexp = ES == 2 ? g_scale_exp(a) : 0;
+  const float gmul = __builtin_ldexpf(1.f, gexp), gdiv = __builtin_ldexpf(1.f, -gexp);
   float g[TJ], lz[TJ];
   int tl[TJ];
   GRows gr;
@@ -1168,7 +1196,7 @@ __device__ __forceinline__ void g_block_epilogue(const BwdArgs& a, const RowData
     tl[j] = -4096;
     if (tok < a.N) {
       const int64_t tg = gr.tg[j];
-      g[j] = (a.has_ignore && tg == a.ignore_index) ? 0.f : gr.dn[j];
+      g[j] = (a.has_ignore && tg == a.ignore_index) ? 0.f : gr.dn[j] * gmul;
       if (g[j] != 0.f) lz[j] = gr.lse[j] * kLog2e;
       const int64_t loc = tg - v0;
       if (loc >= 0 && loc < kBwdVocab) tl[j] = (int)loc - 4 * h;
@@ -1211,26 +1239,37 @@ __device__ __forceinline__ void g_block_epilogue(const BwdArgs& a, const RowData
                                                    lane_off + (uint32_t)((j * 32 * kBwdVocab + i * 32 + q * 8) * ES), 0, 0);
           }
       } else {
-        const uint32_t lane_off = (uint32_t)((row0 + n) * kBwdVocab * ES + h * 8 * ES);
+        // Rows of 256 elements: column 32 i + c of the tile goes to element 64 i + c
+        // (hi) and 64 i + 32 + c (lo), hi = round(G), lo = round(G - hi) (the
+        // difference is exact in fp32).
+        constexpr int RP = 2 * kBwdVocab * ES;  // bytes of one G row
+        const uint32_t lane_off = (uint32_t)((row0 + n) * RP + h * 8 * ES);
 #pragma unroll
         for (int j = 0; j < TJ; ++j) {
-          uint32_t pk[4][2];
+          uint32_t pk[2][4][2];
 #pragma unroll
           for (int q = 0; q < 4; ++q)
 #pragma unroll
-            for (int k = 0; k < 2; ++k) pk[q][k] = pack2<T>(gv[j][4 * q + 2 * k], gv[j][4 * q + 2 * k + 1]);
-#pragma unroll
-          for (int pq = 0; pq < 2; ++pq) {
-            u32x4 v;
-#pragma unroll
             for (int k = 0; k < 2; ++k) {
-              const auto sw = __builtin_amdgcn_permlane32_swap(pk[2 * pq][k], pk[2 * pq + 1][k], false, false);
-              v[k] = sw[0];
-              v[2 + k] = sw[1];
+              const float x0 = gv[j][4 * q + 2 * k], x1 = gv[j][4 * q + 2 * k + 1];
+              const T h0 = (T)x0, h1 = (T)x1;
+              pk[0][q][k] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+              pk[1][q][k] = pack2<T>(x0 - (float)h0, x1 - (float)h1);
             }
-            __builtin_amdgcn_raw_buffer_store_b128(v, grs,
-                                                   lane_off + (uint32_t)((j * 32 * kBwdVocab + i * 32 + pq * 16) * ES), 0, 0);
-          }
+#pragma unroll
+          for (int hl = 0; hl < 2; ++hl)
+#pragma unroll
+            for (int pq = 0; pq < 2; ++pq) {
+              u32x4 v;
+#pragma unroll
+              for (int k = 0; k < 2; ++k) {
+                const auto sw = __builtin_amdgcn_permlane32_swap(pk[hl][2 * pq][k], pk[hl][2 * pq + 1][k], false, false);
+                v[k] = sw[0];
+                v[2 + k] = sw[1];
+              }
+              __builtin_amdgcn_raw_buffer_store_b128(
+                  v, grs, lane_off + (uint32_t)(j * 32 * RP + (i * 64 + hl * 32 + pq * 16) * ES), 0, 0);
+            }
         }
       }
     }
@@ -1244,7 +1283,7 @@ __device__ __forceinline__ void g_block_epilogue(const BwdArgs& a, const RowData
         sm += __shfl_xor(sm, 4);
         sm += __shfl_xor(sm, 8);
         sm += __shfl_xor(sm, 16);
-        if (n == 0) red[i * 32 + (r >> 2) * 8 + h * 4 + (r & 3)] = sm;
+        if (n == 0) red[i * 32 + (r >> 2) * 8 + h * 4 + (r & 3)] = ES == 2 ? sm * gdiv : sm;
       }
     }
   }
@@ -1318,7 +1357,7 @@ __global__ __launch_bounds__(kGThreads, 1) void bwd_g_kernel(BwdArgs a, int chun
         if (o < sched) {
           const int nds = (int)((a.D + kDcSliceCols - 1) / kDcSliceCols);
           const int nb = dc_bins((int)gridDim.x, nds);
-          dc_schedule<kGThreads>(a, pass, nb > 0 ? nb : 1, kBwdTokens * (int)sizeof(T) / 128,
+          dc_schedule<kGThreads>(a, pass, nb > 0 ? nb : 1, kDcStepsPerTile,
                                  smem + 256);  // its tables start past box
         } else {
           empty_owner<T, kGThreads>(a, chunk, pass, o - sched);
@@ -1402,11 +1441,12 @@ __global__ __launch_bounds__(kGThreads, 1) void bwd_g_kernel(BwdArgs a, int chun
 template <typename T>
 using GDLoop = NTMainLoop<T, 2 * kBwdVocab, 2 * kBwdTokens, 2, 4>;  // A = 256 C rows, B = 256 E rows
 // Buffer stores one wave's G block epilogue issues (WANT_G, every one unconditional):
-// 4 column blocks x 2 token blocks x (2 for 16-bit types, 4 for fp32).  The dense
-// kernel's next first stage barrier lets exactly these stay in flight; the count must
-// follow g_block_epilogue's store loops (fewer stores would let prefetch loads through).
+// 4 column blocks x 2 token blocks x (4 for fp32; 2 each for the hi and lo halves of
+// 16-bit types).  The dense kernel's next first stage barrier lets exactly these stay
+// in flight; the count must follow g_block_epilogue's store loops (fewer stores would
+// let prefetch loads through).
 template <typename T>
-constexpr int kGStoresPerWave = sizeof(T) == 4 ? 32 : 16;
+constexpr int kGStoresPerWave = 32;
 constexpr int kGDThreads = GDLoop<__bf16>::NTHREADS;
 
 template <typename T, bool HAS_BIAS, bool WANT_G, bool WANT_DB, bool RAGGED>
@@ -1538,60 +1578,71 @@ __global__ __launch_bounds__(kGDThreads, 1) void bwd_g_dense_kernel(BwdArgs a, i
 // ---------------------------------------------------------------- 5. sums of G_j . X_j
 // Geometry of one sum task: output rows = the owner's 128 rows (tokens for dE,
 // vocabulary for dC), output columns = one DN (512) slice of D; contraction over
-// the owner's kept tiles, 128 deep each, in slices of 128 bytes of a G row.  Eight
-// waves (two per SIMD): wave (wm, wd) = (w % 2, w / 2) owns rows [64 wm, +64) and
-// columns [128 wd, +128) of the slice.  A wide slice loads each G slice once for
-// 512 output columns: the stage's DMA (80 KiB) per 2048 MFMA cycles of a SIMD.
+// the owner's kept tiles, 128 deep each, in slices of KS contraction elements (fp32:
+// 32; 16-bit types: 32 as well, each with its G hi and lo halves).  Eight waves (two
+// per SIMD): wave (wm, wd) = (w % 2, w / 2) owns rows [64 wm, +64) and columns
+// [128 wd, +128) of the slice.  A wide slice loads each G slice once for 512 output
+// columns.
 //   X region of a stage: KS contraction rows x DN columns of E / C, natural
 //     [k][d] layout, 64-byte segments XOR-swizzled by tr_swz(row) so the
 //     transposing fragment reads are free of bank conflicts.
-//   G region: dE — 128 G rows (tokens) x 128 bytes of contraction (vocab), the
-//     main loop's 16-byte-chunk swizzle; dC — KS G rows (tokens = contraction) x
-//     128 vocab columns, read transposed like X.
+//   G region (16 KiB): dE -- 128 G rows (tokens) x 128 bytes of one G row (the
+//     slice's contraction columns; for 16-bit types 32 columns' hi then lo), the
+//     main loop's 16-byte-chunk swizzle; dC -- KS G rows (tokens = contraction) x
+//     the whole 512-byte G row (128 vocab columns), read transposed like X.
+// 16-bit types take one MFMA per G half on the same X fragment: per 16-deep
+// contraction step kp, the hi fragment (chunks 2 kp + kg of the dE row slice, or
+// element columns 64 q + 0..31 of a dC row) and the lo one (chunks 4 + 2 kp + kg,
+// or columns 64 q + 32..63).
 template <typename T>
 struct SumGeo {
   static constexpr int ES = sizeof(T);
+  static constexpr bool SPLIT = g_split(ES);
   static constexpr int NW = 8;                     // waves: 2 (rows) x 4 (column quarters)
   static constexpr int NT = 64 * NW;
   static constexpr int DN = 512;
-  static constexpr int KS = 128 / ES;              // contraction elements per slice
+  static constexpr int KS = 32;                    // contraction elements per slice
   static constexpr int SPT = kBwdVocab / KS;       // slices per 128-deep tile
   static constexpr int XP = DN * ES;               // bytes of one X row in LDS
-  static constexpr int X_BYTES = KS * XP;          // 64 KiB
-  static constexpr int GTP = kBwdVocab * ES;       // bytes of one G row
+  static constexpr int X_BYTES = KS * XP;          // 32 KiB (16-bit), 64 KiB (fp32)
+  static constexpr int GTP = (int)g_tile_bytes(ES) / kBwdTokens;  // bytes of one G row (512)
   static constexpr int G_BYTES = 16384;            // 128 x 128 B (dE) = KS x GTP (dC)
-  static constexpr int STAGE = X_BYTES + G_BYTES;  // 80 KiB
-  static constexpr int STAGES = 2;
-  static constexpr int XLW = X_BYTES / 1024 / NW;  // X loads per wave per stage (8)
+  static constexpr int STAGE = X_BYTES + G_BYTES;  // 48 KiB (16-bit), 80 KiB (fp32)
+  static constexpr int STAGES = SPLIT ? 3 : 2;
+  static constexpr int XLW = X_BYTES / 1024 / NW;  // X loads per wave per stage (4 / 8)
   static constexpr int GLW = G_BYTES / 1024 / NW;  // G loads per wave per stage (2)
   static constexpr int LPW = XLW + GLW;
   static constexpr int KE = 32 / ES;               // contraction elements per MFMA step
-  static_assert(X_BYTES == 65536 && KS * GTP == G_BYTES, "stage geometry");
-  static_assert(STAGES * STAGE <= 163840, "two stages fill the 160 KiB of LDS");
+  static constexpr int NSTORE = 4 * 2 * (ES == 2 ? 2 : 4);  // output stores per wave per task
+  static_assert(GTP == 512 && KS * GTP == G_BYTES && 128 * 128 == G_BYTES, "stage geometry");
+  static_assert(STAGES * STAGE <= 163840, "the stages fit the 160 KiB of LDS");
+  static_assert((STAGES - 2) * LPW + NSTORE < 64, "in-flight operations must fit vmcnt");
 };
 
-// The narrow geometry: 4 waves, 256 output columns, 3 stages of 48 KiB (the dC sums:
-// many owners with one or two kept tiles, where a deeper pipeline and shorter
-// epilogues pay more than the wide slice's halved G traffic).
+// The narrow geometry: 4 waves, 256 output columns, 3 stages of 48 KiB (fp32) or 4 of
+// 32 KiB (16-bit) (the dC sums: many owners with one or two kept tiles, where a deeper
+// pipeline and shorter epilogues pay more than the wide slice's halved G traffic).
 template <typename T>
 struct SumGeoNarrow {
   static constexpr int NT = 256;
   static constexpr int ES = sizeof(T);
+  static constexpr bool SPLIT = g_split(ES);
   static constexpr int DN = 256;
-  static constexpr int KS = 128 / ES;              // contraction elements per slice
+  static constexpr int KS = 32;                    // contraction elements per slice
   static constexpr int SPT = kBwdVocab / KS;       // slices per 128-deep tile
   static constexpr int XP = DN * ES;               // bytes of one X row in LDS
-  static constexpr int X_BYTES = KS * XP;          // 32 KiB
-  static constexpr int GTP = kBwdVocab * ES;       // bytes of one G row
+  static constexpr int X_BYTES = KS * XP;          // 16 KiB (16-bit), 32 KiB (fp32)
+  static constexpr int GTP = (int)g_tile_bytes(ES) / kBwdTokens;  // bytes of one G row (512)
   static constexpr int G_BYTES = 16384;            // 128 x 128 B (dE) = KS x GTP (dC)
-  static constexpr int STAGE = X_BYTES + G_BYTES;  // 48 KiB
-  static constexpr int STAGES = 3;
-  static constexpr int XLW = X_BYTES / 1024 / 4;   // X loads per wave per stage (8)
+  static constexpr int STAGE = X_BYTES + G_BYTES;  // 32 KiB (16-bit), 48 KiB (fp32)
+  static constexpr int STAGES = SPLIT ? 4 : 3;
+  static constexpr int XLW = X_BYTES / 1024 / 4;   // X loads per wave per stage (4 / 8)
   static constexpr int GLW = G_BYTES / 1024 / 4;   // G loads per wave per stage (4)
   static constexpr int LPW = XLW + GLW;
   static constexpr int KE = 32 / ES;               // contraction elements per MFMA step
   static constexpr int NSTORE = 4 * 2 * (ES == 2 ? 2 : 4);  // output stores per wave per task
-  static_assert(X_BYTES == 32768 && KS * GTP == G_BYTES, "stage geometry");
+  static_assert(GTP == 512 && KS * GTP == G_BYTES && 128 * 128 == G_BYTES, "stage geometry");
+  static_assert(STAGES * STAGE <= 163840, "the stages fit the 160 KiB of LDS");
   static_assert((STAGES - 2) * LPW + NSTORE < 64, "in-flight operations must fit vmcnt");
 };
 
@@ -1734,13 +1785,16 @@ __global__ __launch_bounds__(SumGeo<T>::NT, 1) void bwd_sum_kernel(BwdArgs a, in
       goff[j] = tr_off<S::GTP>(row, pb);
     }
   }
-  // Fragment read offsets within a stage (16-bit types).
-  uint32_t xo[4], go_t[2], go_n[2][4];
+  // Fragment read offsets within a stage (16-bit types): go_t[0 / 1][jj] the dC hi /
+  // lo fragments, go_n[jj][ks] the dE row chunks 2 ks + kg.
+  uint32_t xo[4], go_t[2][2], go_n[2][4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) xo[i] = tr_lane_off<S::XP>(wd * 128 + 32 * i);
 #pragma unroll
   for (int jj = 0; jj < 2; ++jj) {
-    go_t[jj] = S::X_BYTES + tr_lane_off<S::GTP>(wm * 64 + 32 * jj);
+#pragma unroll
+    for (int hl = 0; hl < 2; ++hl)
+      go_t[hl][jj] = S::X_BYTES + tr_lane_off<S::GTP>(2 * (wm * 64 + 32 * jj) + 32 * hl);
     const uint32_t row = (uint32_t)(wm * 64 + 32 * jj + n);
     const uint32_t c = (row ^ (row >> 3)) & 7u;
 #pragma unroll
@@ -1817,15 +1871,13 @@ __global__ __launch_bounds__(SumGeo<T>::NT, 1) void bwd_sum_kernel(BwdArgs a, in
   };
 
   f32x16 acc[4][2];
-  // Fragments of one 32-byte contraction step ks of stage st, and its 8 MFMAs.
+  // Fragments of one 32-byte contraction step ks of stage st (fp32), and its 8 MFMAs.
   auto frags = [&](int st, int ks, u32x4 (&xf)[4], u32x4 (&gf)[2]) {
     const char* sp = smem + st * S::STAGE;
 #pragma unroll
     for (int jj = 0; jj < 2; ++jj) {
       if constexpr (PHASE == 0)
         gf[jj] = lds_ld16(sp, go_n[jj][ks]);
-      else if constexpr (ES == 2)
-        gf[jj] = frag_tr16(sp + go_t[jj] + 16 * ks * S::GTP, 4 * S::GTP);
       else
         gf[jj] = frag_tr32<S::GTP>(sp + S::X_BYTES, ks * S::KE, wm * 64 + 32 * jj);
     }
@@ -1843,12 +1895,50 @@ __global__ __launch_bounds__(SumGeo<T>::NT, 1) void bwd_sum_kernel(BwdArgs a, in
 #pragma unroll
       for (int jj = 0; jj < 2; ++jj) acc[i][jj] = Traits<T>::mfma(xf[i], gf[jj], acc[i][jj]);
   };
+  // 16-bit types: all fragments of a stage (two 16-deep steps kp, each an X fragment
+  // per column block and a hi and a lo G fragment per row block), then its 32 MFMAs.
+  u32x4 sxf[2][4], sgf[2][2][2];
+  auto frags_split = [&](int st) {
+    const char* sp = smem + st * S::STAGE;
+#pragma unroll
+    for (int kp = 0; kp < 2; ++kp) {
+#pragma unroll
+      for (int hl = 0; hl < 2; ++hl)
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) {
+          if constexpr (PHASE == 0)
+            sgf[kp][hl][jj] = lds_ld16(sp, go_n[jj][2 * hl + kp]);
+          else
+            sgf[kp][hl][jj] = frag_tr16(sp + go_t[hl][jj] + 16 * kp * S::GTP, 4 * S::GTP);
+        }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sxf[kp][i] = frag_tr16(sp + xo[i] + 16 * kp * S::XP, 4 * S::XP);
+    }
+  };
+  auto mma_split = [&]() {
+#pragma unroll
+    for (int kp = 0; kp < 2; ++kp)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int hl = 0; hl < 2; ++hl)
+#pragma unroll
+          for (int jj = 0; jj < 2; ++jj) acc[i][jj] = Traits<T>::mfma(sxf[kp][i], sgf[kp][hl][jj], acc[i][jj]);
+  };
   // RK = LDS read instructions per contraction step, MK = MFMAs per contraction step.
   constexpr int RK = (ES == 2 ? 8 : 16) + (PHASE == 0 ? 2 : (ES == 2 ? 4 : 8));
   constexpr int MK = 8 * Traits<T>::kInstrPerStep;
+  // fp16 G tiles hold G 2^gexp: the epilogue scales the sums back (exact)
+  const float gdiv = __builtin_ldexpf(1.f, -(ES == 2 ? g_scale_exp(a) : 0));
 
   // acc[i][jj][r]: output column ds DN + 128 wd + 32 i + 8 (r/4) + 4 h + r%4 of row 64 wm + 32 jj + n.
   auto epilogue = [&](const Cur& c) {
+    if (ES == 2 && gdiv != 1.f) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) acc[i][jj] *= gdiv;
+    }
     const int64_t orow0 = (int64_t)(PHASE == 0 ? c.owner : vlo + c.owner) * 128;
     const int64_t orows = PHASE == 0 ? a.N : a.V;
     const int64_t nrows = orows - orow0 < 128 ? orows - orow0 : 128;
@@ -1960,8 +2050,51 @@ __global__ __launch_bounds__(SumGeo<T>::NT, 1) void bwd_sum_kernel(BwdArgs a, in
   //   (task end: epilogue)
   // The epilogue's stores are the newest vector memory operations at the next
   // barrier, so it waits with vmcnt(NSTORE) and lets them drain in the background.
-  constexpr int NSTORE = 4 * 2 * (ES == 2 ? 2 : 4);  // buffer stores per wave per kWriteT epilogue
-  static_assert(NSTORE < 64, "vmcnt is 6 bits");
+  constexpr int NSTORE = S::NSTORE;  // buffer stores per wave per kWriteT epilogue
+  if constexpr (S::SPLIT) {
+    // 16-bit types: three stages; a step's barrier, its DMA two slices ahead, all of
+    // its fragment reads, then its 32 MFMAs (the other wave of the SIMD fills the
+    // matrix pipe while one reads).
+#pragma unroll
+    for (int p = 0; p < S::STAGES - 1; ++p) {
+      issue_next(p);
+      advance_next();
+    }
+    int st = 0;
+    int since_store = S::STAGES;  // steps since the last epilogue that left stores in flight
+    for (;;) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) acc[i][jj] = zero16();
+      for (;;) {
+        if (since_store < S::STAGES)
+          stage_barrier<(S::STAGES - 2) * S::LPW + NSTORE>();
+        else
+          stage_barrier<(S::STAGES - 2) * S::LPW>();
+        issue_next((st + S::STAGES - 1) % S::STAGES);
+        frags_split(st);
+        mma_split();
+        // a step's LDS reads: 16 for X, 8 (dE) or 16 (dC, transposing) for G; the
+        // first 16-deep step's go first, the second's among its MFMAs
+        constexpr int RS = 16 + (PHASE == 0 ? 8 : 16);
+        __builtin_amdgcn_sched_group_barrier(0x100, RS / 2, 0);
+        sched_interleave<0, 16, RS / 2, 0, 0>();
+        sched_interleave<0, 16, 0, 0, 0>();
+        advance_next();
+        ++since_store;
+        st = st + 1 == S::STAGES ? 0 : st + 1;
+        if (++cs.h < S::SPT) continue;
+        cs.h = 0;
+        if (++cs.j == cs.cnt) break;
+      }
+      epilogue(cs);
+      if (mode == kWriteT) since_store = 1;
+      if (!seek(cs.q + 1, cs)) break;
+    }
+    wait_vmcnt<0>();
+    return;
+  }
   issue_next(0);
   advance_next();
   stage_barrier<0>();
@@ -2031,6 +2164,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_narrow_kernel(BwdArgs a, 
   const int vwg = xcd * nper + lidx, nwg = (int)gridDim.x;  // workgroups numbered XCD-major
   // dC: this workgroup's bin of the schedule the G kernel dealt, and its first D slice
   static_assert(PHASE == 0 || S::DN == kDcSliceCols, "the dC schedule assumes this slice width");
+  static_assert(S::SPT == kDcStepsPerTile, "the dC schedule counts these steps per kept tile");
   const int dcb = dc_bins(nwg, nds);
   const int dcm = dcb > 0 ? vwg / nds : 0;
   const int ds0 = dcb > 0 ? vwg - dcm * nds : vwg;
@@ -2072,13 +2206,16 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_narrow_kernel(BwdArgs a, 
       goff[j] = tr_off<S::GTP>(row, pb);
     }
   }
-  // Fragment read offsets within a stage (16-bit types).
-  uint32_t xo[4], go_t[2], go_n[2][4];
+  // Fragment read offsets within a stage (16-bit types): go_t[0 / 1][jj] the dC hi /
+  // lo fragments, go_n[jj][ks] the dE row chunks 2 ks + kg.
+  uint32_t xo[4], go_t[2][2], go_n[2][4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) xo[i] = tr_lane_off<S::XP>(wd * 128 + 32 * i);
 #pragma unroll
   for (int jj = 0; jj < 2; ++jj) {
-    go_t[jj] = S::X_BYTES + tr_lane_off<S::GTP>(wm * 64 + 32 * jj);
+#pragma unroll
+    for (int hl = 0; hl < 2; ++hl)
+      go_t[hl][jj] = S::X_BYTES + tr_lane_off<S::GTP>(2 * (wm * 64 + 32 * jj) + 32 * hl);
     const uint32_t row = (uint32_t)(wm * 64 + 32 * jj + n);
     const uint32_t c = (row ^ (row >> 3)) & 7u;
 #pragma unroll
@@ -2165,22 +2302,29 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_narrow_kernel(BwdArgs a, 
   };
 
   f32x16 acc[4][2];
-  // A step's fragments for its four 32-byte contraction steps (ks): the reads of
-  // ks 0 and 1 go first, those of ks 2 and 3 among the MFMAs of ks 0 and 1.
-  u32x4 xf[4][4], gf[4][2];
+  // A step's fragments, read before its MFMAs: fp32, four 32-byte contraction steps
+  // (ks) of an X and a G fragment each; 16-bit types, two 16-deep steps (kp) of an X
+  // fragment and a G hi and lo fragment each (the lo ones take a second MFMA on the
+  // same X fragment).  The reads of the first half of the step go first, the rest
+  // among the MFMAs of the first half.
+  constexpr int NK = S::SPLIT ? 2 : 4;  // contraction steps per stage
+  constexpr int NH = S::SPLIT ? 2 : 1;  // G fragments per row block and step
+  u32x4 xf[NK][4], gf[NK][NH][2];
   auto frags = [&](int st) {
     const char* sp = smem + st * S::STAGE;
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
+    for (int ks = 0; ks < NK; ++ks) {
 #pragma unroll
-      for (int jj = 0; jj < 2; ++jj) {
-        if constexpr (PHASE == 0)
-          gf[ks][jj] = lds_ld16(sp, go_n[jj][ks]);
-        else if constexpr (ES == 2)
-          gf[ks][jj] = frag_tr16(sp + go_t[jj] + 16 * ks * S::GTP, 4 * S::GTP);
-        else
-          gf[ks][jj] = frag_tr32<S::GTP>(sp + S::X_BYTES, ks * S::KE, wm * 64 + 32 * jj);
-      }
+      for (int hl = 0; hl < NH; ++hl)
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) {
+          if constexpr (PHASE == 0)
+            gf[ks][hl][jj] = lds_ld16(sp, go_n[jj][2 * hl + ks]);
+          else if constexpr (ES == 2)
+            gf[ks][hl][jj] = frag_tr16(sp + go_t[hl][jj] + 16 * ks * S::GTP, 4 * S::GTP);
+          else
+            gf[ks][hl][jj] = frag_tr32<S::GTP>(sp + S::X_BYTES, ks * S::KE, wm * 64 + 32 * jj);
+        }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         if constexpr (ES == 2)
@@ -2192,25 +2336,40 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_narrow_kernel(BwdArgs a, 
   };
   auto mma = [&]() {
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
+    for (int ks = 0; ks < NK; ++ks)
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int jj = 0; jj < 2; ++jj) acc[i][jj] = Traits<T>::mfma(xf[ks][i], gf[ks][jj], acc[i][jj]);
+        for (int hl = 0; hl < NH; ++hl)
+#pragma unroll
+          for (int jj = 0; jj < 2; ++jj) acc[i][jj] = Traits<T>::mfma(xf[ks][i], gf[ks][hl][jj], acc[i][jj]);
   };
   // RK = LDS read instructions per contraction step, MK = MFMAs per contraction step.
-  constexpr int RK = (ES == 2 ? 8 : 16) + (PHASE == 0 ? 2 : (ES == 2 ? 4 : 8));
-  constexpr int MK = 8 * Traits<T>::kInstrPerStep;
+  constexpr int RK = (ES == 2 ? 8 : 16) + NH * (PHASE == 0 ? 2 : (ES == 2 ? 4 : 8));
+  constexpr int MK = 8 * NH * Traits<T>::kInstrPerStep;
   auto schedule = [&]() {
-    __builtin_amdgcn_sched_group_barrier(0x100, 2 * RK, 0);
-    sched_interleave<0, MK, RK, 0, 0>();
-    sched_interleave<0, MK, RK, 0, 0>();
-    sched_interleave<0, MK, 0, 0, 0>();
-    sched_interleave<0, MK, 0, 0, 0>();
+    __builtin_amdgcn_sched_group_barrier(0x100, NK / 2 * RK, 0);
+    if constexpr (NK == 4) {
+      sched_interleave<0, MK, RK, 0, 0>();
+      sched_interleave<0, MK, RK, 0, 0>();
+      sched_interleave<0, MK, 0, 0, 0>();
+      sched_interleave<0, MK, 0, 0, 0>();
+    } else {
+      sched_interleave<0, MK, RK, 0, 0>();
+      sched_interleave<0, MK, 0, 0, 0>();
+    }
   };
+  // fp16 G tiles hold G 2^gexp: the epilogue scales the sums back (exact)
+  const float gdiv = __builtin_ldexpf(1.f, -(ES == 2 ? g_scale_exp(a) : 0));
 
   // acc[i][jj][r]: output column ds DN + 128 wd + 32 i + 8 (r/4) + 4 h + r%4 of row 64 wm + 32 jj + n.
   auto epilogue = [&](const Cur& c) {
+    if (ES == 2 && gdiv != 1.f) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) acc[i][jj] *= gdiv;
+    }
     const int64_t orow0 = (int64_t)(PHASE == 0 ? c.owner : vlo + c.owner) * 128;
     const int64_t orows = PHASE == 0 ? a.N : a.V;
     const int64_t nrows = orows - orow0 < 128 ? orows - orow0 : 128;

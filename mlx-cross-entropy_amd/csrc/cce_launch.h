@@ -75,11 +75,22 @@ constexpr int64_t kQuantDefaultChunkRows = 32768;  // 256 MiB of bf16 scratch at
 // the pass).  A pass holds every token block of its tiles, so dC and dBias of a
 // pass are final when its sums end; dE is carried between passes and chunks in
 // fp32 when the backward takes more than one pass.
+// G tiles keep the softmax gradient to fp32 accuracy for every input dtype: fp32
+// inputs store G in fp32; 16-bit inputs store it as a pair of 16-bit values,
+// hi = round(G) and lo = round(G - hi) (hi + lo = G to about 2^-17 relative), and
+// the sums issue one MFMA per half against the same E / C fragment.  A tile row of
+// 128 vocabulary columns is then 256 16-bit values: columns 32 q + i go to elements
+// 64 q + i (hi) and 64 q + 32 + i (lo), so that a 128-byte slice of a row holds 32
+// columns' hi and lo (the dE sums' contraction slice).  Every tile is 64 KiB.
+constexpr bool g_split(size_t esize) { return esize == 2; }
+constexpr size_t g_tile_bytes(size_t esize) {
+  return (size_t)kBwdTokens * kBwdVocab * esize * (g_split(esize) ? 2 : 1);
+}
 // G-tile budget of one pass, in MiB (the default workspace; a smaller workspace
-// gives smaller passes, down to 2 tiles per token block).  512 MiB holds a quarter of
-// the Llama-3 8B head's tiles (N = 8192, V = 128256: 2.1 GB of bf16 G when nothing is
-// skipped), so a backward launches at most 4 passes there; each pass past the ones the
-// data needs costs one empty launch per kernel (about 4.5 us).
+// gives smaller passes, down to 2 tiles per token block).  512 MiB holds 8192 tiles, an
+// eighth of the Llama-3 8B head's (N = 8192, V = 128256: 4.2 GB of G when nothing is
+// skipped), so a dense backward takes 8 passes there; a filtered one keeps a few
+// hundred tiles and takes one.
 #ifndef CCE_G_SCRATCH_MIB
 #define CCE_G_SCRATCH_MIB 512
 #endif
@@ -95,6 +106,10 @@ constexpr int kMaxDcBins = 256;                        // workgroup bins of the 
 constexpr int64_t kPermMaxN = 65536;   // rows the sort handles
 constexpr int64_t kPermMaxKey = 16384; // tiles + 1 (the key of rows without gradient)
 constexpr int kPermFlag = 15;          // counts[kPermFlag]: 1 when the backward runs on sorted rows
+// counts[kGScaleExp]: fp16 G tiles hold G * 2^s with s = counts[kGScaleExp] (written by
+// the compaction from max |d_nll|, so that G's largest values sit near 2^14 and its
+// small ones stay clear of fp16's subnormal range); the sums scale back by 2^-s.
+constexpr int kGScaleExp = 14;
 
 // Pass table: kPassInts ints per pass of the current chunk, written by the compaction.
 constexpr int kPassInts = 16;
@@ -125,7 +140,8 @@ struct BwdPlan {
   int64_t chunk_pairs;      // nrb * chunk_nvt: the most pairs one chunk may keep
   int64_t cap;              // G tiles per pass: chunk_pairs, or at least 2 nrb
   int64_t max_passes;       // passes launched per chunk
-  size_t g_bytes;           // bytes of one G tile (128 x 128 x sizeof(T))
+  size_t g_bytes;           // bytes of one G tile (g_tile_bytes: hi and lo halves for 16-bit types)
+  int esize;                // bytes of one input element
   bool perm_ok;             // the sorted token order is available (N and tile count in range)
   bool carry;               // the fp32 dE carry is reserved (more than one pass or chunk may run)
   // workspace byte offsets
@@ -161,7 +177,8 @@ inline BwdPlan make_bwd_plan_cap(size_t esize, int64_t N, int64_t D, int64_t V, 
   P.nrb = (N + kBwdTokens - 1) / kBwdTokens;
   P.total = P.nvt * P.nrb;
   P.nwords = (P.nvt + 31) / 32;
-  P.g_bytes = (size_t)kBwdTokens * kBwdVocab * esize;
+  P.g_bytes = g_tile_bytes(esize);
+  P.esize = (int)esize;
   const bool want_g = want_de || want_dc;
   const int64_t cw = plan_chunk_nvt(P.nvt, P.nrb, max_chunk_nvt);
   P.chunk_nvt = cw;
@@ -218,7 +235,7 @@ inline BwdPlan make_bwd_plan_cap(size_t esize, int64_t N, int64_t D, int64_t V, 
 // G tiles of a pass in the default workspace: the budget, at least 2 per token block.
 inline int64_t default_cap(size_t esize, int64_t N) {
   const int64_t nrb = (N + kBwdTokens - 1) / kBwdTokens;
-  const int64_t by_budget = (int64_t)(kGScratchBudget / ((size_t)kBwdTokens * kBwdVocab * esize));
+  const int64_t by_budget = (int64_t)(kGScratchBudget / g_tile_bytes(esize));
   return by_budget > 2 * nrb ? by_budget : 2 * nrb;
 }
 
@@ -302,7 +319,7 @@ struct BwdArgs {
   int* own_vt;        // [chunk_nvt] vocab tiles with kept tiles, by pass, most first (dC owners)
   int* dc_bin_start;  // [kMaxDcBins + 1] dC schedule: owners of bin m are dc_bin_owner[start[m] .. start[m + 1])
   int* dc_bin_owner;  // [chunk_nvt]
-  char* gtile;        // [cap][128 tokens][128 vocab] G tiles of one pass, token-major, dtype
+  char* gtile;        // [cap] G tiles of one pass, token-major (g_tile_bytes each)
   float* colsum;      // [cap][128] per-slot column sums of G (dBias)
   float* de_acc;      // [N, D] fp32, only when the plan reserves the carry
   int64_t* tile_stats;  // [3] or null: kept pairs, all pairs, kept pairs of the input-order token blocks
@@ -324,6 +341,7 @@ struct BwdArgs {
   int dc_geo;           // dC sums geometry: 0 the backward's choice (filter off: wide; on: per pass), 1 wide, 2 narrow
   int dc_zeroed;        // dC already holds zeros: only rows of vocab tiles with kept tiles are written
   int stats32;          // tile_max per 32 columns in the reference's layout [N][ceil(V/32)] (else [nvt][N])
+  int g_scaled;         // fp16: G tiles hold G * 2^counts[kGScaleExp] (else unscaled)
   QuantRows q;          // q.wq set: c is unused; every chunk first dequantizes its rows into q.scratch
 };
 

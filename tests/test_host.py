@@ -81,8 +81,9 @@ def test_backward_workspace_is_bounded(ext, N, D, V):
     chunk_pairs = min(nrb * nvt, nrb * 32 * (8192 // nrb))
     for dtype, es in ((2, 2), (0, 4)):
         ws = lib.cce_backward_workspace_size(dtype, N, D, V, 1, 1, 1)
-        g_slots = max(G_BUDGET // (128 * 128 * es), 2 * nrb)
-        bound = (g_slots * (128 * 128 * es + 512)  # G tiles + their column sums
+        tile = 128 * 128 * 4  # fp32 G, or the hi and lo halves of a 16-bit G
+        g_slots = max(G_BUDGET // tile, 2 * nrb)
+        bound = (g_slots * (tile + 512)  # G tiles + their column sums
                  + N * D * (4 + es)                # fp32 dE carry + the sorted copy of E
                  + N * nwords * 4 + 2 * nrb * nwords * 4  # keep bits per row / per block
                  + 40 * chunk_pairs + 64 * N + (4 << 20))
