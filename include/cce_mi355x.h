@@ -186,6 +186,20 @@ int cce_backward(int dtype, const void* e, const void* c, const void* bias,
 /* tile_max is in the reference's layout (cce_forward_ref: per 32 columns, [N][ceil(V/32)]);
  * the filter takes each 128-column tile's max as the max of its four 32-column maxima. */
 #define CCE_BWD_REF_STATS 128
+/* Launch the passes of the dense worst case and let the device skip the ones the data
+ * does not need, instead of waiting on the host, once per vocabulary chunk, for the
+ * compaction's pass count (which then launches exactly the passes needed).  The wait
+ * is skipped anyway while the stream is being captured into a graph, and by
+ * cce_backward_noalloc. */
+#define CCE_BWD_DEVICE_PASSES 256
+/* Precision of the softmax gradient G between the backward's two products (16-bit
+ * inputs; fp32 inputs keep G in fp32).  By default G is carried as a pair of 16-bit
+ * values (hi + lo, fp32-accurate: the reference keeps it in fp32 through both
+ * products) when the filter is disabled, and rounded once to the input dtype when it
+ * is on (the filter's own tolerance is 2e-2; the rounding adds about 2e-3).  These
+ * force one or the other. */
+#define CCE_BWD_G_PAIR 512
+#define CCE_BWD_G_SINGLE 1024
 
 /* As cce_backward, with flags (CCE_BWD_*) and vocabulary chunks of at most
  * max_chunk_tiles tiles (0: the library's choice; else a multiple of 32; the workspace

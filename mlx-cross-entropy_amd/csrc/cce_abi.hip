@@ -231,6 +231,47 @@ int cce_backward(int dtype, const void* e, const void* c, const void* bias, cons
 
 namespace {
 
+// Pinned host ints the compaction writes the pass count into, and the event the host
+// waits on for them: one set per host thread and device (a thread waits for its own
+// call's count before it returns), grown as needed (a few KiB at most) and kept until
+// the process ends.
+hipError_t host_pass_buffer(size_t n, int** buf, hipEvent_t* ev) {
+  struct Slot {
+    int dev = -1;
+    int* buf = nullptr;
+    size_t n = 0;
+    hipEvent_t ev = nullptr;
+  };
+  thread_local Slot slots[8];
+  int dev = 0;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return err;
+  Slot* sl = nullptr;
+  for (Slot& x : slots)
+    if (x.dev == dev || (sl == nullptr && x.dev < 0)) {
+      sl = &x;
+      if (x.dev == dev) break;
+    }
+  if (sl == nullptr) return hipErrorOutOfMemory;  // more devices than slots: the device-only schedule
+  if (sl->ev == nullptr) {
+    if ((err = hipEventCreateWithFlags(&sl->ev, hipEventDisableTiming)) != hipSuccess) return err;
+    sl->dev = dev;
+  }
+  if (sl->n < n) {
+    const size_t want = n < 256 ? 256 : n;
+    int* p = nullptr;
+    if ((err = hipHostMalloc(reinterpret_cast<void**>(&p), want * sizeof(int), hipHostMallocDefault)) != hipSuccess)
+      return err;
+    // the smaller buffer is not freed: a call that failed after queueing its compaction
+    // may still have it written into
+    sl->buf = p;
+    sl->n = want;
+  }
+  *buf = sl->buf;
+  *ev = sl->ev;
+  return hipSuccess;
+}
+
 // The backward over plain (q == null) or quantized classifier rows.  Quantized rows
 // reserve the scratch of one chunk in the workspace, and the chunks are capped at
 // q->chunk_rows rows.
@@ -322,6 +363,8 @@ int backward_impl(int dtype, const void* e, const void* c, const void* bias, con
   a.dc_zeroed = (flags & CCE_BWD_DC_ZEROED) ? 1 : 0;
   a.stats32 = (flags & CCE_BWD_REF_STATS) ? 1 : 0;
   a.g_scaled = dtype == CCE_DTYPE_F16 ? 1 : 0;  // fp16 G tiles are scaled into fp16's normal range
+  // 16-bit G as the hi / lo pair with the filter off (the 1e-3 bar), rounded once with it on
+  a.g_split = es == 2 && !(flags & CCE_BWD_G_SINGLE) && ((flags & CCE_BWD_G_PAIR) || !(filter_log_eps > -INFINITY));
   a.plan = P;
   a.num_cus = cus;
   if (q) {
@@ -329,7 +372,17 @@ int backward_impl(int dtype, const void* e, const void* c, const void* bias, con
     a.q.scratch = ws + P.qrows;
   }
 
-  const hipError_t err = cce::launch_backward(dtype, a, s);
+  // The host waits for each chunk's pass count and launches exactly those passes,
+  // unless told not to or the stream is being captured (a graph cannot wait).
+  hipEvent_t pass_ev = nullptr;
+  if (!(flags & CCE_BWD_DEVICE_PASSES)) {
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &cap) == hipSuccess && cap == hipStreamCaptureStatusNone) {
+      int* hp = nullptr;
+      if (host_pass_buffer((size_t)P.max_passes + 1, &hp, &pass_ev) == hipSuccess) a.host_pass = hp;
+    }
+  }
+  const hipError_t err = cce::launch_backward(dtype, a, s, a.host_pass ? pass_ev : nullptr);
   if (err != hipSuccess)
     return fail(CCE_ERR_LAUNCH, "[cce_backward] kernel launch failed: %s", hipGetErrorString(err));
   return CCE_OK;
@@ -347,13 +400,15 @@ int cce_backward_ex(int dtype, const void* e, const void* c, const void* bias, c
   g_err[0] = 0;
   constexpr int kKnown = CCE_BWD_DC_ZEROED | CCE_BWD_TOKENS_INPUT | CCE_BWD_TOKENS_SORTED | CCE_BWD_DE_SUMS_WIDE |
                          CCE_BWD_DE_SUMS_NARROW | CCE_BWD_DC_SUMS_WIDE | CCE_BWD_DC_SUMS_NARROW |
-                         CCE_BWD_REF_STATS;
+                         CCE_BWD_REF_STATS | CCE_BWD_DEVICE_PASSES | CCE_BWD_G_PAIR | CCE_BWD_G_SINGLE;
   if (flags & ~kKnown) return fail(CCE_ERR_INVALID_ARGUMENT, "[cce_backward] unknown flags 0x%x", flags);
   if ((flags & CCE_BWD_TOKENS_INPUT) && (flags & CCE_BWD_TOKENS_SORTED))
     return fail(CCE_ERR_INVALID_ARGUMENT, "[cce_backward] CCE_BWD_TOKENS_INPUT and CCE_BWD_TOKENS_SORTED exclude each other");
   if (((flags & CCE_BWD_DE_SUMS_WIDE) && (flags & CCE_BWD_DE_SUMS_NARROW)) ||
       ((flags & CCE_BWD_DC_SUMS_WIDE) && (flags & CCE_BWD_DC_SUMS_NARROW)))
     return fail(CCE_ERR_INVALID_ARGUMENT, "[cce_backward] a sums geometry flag pair excludes each other");
+  if ((flags & CCE_BWD_G_PAIR) && (flags & CCE_BWD_G_SINGLE))
+    return fail(CCE_ERR_INVALID_ARGUMENT, "[cce_backward] CCE_BWD_G_PAIR and CCE_BWD_G_SINGLE exclude each other");
   if (max_chunk_tiles < 0 || (max_chunk_tiles > 0 && max_chunk_tiles % 32 != 0))
     return fail(CCE_ERR_INVALID_ARGUMENT, "[cce_backward] max_chunk_tiles must be 0 or a positive multiple of 32, got %lld",
                 (long long)max_chunk_tiles);
@@ -406,12 +461,13 @@ int cce_backward_noalloc(int dtype, const void* e, const void* c, const void* bi
   g_err[0] = 0;
   constexpr int kKnown = CCE_BWD_DC_ZEROED | CCE_BWD_TOKENS_INPUT | CCE_BWD_TOKENS_SORTED | CCE_BWD_DE_SUMS_WIDE |
                          CCE_BWD_DE_SUMS_NARROW | CCE_BWD_DC_SUMS_WIDE | CCE_BWD_DC_SUMS_NARROW |
-                         CCE_BWD_REF_STATS;
+                         CCE_BWD_REF_STATS | CCE_BWD_DEVICE_PASSES | CCE_BWD_G_PAIR | CCE_BWD_G_SINGLE;
   if (flags & ~kKnown)
     return fail(CCE_ERR_INVALID_ARGUMENT, "[cce_backward_noalloc] unknown flags 0x%x", flags);
   if (((flags & CCE_BWD_TOKENS_INPUT) && (flags & CCE_BWD_TOKENS_SORTED)) ||
       ((flags & CCE_BWD_DE_SUMS_WIDE) && (flags & CCE_BWD_DE_SUMS_NARROW)) ||
-      ((flags & CCE_BWD_DC_SUMS_WIDE) && (flags & CCE_BWD_DC_SUMS_NARROW)))
+      ((flags & CCE_BWD_DC_SUMS_WIDE) && (flags & CCE_BWD_DC_SUMS_NARROW)) ||
+      ((flags & CCE_BWD_G_PAIR) && (flags & CCE_BWD_G_SINGLE)))
     return fail(CCE_ERR_INVALID_ARGUMENT, "[cce_backward_noalloc] a pair of flags excludes each other");
   int rc = check_common("cce_backward_noalloc", dtype, e, c, targets, N, D, V);
   if (rc != CCE_OK) return rc;
@@ -431,9 +487,10 @@ int cce_backward_noalloc(int dtype, const void* e, const void* c, const void* bi
   }
   void* ws = nullptr;
   if ((rc = scratch_of_current_device("cce_backward_noalloc", &ws)) != CCE_OK) return rc;
+  // no host wait for the pass count (its pinned buffer would be an allocation)
   return backward_impl(dtype, e, c, bias, targets, ignore_index, has_ignore, N, D, V, lse, tile_max, d_nll,
-                       filter_log_eps, dE, dC, dBias, ws, (size_t)CCE_NOALLOC_SCRATCH_BYTES, tile_stats, flags, 0,
-                       nullptr, hip_stream);
+                       filter_log_eps, dE, dC, dBias, ws, (size_t)CCE_NOALLOC_SCRATCH_BYTES, tile_stats,
+                       flags | CCE_BWD_DEVICE_PASSES, 0, nullptr, hip_stream);
 }
 
 int cce_dequantize(int dtype, const uint32_t* weight, const void* scales, const void* qbiases, int group_size,

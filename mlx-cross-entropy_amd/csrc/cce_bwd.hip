@@ -871,6 +871,7 @@ __global__ __launch_bounds__(1024) void bwd_compact_kernel(BwdArgs a, int chunk)
       a.pinfo[p * kPassInts + kPiOwnRb] = n_rb;
       a.pinfo[p * kPassInts + kPiOwnVt] = n_vt;
       a.pinfo[p * kPassInts + kPiDcWide] = (int64_t)mk * gwg <= kept_p * nds_w ? 1 : 0;
+      if (a.host_pass) a.host_pass[1 + p] = a.pinfo[p * kPassInts + kPiDcWide];
     }
     __syncthreads();  // wsum is the next scan's
   }
@@ -899,6 +900,10 @@ __global__ __launch_bounds__(1024) void bwd_compact_kernel(BwdArgs a, int chunk)
       pi[kPiOwnVt] = 0;
       pi[kPiDeMode] = -1;
     }
+  }
+  if (tid == 0 && a.host_pass) {  // the host launches exactly these passes
+    a.host_pass[0] = npass;
+    __threadfence_system();
   }
   if (tid == 0 && a.tile_stats) {  // [2]: already set from the whole bitmap when the sorted order was available
     if (chunk == 0) {
@@ -990,7 +995,11 @@ __host__ __device__ inline int dc_bins(int nwg, int nds) {
 // dealing order.  Run by one workgroup of NT threads (the bisection by wave 0);
 // smem holds its tables.
 constexpr int kDcOwnerCost = 3;  // a task's epilogue and restart, in pipeline steps (measured at c3)
-constexpr int kDcStepsPerTile = 4;  // pipeline steps of the narrow dC sums per kept tile (32-deep slices)
+// pipeline steps of the narrow dC sums per kept tile: one per 128-byte G row slice
+template <typename T>
+constexpr int dc_steps_per_tile(bool split) {
+  return kBwdVocab / (split ? 32 : 128 / (int)sizeof(T));
+}
 
 __device__ __forceinline__ int wave_sum(int v) {
 #pragma unroll
@@ -1142,8 +1151,9 @@ constexpr int kGThreads = GLoop<__bf16>::NTHREADS;
 // G of one wave's 128 x 64 block of a tile from its logits w: w[i][j][r] is the logit
 // of vocabulary v0 + 32 i + 8 (r/4) + 4 h + r%4 and token tok0 + 32 j + n.  Stored
 // token-major into the slot's G tile gtile at rows row0 + 32 j + n: fp32 as it is,
-// 16-bit types as the hi / lo pair of g_tile_bytes's layout (fp16 scaled by 2^gexp);
-// with WANT_DB the block's (unscaled) column sums over its 64 tokens go to red[0, 128).  Per token: g (0 for masked / out-of-range rows), lz =
+// 16-bit types rounded once (rows of 128 columns) or, with a.g_split, as the hi / lo
+// pair of g_tile_bytes's layout (fp16 scaled by 2^gexp either way); with WANT_DB the
+// block's (unscaled) column sums over its 64 tokens go to red[0, 128).  Per token: g (0 for masked / out-of-range rows), lz =
 // lse log2(e), or +inf when g == 0 so that p = 0 and G = 0 without a select, and the
 // target's place in the tile as tl - 4 h, which register (i, r) holds iff it equals
 // 32 i + 8 (r/4) + r%4 (a compile-time constant).  Columns past V (last vocabulary
@@ -1238,10 +1248,32 @@ __device__ __forceinline__ void g_block_epilogue(const BwdArgs& a, const RowData
             __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), grs,
                                                    lane_off + (uint32_t)((j * 32 * kBwdVocab + i * 32 + q * 8) * ES), 0, 0);
           }
+      } else if (!a.g_split) {
+        const uint32_t lane_off = (uint32_t)((row0 + n) * kBwdVocab * ES + h * 8 * ES);
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) {
+          uint32_t pk[4][2];
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int k = 0; k < 2; ++k) pk[q][k] = pack2<T>(gv[j][4 * q + 2 * k], gv[j][4 * q + 2 * k + 1]);
+#pragma unroll
+          for (int pq = 0; pq < 2; ++pq) {
+            u32x4 v;
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+              const auto sw = __builtin_amdgcn_permlane32_swap(pk[2 * pq][k], pk[2 * pq + 1][k], false, false);
+              v[k] = sw[0];
+              v[2 + k] = sw[1];
+            }
+            __builtin_amdgcn_raw_buffer_store_b128(v, grs,
+                                                   lane_off + (uint32_t)((j * 32 * kBwdVocab + i * 32 + pq * 16) * ES), 0, 0);
+          }
+        }
       } else {
-        // Rows of 256 elements: column 32 i + c of the tile goes to element 64 i + c
-        // (hi) and 64 i + 32 + c (lo), hi = round(G), lo = round(G - hi) (the
-        // difference is exact in fp32).
+        // The hi / lo pair: rows of 256 elements, column 32 i + c of the tile at
+        // element 64 i + c (hi) and 64 i + 32 + c (lo), hi = round(G), lo =
+        // round(G - hi) (the difference is exact in fp32).
         constexpr int RP = 2 * kBwdVocab * ES;  // bytes of one G row
         const uint32_t lane_off = (uint32_t)((row0 + n) * RP + h * 8 * ES);
 #pragma unroll
@@ -1357,7 +1389,7 @@ __global__ __launch_bounds__(kGThreads, 1) void bwd_g_kernel(BwdArgs a, int chun
         if (o < sched) {
           const int nds = (int)((a.D + kDcSliceCols - 1) / kDcSliceCols);
           const int nb = dc_bins((int)gridDim.x, nds);
-          dc_schedule<kGThreads>(a, pass, nb > 0 ? nb : 1, kDcStepsPerTile,
+          dc_schedule<kGThreads>(a, pass, nb > 0 ? nb : 1, dc_steps_per_tile<T>(a.g_split != 0),
                                  smem + 256);  // its tables start past box
         } else {
           empty_owner<T, kGThreads>(a, chunk, pass, o - sched);
@@ -1442,9 +1474,10 @@ template <typename T>
 using GDLoop = NTMainLoop<T, 2 * kBwdVocab, 2 * kBwdTokens, 2, 4>;  // A = 256 C rows, B = 256 E rows
 // Buffer stores one wave's G block epilogue issues (WANT_G, every one unconditional):
 // 4 column blocks x 2 token blocks x (4 for fp32; 2 each for the hi and lo halves of
-// 16-bit types).  The dense kernel's next first stage barrier lets exactly these stay
-// in flight; the count must follow g_block_epilogue's store loops (fewer stores would
-// let prefetch loads through).
+// the 16-bit pair).  The dense kernel's next first stage barrier lets exactly these
+// stay in flight; the count must follow g_block_epilogue's store loops (fewer stores
+// would let prefetch loads through), so after a single 16-bit G (16 stores) that
+// barrier waits for all of them instead.
 template <typename T>
 constexpr int kGStoresPerWave = 32;
 constexpr int kGDThreads = GDLoop<__bf16>::NTHREADS;
@@ -1544,7 +1577,7 @@ __global__ __launch_bounds__(kGDThreads, 1) void bwd_g_dense_kernel(BwdArgs a, i
                                                        (int64_t)rb * kBwdTokens + half * 64, half * 64,
                                                        a.gtile + (size_t)(slot - s0) * a.plan.g_bytes,
                                                        red + wave * kBwdVocab, &gr);
-      stored = WANT_G && !WANT_DB && slot >= 0;
+      stored = WANT_G && !WANT_DB && slot >= 0 && (sizeof(T) == 4 || a.g_split);
       if constexpr (WANT_DB) {
         // the two token halves of a tile are waves wave and wave + 2
         __syncthreads();
@@ -1578,70 +1611,70 @@ __global__ __launch_bounds__(kGDThreads, 1) void bwd_g_dense_kernel(BwdArgs a, i
 // ---------------------------------------------------------------- 5. sums of G_j . X_j
 // Geometry of one sum task: output rows = the owner's 128 rows (tokens for dE,
 // vocabulary for dC), output columns = one DN (512) slice of D; contraction over
-// the owner's kept tiles, 128 deep each, in slices of KS contraction elements (fp32:
-// 32; 16-bit types: 32 as well, each with its G hi and lo halves).  Eight waves (two
-// per SIMD): wave (wm, wd) = (w % 2, w / 2) owns rows [64 wm, +64) and columns
-// [128 wd, +128) of the slice.  A wide slice loads each G slice once for 512 output
-// columns.
+// the owner's kept tiles, 128 deep each, in slices of KS contraction elements: a
+// 128-byte G row slice (fp32 and single 16-bit G: 32 and 64 columns; the hi / lo
+// pair of 16-bit G: 32 columns' hi then lo).  Eight waves (two per SIMD): wave
+// (wm, wd) = (w % 2, w / 2) owns rows [64 wm, +64) and columns [128 wd, +128) of the
+// slice.  A wide slice loads each G slice once for 512 output columns.
 //   X region of a stage: KS contraction rows x DN columns of E / C, natural
 //     [k][d] layout, 64-byte segments XOR-swizzled by tr_swz(row) so the
 //     transposing fragment reads are free of bank conflicts.
-//   G region (16 KiB): dE -- 128 G rows (tokens) x 128 bytes of one G row (the
-//     slice's contraction columns; for 16-bit types 32 columns' hi then lo), the
-//     main loop's 16-byte-chunk swizzle; dC -- KS G rows (tokens = contraction) x
-//     the whole 512-byte G row (128 vocab columns), read transposed like X.
-// 16-bit types take one MFMA per G half on the same X fragment: per 16-deep
-// contraction step kp, the hi fragment (chunks 2 kp + kg of the dE row slice, or
-// element columns 64 q + 0..31 of a dC row) and the lo one (chunks 4 + 2 kp + kg,
-// or columns 64 q + 32..63).
-template <typename T>
+//   G region (16 KiB): dE -- 128 G rows (tokens) x the 128-byte row slice, the main
+//     loop's 16-byte-chunk swizzle; dC -- KS G rows (tokens = contraction) x the
+//     whole G row (128 vocab columns; GTP bytes), read transposed like X.
+// With the hi / lo pair (SPLIT) every 16-deep contraction step kp takes one MFMA per
+// G half on the same X fragment: the hi fragment (chunks 2 kp + kg of the dE row
+// slice, or element columns 64 q + 0..31 of a dC row) and the lo one (chunks
+// 4 + 2 kp + kg, or columns 64 q + 32..63).
+template <typename T, bool SPLIT>
 struct SumGeo {
   static constexpr int ES = sizeof(T);
-  static constexpr bool SPLIT = g_split(ES);
+  static_assert(!SPLIT || ES == 2, "the hi / lo pair is a 16-bit layout");
   static constexpr int NW = 8;                     // waves: 2 (rows) x 4 (column quarters)
   static constexpr int NT = 64 * NW;
   static constexpr int DN = 512;
-  static constexpr int KS = 32;                    // contraction elements per slice
+  static constexpr int KS = SPLIT ? 32 : 128 / ES;  // contraction elements per slice
   static constexpr int SPT = kBwdVocab / KS;       // slices per 128-deep tile
   static constexpr int XP = DN * ES;               // bytes of one X row in LDS
-  static constexpr int X_BYTES = KS * XP;          // 32 KiB (16-bit), 64 KiB (fp32)
-  static constexpr int GTP = (int)g_tile_bytes(ES) / kBwdTokens;  // bytes of one G row (512)
+  static constexpr int X_BYTES = KS * XP;          // 32 KiB (hi / lo), 64 KiB (otherwise)
+  static constexpr int GTP = (SPLIT ? 2 : 1) * kBwdVocab * ES;  // bytes of one G row
   static constexpr int G_BYTES = 16384;            // 128 x 128 B (dE) = KS x GTP (dC)
-  static constexpr int STAGE = X_BYTES + G_BYTES;  // 48 KiB (16-bit), 80 KiB (fp32)
+  static constexpr int STAGE = X_BYTES + G_BYTES;  // 48 KiB (hi / lo), 80 KiB (otherwise)
   static constexpr int STAGES = SPLIT ? 3 : 2;
   static constexpr int XLW = X_BYTES / 1024 / NW;  // X loads per wave per stage (4 / 8)
   static constexpr int GLW = G_BYTES / 1024 / NW;  // G loads per wave per stage (2)
   static constexpr int LPW = XLW + GLW;
   static constexpr int KE = 32 / ES;               // contraction elements per MFMA step
   static constexpr int NSTORE = 4 * 2 * (ES == 2 ? 2 : 4);  // output stores per wave per task
-  static_assert(GTP == 512 && KS * GTP == G_BYTES && 128 * 128 == G_BYTES, "stage geometry");
+  static_assert(KS * GTP == G_BYTES && 128 * 128 == G_BYTES, "stage geometry");
   static_assert(STAGES * STAGE <= 163840, "the stages fit the 160 KiB of LDS");
   static_assert((STAGES - 2) * LPW + NSTORE < 64, "in-flight operations must fit vmcnt");
 };
 
-// The narrow geometry: 4 waves, 256 output columns, 3 stages of 48 KiB (fp32) or 4 of
-// 32 KiB (16-bit) (the dC sums: many owners with one or two kept tiles, where a deeper
-// pipeline and shorter epilogues pay more than the wide slice's halved G traffic).
-template <typename T>
+// The narrow geometry: 4 waves, 256 output columns, 3 stages of 48 KiB (or 4 of 32 KiB
+// with the hi / lo pair) (the dC sums: many owners with one or two kept tiles, where
+// a deeper pipeline and shorter epilogues pay more than the wide slice's halved G
+// traffic).
+template <typename T, bool SPLIT>
 struct SumGeoNarrow {
   static constexpr int NT = 256;
   static constexpr int ES = sizeof(T);
-  static constexpr bool SPLIT = g_split(ES);
+  static_assert(!SPLIT || ES == 2, "the hi / lo pair is a 16-bit layout");
   static constexpr int DN = 256;
-  static constexpr int KS = 32;                    // contraction elements per slice
+  static constexpr int KS = SPLIT ? 32 : 128 / ES;  // contraction elements per slice
   static constexpr int SPT = kBwdVocab / KS;       // slices per 128-deep tile
   static constexpr int XP = DN * ES;               // bytes of one X row in LDS
-  static constexpr int X_BYTES = KS * XP;          // 16 KiB (16-bit), 32 KiB (fp32)
-  static constexpr int GTP = (int)g_tile_bytes(ES) / kBwdTokens;  // bytes of one G row (512)
+  static constexpr int X_BYTES = KS * XP;          // 16 KiB (hi / lo), 32 KiB (otherwise)
+  static constexpr int GTP = (SPLIT ? 2 : 1) * kBwdVocab * ES;  // bytes of one G row
   static constexpr int G_BYTES = 16384;            // 128 x 128 B (dE) = KS x GTP (dC)
-  static constexpr int STAGE = X_BYTES + G_BYTES;  // 32 KiB (16-bit), 48 KiB (fp32)
+  static constexpr int STAGE = X_BYTES + G_BYTES;  // 32 KiB (hi / lo), 48 KiB (otherwise)
   static constexpr int STAGES = SPLIT ? 4 : 3;
   static constexpr int XLW = X_BYTES / 1024 / 4;   // X loads per wave per stage (4 / 8)
   static constexpr int GLW = G_BYTES / 1024 / 4;   // G loads per wave per stage (4)
   static constexpr int LPW = XLW + GLW;
   static constexpr int KE = 32 / ES;               // contraction elements per MFMA step
   static constexpr int NSTORE = 4 * 2 * (ES == 2 ? 2 : 4);  // output stores per wave per task
-  static_assert(GTP == 512 && KS * GTP == G_BYTES && 128 * 128 == G_BYTES, "stage geometry");
+  static_assert(KS * GTP == G_BYTES && 128 * 128 == G_BYTES, "stage geometry");
   static_assert(STAGES * STAGE <= 163840, "the stages fit the 160 KiB of LDS");
   static_assert((STAGES - 2) * LPW + NSTORE < 64, "in-flight operations must fit vmcnt");
 };
@@ -1712,6 +1745,66 @@ __device__ __forceinline__ void dma16_s(const char* sbase, uint32_t voff, uint32
                : "memory", "m0");
 }
 
+// Software pipeline of the sums for 16-bit types (the G hi / lo geometry): stage st
+// holds two 16-deep contraction steps, and the loop runs them half a stage apart:
+//   read step 1 of st | MFMAs of step 0 of st
+//   barrier: stage st + 1 has landed and every wave is done reading st
+//   DMA of the stage STAGES - 1 ahead into st
+//   read step 0 of st + 1 | MFMAs of step 1 of st      (task end: epilogue)
+// so the matrix pipe has queued work across every barrier.  The fragments of one step
+// are in registers before the barrier that precedes their MFMAs.  The epilogue's
+// stores are the newest vector memory operations at the next STAGES - 1 barriers,
+// which then wait with vmcnt(NSTORE) on top of the STAGES - 2 stages left in flight.
+template <int STAGES, int LPW, int NSTORE, int SPT, int RS, typename Cur, typename IssueNext, typename AdvanceNext,
+          typename FragStep, typename MmaStep, typename Epilogue, typename Seek>
+__device__ __forceinline__ void sum_split_pipeline(Cur& cs, f32x16 (&acc)[4][2], int mode, IssueNext& issue_next,
+                                                   AdvanceNext& advance_next, FragStep& frag_step,
+                                                   MmaStep& mma_step, Epilogue& epilogue, Seek& seek) {
+  static_assert(STAGES >= 3 && (STAGES - 2) * LPW + NSTORE < 64, "in-flight operations must fit vmcnt");
+#pragma unroll
+  for (int p = 0; p < STAGES - 1; ++p) {
+    issue_next(p);
+    advance_next();
+  }
+  stage_barrier<(STAGES - 2) * LPW>();  // stage 0 has landed
+  issue_next(STAGES - 1);
+  advance_next();
+  u32x4 xa[4], ga[2][2], xb[4], gb[2][2];
+  frag_step(0, 0, xa, ga);
+  int st = 0;
+  int since_store = STAGES;  // barriers since the last epilogue that left stores in flight
+  for (;;) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) acc[i][jj] = zero16();
+    for (;;) {
+      frag_step(st, 1, xb, gb);
+      mma_step(xa, ga);
+      sched_interleave<0, 16, RS, 0, 0>();
+      __builtin_amdgcn_sched_barrier(0);
+      if (++since_store < STAGES)
+        stage_barrier<(STAGES - 2) * LPW + NSTORE>();
+      else
+        stage_barrier<(STAGES - 2) * LPW>();
+      issue_next(st);
+      advance_next();
+      __builtin_amdgcn_sched_barrier(0);
+      st = st + 1 == STAGES ? 0 : st + 1;
+      frag_step(st, 0, xa, ga);
+      mma_step(xb, gb);
+      sched_interleave<0, 16, RS, 0, 0>();
+      if (++cs.h < SPT) continue;
+      cs.h = 0;
+      if (++cs.j == cs.cnt) break;
+    }
+    epilogue(cs);
+    if (mode == kWriteT) since_store = 0;
+    if (!seek(cs.q + 1, cs)) break;
+  }
+  wait_vmcnt<0>();
+}
+
 // Output of a finished dE / dC task: kWriteT stores the output dtype (one pass over
 // everything, and always for dC); the fp32 modes carry dE between passes (WriteMode).
 
@@ -1732,9 +1825,9 @@ __device__ __forceinline__ void dma16_s(const char* sbase, uint32_t voff, uint32
 // lanes are dropped by the buffer's range check).  Every per-step address is a
 // wave-uniform base plus a per-lane constant computed once: DMA sources in the
 // saddr form, fragment reads as constant LDS offsets.
-template <typename T, int PHASE>
-__global__ __launch_bounds__(SumGeo<T>::NT, 1) void bwd_sum_kernel(BwdArgs a, int chunk, int pass) {
-  using S = SumGeo<T>;
+template <typename T, int PHASE, bool SPLIT>
+__global__ __launch_bounds__((SumGeo<T, SPLIT>::NT), 1) void bwd_sum_kernel(BwdArgs a, int chunk, int pass) {
+  using S = SumGeo<T, SPLIT>;
   __shared__ __attribute__((aligned(16))) char smem[S::STAGES * S::STAGE];
   constexpr int ES = S::ES;
   const int nrb = (int)a.plan.nrb, nds = (int)((a.D + S::DN - 1) / S::DN);
@@ -1785,8 +1878,9 @@ __global__ __launch_bounds__(SumGeo<T>::NT, 1) void bwd_sum_kernel(BwdArgs a, in
       goff[j] = tr_off<S::GTP>(row, pb);
     }
   }
-  // Fragment read offsets within a stage (16-bit types): go_t[0 / 1][jj] the dC hi /
-  // lo fragments, go_n[jj][ks] the dE row chunks 2 ks + kg.
+  // Fragment read offsets within a stage (16-bit types): go_t[hl][jj] the dC
+  // fragments (hl: the hi / lo halves of the pair; 0 only for a single G), go_n[jj][ks]
+  // the dE row chunks 2 ks + kg.
   uint32_t xo[4], go_t[2][2], go_n[2][4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) xo[i] = tr_lane_off<S::XP>(wd * 128 + 32 * i);
@@ -1794,7 +1888,7 @@ __global__ __launch_bounds__(SumGeo<T>::NT, 1) void bwd_sum_kernel(BwdArgs a, in
   for (int jj = 0; jj < 2; ++jj) {
 #pragma unroll
     for (int hl = 0; hl < 2; ++hl)
-      go_t[hl][jj] = S::X_BYTES + tr_lane_off<S::GTP>(2 * (wm * 64 + 32 * jj) + 32 * hl);
+      go_t[hl][jj] = S::X_BYTES + tr_lane_off<S::GTP>(SPLIT ? 2 * (wm * 64 + 32 * jj) + 32 * hl : wm * 64 + 32 * jj);
     const uint32_t row = (uint32_t)(wm * 64 + 32 * jj + n);
     const uint32_t c = (row ^ (row >> 3)) & 7u;
 #pragma unroll
@@ -1871,13 +1965,15 @@ __global__ __launch_bounds__(SumGeo<T>::NT, 1) void bwd_sum_kernel(BwdArgs a, in
   };
 
   f32x16 acc[4][2];
-  // Fragments of one 32-byte contraction step ks of stage st (fp32), and its 8 MFMAs.
+  // Fragments of one 32-byte contraction step ks of stage st, and its 8 MFMAs.
   auto frags = [&](int st, int ks, u32x4 (&xf)[4], u32x4 (&gf)[2]) {
     const char* sp = smem + st * S::STAGE;
 #pragma unroll
     for (int jj = 0; jj < 2; ++jj) {
       if constexpr (PHASE == 0)
         gf[jj] = lds_ld16(sp, go_n[jj][ks]);
+      else if constexpr (ES == 2)
+        gf[jj] = frag_tr16(sp + go_t[0][jj] + 16 * ks * S::GTP, 4 * S::GTP);
       else
         gf[jj] = frag_tr32<S::GTP>(sp + S::X_BYTES, ks * S::KE, wm * 64 + 32 * jj);
     }
@@ -1895,35 +1991,30 @@ __global__ __launch_bounds__(SumGeo<T>::NT, 1) void bwd_sum_kernel(BwdArgs a, in
 #pragma unroll
       for (int jj = 0; jj < 2; ++jj) acc[i][jj] = Traits<T>::mfma(xf[i], gf[jj], acc[i][jj]);
   };
-  // 16-bit types: all fragments of a stage (two 16-deep steps kp, each an X fragment
-  // per column block and a hi and a lo G fragment per row block), then its 32 MFMAs.
-  u32x4 sxf[2][4], sgf[2][2][2];
-  auto frags_split = [&](int st) {
+  // The hi / lo pair: the fragments of one 16-deep contraction step kp of a stage (an
+  // X fragment per column block, a G hi and lo fragment per row block) and its 16
+  // MFMAs, hi ones first: the 8 accumulators then separate each dependent pair.
+  auto frag_step = [&](int st, int kp, u32x4 (&x)[4], u32x4 (&g)[2][2]) {
     const char* sp = smem + st * S::STAGE;
 #pragma unroll
-    for (int kp = 0; kp < 2; ++kp) {
+    for (int hl = 0; hl < 2; ++hl)
 #pragma unroll
-      for (int hl = 0; hl < 2; ++hl)
+      for (int jj = 0; jj < 2; ++jj) {
+        if constexpr (PHASE == 0)
+          g[hl][jj] = lds_ld16(sp, go_n[jj][2 * hl + kp]);
+        else
+          g[hl][jj] = frag_tr16(sp + go_t[hl][jj] + 16 * kp * S::GTP, 4 * S::GTP);
+      }
 #pragma unroll
-        for (int jj = 0; jj < 2; ++jj) {
-          if constexpr (PHASE == 0)
-            sgf[kp][hl][jj] = lds_ld16(sp, go_n[jj][2 * hl + kp]);
-          else
-            sgf[kp][hl][jj] = frag_tr16(sp + go_t[hl][jj] + 16 * kp * S::GTP, 4 * S::GTP);
-        }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) sxf[kp][i] = frag_tr16(sp + xo[i] + 16 * kp * S::XP, 4 * S::XP);
-    }
+    for (int i = 0; i < 4; ++i) x[i] = frag_tr16(sp + xo[i] + 16 * kp * S::XP, 4 * S::XP);
   };
-  auto mma_split = [&]() {
+  auto mma_step = [&](const u32x4 (&x)[4], const u32x4 (&g)[2][2]) {
 #pragma unroll
-    for (int kp = 0; kp < 2; ++kp)
+    for (int hl = 0; hl < 2; ++hl)
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int hl = 0; hl < 2; ++hl)
-#pragma unroll
-          for (int jj = 0; jj < 2; ++jj) acc[i][jj] = Traits<T>::mfma(sxf[kp][i], sgf[kp][hl][jj], acc[i][jj]);
+        for (int jj = 0; jj < 2; ++jj) acc[i][jj] = Traits<T>::mfma(x[i], g[hl][jj], acc[i][jj]);
   };
   // RK = LDS read instructions per contraction step, MK = MFMAs per contraction step.
   constexpr int RK = (ES == 2 ? 8 : 16) + (PHASE == 0 ? 2 : (ES == 2 ? 4 : 8));
@@ -2051,48 +2142,10 @@ __global__ __launch_bounds__(SumGeo<T>::NT, 1) void bwd_sum_kernel(BwdArgs a, in
   // The epilogue's stores are the newest vector memory operations at the next
   // barrier, so it waits with vmcnt(NSTORE) and lets them drain in the background.
   constexpr int NSTORE = S::NSTORE;  // buffer stores per wave per kWriteT epilogue
-  if constexpr (S::SPLIT) {
-    // 16-bit types: three stages; a step's barrier, its DMA two slices ahead, all of
-    // its fragment reads, then its 32 MFMAs (the other wave of the SIMD fills the
-    // matrix pipe while one reads).
-#pragma unroll
-    for (int p = 0; p < S::STAGES - 1; ++p) {
-      issue_next(p);
-      advance_next();
-    }
-    int st = 0;
-    int since_store = S::STAGES;  // steps since the last epilogue that left stores in flight
-    for (;;) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int jj = 0; jj < 2; ++jj) acc[i][jj] = zero16();
-      for (;;) {
-        if (since_store < S::STAGES)
-          stage_barrier<(S::STAGES - 2) * S::LPW + NSTORE>();
-        else
-          stage_barrier<(S::STAGES - 2) * S::LPW>();
-        issue_next((st + S::STAGES - 1) % S::STAGES);
-        frags_split(st);
-        mma_split();
-        // a step's LDS reads: 16 for X, 8 (dE) or 16 (dC, transposing) for G; the
-        // first 16-deep step's go first, the second's among its MFMAs
-        constexpr int RS = 16 + (PHASE == 0 ? 8 : 16);
-        __builtin_amdgcn_sched_group_barrier(0x100, RS / 2, 0);
-        sched_interleave<0, 16, RS / 2, 0, 0>();
-        sched_interleave<0, 16, 0, 0, 0>();
-        advance_next();
-        ++since_store;
-        st = st + 1 == S::STAGES ? 0 : st + 1;
-        if (++cs.h < S::SPT) continue;
-        cs.h = 0;
-        if (++cs.j == cs.cnt) break;
-      }
-      epilogue(cs);
-      if (mode == kWriteT) since_store = 1;
-      if (!seek(cs.q + 1, cs)) break;
-    }
-    wait_vmcnt<0>();
+  if constexpr (SPLIT) {
+    // LDS reads of one 16-deep step: 8 for X, 4 (dE) or 8 (dC, transposing) for G
+    sum_split_pipeline<S::STAGES, S::LPW, NSTORE, S::SPT, 8 + (PHASE == 0 ? 4 : 8)>(
+        cs, acc, mode, issue_next, advance_next, frag_step, mma_step, epilogue, seek);
     return;
   }
   issue_next(0);
@@ -2144,9 +2197,9 @@ __global__ __launch_bounds__(SumGeo<T>::NT, 1) void bwd_sum_kernel(BwdArgs a, in
 }
 
 // As bwd_sum_kernel, in the narrow geometry (one 4-wave pipeline of 48 KiB stages).
-template <typename T, int PHASE>
+template <typename T, int PHASE, bool SPLIT>
 __global__ __launch_bounds__(kThreads, 1) void bwd_sum_narrow_kernel(BwdArgs a, int chunk, int pass) {
-  using S = SumGeoNarrow<T>;
+  using S = SumGeoNarrow<T, SPLIT>;
   __shared__ __attribute__((aligned(16))) char smem[S::STAGES * S::STAGE];
   constexpr int ES = S::ES;
   const int nrb = (int)a.plan.nrb, nds = (int)((a.D + S::DN - 1) / S::DN);
@@ -2164,7 +2217,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_narrow_kernel(BwdArgs a, 
   const int vwg = xcd * nper + lidx, nwg = (int)gridDim.x;  // workgroups numbered XCD-major
   // dC: this workgroup's bin of the schedule the G kernel dealt, and its first D slice
   static_assert(PHASE == 0 || S::DN == kDcSliceCols, "the dC schedule assumes this slice width");
-  static_assert(S::SPT == kDcStepsPerTile, "the dC schedule counts these steps per kept tile");
+  static_assert(S::SPT == dc_steps_per_tile<T>(SPLIT), "the dC schedule counts these steps per kept tile");
   const int dcb = dc_bins(nwg, nds);
   const int dcm = dcb > 0 ? vwg / nds : 0;
   const int ds0 = dcb > 0 ? vwg - dcm * nds : vwg;
@@ -2206,8 +2259,9 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_narrow_kernel(BwdArgs a, 
       goff[j] = tr_off<S::GTP>(row, pb);
     }
   }
-  // Fragment read offsets within a stage (16-bit types): go_t[0 / 1][jj] the dC hi /
-  // lo fragments, go_n[jj][ks] the dE row chunks 2 ks + kg.
+  // Fragment read offsets within a stage (16-bit types): go_t[hl][jj] the dC
+  // fragments (hl: the hi / lo halves of the pair; 0 only for a single G), go_n[jj][ks]
+  // the dE row chunks 2 ks + kg.
   uint32_t xo[4], go_t[2][2], go_n[2][4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) xo[i] = tr_lane_off<S::XP>(wd * 128 + 32 * i);
@@ -2215,7 +2269,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_narrow_kernel(BwdArgs a, 
   for (int jj = 0; jj < 2; ++jj) {
 #pragma unroll
     for (int hl = 0; hl < 2; ++hl)
-      go_t[hl][jj] = S::X_BYTES + tr_lane_off<S::GTP>(2 * (wm * 64 + 32 * jj) + 32 * hl);
+      go_t[hl][jj] = S::X_BYTES + tr_lane_off<S::GTP>(SPLIT ? 2 * (wm * 64 + 32 * jj) + 32 * hl : wm * 64 + 32 * jj);
     const uint32_t row = (uint32_t)(wm * 64 + 32 * jj + n);
     const uint32_t c = (row ^ (row >> 3)) & 7u;
 #pragma unroll
@@ -2302,29 +2356,22 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_narrow_kernel(BwdArgs a, 
   };
 
   f32x16 acc[4][2];
-  // A step's fragments, read before its MFMAs: fp32, four 32-byte contraction steps
-  // (ks) of an X and a G fragment each; 16-bit types, two 16-deep steps (kp) of an X
-  // fragment and a G hi and lo fragment each (the lo ones take a second MFMA on the
-  // same X fragment).  The reads of the first half of the step go first, the rest
-  // among the MFMAs of the first half.
-  constexpr int NK = S::SPLIT ? 2 : 4;  // contraction steps per stage
-  constexpr int NH = S::SPLIT ? 2 : 1;  // G fragments per row block and step
-  u32x4 xf[NK][4], gf[NK][NH][2];
+  // A step's fragments for its four 32-byte contraction steps (ks): the reads of
+  // ks 0 and 1 go first, those of ks 2 and 3 among the MFMAs of ks 0 and 1.
+  u32x4 xf[4][4], gf[4][2];
   auto frags = [&](int st) {
     const char* sp = smem + st * S::STAGE;
 #pragma unroll
-    for (int ks = 0; ks < NK; ++ks) {
+    for (int ks = 0; ks < 4; ++ks) {
 #pragma unroll
-      for (int hl = 0; hl < NH; ++hl)
-#pragma unroll
-        for (int jj = 0; jj < 2; ++jj) {
-          if constexpr (PHASE == 0)
-            gf[ks][hl][jj] = lds_ld16(sp, go_n[jj][2 * hl + ks]);
-          else if constexpr (ES == 2)
-            gf[ks][hl][jj] = frag_tr16(sp + go_t[hl][jj] + 16 * ks * S::GTP, 4 * S::GTP);
-          else
-            gf[ks][hl][jj] = frag_tr32<S::GTP>(sp + S::X_BYTES, ks * S::KE, wm * 64 + 32 * jj);
-        }
+      for (int jj = 0; jj < 2; ++jj) {
+        if constexpr (PHASE == 0)
+          gf[ks][jj] = lds_ld16(sp, go_n[jj][ks]);
+        else if constexpr (ES == 2)
+          gf[ks][jj] = frag_tr16(sp + go_t[0][jj] + 16 * ks * S::GTP, 4 * S::GTP);
+        else
+          gf[ks][jj] = frag_tr32<S::GTP>(sp + S::X_BYTES, ks * S::KE, wm * 64 + 32 * jj);
+      }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         if constexpr (ES == 2)
@@ -2336,28 +2383,46 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_narrow_kernel(BwdArgs a, 
   };
   auto mma = [&]() {
 #pragma unroll
-    for (int ks = 0; ks < NK; ++ks)
+    for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int hl = 0; hl < NH; ++hl)
-#pragma unroll
-          for (int jj = 0; jj < 2; ++jj) acc[i][jj] = Traits<T>::mfma(xf[ks][i], gf[ks][hl][jj], acc[i][jj]);
+        for (int jj = 0; jj < 2; ++jj) acc[i][jj] = Traits<T>::mfma(xf[ks][i], gf[ks][jj], acc[i][jj]);
   };
   // RK = LDS read instructions per contraction step, MK = MFMAs per contraction step.
-  constexpr int RK = (ES == 2 ? 8 : 16) + NH * (PHASE == 0 ? 2 : (ES == 2 ? 4 : 8));
-  constexpr int MK = 8 * NH * Traits<T>::kInstrPerStep;
+  constexpr int RK = (ES == 2 ? 8 : 16) + (PHASE == 0 ? 2 : (ES == 2 ? 4 : 8));
+  constexpr int MK = 8 * Traits<T>::kInstrPerStep;
   auto schedule = [&]() {
-    __builtin_amdgcn_sched_group_barrier(0x100, NK / 2 * RK, 0);
-    if constexpr (NK == 4) {
-      sched_interleave<0, MK, RK, 0, 0>();
-      sched_interleave<0, MK, RK, 0, 0>();
-      sched_interleave<0, MK, 0, 0, 0>();
-      sched_interleave<0, MK, 0, 0, 0>();
-    } else {
-      sched_interleave<0, MK, RK, 0, 0>();
-      sched_interleave<0, MK, 0, 0, 0>();
-    }
+    __builtin_amdgcn_sched_group_barrier(0x100, 2 * RK, 0);
+    sched_interleave<0, MK, RK, 0, 0>();
+    sched_interleave<0, MK, RK, 0, 0>();
+    sched_interleave<0, MK, 0, 0, 0>();
+    sched_interleave<0, MK, 0, 0, 0>();
+  };
+  // The hi / lo pair: the fragments of one 16-deep contraction step kp of a stage (an
+  // X fragment per column block, a G hi and lo fragment per row block) and its 16
+  // MFMAs, hi ones first: the 8 accumulators then separate each dependent pair.
+  auto frag_step = [&](int st, int kp, u32x4 (&x)[4], u32x4 (&g)[2][2]) {
+    const char* sp = smem + st * S::STAGE;
+#pragma unroll
+    for (int hl = 0; hl < 2; ++hl)
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) {
+        if constexpr (PHASE == 0)
+          g[hl][jj] = lds_ld16(sp, go_n[jj][2 * hl + kp]);
+        else
+          g[hl][jj] = frag_tr16(sp + go_t[hl][jj] + 16 * kp * S::GTP, 4 * S::GTP);
+      }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x[i] = frag_tr16(sp + xo[i] + 16 * kp * S::XP, 4 * S::XP);
+  };
+  auto mma_step = [&](const u32x4 (&x)[4], const u32x4 (&g)[2][2]) {
+#pragma unroll
+    for (int hl = 0; hl < 2; ++hl)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) acc[i][jj] = Traits<T>::mfma(x[i], g[hl][jj], acc[i][jj]);
   };
   // fp16 G tiles hold G 2^gexp: the epilogue scales the sums back (exact)
   const float gdiv = __builtin_ldexpf(1.f, -(ES == 2 ? g_scale_exp(a) : 0));
@@ -2473,6 +2538,12 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_narrow_kernel(BwdArgs a, 
       have = advance(nx);
     }
   };
+  if constexpr (SPLIT) {
+    // LDS reads of one 16-deep step: 8 for X, 4 (dE) or 8 (dC, transposing) for G
+    sum_split_pipeline<S::STAGES, S::LPW, S::NSTORE, S::SPT, 8 + (PHASE == 0 ? 4 : 8)>(
+        cs, acc, mode, issue_next, advance_next, frag_step, mma_step, epilogue, seek);
+    return;
+  }
 #pragma unroll
   for (int p = 0; p < S::STAGES - 1; ++p) {
     issue_next(p);
@@ -2565,6 +2636,28 @@ static void launch_g_dense(const BwdArgs& a, int chunk, int pass, dim3 grid, hip
 #undef CCE_GD
 }
 
+// The sums of one phase (0 dE, 1 dC) in the wide or narrow geometry, over G tiles
+// rounded once or (16-bit a.g_split) held as the hi / lo pair.
+template <typename T, int PHASE>
+static void launch_sum(const BwdArgs& a, bool wide, int chunk, int pass, int grid, hipStream_t s) {
+  if constexpr (sizeof(T) == 2) {
+    if (a.g_split) {
+      if (wide)
+        hipLaunchKernelGGL((bwd_sum_kernel<T, PHASE, true>), dim3(grid), dim3(SumGeo<T, true>::NT), 0, s, a, chunk,
+                           pass);
+      else
+        hipLaunchKernelGGL((bwd_sum_narrow_kernel<T, PHASE, true>), dim3(grid), dim3(SumGeoNarrow<T, true>::NT), 0, s,
+                           a, chunk, pass);
+      return;
+    }
+  }
+  if (wide)
+    hipLaunchKernelGGL((bwd_sum_kernel<T, PHASE, false>), dim3(grid), dim3(SumGeo<T, false>::NT), 0, s, a, chunk, pass);
+  else
+    hipLaunchKernelGGL((bwd_sum_narrow_kernel<T, PHASE, false>), dim3(grid), dim3(SumGeoNarrow<T, false>::NT), 0, s, a,
+                       chunk, pass);
+}
+
 // dE sums: the wide geometry (512 columns per task, measured 0.85x the time of two
 // narrow tasks) unless it leaves so few tasks that the narrow one finishes in fewer
 // rounds of equal tasks over the persistent grid.  With the filter on the owners' kept
@@ -2595,7 +2688,7 @@ static bool use_wide_dc_sums(const BwdArgs& a) {
 }
 
 template <typename T>
-static hipError_t backward_typed(const BwdArgs& a, hipStream_t s) {
+static hipError_t backward_typed(const BwdArgs& a, hipStream_t s, hipEvent_t pass_ev) {
   const BwdPlan& P = a.plan;
   const int items = (int)(P.nrb * P.nwords);
   const bool sorted_ok = a.perm != nullptr;  // the workspace holds the sorted token order
@@ -2636,6 +2729,7 @@ static hipError_t backward_typed(const BwdArgs& a, hipStream_t s) {
     hipLaunchKernelGGL(bwd_compact_kernel, dim3(cg), dim3(1024), 0, s, a, chunk);
     if ((err = hipGetLastError()) != hipSuccess) return err;
     if (!(want_de || want_dc || want_db)) continue;
+    if (a.host_pass != nullptr && (err = hipEventRecord(pass_ev, s)) != hipSuccess) return err;
     // Quantized classifier rows: dequantize the rows of this chunk's tiles that keep
     // pairs (the compaction's vt_start) into the scratch and let c address it at global
     // row numbers (only the G kernel and the dE sums read c, and only kept tiles' rows).
@@ -2647,8 +2741,7 @@ static hipError_t backward_typed(const BwdArgs& a, hipStream_t s) {
       if (err != hipSuccess) return err;
       ac.c = reinterpret_cast<const char*>(a.q.scratch) - r0 * a.D * (int64_t)sizeof(T);
     }
-    // Every pass the chunk may need; passes past the data's last return at once.
-    for (int pass = 0; pass < (int)P.max_passes; ++pass) {
+    auto launch_g_pass = [&](int pass) {
       if (dense_g && a.bias)
         launch_g_dense<T, true>(ac, chunk, pass, dim3(gp), s);
       else if (dense_g)
@@ -2657,42 +2750,62 @@ static hipError_t backward_typed(const BwdArgs& a, hipStream_t s) {
         launch_g<T, true>(ac, chunk, pass, dim3(gp), s);
       else
         launch_g<T, false>(ac, chunk, pass, dim3(gp), s);
-      if ((err = hipGetLastError()) != hipSuccess) return err;
+      return hipGetLastError();
+    };
+    // The sums of one pass; dc_pick: the dC geometry the compaction chose for it (1
+    // wide, 0 narrow), or -1 when unknown on the host (both are launched, and the one
+    // not chosen returns at once).
+    auto launch_sums = [&](int pass, int dc_pick) {
+      hipError_t e2;
       if (want_de) {
-        if (wide_de)
-          hipLaunchKernelGGL((bwd_sum_kernel<T, 0>), dim3(gp), dim3(SumGeo<T>::NT), 0, s, ac, chunk, pass);
-        else
-          hipLaunchKernelGGL((bwd_sum_narrow_kernel<T, 0>), dim3(gp), dim3(SumGeoNarrow<T>::NT), 0, s, ac, chunk,
-                             pass);
-        if ((err = hipGetLastError()) != hipSuccess) return err;
+        launch_sum<T, 0>(ac, wide_de, chunk, pass, gp, s);
+        if ((e2 = hipGetLastError()) != hipSuccess) return e2;
       }
       if (want_dc) {
-        if (auto_dc) {
-          hipLaunchKernelGGL((bwd_sum_narrow_kernel<T, 1>), dim3(gp), dim3(SumGeoNarrow<T>::NT), 0, s, a, chunk, pass);
-          hipLaunchKernelGGL((bwd_sum_kernel<T, 1>), dim3(gp), dim3(SumGeo<T>::NT), 0, s, a, chunk, pass);
-        } else if (wide_dc)
-          hipLaunchKernelGGL((bwd_sum_kernel<T, 1>), dim3(gp), dim3(SumGeo<T>::NT), 0, s, a, chunk, pass);
-        else
-          hipLaunchKernelGGL((bwd_sum_narrow_kernel<T, 1>), dim3(gp), dim3(SumGeoNarrow<T>::NT), 0, s, a, chunk, pass);
-        if ((err = hipGetLastError()) != hipSuccess) return err;
+        const bool narrow = auto_dc ? dc_pick != 1 : !wide_dc;
+        const bool wide = auto_dc ? dc_pick != 0 : wide_dc;
+        if (narrow) launch_sum<T, 1>(a, false, chunk, pass, gp, s);
+        if (wide) launch_sum<T, 1>(a, true, chunk, pass, gp, s);
+        if ((e2 = hipGetLastError()) != hipSuccess) return e2;
       }
       if (want_db) {
         hipLaunchKernelGGL((bwd_dbias_kernel<T>), dim3((unsigned)nv), dim3(kBwdVocab), 0, s, a, chunk, pass);
-        if ((err = hipGetLastError()) != hipSuccess) return err;
+        if ((e2 = hipGetLastError()) != hipSuccess) return e2;
       }
+      return hipSuccess;
+    };
+    if (a.host_pass != nullptr) {
+      // The host reads the compaction's pass summary: the first G kernel is queued
+      // before the wait (it runs while the host waits and launches the rest), then
+      // exactly the passes the data needs, each with the dC geometry chosen for it.
+      if ((err = launch_g_pass(0)) != hipSuccess) return err;
+      if ((err = hipEventSynchronize(pass_ev)) != hipSuccess) return err;
+      const int npass = a.host_pass[0];
+      if (npass < 1 || npass > (int)P.max_passes) return hipErrorInvalidValue;
+      for (int pass = 0; pass < npass; ++pass) {
+        if (pass > 0 && (err = launch_g_pass(pass)) != hipSuccess) return err;
+        if ((err = launch_sums(pass, a.host_pass[1 + pass])) != hipSuccess) return err;
+      }
+      continue;
+    }
+    // Every pass the chunk may need; passes past the data's last return at once.
+    for (int pass = 0; pass < (int)P.max_passes; ++pass) {
+      if ((err = launch_g_pass(pass)) != hipSuccess) return err;
+      if ((err = launch_sums(pass, -1)) != hipSuccess) return err;
     }
   }
   return hipGetLastError();
 }
 
-hipError_t launch_backward(int dtype, const BwdArgs& a, hipStream_t s) {
+hipError_t launch_backward(int dtype, const BwdArgs& a, hipStream_t s, hipEvent_t pass_ev) {
+  if (a.host_pass != nullptr && pass_ev == nullptr) return hipErrorInvalidValue;
   switch (dtype) {
     case 0:
-      return backward_typed<float>(a, s);
+      return backward_typed<float>(a, s, pass_ev);
     case 1:
-      return backward_typed<_Float16>(a, s);
+      return backward_typed<_Float16>(a, s, pass_ev);
     default:
-      return backward_typed<__bf16>(a, s);
+      return backward_typed<__bf16>(a, s, pass_ev);
   }
 }
 

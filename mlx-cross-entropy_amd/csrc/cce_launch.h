@@ -75,16 +75,16 @@ constexpr int64_t kQuantDefaultChunkRows = 32768;  // 256 MiB of bf16 scratch at
 // the pass).  A pass holds every token block of its tiles, so dC and dBias of a
 // pass are final when its sums end; dE is carried between passes and chunks in
 // fp32 when the backward takes more than one pass.
-// G tiles keep the softmax gradient to fp32 accuracy for every input dtype: fp32
-// inputs store G in fp32; 16-bit inputs store it as a pair of 16-bit values,
-// hi = round(G) and lo = round(G - hi) (hi + lo = G to about 2^-17 relative), and
-// the sums issue one MFMA per half against the same E / C fragment.  A tile row of
-// 128 vocabulary columns is then 256 16-bit values: columns 32 q + i go to elements
-// 64 q + i (hi) and 64 q + 32 + i (lo), so that a 128-byte slice of a row holds 32
-// columns' hi and lo (the dE sums' contraction slice).  Every tile is 64 KiB.
-constexpr bool g_split(size_t esize) { return esize == 2; }
+// G tiles: fp32 inputs store G in fp32.  16-bit inputs store it either rounded once
+// to the input dtype (rows of 128 columns), or (g_split) as a pair of 16-bit values,
+// hi = round(G) and lo = round(G - hi) (hi + lo = G to about 2^-17 relative), with
+// the sums issuing one MFMA per half against the same E / C fragment: the reference
+// keeps the softmax weight in fp32 through both products.  A tile row of the pair is
+// 256 16-bit values: columns 32 q + i go to elements 64 q + i (hi) and 64 q + 32 + i
+// (lo), so that a 128-byte slice of a row holds 32 columns' hi and lo (the dE sums'
+// contraction slice).  A tile slot is 64 KiB either way.
 constexpr size_t g_tile_bytes(size_t esize) {
-  return (size_t)kBwdTokens * kBwdVocab * esize * (g_split(esize) ? 2 : 1);
+  return (size_t)kBwdTokens * kBwdVocab * (esize == 2 ? 2 * esize : esize);
 }
 // G-tile budget of one pass, in MiB (the default workspace; a smaller workspace
 // gives smaller passes, down to 2 tiles per token block).  512 MiB holds 8192 tiles, an
@@ -342,6 +342,12 @@ struct BwdArgs {
   int dc_zeroed;        // dC already holds zeros: only rows of vocab tiles with kept tiles are written
   int stats32;          // tile_max per 32 columns in the reference's layout [N][ceil(V/32)] (else [nvt][N])
   int g_scaled;         // fp16: G tiles hold G * 2^counts[kGScaleExp] (else unscaled)
+  int g_split;          // 16-bit: G tiles hold the hi / lo pair (else G rounded once)
+  // Pinned host memory of 1 + max_passes ints, or null.  The compaction writes the
+  // chunk's pass count to [0] and each pass's kPiDcWide to [1 + p]; the host then
+  // launches only those passes and only the dC geometry picked (launch_backward's
+  // event), instead of max_passes passes with both geometries.
+  int* host_pass;
   QuantRows q;          // q.wq set: c is unused; every chunk first dequantizes its rows into q.scratch
 };
 
@@ -354,7 +360,10 @@ hipError_t launch_forward_q(int dtype, const FwdArgs& a, const QuantRows& q, hip
 // rows of the tiles needed.
 hipError_t launch_dequantize(int dtype, const QuantRows& q, int64_t row0, int64_t rows, int64_t D, void* out,
                              hipStream_t s, const int* keep = nullptr);
-hipError_t launch_backward(int dtype, const BwdArgs& a, hipStream_t s);
+// With a.host_pass set, pass_ev (an event of the current device) is recorded after
+// each chunk's compaction and waited for on the host before the chunk's passes past
+// the first G kernel are launched.
+hipError_t launch_backward(int dtype, const BwdArgs& a, hipStream_t s, hipEvent_t pass_ev = nullptr);
 hipError_t launch_reduce_loss(const float* nll, const int64_t* targets, int64_t ignore_index, int has_ignore,
                               int64_t N, int mode, float* loss, float* scale, hipStream_t s);
 hipError_t launch_broadcast_grad(const float* grad, const float* scale, int64_t N, float* d_nll, hipStream_t s);

@@ -149,6 +149,39 @@ def test_dense_16bit_matches_reference_rounding(m, cuda, case, dtype):
         assert err <= 1e-3, (name, err)
 
 
+def _single_g_model(dtype, d_nll):
+    """The one rounding of G a backward with CCE_BWD_G_SINGLE applies: bf16 as it is; fp16
+    after scaling by 2^s with max |d_nll| 2^s in [2^13, 2^14) (the compaction's rule),
+    taken back out after the products."""
+    if dtype == torch.bfloat16:
+        return O.round_bf16
+    gmax = float(np.max(np.abs(d_nll)))
+    s = 0 if gmax == 0.0 else 14 - math.frexp(gmax)[1]
+    return lambda g: O.round_f16(g * 2.0 ** s) / 2.0 ** s
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("case", DENSE16_CASES[:-2])
+def test_single_rounded_g_matches_its_model(m, cuda, case, dtype):
+    """CCE_BWD_G_SINGLE with the filter off (the fast, lower-precision mode): dE / dC
+    against the float64 oracle with G rounded once where the kernel rounds it (fp16 with
+    its power-of-two scale, so no subnormal G), then to the output dtype, at 1e-3.  What
+    is left is the kernels' own fp32 arithmetic."""
+    e, c, t, b, red, ign, up = _dense16_case(case, dtype, cuda)
+    assert up == 1.0
+    with m._ext.backward_options(g_precision="single"):
+        _, dE, dC, dB = run(m, e, c, t, b, red, ign, filter_eps=None)
+    rnd = ROUND[dtype]
+    ee, cc, tt = f64(e), f64(c), t.cpu().numpy()
+    dn = O.upstream(O.valid_mask(tt, ign), red)  # max |d_nll| sets the fp16 scale
+    sE, sC, sB = O.grads_staged(ee, cc, tt, f64(b), red, ign, stage=_single_g_model(dtype, dn))
+    pairs = [("dE", dE, sE), ("dC", dC, sC)] + ([("dBias", dB, sB)] if b is not None else [])
+    for name, got, staged in pairs:
+        err = O.rel_fro(f64(got), rnd(staged))
+        print(f"{case} {dtype} single G {name}: vs its model {err:.2e}")
+        assert err <= 1e-3, (name, err)
+
+
 def test_integer_inputs_exact(m, cuda):
     """Integer inputs: every logit is exact in fp32, so the gather, tile max and mask must match bit for bit."""
     z = np.load(os.path.join(os.path.dirname(__file__), "golden", "g_int_bias_none.npz"))
@@ -393,16 +426,19 @@ def _sorted_rows(tt, d_nll, V, ignore_index=-100, head_run=16):
     return perm
 
 
+@pytest.mark.parametrize("precision", [None, "pair"])
 @pytest.mark.parametrize("order", ["input", "sorted"])
-def test_filtered_backward_matches_filter_emulation(m, cuda, order):
+def test_filtered_backward_matches_filter_emulation(m, cuda, order, precision):
     """Kept-tile set is exact against the kernel's own fp32 statistics (token blocks of the
-    input order, or of the rows sorted by target tile); gradients match the oracle over it."""
+    input order, or of the rows sorted by target tile); gradients match the oracle over it:
+    within the bf16 tolerance with G rounded once (the filter-on default), and within 1e-3
+    of the emulation rounded to bf16 with G as the hi + lo pair (CCE_BWD_G_PAIR)."""
     e, c, t = _peaked(cuda)
     tm, _, _, lse, _ = m._ext.forward(e, c, t, None, -100)
     N, V = e.shape[0], c.shape[0]
     d_nll = torch.full((N,), 1.0 / N, device=cuda)
     stats = torch.zeros(3, dtype=torch.int64, device=cuda)
-    with m._ext.backward_options(token_order=order):
+    with m._ext.backward_options(token_order=order, g_precision=precision):
         dE, dC, _ = m._ext.backward(e, c, t, lse, tm, d_nll, None, -100, m.FILTER_LOG_EPS, True, True, False,
                                     tile_stats=stats)
     torch.cuda.synchronize()
@@ -428,8 +464,12 @@ def test_filtered_backward_matches_filter_emulation(m, cuda, order):
     fE = np.empty_like(fE_p)
     fE[perm] = fE_p
     emu = [O.rel_fro(f64(dE), fE), O.rel_fro(f64(dC), fC)]
-    print(f"kernel vs filter emulation: dE {emu[0]:.3e} dC {emu[1]:.3e}")
+    emu_r = [O.rel_fro(f64(dE), O.round_bf16(fE)), O.rel_fro(f64(dC), O.round_bf16(fC))]
+    print(f"kernel vs filter emulation ({precision or 'default'} G): dE {emu[0]:.3e} dC {emu[1]:.3e}; "
+          f"vs the emulation rounded to bf16: dE {emu_r[0]:.3e} dC {emu_r[1]:.3e}")
     assert emu[0] < 2e-2 and emu[1] < 2e-2  # bf16 tolerance against the same kept-tile set
+    if precision == "pair":
+        assert emu_r[0] <= 1e-3 and emu_r[1] <= 1e-3
     # The 2^-12 filter itself drops softmax mass; against the dense gradient the error must be
     # no larger than the reference's own 32x32 filter produces on the same inputs.
     dense = O.grads(ee, cc, tt, None, "mean")
@@ -521,6 +561,33 @@ def _zero_fill_case(m, cuda):
     c2 = c.detach().clone().requires_grad_(True)
     m.linear_cross_entropy(e2, c2, t).backward()
     assert torch.equal(c2.grad.view(torch.int16), dC_ref.view(torch.int16))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("filtered", [False, True])
+@pytest.mark.parametrize("split", ["one", "passes", "both"])
+def test_host_and_device_pass_schedules_agree(m, cuda, dtype, filtered, split):
+    """The host waits for the compaction's pass count and launches only the passes
+    (and the dC geometry) the data needs; CCE_BWD_DEVICE_PASSES launches the dense
+    worst case and lets the device skip the rest.  Same kernels, same plan: the
+    gradients agree bit for bit, in one pass, in several passes, and in several
+    passes of several vocabulary chunks."""
+    N, D, V = 300, 264, 9000
+    if filtered:
+        e, c, t = _peaked(cuda, N=N, D=D, V=V, dtype=dtype, seed=17)
+    else:
+        e, c, t = normal_case(N, D, V, dtype, cuda, seed=17, std=0.05)
+    t[5] = -100
+    b = (torch.randn(V, device=cuda) * 0.1).to(dtype)
+    feps = m.FILTER_LOG_EPS if filtered else None
+    opts = {"one": {}, "passes": {"max_g_tiles": 8}, "both": {"max_g_tiles": 8, "max_chunk_tiles": 32}}[split]
+    with m._ext.backward_options(**opts):
+        host = run(m, e, c, t, b, reduction="sum", filter_eps=feps)
+    with m._ext.backward_options(passes="device", **opts):
+        dev = run(m, e, c, t, b, reduction="sum", filter_eps=feps)
+    bits = torch.int32 if dtype == torch.float32 else torch.int16
+    for x, y in zip(host[1:], dev[1:]):
+        assert torch.equal(x.view(bits), y.view(bits))
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
