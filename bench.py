@@ -9,12 +9,13 @@ V=128256, bf16), the configuration the headline metric is quoted on.
 
 Prints one JSON line.  `value` is tokens/s of the whole job; `roofline` is the
 forward kernel pair (tile kernel + lse combine, timed with HIP events on the
-stream they run on) against the bf16 MFMA peak; `step.mfma_frac` is the whole step
+stream they run on) against the bf16 MFMA peak; `step_roofline` is the whole step
 against the peak for the MFMA work it performed (forward + the backward's three
-products over the tiles it computed); `dense` is the same step with the tile filter
-off (every tile: 8 N D V FLOPs), timed in the same run; `cpu_baseline` is the
-float32 torch-CPU restatement of the reference's materialised-logits path timed on a
-bounded slice of the same workload on this host.
+products over the tiles it computed: the metric's fwd+bwd fraction); `dense` is the
+same step with the tile filter off (every tile: 8 N D V FLOPs, 16-bit G as the
+fp32-accurate hi + lo pair, and again rounded once), timed in the same run;
+`cpu_baseline` is the float32 torch-CPU restatement of the reference's
+materialised-logits path timed on a bounded slice of the same workload on this host.
 
 --quantize BITS (2, 4 or 8; not the default) stores the classifier rows in affine
 groups of 64 and passes them to the loss quantized (the frozen-head case: dE and dBias,
@@ -155,25 +156,45 @@ def main():
     _ext.set_timing(False)
     dense = None
     if args.dense_steps > 0 and feps is not None:
-        # The conservative figure: every tile computed (filter off), same inputs.
-        _ext.set_timing(True)
-        step(None)
-        torch.cuda.synchronize()
-        _ext.set_timing(True)
-        td0 = time.perf_counter()
-        for i in range(args.dense_steps):
-            step(None)
-        torch.cuda.synchronize()
-        dense_ms = (time.perf_counter() - td0) * 1e3 / args.dense_steps
-        tmd = _ext.timings_ms()
-        _ext.set_timing(False)
+        # The conservative figure: every tile computed (filter off), same inputs, with
+        # the library's default for it -- 16-bit G carried as a hi + lo pair (fp32-
+        # accurate, the reference's precision) -- and again with G rounded once to the
+        # input dtype (CCE_BWD_G_SINGLE) for the cost of that precision.
+        def dense_leg(precision):
+            with _ext.backward_options(g_precision=precision):
+                _ext.set_timing(True)
+                step(None)
+                torch.cuda.synchronize()
+                _ext.set_timing(True)
+                td0 = time.perf_counter()
+                for i in range(args.dense_steps):
+                    step(None)
+                torch.cuda.synchronize()
+                d_ms = (time.perf_counter() - td0) * 1e3 / args.dense_steps
+                tmd = _ext.timings_ms()
+                _ext.set_timing(False)
+            return d_ms, statistics.mean(tmd["forward"]), statistics.mean(tmd["backward"])
+
         dfl = workloads.flops(N, D, V, 0.0, qw is None)
+        pair = dt != "f32"
+        dense_ms, dfwd, dbwd = dense_leg(None)
+        # MFMA work the hardware does: the pair's lo halves take a second MFMA in each sum
+        hw = dfl + (2.0 if qw is None else 1.0) * 2.0 * N * D * V if pair else dfl
         dense = {"ms_per_step": dense_ms, "tokens_per_s": N / (dense_ms * 1e-3), "flops": dfl,
                  "tflops": dfl / (dense_ms * 1e-3) / 1e12,
                  "mfma_frac": dfl / (dense_ms * 1e-3) / 1e12 / PEAK_TFLOPS[dt],
-                 "fwd_ms": statistics.mean(tmd["forward"]), "bwd_ms": statistics.mean(tmd["backward"]),
+                 "g_precision": "hi+lo pair (fp32-accurate)" if pair else "fp32",
+                 "mfma_instr_flops": hw, "mfma_instr_frac": hw / (dense_ms * 1e-3) / 1e12 / PEAK_TFLOPS[dt],
+                 "fwd_ms": dfwd, "bwd_ms": dbwd,
                  "steps": args.dense_steps, "note": "filter off: every 128x128 tile, 8NDV (6NDV without dC)"}
         log(f"bench: dense leg {dense_ms:.2f} ms/step")
+        if pair:
+            s_ms, s_fwd, s_bwd = dense_leg("single")
+            dense["single_rounded_g"] = {"ms_per_step": s_ms, "tokens_per_s": N / (s_ms * 1e-3),
+                                         "mfma_frac": dfl / (s_ms * 1e-3) / 1e12 / PEAK_TFLOPS[dt],
+                                         "fwd_ms": s_fwd, "bwd_ms": s_bwd,
+                                         "note": "CCE_BWD_G_SINGLE: G rounded to the input dtype before the products"}
+            log(f"bench: dense leg, single-rounded G {s_ms:.2f} ms/step")
     if args.calib_copy_mib > 0:
         src = torch.empty(args.calib_copy_mib << 20, dtype=torch.uint8, device=dev)
         dst = torch.empty_like(src)
@@ -224,6 +245,12 @@ def main():
                      "achieved": achieved, "peak": peak, "unit": "TFLOP/s", "frac": achieved / peak,
                      "traffic": traffic_from_profiles(args.workload, args.filter) if qw is None else None,
                      "flops_per_launch": fwd_flops, "avg_launch_ms": fwd_ms},
+        # The whole step against the peak for the MFMA work it performed: the metric's
+        # fwd + bwd fraction (roofline above is the dominant kernel's alone).
+        "step_roofline": {"bound": "mfma", "achieved": performed_flops / (ms * 1e-3) / 1e12, "peak": peak,
+                          "unit": "TFLOP/s", "frac": performed_flops / (ms * 1e-3) / 1e12 / peak,
+                          "flops": performed_flops, "ms_per_step": ms,
+                          "flops_formula": "2NDV + 6NDV(1 - tile_skip) (4NDV without dC)"},
         "step": {"fwd_ms": fwd_ms, "bwd_ms": bwd_ms, "total_tiles": total,
                  "rows_grouped_by_target": bool(fs["sorted_rows"]), "tile_skip": skip, "kept_tiles": kept,
                  "performed_flops": performed_flops, "tflops": performed_flops / (ms * 1e-3) / 1e12,

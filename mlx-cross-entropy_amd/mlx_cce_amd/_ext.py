@@ -374,6 +374,18 @@ def backward_noalloc(e, c, targets, lse, tile_max, d_nll, bias=None, ignore_inde
     if d_nll.shape != (N,) or lse.shape != (N,):
         raise ValueError("[cce_backward_noalloc] lse and d_nll must be [N]")
     ref = _ref_stats_layout(tile_max, N, c.shape[0], "cce_backward_noalloc")
+    # caller-provided outputs are written through as raw pointers: they must be exactly
+    # like the tensor whose gradient they hold
+    for name, out, like in (("dE", dE, e), ("dC", dC, c), ("dB", dB, bias)):
+        if out is not None and like is not None and (
+                out.shape != like.shape or out.dtype != like.dtype or out.device != like.device
+                or not out.is_contiguous()):
+            raise ValueError(f"[cce_backward_noalloc] {name} must be a contiguous tensor like its input "
+                             f"({tuple(like.shape)}, {like.dtype}, {like.device}), got "
+                             f"{tuple(out.shape)}, {out.dtype}, {out.device}")
+    if tile_stats is not None and (tile_stats.shape != (3,) or tile_stats.dtype != torch.int64
+                                   or tile_stats.device != e.device or not tile_stats.is_contiguous()):
+        raise ValueError("[cce_backward_noalloc] tile_stats must be a contiguous int64 [3] tensor on e's device")
     if want_de and dE is None:
         dE = torch.empty_like(e)
     if want_dc and dC is None:

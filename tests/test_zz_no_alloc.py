@@ -64,3 +64,22 @@ def test_noalloc_refuses_problems_past_the_scratch(cuda):
     tm = torch.zeros((1002, 8192), device=cuda)
     with pytest.raises(ValueError, match="static scratch"):
         ext.backward_noalloc(e, c, t, lse, tm, lse, None, -100, None, True, True, False)
+
+
+def test_noalloc_refuses_outputs_unlike_their_inputs(cuda):
+    """Caller-provided outputs are written through raw pointers, so each must be a
+    contiguous tensor of its input's shape, dtype and device (and tile_stats int64[3]):
+    anything else raises before the library is called."""
+    import mlx_cce_amd as m
+    ext = m._ext
+    e, c, b, t = _case(cuda, 256, 64, 1000, torch.bfloat16, 3, True)
+    tm, _, _, lse, _ = ext.forward(e, c, t, b, -100)
+    d_nll = torch.full((256,), 1.0 / 256, device=cuda)
+    bad = {"dE": torch.empty((255, 64), dtype=torch.bfloat16, device=cuda),
+           "dC": torch.empty((1000, 64), dtype=torch.float32, device=cuda),
+           "dB": torch.empty((2000,), dtype=torch.bfloat16, device=cuda)[::2]}
+    for name, out in bad.items():
+        with pytest.raises(ValueError, match=name):
+            ext.backward_noalloc(e, c, t, lse, tm, d_nll, b, **{name: out})
+    with pytest.raises(ValueError, match="tile_stats"):
+        ext.backward_noalloc(e, c, t, lse, tm, d_nll, b, tile_stats=torch.zeros(3, dtype=torch.int32, device=cuda))
