@@ -200,6 +200,11 @@ int cce_backward(int dtype, const void* e, const void* c, const void* bias,
  * force one or the other. */
 #define CCE_BWD_G_PAIR 512
 #define CCE_BWD_G_SINGLE 1024
+/* The narrow dC sums (16-bit inputs, G rounded once) run the owners with one kept
+ * tile as tasks per (token block, D slice): the block's E slice is loaded once and
+ * the G tiles of its one-tile owners are streamed through it.  This runs every owner
+ * as its own task instead (the results are the same bit for bit). */
+#define CCE_BWD_DC_OWNER_TASKS 2048
 
 /* As cce_backward, with flags (CCE_BWD_*) and vocabulary chunks of at most
  * max_chunk_tiles tiles (0: the library's choice; else a multiple of 32; the workspace

@@ -343,6 +343,8 @@ int backward_impl(int dtype, const void* e, const void* c, const void* bias, con
   a.own_vt = reinterpret_cast<int*>(ws + P.own_vt);
   a.dc_bin_start = reinterpret_cast<int*>(ws + P.dc_bin_start);
   a.dc_bin_owner = reinterpret_cast<int*>(ws + P.dc_bin_owner);
+  a.dc_blk_task = reinterpret_cast<int*>(ws + P.dc_blk_task);
+  a.dc_blk_own = reinterpret_cast<int*>(ws + P.dc_blk_own);
   a.gtile = (dE || dC) ? ws + P.gtile : nullptr;
   a.colsum = dBias ? reinterpret_cast<float*>(ws + P.colsum) : nullptr;
   a.de_acc = P.carry ? reinterpret_cast<float*>(ws + P.de_acc) : nullptr;
@@ -365,6 +367,8 @@ int backward_impl(int dtype, const void* e, const void* c, const void* bias, con
   a.g_scaled = dtype == CCE_DTYPE_F16 ? 1 : 0;  // fp16 G tiles are scaled into fp16's normal range
   // 16-bit G as the hi / lo pair with the filter off (the 1e-3 bar), rounded once with it on
   a.g_split = es == 2 && !(flags & CCE_BWD_G_SINGLE) && ((flags & CCE_BWD_G_PAIR) || !(filter_log_eps > -INFINITY));
+  // one-tile dC owners by token block: 16-bit inputs with G rounded once
+  a.dc_blk = es == 2 && !a.g_split && dC != nullptr && P.nrb <= cce::kDcBlkMaxRb && !(flags & CCE_BWD_DC_OWNER_TASKS);
   a.plan = P;
   a.num_cus = cus;
   if (q) {
@@ -400,7 +404,8 @@ int cce_backward_ex(int dtype, const void* e, const void* c, const void* bias, c
   g_err[0] = 0;
   constexpr int kKnown = CCE_BWD_DC_ZEROED | CCE_BWD_TOKENS_INPUT | CCE_BWD_TOKENS_SORTED | CCE_BWD_DE_SUMS_WIDE |
                          CCE_BWD_DE_SUMS_NARROW | CCE_BWD_DC_SUMS_WIDE | CCE_BWD_DC_SUMS_NARROW |
-                         CCE_BWD_REF_STATS | CCE_BWD_DEVICE_PASSES | CCE_BWD_G_PAIR | CCE_BWD_G_SINGLE;
+                         CCE_BWD_REF_STATS | CCE_BWD_DEVICE_PASSES | CCE_BWD_G_PAIR | CCE_BWD_G_SINGLE |
+                         CCE_BWD_DC_OWNER_TASKS;
   if (flags & ~kKnown) return fail(CCE_ERR_INVALID_ARGUMENT, "[cce_backward] unknown flags 0x%x", flags);
   if ((flags & CCE_BWD_TOKENS_INPUT) && (flags & CCE_BWD_TOKENS_SORTED))
     return fail(CCE_ERR_INVALID_ARGUMENT, "[cce_backward] CCE_BWD_TOKENS_INPUT and CCE_BWD_TOKENS_SORTED exclude each other");
@@ -461,7 +466,8 @@ int cce_backward_noalloc(int dtype, const void* e, const void* c, const void* bi
   g_err[0] = 0;
   constexpr int kKnown = CCE_BWD_DC_ZEROED | CCE_BWD_TOKENS_INPUT | CCE_BWD_TOKENS_SORTED | CCE_BWD_DE_SUMS_WIDE |
                          CCE_BWD_DE_SUMS_NARROW | CCE_BWD_DC_SUMS_WIDE | CCE_BWD_DC_SUMS_NARROW |
-                         CCE_BWD_REF_STATS | CCE_BWD_DEVICE_PASSES | CCE_BWD_G_PAIR | CCE_BWD_G_SINGLE;
+                         CCE_BWD_REF_STATS | CCE_BWD_DEVICE_PASSES | CCE_BWD_G_PAIR | CCE_BWD_G_SINGLE |
+                         CCE_BWD_DC_OWNER_TASKS;
   if (flags & ~kKnown)
     return fail(CCE_ERR_INVALID_ARGUMENT, "[cce_backward_noalloc] unknown flags 0x%x", flags);
   if (((flags & CCE_BWD_TOKENS_INPUT) && (flags & CCE_BWD_TOKENS_SORTED)) ||

@@ -509,6 +509,7 @@ __global__ __launch_bounds__(1024) void bwd_compact_kernel(BwdArgs a, int chunk)
   __shared__ int pvt[kCompactMaxVt + 1];    // first tile of each pass (nv from the pass after the last on)
   __shared__ int rbs_l[kRbsLds + 1];        // rb_start, when the chunk's (pass, block) pairs fit
   __shared__ int hist[kCompactMaxVt + 1];   // the G-task run indices before each pass (kbp), then order_by_size's
+  __shared__ uint16_t vt1_rb[kCompactMaxVt];  // the token block of each tile that keeps exactly one
   __shared__ int wsum[16];
   static_assert(kOrderBuckets <= kCompactMaxVt, "order_by_size's buckets fit hist");
   int* kbp = hist;  // G-task run indices of the passes before pass p (free again once the tasks are written)
@@ -739,6 +740,7 @@ __global__ __launch_bounds__(1024) void bwd_compact_kernel(BwdArgs a, int chunk)
           const int rb = r0 + __builtin_ctzll(col);
           col &= col - 1ull;
           vt_slot[q++] = slot_of(p, rb, v);
+          vt1_rb[v] = (uint16_t)rb;  // (read only for tiles that keep one block)
         }
       }
     }
@@ -849,6 +851,7 @@ __global__ __launch_bounds__(1024) void bwd_compact_kernel(BwdArgs a, int chunk)
   __syncthreads();
 
   // the owners of every pass's sums, most kept tiles first
+  __shared__ int pblk;  // the pass's dC sums run block tasks
   for (int p = 0; p < npass; ++p) {
     const int n_rb = order_by_size(nrb, [&](int rb) { return rbs(p * nrb + rb + 1) - rbs(p * nrb + rb); },
                                    a.own_rb + (size_t)p * nrb, 0, hist, wsum);
@@ -870,10 +873,70 @@ __global__ __launch_bounds__(1024) void bwd_compact_kernel(BwdArgs a, int chunk)
       const int64_t nds_w = (a.D + 511) / 512;
       a.pinfo[p * kPassInts + kPiOwnRb] = n_rb;
       a.pinfo[p * kPassInts + kPiOwnVt] = n_vt;
-      a.pinfo[p * kPassInts + kPiDcWide] = (int64_t)mk * gwg <= kept_p * nds_w ? 1 : 0;
-      if (a.host_pass) a.host_pass[1 + p] = a.pinfo[p * kPassInts + kPiDcWide];
+      const int wide = (int64_t)mk * gwg <= kept_p * nds_w ? 1 : 0;
+      a.pinfo[p * kPassInts + kPiDcWide] = wide;
+      if (a.host_pass) a.host_pass[1 + p] = wide;
+      // block tasks when the pass's dC sums run in the narrow geometry
+      pblk = a.dc_blk && nrb <= kDcBlkMaxRb &&
+             (a.dc_geo == 2 || (a.dc_geo == 0 && a.filter_log_eps > -INFINITY && wide == 0));
+      a.pinfo[p * kPassInts + kPiDcBlk] = 0;
+      a.pinfo[p * kPassInts + kPiDcDeal] = n_vt;
     }
     __syncthreads();  // wsum is the next scan's
+    if (pblk) {
+      // The pass's tiles that keep one token block (its last owners in own_vt), grouped
+      // by that block: counts per block (hist, free until the next pass's ordering) and
+      // each tile's place among its block's tiles, in the order the LDS atomics hand
+      // out (the sums do not depend on it); tasks listed in token-block order.
+      int* cntb = hist;
+      for (int r = tid; r < nrb; r += 1024) cntb[r] = 0;
+      __syncthreads();
+      constexpr int kTq = kCompactMaxVt / 1024;
+      int rk[kTq];
+#pragma unroll
+      for (int q = 0; q < kTq; ++q) {
+        const int v = vt0 + tid + 1024 * q;
+        rk[q] = v < pvt[p + 1] && vpre[v + 1] - vpre[v] == 1 ? atomicAdd(&cntb[vt1_rb[v]], 1) : -1;
+      }
+      __syncthreads();
+      // tasks of at most kDcBlkChunk owners of one block
+      const int perb = (nrb + 1023) >> 10;
+      const int r0 = min(nrb, tid * perb), r1 = min(nrb, r0 + perb);
+      int fb = 0, cb = 0;
+      for (int r = r0; r < r1; ++r) {
+        fb += (cntb[r] + kDcBlkChunk - 1) / kDcBlkChunk;
+        cb += cntb[r];
+      }
+      int ntk, ones;
+      int kb = block_excl_scan(fb, wsum, ntk);
+      int ob = block_excl_scan(cb, wsum, ones);
+      int* task = a.dc_blk_task + 4 * vt0;
+      for (int r = r0; r < r1; ++r) {
+        const int c = cntb[r];
+        for (int e = 0; e < c; e += kDcBlkChunk, ++kb) {
+          task[4 * kb] = r;
+          task[4 * kb + 1] = ob + e;
+          task[4 * kb + 2] = ob + min(c, e + kDcBlkChunk);
+          task[4 * kb + 3] = 0;
+        }
+        cntb[r] = ob;  // the block's first entry
+        ob += c;
+      }
+      if (tid == 0) {
+        a.pinfo[p * kPassInts + kPiDcBlk] = ntk;
+        a.pinfo[p * kPassInts + kPiDcDeal] = n_vt - ones;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int q = 0; q < kTq; ++q) {
+        if (rk[q] < 0) continue;
+        const int v = vt0 + tid + 1024 * q, rb = vt1_rb[v];
+        const int e = vt0 + cntb[rb] + rk[q];
+        a.dc_blk_own[2 * e] = v;
+        a.dc_blk_own[2 * e + 1] = slot_of(p, rb, v);
+      }
+      __syncthreads();  // hist is the next pass's
+    }
   }
   // the rest of the pass table
   const bool multi = a.plan.n_chunks > 1 || npass > 1;
@@ -881,6 +944,7 @@ __global__ __launch_bounds__(1024) void bwd_compact_kernel(BwdArgs a, int chunk)
   for (int p = tid; p < maxp; p += 1024) {
     int* pi = a.pinfo + p * kPassInts;
     pi[kPiTail] = 0;
+    pi[kPiDcQueue] = 0;
     if (p < npass) {
       pi[kPiVt0] = pvt[p];
       pi[kPiVt1] = pvt[p + 1];
@@ -898,6 +962,8 @@ __global__ __launch_bounds__(1024) void bwd_compact_kernel(BwdArgs a, int chunk)
       pi[kPiTask1] = ntask;
       pi[kPiOwnRb] = 0;
       pi[kPiOwnVt] = 0;
+      pi[kPiDcBlk] = 0;
+      pi[kPiDcDeal] = 0;
       pi[kPiDeMode] = -1;
     }
   }
@@ -1017,7 +1083,7 @@ __device__ void dc_schedule(const BwdArgs& a, int pass, int nbins, int spt, char
   constexpr int NW = NT / 64;
   const int tid = threadIdx.x;
   const int* pi = a.pinfo + pass * kPassInts;
-  const int n = ldu(pi, kPiOwnVt);
+  const int n = ldu(pi, kPiDcDeal);  // owners dealt to bins: the rest are block tasks
   const int* own_vt = a.own_vt + ldu(pi, kPiVt0);
   int* sz = reinterpret_cast<int*>(smem);  // [n] kept blocks of owner i
   int* bst = sz + kCompactMaxVt;           // [batches + 1] first owner of each batch
@@ -1674,8 +1740,9 @@ struct SumGeoNarrow {
   static constexpr int LPW = XLW + GLW;
   static constexpr int KE = 32 / ES;               // contraction elements per MFMA step
   static constexpr int NSTORE = 4 * 2 * (ES == 2 ? 2 : 4);  // output stores per wave per task
+  static constexpr int TP_BYTES = ES == 2 ? 32 * 128 : 0;    // per wave: the epilogue's transpose unit
   static_assert(KS * GTP == G_BYTES && 128 * 128 == G_BYTES, "stage geometry");
-  static_assert(STAGES * STAGE <= 163840, "the stages fit the 160 KiB of LDS");
+  static_assert(STAGES * STAGE + 4 * TP_BYTES <= 163840, "the stages and transpose units fit the 160 KiB of LDS");
   static_assert((STAGES - 2) * LPW + NSTORE < 64, "in-flight operations must fit vmcnt");
 };
 
@@ -1755,12 +1822,19 @@ __device__ __forceinline__ void dma16_s(const char* sbase, uint32_t voff, uint32
 // are in registers before the barrier that precedes their MFMAs.  The epilogue's
 // stores are the newest vector memory operations at the next STAGES - 1 barriers,
 // which then wait with vmcnt(NSTORE) on top of the STAGES - 2 stages left in flight.
-template <int STAGES, int LPW, int NSTORE, int SPT, int RS, typename Cur, typename IssueNext, typename AdvanceNext,
-          typename FragStep, typename MmaStep, typename Epilogue, typename Seek>
+// NK steps per stage (even), MF MFMAs and RS LDS reads per step; XF, GF: the fragment
+// arrays of one step (the hi / lo pair: a 16-deep step with X per column block and G
+// hi / lo per row block, 2 per 32-deep stage; a single G: a 16-deep step with X per
+// column block and G per row block, 4 per 64-deep stage), read into one set while the
+// MFMAs consume the other.
+template <int STAGES, int LPW, int NSTORE, int SPT, int RS, int NK = 2, int MF = 16, typename XF = u32x4[4],
+          typename GF = u32x4[2][2], typename Cur, typename IssueNext, typename AdvanceNext, typename FragStep,
+          typename MmaStep, typename Epilogue, typename Seek>
 __device__ __forceinline__ void sum_split_pipeline(Cur& cs, f32x16 (&acc)[4][2], int mode, IssueNext& issue_next,
                                                    AdvanceNext& advance_next, FragStep& frag_step,
                                                    MmaStep& mma_step, Epilogue& epilogue, Seek& seek) {
   static_assert(STAGES >= 3 && (STAGES - 2) * LPW + NSTORE < 64, "in-flight operations must fit vmcnt");
+  static_assert(NK >= 2 && NK % 2 == 0, "the last step of a stage reads into the second fragment set");
 #pragma unroll
   for (int p = 0; p < STAGES - 1; ++p) {
     issue_next(p);
@@ -1769,7 +1843,8 @@ __device__ __forceinline__ void sum_split_pipeline(Cur& cs, f32x16 (&acc)[4][2],
   stage_barrier<(STAGES - 2) * LPW>();  // stage 0 has landed
   issue_next(STAGES - 1);
   advance_next();
-  u32x4 xa[4], ga[2][2], xb[4], gb[2][2];
+  XF xa, xb;
+  GF ga, gb;
   frag_step(0, 0, xa, ga);
   int st = 0;
   int since_store = STAGES;  // barriers since the last epilogue that left stores in flight
@@ -1779,10 +1854,18 @@ __device__ __forceinline__ void sum_split_pipeline(Cur& cs, f32x16 (&acc)[4][2],
 #pragma unroll
       for (int jj = 0; jj < 2; ++jj) acc[i][jj] = zero16();
     for (;;) {
-      frag_step(st, 1, xb, gb);
-      mma_step(xa, ga);
-      sched_interleave<0, 16, RS, 0, 0>();
-      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int k = 1; k < NK; ++k) {  // steps 1 .. NK - 1 of stage st: read step k, MFMAs of step k - 1
+        if (k & 1) {
+          frag_step(st, k, xb, gb);
+          mma_step(xa, ga);
+        } else {
+          frag_step(st, k, xa, ga);
+          mma_step(xb, gb);
+        }
+        sched_interleave<0, MF, RS, 0, 0>();
+        __builtin_amdgcn_sched_barrier(0);
+      }
       if (++since_store < STAGES)
         stage_barrier<(STAGES - 2) * LPW + NSTORE>();
       else
@@ -1793,7 +1876,7 @@ __device__ __forceinline__ void sum_split_pipeline(Cur& cs, f32x16 (&acc)[4][2],
       st = st + 1 == STAGES ? 0 : st + 1;
       frag_step(st, 0, xa, ga);
       mma_step(xb, gb);
-      sched_interleave<0, 16, RS, 0, 0>();
+      sched_interleave<0, MF, RS, 0, 0>();
       if (++cs.h < SPT) continue;
       cs.h = 0;
       if (++cs.j == cs.cnt) break;
@@ -2200,7 +2283,7 @@ __global__ __launch_bounds__((SumGeo<T, SPLIT>::NT), 1) void bwd_sum_kernel(BwdA
 template <typename T, int PHASE, bool SPLIT>
 __global__ __launch_bounds__(kThreads, 1) void bwd_sum_narrow_kernel(BwdArgs a, int chunk, int pass) {
   using S = SumGeoNarrow<T, SPLIT>;
-  __shared__ __attribute__((aligned(16))) char smem[S::STAGES * S::STAGE];
+  __shared__ __attribute__((aligned(16))) char smem[S::STAGES * S::STAGE + 4 * S::TP_BYTES];
   constexpr int ES = S::ES;
   const int nrb = (int)a.plan.nrb, nds = (int)((a.D + S::DN - 1) / S::DN);
   const int vlo = chunk * (int)a.plan.chunk_nvt;
@@ -2239,14 +2322,18 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_narrow_kernel(BwdArgs a, 
 
   // This wave's DMA loads: XLW into the X region, GLW into the G region.  Per lane:
   // the region row it fills and the byte of the source row that belongs there.
-  uint32_t xrow[S::XLW], xcol[S::XLW], xoff[S::XLW], goff[S::GLW];
+  // (Recomputed where the ragged loads need them rather than held in registers.)
+  auto xslot = [&](int j, uint32_t& row, uint32_t& col) {
+    const uint32_t o = (uint32_t)(wave * S::XLW + j) * 1024u + lane * 16u;
+    row = o / S::XP;
+    col = tr_off<S::XP>(row, o % S::XP) - row * S::XP;  // the swizzle is an involution on the segment index
+  };
+  uint32_t xoff[S::XLW], goff[S::GLW];
 #pragma unroll
   for (int j = 0; j < S::XLW; ++j) {
-    const uint32_t o = (uint32_t)(wave * S::XLW + j) * 1024u + lane * 16u;
-    const uint32_t row = o / S::XP, pb = o % S::XP;
-    xrow[j] = row;
-    xcol[j] = tr_off<S::XP>(row, pb) - row * S::XP;  // the swizzle is an involution on the segment index
-    xoff[j] = (uint32_t)(row * pitch) + xcol[j];
+    uint32_t row, col;
+    xslot(j, row, col);
+    xoff[j] = (uint32_t)(row * pitch) + col;
   }
 #pragma unroll
   for (int j = 0; j < S::GLW; ++j) {
@@ -2332,10 +2419,9 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_narrow_kernel(BwdArgs a, 
   // compiler then adds no vmcnt wait for them in front of the fragment reads of
   // other stages (the stage barriers order them).
   const uint32_t smem_lds = lds_addr(smem);
-  auto issue = [&](const Cur& c, int st) {
-    const uint32_t sb = smem_lds + (uint32_t)(st * S::STAGE);
-    const int64_t xr0 = c.xrow + c.h * S::KS;
-    const int64_t dcol = (int64_t)c.ds * S::DN * ES;
+  // X rows [xr0, xr0 + KS) of D slice ds into the X region at LDS address sb
+  auto issue_x = [&](int64_t xr0, int ds, uint32_t sb) {
+    const int64_t dcol = (int64_t)ds * S::DN * ES;
     const char* xbase = X + xr0 * pitch + dcol;
     if (xr0 + S::KS <= xrows && dcol + S::DN * ES <= pitch) {
 #pragma unroll
@@ -2343,16 +2429,26 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_narrow_kernel(BwdArgs a, 
     } else {  // last row block or ragged D slice: zeros past the last row and the row end
 #pragma unroll
       for (int j = 0; j < S::XLW; ++j) {
-        const int64_t r = xr0 + xrow[j];
-        const int64_t cb = dcol + xcol[j];
+        uint32_t xr, xc;
+        xslot(j, xr, xc);
+        const int64_t r = xr0 + xr;
+        const int64_t cb = dcol + xc;
         const char* src = (r < xrows && cb < pitch) ? X + r * pitch + cb : reinterpret_cast<const char*>(g_zero16);
         dma16(src, sb + (wave * S::XLW + j) * 1024);
       }
     }
+  };
+  // slice h of slot's G tile into the G region of the stage at LDS address sb
+  auto issue_g = [&](int slot, int h, uint32_t sb) {
     const char* gbase =
-        a.gtile + (size_t)(c.slot - s0) * a.plan.g_bytes + (PHASE == 0 ? c.h * 128 : c.h * S::KS * S::GTP);
+        a.gtile + (size_t)(slot - s0) * a.plan.g_bytes + (PHASE == 0 ? h * 128 : h * S::KS * S::GTP);
 #pragma unroll
     for (int j = 0; j < S::GLW; ++j) dma16_s(gbase, goff[j], sb + S::X_BYTES + (wave * S::GLW + j) * 1024);
+  };
+  auto issue = [&](const Cur& c, int st) {
+    const uint32_t sb = smem_lds + (uint32_t)(st * S::STAGE);
+    issue_x(c.xrow + c.h * S::KS, c.ds, sb);
+    issue_g(c.slot, c.h, sb);
   };
 
   f32x16 acc[4][2];
@@ -2443,22 +2539,26 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_narrow_kernel(BwdArgs a, 
     // owner's end get an out-of-range offset, so every lane issues every store.
     const int* map = PHASE == 0 ? rd.map : nullptr;
     T* out = reinterpret_cast<T*>(PHASE == 0 ? a.dE : a.dC) + (map ? 0 : orow0 * D);
+    // the dE sums (a few tasks per workgroup) store straight from the accumulators: the
+    // transpose's registers would spill there
+    constexpr bool kDirect16 = PHASE == 0;
     uint32_t rowoff[2];
+    if (ES == 4 || kDirect16 || mode != kWriteT) {
 #pragma unroll
-    for (int jj = 0; jj < 2; ++jj) {
-      const int64_t m = wm * 64 + 32 * jj + n;
-      rowoff[jj] = m >= nrows ? 0x80000000u : (uint32_t)((map ? (int64_t)map[orow0 + m] : m) * D * ES);
+      for (int jj = 0; jj < 2; ++jj) {
+        const int64_t m = wm * 64 + 32 * jj + n;
+        rowoff[jj] = m >= nrows ? 0x80000000u : (uint32_t)((map ? (int64_t)map[orow0 + m] : m) * D * ES);
+      }
     }
     const int64_t d00 = (int64_t)c.ds * S::DN + wd * 128 + h * 4;
     if (mode == kWriteT) {
       const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
           out, (short)0, (int)((map ? a.N : nrows) * D * ES), 0x00020000);
+      if constexpr (ES == 4) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < 4; ++i) {
 #pragma unroll
-        for (int jj = 0; jj < 2; ++jj) {
-          const int64_t m = wm * 64 + 32 * jj + n;
-          if constexpr (ES == 4) {
+          for (int jj = 0; jj < 2; ++jj) {
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
               const int64_t d = d00 + 32 * i + 8 * q;
@@ -2467,10 +2567,15 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_narrow_kernel(BwdArgs a, 
                             __float_as_uint(acc[i][jj][4 * q + 2]), __float_as_uint(acc[i][jj][4 * q + 3])};
               __builtin_amdgcn_raw_buffer_store_b128(v, rs, off, 0, 0);
             }
-          } else {
-            // Lane (n, h) holds columns 8 q + 4 h + 0..3 of its row; one lane swap
-            // between the halves per q pair gives every lane 8 consecutive columns:
-            // 16 p + 8 h + 0..7 for the pair (2 p, 2 p + 1), stored as 16 bytes.
+          }
+        }
+      } else if constexpr (kDirect16) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+          for (int jj = 0; jj < 2; ++jj) {
+            // lane (n, h) holds columns 8 q + 4 h + 0..3 of its row; one lane swap between
+            // the halves per q pair gives it columns 16 pq + 8 h + 0..7, stored as 16 bytes
             uint32_t pk[4][2];
 #pragma unroll
             for (int q = 0; q < 4; ++q)
@@ -2488,6 +2593,57 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_narrow_kernel(BwdArgs a, 
               const int64_t d = d00 - h * 4 + 32 * i + 16 * pq + 8 * h;
               const uint32_t off = d < D ? rowoff[jj] + (uint32_t)(d * ES) : 0x80000000u;
               __builtin_amdgcn_raw_buffer_store_b128(v, rs, off, 0, 0);
+            }
+          }
+        }
+      } else {
+        // 16-bit output through the wave's 4 KiB of LDS past the stages, one 32-row x
+        // 64-column unit (jj, ip) at a time: lane (n, h) holds 16 bytes (8 columns) of
+        // row n per (i, pq); they go in as rows of 128 bytes (16-byte chunk
+        // 4 il + 2 pq + h, swizzled by bits 1..3 of the row) and come out as 8 rows x
+        // 128 bytes per read, so every store covers 8 whole 128-byte row pieces
+        // instead of 32 pieces of 32 bytes (a quarter of the L2 write requests).  The
+        // region is this wave's alone and no DMA writes it: no barrier is needed.
+        char* const tp = smem + S::STAGES * S::STAGE + wave * S::TP_BYTES;
+        const int rl = lane >> 3, cl = lane & 7;
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) {
+#pragma unroll
+          for (int ip = 0; ip < 2; ++ip) {
+#pragma unroll
+            for (int il = 0; il < 2; ++il) {
+              const int i = 2 * ip + il;
+              // lane (n, h) holds columns 8 q + 4 h + 0..3 of its row; one lane swap
+              // between the halves per q pair gives it columns 16 pq + 8 h + 0..7
+              uint32_t pk[4][2];
+#pragma unroll
+              for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int k = 0; k < 2; ++k) pk[q][k] = pack2<T>(acc[i][jj][4 * q + 2 * k], acc[i][jj][4 * q + 2 * k + 1]);
+#pragma unroll
+              for (int pq = 0; pq < 2; ++pq) {
+                u32x4 v;
+#pragma unroll
+                for (int k = 0; k < 2; ++k) {
+                  const auto sw = __builtin_amdgcn_permlane32_swap(pk[2 * pq][k], pk[2 * pq + 1][k], false, false);
+                  v[k] = sw[0];
+                  v[2 + k] = sw[1];
+                }
+                const int ck = 4 * il + 2 * pq + h;
+                *reinterpret_cast<u32x4*>(tp + n * 128 + ((ck ^ ((n >> 1) & 7)) << 4)) = v;
+              }
+            }
+            // the buffer spans under 2^31 bytes: 32-bit offsets
+            const int d = c.ds * S::DN + wd * 128 + 64 * ip + 8 * cl;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+              const int r = 8 * t + rl;
+              const u32x4 w = *reinterpret_cast<const u32x4*>(tp + r * 128 + ((cl ^ ((r >> 1) & 7)) << 4));
+              const int m = wm * 64 + 32 * jj + r;  // row of the owner (past its end: a dropped offset)
+              const uint32_t off = m < nrows && d < D
+                                       ? (uint32_t)(map ? map[orow0 + m] : m) * (uint32_t)(D * ES) + (uint32_t)(d * ES)
+                                       : 0x80000000u;
+              __builtin_amdgcn_raw_buffer_store_b128(w, rs, off, 0, 0);
             }
           }
         }
@@ -2524,7 +2680,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_narrow_kernel(BwdArgs a, 
   };
 
   Cur cs;
-  if (!seek(0, cs)) return;
+  if (seek(0, cs)) {  // this workgroup's bin or tasks
   prep(cs);
   Cur nx = cs, last = cs;
   bool have = true;
@@ -2542,8 +2698,33 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_narrow_kernel(BwdArgs a, 
     // LDS reads of one 16-deep step: 8 for X, 4 (dE) or 8 (dC, transposing) for G
     sum_split_pipeline<S::STAGES, S::LPW, S::NSTORE, S::SPT, 8 + (PHASE == 0 ? 4 : 8)>(
         cs, acc, mode, issue_next, advance_next, frag_step, mma_step, epilogue, seek);
-    return;
-  }
+  } else if constexpr (ES == 2) {
+    // A single G: the same pipeline over the four 16-deep steps of each 64-deep stage,
+    // so the MFMAs of a stage's last step run across the barrier while the next
+    // stage's first fragments are read.  LDS reads per step: 8 for X, 2 (dE) or 4 (dC,
+    // transposing) for G.
+    auto frag_ks = [&](int st, int ks, u32x4 (&x)[4], u32x4 (&g)[2]) {
+      const char* sp = smem + st * S::STAGE;
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) {
+        if constexpr (PHASE == 0)
+          g[jj] = lds_ld16(sp, go_n[jj][ks]);
+        else
+          g[jj] = frag_tr16(sp + go_t[0][jj] + 16 * ks * S::GTP, 4 * S::GTP);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) x[i] = frag_tr16(sp + xo[i] + 16 * ks * S::XP, 4 * S::XP);
+    };
+    auto mma_ks = [&](const u32x4 (&x)[4], const u32x4 (&g)[2]) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) acc[i][jj] = Traits<T>::mfma(x[i], g[jj], acc[i][jj]);
+    };
+    static_assert(S::KS == 4 * S::KE, "four 16-deep steps per stage");
+    sum_split_pipeline<S::STAGES, S::LPW, S::NSTORE, S::SPT, 8 + (PHASE == 0 ? 2 : 4), 4, 8, u32x4[4], u32x4[2]>(
+        cs, acc, mode, issue_next, advance_next, frag_ks, mma_ks, epilogue, seek);
+  } else {
 #pragma unroll
   for (int p = 0; p < S::STAGES - 1; ++p) {
     issue_next(p);
@@ -2581,6 +2762,100 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_narrow_kernel(BwdArgs a, 
     if (!seek(cs.q + 1, cs)) break;
   }
   wait_vmcnt<0>();
+  }
+  }
+  if constexpr (PHASE == 1 && ES == 2 && !SPLIT) {
+    // Block tasks: up to kDcBlkChunk owners with one kept tile in the same token block,
+    // per D slice, taken from the pass's counter once the bins are done.  The block's E
+    // slice (128 rows x 256 columns) is loaded once into the X regions of stages 0 and
+    // 1; the owners' G
+    // tiles stream through two buffers: buffer 0 in the G regions of stages 0 and 1,
+    // buffer 1 in the G region of stage 2 and the first 16 KiB of its X region.  Each
+    // owner's sums are the bin path's: the same MFMAs in the same order.
+    const int nbt = ldu(pi, kPiDcBlk) * nds;
+    if (nbt == 0) return;
+    const int* blk_task = a.dc_blk_task + 4 * ldu(pi, kPiVt0);
+    const int* blk_own = a.dc_blk_own + 2 * ldu(pi, kPiVt0);
+    // stage base whose G region (base + X_BYTES) holds half hh of buffer buf
+    auto gsb = [&](int buf, int hh) -> uint32_t {
+      return buf == 0 ? (uint32_t)(hh * S::STAGE) : (uint32_t)(2 * S::STAGE - (hh ? S::X_BYTES : 0));
+    };
+    static_assert(2 * S::STAGE - S::X_BYTES + S::X_BYTES + S::G_BYTES <= 2 * S::STAGE + S::X_BYTES,
+                  "buffer 1's second half ends inside stage 2's X region");
+    auto blk_ks = [&](int buf, int st, u32x4 (&x)[4], u32x4 (&g)[2]) {  // step st = 4 hh + ks
+      const char* spe = smem + (st >> 2) * S::STAGE;
+      const char* spg = smem + gsb(buf, st >> 2);
+      const int ks = st & 3;
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) g[jj] = frag_tr16(spg + go_t[0][jj] + 16 * ks * S::GTP, 4 * S::GTP);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) x[i] = frag_tr16(spe + xo[i] + 16 * ks * S::XP, 4 * S::XP);
+    };
+    auto blk_mma = [&](const u32x4 (&x)[4], const u32x4 (&g)[2]) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) acc[i][jj] = Traits<T>::mfma(x[i], g[jj], acc[i][jj]);
+    };
+    int* box = reinterpret_cast<int*>(smem);
+    for (;;) {
+      wait_vmcnt<0>();
+      __syncthreads();  // every wave is done with the LDS of the last task
+      if (threadIdx.x == 0) box[0] = atomicAdd(&a.pinfo[pass * kPassInts + kPiDcQueue], 1);
+      __syncthreads();
+      const int t = __builtin_amdgcn_readfirstlane(box[0]);
+      if (t >= nbt) break;
+      __syncthreads();  // box is read before the DMA below overwrites it
+      const int bi = t / nds, ds = t - bi * nds;
+      const int o0 = ldu(blk_task, 4 * bi + 1), o1 = ldu(blk_task, 4 * bi + 2);
+      const int64_t xr = (int64_t)ldu(blk_task, 4 * bi) * kBwdTokens;
+      issue_x(xr, ds, smem_lds);
+      issue_x(xr + S::KS, ds, smem_lds + S::STAGE);
+      const int slot0 = ldu(blk_own, 2 * o0 + 1);
+      issue_g(slot0, 0, smem_lds + gsb(0, 0));
+      issue_g(slot0, 1, smem_lds + gsb(0, 1));
+      for (int o = o0; o < o1; ++o) {
+        const int buf = (o - o0) & 1;
+        // this owner's G tile (and, first, the E slice) has landed: only the last
+        // owner's stores may still be in flight
+        if (o == o0)
+          wait_vmcnt<0>();
+        else
+          wait_vmcnt<S::NSTORE>();
+        __syncthreads();  // ... for every wave, and every wave is done with the other buffer
+        if (o + 1 < o1) {
+          const int ns = ldu(blk_own, 2 * (o + 1) + 1);
+          issue_g(ns, 0, smem_lds + gsb(buf ^ 1, 0));
+          issue_g(ns, 1, smem_lds + gsb(buf ^ 1, 1));
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int jj = 0; jj < 2; ++jj) acc[i][jj] = zero16();
+        u32x4 xa[4], ga[2], xb[4], gb[2];
+        blk_ks(buf, 0, xa, ga);
+#pragma unroll
+        for (int st = 0; st < 8; st += 2) {  // read step st + 1 while the MFMAs of step st run
+          blk_ks(buf, st + 1, xb, gb);
+          blk_mma(xa, ga);
+          sched_interleave<0, 8, 12, 0, 0>();
+          __builtin_amdgcn_sched_barrier(0);
+          if (st + 2 < 8) blk_ks(buf, st + 2, xa, ga);
+          blk_mma(xb, gb);
+          if (st + 2 < 8)
+            sched_interleave<0, 8, 12, 0, 0>();
+          else
+            sched_interleave<0, 8, 0, 0, 0>();
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        Cur c;
+        c.owner = ldu(blk_own, 2 * o);
+        c.ds = ds;
+        epilogue(c);
+      }
+    }
+    wait_vmcnt<0>();
+  }
 }
 
 // ---------------------------------------------------------------- 6. dBias

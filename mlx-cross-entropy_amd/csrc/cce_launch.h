@@ -98,6 +98,8 @@ constexpr size_t kGScratchBudget = size_t(CCE_G_SCRATCH_MIB) << 20;
 constexpr int kCompactMaxWords = 8192;                 // bitmap words one compaction holds in LDS
 constexpr int kCompactMaxVt = 4096;                    // vocabulary tiles per chunk (LDS counts)
 constexpr int kMaxDcBins = 256;                        // workgroup bins of the dC sums' schedule
+constexpr int kDcBlkMaxRb = 4096;                      // token blocks the dC block tasks group by (LDS counts)
+constexpr int kDcBlkChunk = 4;                         // one-tile owners per dC block task at most
 // Token order of the backward.  The token blocks of the tile filter can be formed
 // from the rows grouped by the vocabulary tile of their target: with a peaked
 // softmax a block then keeps a few tiles instead of one per distinct target.  The
@@ -126,6 +128,9 @@ enum PassField {
   kPiDeMode = 9,   // -1: no work (past the passes the data needs); else a dE write mode (WriteMode)
   kPiRun = 10,     // G tasks are runs of at most this many slots of one token block
   kPiDcWide = 11,  // filter on: 1 if the dC sums of the pass run in the wide geometry, 0 narrow
+  kPiDcBlk = 12,   // dC block tasks per D slice: dc_blk_task[vt0 + i], i < this count
+  kPiDcQueue = 13, // dC block tasks: counter of the tasks taken (zeroed by the compaction)
+  kPiDcDeal = 14,  // dC owners dealt to the schedule's bins: own_vt[vt0 + i], i < this count (the rest: block tasks)
 };
 // dE write mode of a pass: one pass over everything writes dE directly; with more
 // passes (or chunks) dE is summed in an fp32 carry: the first pass stores it, the
@@ -146,7 +151,7 @@ struct BwdPlan {
   bool carry;               // the fp32 dE carry is reserved (more than one pass or chunk may run)
   // workspace byte offsets
   size_t bits, counts, pinfo, rb_start, slot_vt, slot_rb, vt_start, vt_slot, g_task, g_task_rb, own_rb, own_vt,
-      dc_bin_start, dc_bin_owner, gtile, colsum, de_acc;
+      dc_bin_start, dc_bin_owner, dc_blk_task, dc_blk_own, gtile, colsum, de_acc;
   size_t perm, sort_buf, rowbits, bits_p, t_perm, lse_perm, dnll_perm, e_perm;  // sorted order (perm_ok)
   size_t qrows;  // dequantized classifier rows of one chunk (quantized classifier only)
   size_t total_bytes;
@@ -211,6 +216,8 @@ inline BwdPlan make_bwd_plan_cap(size_t esize, int64_t N, int64_t D, int64_t V, 
   P.own_vt = take((size_t)cw * 4);
   P.dc_bin_start = take((size_t)(kMaxDcBins + 1) * 4);
   P.dc_bin_owner = take((size_t)cw * 4);
+  P.dc_blk_task = take((size_t)cw * 16);
+  P.dc_blk_own = take((size_t)cw * 8);
   P.gtile = want_g ? take((size_t)P.cap * P.g_bytes) : 0;
   P.colsum = want_db ? take((size_t)P.cap * kBwdVocab * sizeof(float)) : 0;
   P.de_acc = P.carry ? take((size_t)N * (size_t)D * sizeof(float)) : 0;
@@ -319,6 +326,12 @@ struct BwdArgs {
   int* own_vt;        // [chunk_nvt] vocab tiles with kept tiles, by pass, most first (dC owners)
   int* dc_bin_start;  // [kMaxDcBins + 1] dC schedule: owners of bin m are dc_bin_owner[start[m] .. start[m + 1])
   int* dc_bin_owner;  // [chunk_nvt]
+  // dC block tasks (dc_blk): the owners with one kept tile of a pass, grouped by the
+  // token block of that tile, at most kDcBlkChunk per task.  Task i of the pass (per D
+  // slice) is dc_blk_task[vt0 + i] = (token block, e0, e1, 0): its owners are the
+  // (owner, slot) pairs dc_blk_own[vt0 + e], e0 <= e < e1 (vt0: the pass's first tile).
+  int* dc_blk_task;   // [chunk_nvt][4]
+  int* dc_blk_own;    // [chunk_nvt][2]
   char* gtile;        // [cap] G tiles of one pass, token-major (g_tile_bytes each)
   float* colsum;      // [cap][128] per-slot column sums of G (dBias)
   float* de_acc;      // [N, D] fp32, only when the plan reserves the carry
@@ -343,6 +356,7 @@ struct BwdArgs {
   int stats32;          // tile_max per 32 columns in the reference's layout [N][ceil(V/32)] (else [nvt][N])
   int g_scaled;         // fp16: G tiles hold G * 2^counts[kGScaleExp] (else unscaled)
   int g_split;          // 16-bit: G tiles hold the hi / lo pair (else G rounded once)
+  int dc_blk;           // the narrow dC sums run owners with one kept tile as tasks per (token block, D slice)
   // Pinned host memory of 1 + max_passes ints, or null.  The compaction writes the
   // chunk's pass count to [0] and each pass's kPiDcWide to [1 + p]; the host then
   // launches only those passes and only the dC geometry picked (launch_backward's

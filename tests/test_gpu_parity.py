@@ -1012,3 +1012,71 @@ def test_raw_forward_then_raw_backward(m, cuda):
         assert err <= 1e-3, (name, err)
     np.testing.assert_allclose(f64(lse), O.per_token(f64(e), f64(c), tt, f64(b))[1], rtol=1e-6)
 
+
+
+@pytest.mark.parametrize("filtered", [False, True])
+def test_backward_captured_in_a_graph(m, cuda, filtered):
+    """The backward inside HIP graph capture: the host cannot wait for the pass count
+    there, so the library launches the worst case of passes and the device skips the
+    empty ones.  Replays (with eager work and synchronisation between them) equal the
+    eager backward bit for bit; the passes are several (max_g_tiles) so that the
+    skipped ones are exercised."""
+    e, c, t = _peaked(cuda, N=300, D=264, V=9000, seed=19) if filtered else \
+        normal_case(300, 264, 9000, torch.bfloat16, cuda, seed=19, std=0.05)
+    t[3] = -100
+    feps = m.FILTER_LOG_EPS if filtered else None
+    tm, _, _, lse, _ = m._ext.forward(e, c, t, None, -100)
+    d_nll = torch.full((300,), 1.0 / 300, device=cuda)
+    with m._ext.backward_options(max_g_tiles=8):
+        ref = m._ext.backward(e, c, t, lse, tm, d_nll, None, -100, feps, True, True, False)
+        torch.cuda.synchronize()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):  # warm-up off the capturing stream
+            m._ext.backward(e, c, t, lse, tm, d_nll, None, -100, feps, True, True, False)
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            out = m._ext.backward(e, c, t, lse, tm, d_nll, None, -100, feps, True, True, False)
+    for rep in range(3):
+        junk = torch.randn(1 << 20, device=cuda).sum()  # eager work between the replays
+        graph.replay()
+        torch.cuda.synchronize()
+        assert bool(torch.isfinite(junk))
+        for x, y in zip(out[:2], ref[:2]):
+            assert torch.equal(x.view(torch.int16), y.view(torch.int16)), rep
+
+
+@pytest.mark.parametrize("case", ["peaked", "uniform", "passes"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_dc_block_tasks_match_owner_tasks(m, cuda, case, dtype):
+    """The narrow dC sums run the owners that keep one token block as tasks per (token
+    block, D slice); the same owners as tasks of their own (CCE_BWD_DC_OWNER_TASKS)
+    give dC bit for bit: the same MFMAs in the same order.  Cases: skewed targets (a
+    few owners keep many blocks, most keep one), near-uniform targets with the narrow
+    geometry forced, and several passes of a small G scratch; D = 264 has a ragged
+    last slice."""
+    if case == "peaked":
+        e, c, t = _peaked(cuda, N=1000, D=264, V=20000, dtype=dtype, seed=23)
+    else:
+        e, c, t = normal_case(1000, 264, 20000, dtype, cuda, seed=23, std=0.05)
+    t[5] = -100
+    lse_tm = m._ext.forward(e, c, t, None, -100)
+    tm, lse = lse_tm[0], lse_tm[3]
+    d_nll = torch.linspace(0.5, 1.5, 1000, device=cuda) / 1000
+    opts = {"dc_sums": "narrow", "g_precision": "single"}
+    if case == "passes":
+        opts["max_g_tiles"] = 24
+    stats = torch.zeros(3, dtype=torch.int64, device=cuda)
+    with m._ext.backward_options(**opts):
+        dE1, dC1, _ = m._ext.backward(e, c, t, lse, tm, d_nll, None, -100, m.FILTER_LOG_EPS, True, True, False,
+                                      tile_stats=stats)
+    with m._ext.backward_options(dc_tasks="owners", **opts):
+        dE2, dC2, _ = m._ext.backward(e, c, t, lse, tm, d_nll, None, -100, m.FILTER_LOG_EPS, True, True, False)
+    torch.cuda.synchronize()
+    print(f"{case} {dtype}: kept tiles {int(stats[0])} of {int(stats[1])}")
+    assert int(stats[0]) > 0
+    assert torch.equal(dC1.view(torch.int16), dC2.view(torch.int16))
+    assert torch.equal(dE1.view(torch.int16), dE2.view(torch.int16))
+    assert float(dC1.float().abs().sum()) > 0

@@ -149,7 +149,7 @@ def test_backward_validation_errors(ext):
     assert _bwd(lib, ext, dbias=FAKE) == ext.CCE_ERR_INVALID_ARGUMENT  # dBias without bias
     assert _bwd(lib, ext, eps=float("nan")) == ext.CCE_ERR_INVALID_ARGUMENT
     assert _bwd(lib, ext, dtype=3) == ext.CCE_ERR_UNSUPPORTED_DTYPE
-    assert _bwd_ex(lib, flags=1 << 11) == ext.CCE_ERR_INVALID_ARGUMENT  # unknown flag
+    assert _bwd_ex(lib, flags=1 << 12) == ext.CCE_ERR_INVALID_ARGUMENT  # unknown flag
     assert b"unknown flags" in lib.cce_last_error()
     assert _bwd_ex(lib, flags=ext.CCE_BWD_G_PAIR | ext.CCE_BWD_G_SINGLE) == ext.CCE_ERR_INVALID_ARGUMENT
     assert _bwd_ex(lib, flags=ext.CCE_BWD_TOKENS_INPUT | ext.CCE_BWD_TOKENS_SORTED) == ext.CCE_ERR_INVALID_ARGUMENT
