@@ -396,6 +396,132 @@ __global__ __launch_bounds__(1024) void bwd_filter_sort_kernel(BwdArgs a) {
   filter_item(a, (blockIdx.x - 1) * 16 + (threadIdx.x >> 6));
 }
 
+// The same token order by a counting sort, for up to kCsKeys keys and 16 rounds
+// (N <= 16384), in far fewer workgroup-wide steps than the radix passes.  Wave w
+// holds rows [w S, (w + 1) S), S = ceil(N / 16), 64 per round in row order.
+//   1. Per round, the lanes holding the same key find each other (a ballot per key
+//      bit); a lane's place among the wave's earlier rows of its key is the wave's
+//      running count of that key (an LDS counter per wave and key) plus the lower
+//      lanes with its key; the highest such lane advances the counter.
+//   2. Per key, the counters become an exclusive prefix over the waves and give the
+//      key's total; scans over the keys (two per thread, in key order) give every
+//      key's first place among the head rows (keys with kSortHeadRun or more rows)
+//      or among the tail rows.
+//   3. A row's head or tail rank is its key's start plus its place among the key's
+//      rows; the block placement is the radix path's.
+constexpr int kCsKeys = 2048;
+template <int MAXR>
+__device__ void csort_rows(const BwdArgs& a) {
+  static_assert(MAXR <= 16, "per-wave counts fit 16 bits: N <= 16384");
+  __shared__ uint16_t cnt[16 * kCsKeys];          // [wave][key]
+  __shared__ int kinfo[kCsKeys];                  // 2 (first head or tail rank of the key) + is-head
+  __shared__ int tbl[MAXR * 1024 / kBwdTokens + 1];  // tail rows before each block
+  __shared__ int wsum[16];
+  const int N = (int)a.N, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nvt = (int)a.plan.nvt;
+  const int S = (N + 15) >> 4;
+  const uint64_t lt = (1ull << lane) - 1ull;
+  for (int i = tid; i < 16 * kCsKeys / 2; i += 1024) reinterpret_cast<uint32_t*>(cnt)[i] = 0u;
+  uint32_t key[MAXR];
+  bool val[MAXR];
+#pragma unroll
+  for (int r0 = 0; r0 < MAXR; r0 += 8) {
+    int64_t t[8];
+    float g[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int j = (r0 + k) * 64 + lane, row = wave * S + j;
+      val[r0 + k] = j < S && row < N;
+      t[k] = val[r0 + k] ? a.targets[row] : -1;
+      g[k] = val[r0 + k] ? a.d_nll[row] : 0.f;
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const bool act = g[k] != 0.f && !(a.has_ignore && t[k] == a.ignore_index) && t[k] >= 0 && t[k] < a.V;
+      key[r0 + k] = act ? (uint32_t)(t[k] >> 7) : (uint32_t)nvt;  // t / kBwdVocab
+    }
+  }
+  static_assert(kBwdVocab == 128, "key = target >> 7");
+  __syncthreads();
+  uint16_t* mine = cnt + wave * kCsKeys;
+  int rk[MAXR];  // place among the wave's earlier rows of the key
+#pragma unroll
+  for (int j = 0; j < MAXR; ++j) {
+    rk[j] = 0;
+    if (j * 64 >= S) continue;  // uniform
+    uint64_t m = __ballot(val[j]);
+#pragma unroll
+    for (int b = 0; b < 11; ++b) {
+      const uint64_t q = __ballot((key[j] >> b) & 1u);
+      m &= ((key[j] >> b) & 1u) ? q : ~q;
+    }
+    const int base = val[j] ? (int)mine[key[j]] : 0;
+    rk[j] = base + __popcll(m & lt);
+    if (val[j] && (m >> lane) == 1ull) mine[key[j]] = (uint16_t)(base + __popcll(m));
+  }
+  __syncthreads();
+  // keys 2 tid and 2 tid + 1: prefix over the waves, totals, head / tail starts
+  int tot[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int k = 2 * tid + u;
+    int run = 0;
+    if (k <= nvt) {
+#pragma unroll
+      for (int w = 0; w < 16; ++w) {
+        const int c = cnt[w * kCsKeys + k];
+        cnt[w * kCsKeys + k] = (uint16_t)run;
+        run += c;
+      }
+    }
+    tot[u] = run;
+  }
+  const int h0 = tot[0] >= kSortHeadRun ? tot[0] : 0, h1 = tot[1] >= kSortHeadRun ? tot[1] : 0;
+  int nH, nall;
+  const int hs = block_excl_scan(h0 + h1, wsum, nH);
+  const int as = block_excl_scan(tot[0] + tot[1], wsum, nall);
+  if (2 * tid <= nvt) kinfo[2 * tid] = h0 ? (hs << 1) | 1 : (as - hs) << 1;
+  if (2 * tid + 1 <= nvt) kinfo[2 * tid + 1] = h1 ? ((hs + h0) << 1) | 1 : (as + tot[0] - hs - h0) << 1;
+  const int nT = N - nH;
+  const int nrb = (N + kBwdTokens - 1) / kBwdTokens;
+  for (int b = tid; b <= nrb; b += 1024) tbl[b] = (int)((int64_t)min(b * kBwdTokens, N) * nT / N);
+  __syncthreads();
+  auto tb = [&](int b) { return tbl[b]; };                              // tail rows before block b
+  auto hb = [&](int b) { return min(b * kBwdTokens, N) - tbl[b]; };   // head rows before block b
+#pragma unroll
+  for (int j = 0; j < MAXR; ++j) {
+    if (!val[j]) continue;
+    const int info = kinfo[key[j]];
+    const int r = (info >> 1) + (int)cnt[wave * kCsKeys + key[j]] + rk[j];
+    int pos;
+    if (info & 1) {  // head rank r: the last block b with hb(b) <= r
+      int lo = 0, hi = nrb - 1;
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (hb(mid) <= r) lo = mid; else hi = mid - 1;
+      }
+      pos = lo * kBwdTokens + (tb(lo + 1) - tb(lo)) + (r - hb(lo));
+    } else {  // tail rank r: the last block b with tb(b) <= r
+      int lo = 0, hi = nrb - 1;
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (tb(mid) <= r) lo = mid; else hi = mid - 1;
+      }
+      pos = lo * kBwdTokens + (r - tb(lo));
+    }
+    a.perm[pos] = wave * S + j * 64 + lane;
+  }
+}
+
+template <int MAXR>
+__global__ __launch_bounds__(1024) void bwd_filter_csort_kernel(BwdArgs a) {
+  if (blockIdx.x == 0) {
+    csort_rows<MAXR>(a);
+    return;
+  }
+  filter_item(a, (blockIdx.x - 1) * 16 + (threadIdx.x >> 6));
+}
+
 // Pointers of the per-row data the G kernel and the sums read -- the sorted copies
 // when the compaction chose the sorted token order -- and the map from the row
 // order they work in to the rows of dE (perm; null for the input order).
@@ -2970,7 +3096,11 @@ static hipError_t backward_typed(const BwdArgs& a, hipStream_t s, hipEvent_t pas
   hipError_t err;
   if (sorted_ok) {
     const dim3 fg((unsigned)(1 + (items + 15) / 16));
-    if (a.N <= 8 * 1024)
+    if (a.N <= 8 * 1024 && P.nvt < kCsKeys)
+      hipLaunchKernelGGL(bwd_filter_csort_kernel<8>, fg, dim3(1024), 0, s, a);
+    else if (a.N <= 16 * 1024 && P.nvt < kCsKeys)
+      hipLaunchKernelGGL(bwd_filter_csort_kernel<16>, fg, dim3(1024), 0, s, a);
+    else if (a.N <= 8 * 1024)
       hipLaunchKernelGGL(bwd_filter_sort_kernel<8>, fg, dim3(1024), 0, s, a);
     else if (a.N <= 16 * 1024)
       hipLaunchKernelGGL(bwd_filter_sort_kernel<16>, fg, dim3(1024), 0, s, a);
