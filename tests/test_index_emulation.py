@@ -1,0 +1,246 @@
+"""CPU restatements of the backward's index logic, checked against what it must compute.
+
+Each function below restates, step for step, the indexing of one piece of device code
+(the kernel named in its docstring), so that a mistake in the restated scheme -- a lost
+row, an index past its array, two writers of one slot -- fails here, on the CPU:
+
+- the counting sort of the token order (`csort_rows`, cce_bwd.hip) against the stable
+  sort by target tile with the rare targets spread over the blocks, the order the
+  backward's token blocks are defined by (the reference has no counterpart: it runs
+  its filter on input-order blocks, cce.metal:191-204);
+- the dC block tasks (the compaction's lists, `bwd_compact_kernel`, and the walk of the
+  narrow dC sums, `bwd_sum_narrow_kernel`) against the set of one-tile owners and slices;
+- the 16-bit epilogue's transpose through LDS (`bwd_sum_narrow_kernel`): a bijection from
+  the MFMA register layout to whole 128-byte row pieces, free of LDS bank conflicts.
+"""
+import numpy as np
+import pytest
+
+HEAD_RUN = 16  # kSortHeadRun
+BLOCK = 128    # kBwdTokens == kBwdVocab
+
+
+def token_order(tt, d_nll, V, ignore_index=-100):
+    """The definition: rows stably sorted by the 128-column tile of their target (rows
+    without gradient keyed past the last tile); rows of keys with fewer than HEAD_RUN
+    rows dealt evenly over the 128-row blocks, each block taking its share of them
+    first, then the next rows of the long runs.  perm[p] = input row at position p."""
+    N = len(tt)
+    nvt = (V + BLOCK - 1) // BLOCK
+    act = (d_nll != 0) & (tt != ignore_index) & (tt >= 0) & (tt < V)
+    key = np.where(act, tt // BLOCK, nvt)
+    srt = np.argsort(key, kind="stable")
+    head = np.bincount(key, minlength=nvt + 1)[key[srt]] >= HEAD_RUN
+    heads, tails = srt[head], srt[~head]
+    nT, nrb = len(tails), (N + BLOCK - 1) // BLOCK
+    tb = [min(BLOCK * b, N) * nT // N for b in range(nrb + 1)]
+    perm, h = np.empty(N, dtype=np.int64), 0
+    for b in range(nrb):
+        p0, nt = BLOCK * b, tb[b + 1] - tb[b]
+        perm[p0:p0 + nt] = tails[tb[b]:tb[b + 1]]
+        nh = min(BLOCK * (b + 1), N) - p0 - nt
+        perm[p0 + nt:p0 + nt + nh] = heads[h:h + nh]
+        h += nh
+    return perm
+
+
+def csort_restated(tt, d_nll, V, ignore_index=-100, maxr=16, nkeys=2048, wave_prefix=True):
+    """csort_rows: wave w holds rows [w S, (w+1) S), S = ceil(N / 16), 64 per round;
+    per round a lane's rank is its wave's running count of its key plus the lower lanes
+    with that key (the highest of them advances the 16-bit counter); per key the 16
+    counters become a prefix over the waves; head / tail starts come from scans over
+    the keys; the block placement is a bisection over the per-block head / tail counts."""
+    N = len(tt)
+    nvt = (V + BLOCK - 1) // BLOCK
+    assert nvt < nkeys and N <= 1024 * maxr
+    act = (d_nll != 0) & (tt != ignore_index) & (tt >= 0) & (tt < V)
+    key = np.where(act, tt // BLOCK, nvt)
+    S = (N + 15) >> 4
+    cnt = np.zeros((16, nkeys), dtype=np.int64)
+    rank = np.zeros(N, dtype=np.int64)
+    for w in range(16):
+        for j in range(maxr):
+            if j * 64 >= S:
+                continue
+            lanes = [l for l in range(64) if j * 64 + l < S and w * S + j * 64 + l < N]
+            seen = {}
+            for l in lanes:  # lanes in order: the lower lanes with the key come first
+                row = w * S + j * 64 + l
+                k = key[row]
+                rank[row] = cnt[w, k] + seen.get(k, 0)
+                seen[k] = seen.get(k, 0) + 1
+            for k, c in seen.items():
+                cnt[w, k] += c
+                assert cnt[w, k] < 1 << 16  # 16-bit counters
+    tot = np.zeros(nkeys, dtype=np.int64)
+    for k in range(nvt + 1):
+        run = 0
+        for w in range(16):
+            c = cnt[w, k]
+            cnt[w, k] = run if wave_prefix else 0
+            run += c
+        tot[k] = run
+    is_head = tot >= HEAD_RUN
+    hs = np.concatenate([[0], np.cumsum(np.where(is_head, tot, 0))])
+    allst = np.concatenate([[0], np.cumsum(tot)])
+    nH = int(hs[nkeys])
+    nT, nrb = N - nH, (N + BLOCK - 1) // BLOCK
+    tbl = [min(b * BLOCK, N) * nT // N for b in range(nrb + 1)]
+
+    def last_block(r, before):  # the last block b with before(b) <= r
+        lo, hi = 0, nrb - 1
+        while lo < hi:
+            mid = (lo + hi + 1) >> 1
+            if before(mid) <= r:
+                lo = mid
+            else:
+                hi = mid - 1
+        return lo
+
+    perm = np.full(N, -1, dtype=np.int64)
+    for row in range(N):
+        k, w = key[row], row // S
+        start = hs[k] if is_head[k] else allst[k] - hs[k]
+        r = start + cnt[w, k] + rank[row]
+        if is_head[k]:
+            hb = lambda b: min(b * BLOCK, N) - tbl[b]
+            b = last_block(r, hb)
+            pos = b * BLOCK + (tbl[b + 1] - tbl[b]) + (r - hb(b))
+        else:
+            b = last_block(r, lambda b: tbl[b])
+            pos = b * BLOCK + (r - tbl[b])
+        assert 0 <= pos < N and perm[pos] == -1
+        perm[pos] = row
+    return perm
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_counting_sort_equals_the_token_order(seed):
+    rng = np.random.default_rng(seed)
+    N = int(rng.choice([1, 15, 16, 17, 127, 128, 129, 1000, 4096, 8191, 8192, 12345, 16384]))
+    V = int(rng.choice([128, 1000, 20000, 128256, 256000, 262015]))
+    kind = seed % 3
+    if kind == 0:
+        tt = rng.integers(0, V, N)
+    elif kind == 1:  # Zipf: long head runs
+        tt = np.minimum(rng.zipf(1.3, N) - 1, V - 1)
+    else:  # few keys
+        tt = rng.integers(0, min(V, 300), N)
+    tt[rng.random(N) < 0.05] = -100
+    d = rng.random(N).astype(np.float32)
+    d[rng.random(N) < 0.03] = 0
+    assert np.array_equal(csort_restated(tt, d, V), token_order(tt, d, V))
+
+
+def test_counting_sort_mutant_is_caught():
+    """A counting sort that forgets the earlier waves' rows of a key (no prefix over the
+    waves) places two rows at one position or differs from the definition."""
+    rng = np.random.default_rng(5)
+    N, V = 4096, 20000
+    tt = rng.integers(0, 300, N)
+    d = np.ones(N, dtype=np.float32)
+    assert np.array_equal(csort_restated(tt, d, V), token_order(tt, d, V))
+    try:
+        bad = csort_restated(tt, d, V, wave_prefix=False)
+    except AssertionError:
+        return
+    assert not np.array_equal(bad, token_order(tt, d, V))
+
+
+def block_tasks_restated(cnts, vt0, vt1, rb_of, slot_of, chunk=4):
+    """bwd_compact_kernel's block tasks of one pass: the pass's tiles that keep one
+    token block, counted per block (any order among a block's tiles: LDS atomics), then
+    tasks of at most `chunk` of one block's tiles in token-block order.  Returns the
+    tasks (rb, e0, e1) and the (owner, slot) pairs by entry."""
+    order = [v for v in range(vt0, vt1) if cnts[v] == 1]
+    rng = np.random.default_rng(vt0 + 7)
+    rng.shuffle(order)
+    nrb = max(rb_of.values()) + 1 if rb_of else 1
+    cntb = [0] * nrb
+    place = {}
+    for v in order:
+        place[v] = cntb[rb_of[v]]
+        cntb[rb_of[v]] += 1
+    tasks, first, ob = [], [0] * nrb, 0
+    for r in range(nrb):
+        c = cntb[r]
+        for e in range(0, c, chunk):
+            tasks.append((r, ob + e, ob + min(c, e + chunk)))
+        first[r] = ob
+        ob += c
+    own = {}
+    for v in order:
+        e = first[rb_of[v]] + place[v]
+        assert e not in own and 0 <= e < len(order)
+        own[e] = (v, slot_of[(rb_of[v], v)])
+    assert len(tasks) <= vt1 - vt0  # the tasks of a pass fit its tiles' entries
+    return tasks, own
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_block_tasks_cover_every_one_tile_owner_once(seed):
+    rng = np.random.default_rng(seed)
+    nrb = int(rng.choice([1, 2, 7, 64, 300]))
+    nvt = int(rng.integers(1, 3000))
+    cnts = [int(min(nrb, rng.choice([0, 1, 1, 1, 2, 46, int(rng.integers(0, 60))]))) for _ in range(nvt)]
+    slot, slot_of, rb_of = 0, {}, {}
+    for v in range(nvt):
+        for rb in sorted(rng.choice(nrb, cnts[v], replace=False).tolist()):
+            slot_of[(rb, v)] = slot
+            slot += 1
+            if cnts[v] == 1:
+                rb_of[v] = rb
+    vt0 = int(rng.integers(0, nvt))
+    vt1 = int(rng.integers(vt0 + 1, nvt + 1))
+    tasks, own = block_tasks_restated(cnts, vt0, vt1, rb_of, slot_of)
+    nds = int(rng.choice([1, 8, 16, 23]))
+    seen = set()
+    for t in range(len(tasks) * nds):  # the kernel's walk: task t = (tasks[t / nds], slice t % nds)
+        (rb, e0, e1), ds = tasks[t // nds], t % nds
+        assert e0 < e1 and e1 - e0 <= 4
+        for e in range(e0, e1):
+            v, s = own[e]
+            assert rb_of[v] == rb and slot_of[(rb, v)] == s
+            assert (v, ds) not in seen
+            seen.add((v, ds))
+    assert seen == {(v, ds) for v in range(vt0, vt1) if cnts[v] == 1 for ds in range(nds)}
+    # the owners dealt to bins are exactly those before the one-tile ones in own_vt
+    own_vt = sorted((v for v in range(vt0, vt1) if cnts[v] > 0), key=lambda v: -cnts[v])
+    deal = len(own_vt) - len(own)
+    assert all(cnts[v] >= 2 for v in own_vt[:deal]) and all(cnts[v] == 1 for v in own_vt[deal:])
+
+
+def test_epilogue_transpose_is_a_conflict_free_bijection():
+    """The 16-bit epilogue: lane (n, h) of a wave holds, per (il, pq), 8 consecutive
+    columns 32 il + 16 pq + 8 h of row n of a 32-row x 64-column unit; it writes them to
+    16-byte chunk c = 4 il + 2 pq + h of row n, at chunk c ^ ((n >> 1) & 7) of a
+    128-byte LDS row; lane l then reads row 8 t + (l >> 3), chunk l & 7 (same swizzle)
+    and stores it.  Every chunk is written once and read back by the lane that stores
+    its row piece; each group of 8 lanes of a 16-byte access hits 8 distinct 4-bank
+    groups of the 64 banks."""
+    slot = {}
+    for lane in range(64):
+        n, h = lane & 31, lane >> 5
+        for il in range(2):
+            for pq in range(2):
+                ck = 4 * il + 2 * pq + h
+                addr = n * 128 + ((ck ^ ((n >> 1) & 7)) << 4)
+                assert 0 <= addr and addr + 16 <= 4096 and addr not in slot
+                slot[addr] = (n, 32 * il + 16 * pq + 8 * h)
+    assert len(slot) == 256
+    for t in range(4):
+        for lane in range(64):
+            r, cl = 8 * t + (lane >> 3), lane & 7
+            assert slot[r * 128 + ((cl ^ ((r >> 1) & 7)) << 4)] == (r, 8 * cl)
+    groups = lambda addrs: {((a // 4) % 64) // 4 for a in addrs}
+    for il in range(2):
+        for pq in range(2):
+            for g in range(8):
+                lanes = range(8 * g, 8 * g + 8)
+                addrs = [(l & 31) * 128 + (((4 * il + 2 * pq + (l >> 5)) ^ (((l & 31) >> 1) & 7)) << 4) for l in lanes]
+                assert len(groups(addrs)) == 8
+    for t in range(4):
+        for g in range(8):
+            addrs = [(8 * t + (l >> 3)) * 128 + (((l & 7) ^ (((8 * t + (l >> 3)) >> 1) & 7)) << 4)
+                     for l in range(8 * g, 8 * g + 8)]
+            assert len(groups(addrs)) == 8
