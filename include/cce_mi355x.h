@@ -79,7 +79,10 @@ int64_t cce_num_ref_tiles(int64_t V);
  *   nll[r] = lse[r] + neg_target_logit[r]     for rows kept by the ignore mask,
  *            0                                for masked rows (mlx_cce/__init__.py:59-70),
  *            NaN                              for kept rows whose target is outside [0, V).
- * tile_sum_exp is required (it is the combine kernel's input).
+ * tile_sum_exp is required (it is the combine kernel's input).  neg_target_logit[r] is
+ * written only for rows whose target lies in [0, V); other entries keep what the buffer
+ * held, as the reference's kernel leaves them (cce.metal:108-114 writes it only where
+ * the target falls in the tile).
  */
 int cce_forward(int dtype, const void* e, const void* c, const void* bias,
                 const int64_t* targets, int64_t ignore_index, int has_ignore,
