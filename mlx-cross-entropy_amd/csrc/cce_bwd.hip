@@ -169,6 +169,15 @@ __device__ __forceinline__ int wave_incl_scan(int v) {
   return v;
 }
 
+// Sum across the 64 lanes of a wave (every lane gets it).  Counters in LDS take one
+// atomic per wave of such a sum: an atomic from many lanes to one address becomes a
+// loop over the active lanes, ~35 ns per lane here.
+__device__ __forceinline__ int wave_sum(int v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
 // Exclusive prefix sum over the NW waves of a workgroup (all threads call it);
 // `total` gets the sum.
 template <int NW = 16>
@@ -408,7 +417,8 @@ __global__ __launch_bounds__(1024) void bwd_filter_sort_kernel(BwdArgs a) {
 //      key's first place among the head rows (keys with kSortHeadRun or more rows)
 //      or among the tail rows.
 //   3. A row's head or tail rank is its key's start plus its place among the key's
-//      rows; the block placement is the radix path's.
+//      rows; the block placement is the radix path's.  The order is assembled in
+//      LDS and written out in row order.
 constexpr int kCsKeys = 2048;
 template <int MAXR>
 __device__ void csort_rows(const BwdArgs& a) {
@@ -417,6 +427,8 @@ __device__ void csort_rows(const BwdArgs& a) {
   __shared__ int kinfo[kCsKeys];                  // 2 (first head or tail rank of the key) + is-head
   __shared__ int tbl[MAXR * 1024 / kBwdTokens + 1];  // tail rows before each block
   __shared__ int wsum[16];
+  __shared__ int pl[MAXR * 1024];  // the order, written out in one coalesced pass (stores
+                                   // from one workgroup to scattered places run ~1 ns each)
   const int N = (int)a.N, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nvt = (int)a.plan.nvt;
   const int S = (N + 15) >> 4;
@@ -486,31 +498,31 @@ __device__ void csort_rows(const BwdArgs& a) {
   const int nrb = (N + kBwdTokens - 1) / kBwdTokens;
   for (int b = tid; b <= nrb; b += 1024) tbl[b] = (int)((int64_t)min(b * kBwdTokens, N) * nT / N);
   __syncthreads();
-  auto tb = [&](int b) { return tbl[b]; };                              // tail rows before block b
-  auto hb = [&](int b) { return min(b * kBwdTokens, N) - tbl[b]; };   // head rows before block b
+  // A head rank r goes to the last block b with hb(b) <= r, a tail rank to the last
+  // with tb(b) <= r (tb(b) = tbl[b] tail rows and hb(b) = min(128 b, N) - tbl[b] head
+  // rows before block b, both non-decreasing from 0).  The search is binary lifting
+  // over fixed steps (nrb <= 8 MAXR) without branches, so that the rows' chains of
+  // LDS reads interleave; rows past N compute a place and store nothing.
+  static_assert(MAXR * 1024 / kBwdTokens <= 8 * MAXR, "the steps reach every block");
 #pragma unroll
   for (int j = 0; j < MAXR; ++j) {
-    if (!val[j]) continue;
     const int info = kinfo[key[j]];
     const int r = (info >> 1) + (int)cnt[wave * kCsKeys + key[j]] + rk[j];
-    int pos;
-    if (info & 1) {  // head rank r: the last block b with hb(b) <= r
-      int lo = 0, hi = nrb - 1;
-      while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (hb(mid) <= r) lo = mid; else hi = mid - 1;
-      }
-      pos = lo * kBwdTokens + (tb(lo + 1) - tb(lo)) + (r - hb(lo));
-    } else {  // tail rank r: the last block b with tb(b) <= r
-      int lo = 0, hi = nrb - 1;
-      while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (tb(mid) <= r) lo = mid; else hi = mid - 1;
-      }
-      pos = lo * kBwdTokens + (r - tb(lo));
+    const bool head = (info & 1) != 0;
+    int lo = 0;
+#pragma unroll
+    for (int step = 4 * MAXR; step >= 1; step >>= 1) {
+      const int c = lo + step;  // <= 8 MAXR - 1: inside tbl
+      const int t = tbl[min(c, nrb)];
+      const int f = head ? min(c * kBwdTokens, N) - t : t;
+      lo = c < nrb && f <= r ? c : lo;
     }
-    a.perm[pos] = wave * S + j * 64 + lane;
+    const int t0 = tbl[lo], t1 = tbl[lo + 1];
+    const int pos = lo * kBwdTokens + (head ? (t1 - t0) + r - (min(lo * kBwdTokens, N) - t0) : r - t0);
+    if (val[j]) pl[pos] = wave * S + j * 64 + lane;
   }
+  __syncthreads();
+  for (int i = tid; i < N; i += 1024) a.perm[i] = pl[i];
 }
 
 template <int MAXR>
@@ -709,6 +721,7 @@ __global__ __launch_bounds__(1024) void bwd_compact_kernel(BwdArgs a, int chunk)
   __syncthreads();
   for (int rb = tid; rb < nrb; rb += 1024) {
     int acc = 0;
+#pragma unroll 8
     for (int wl = 0; wl < cwd; ++wl) {
       pre[rb * cwd + wl] = acc;
       acc += __builtin_popcount(bm[rb * cwd + wl]);
@@ -723,6 +736,7 @@ __global__ __launch_bounds__(1024) void bwd_compact_kernel(BwdArgs a, int chunk)
     for (int v = v0; v < v1; ++v) {
       const int wl = v >> 5, bit = v & 31;
       int c = 0;
+#pragma unroll 16
       for (int rb = 0; rb < nrb; ++rb) c += (bm[rb * cwd + wl] >> bit) & 1u;
       vpre[v] = c;
       vs += c;
@@ -780,8 +794,10 @@ __global__ __launch_bounds__(1024) void bwd_compact_kernel(BwdArgs a, int chunk)
       for (int r = 0; r < 4; ++r) tr[r] += (c + r) / (r + 1);
     }
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-      if (tr[r] > 0) atomicAdd(&ntr[r], tr[r]);
+    for (int r = 0; r < 4; ++r) {
+      const int tw = wave_sum(tr[r]);
+      if ((tid & 63) == 0 && tw > 0) atomicAdd(&ntr[r], tw);
+    }
   }
   for (int i = I + tid; i <= maxp * nrb; i += 1024) a.rb_start[i] = kept;
   if (tid == 0 && I <= kRbsLds) rbs_l[I] = kept;
@@ -844,14 +860,26 @@ __global__ __launch_bounds__(1024) void bwd_compact_kernel(BwdArgs a, int chunk)
     gint* vt_slot = (gint*)a.vt_slot;
     gint* vt_start = (gint*)a.vt_start;
     constexpr int kVtWave = 8, kVtWaveTiles = 64;
+    const int lane = tid & 63, wv = tid >> 6;
+    const uint64_t below = (1ull << lane) - 1ull;
+    // the heavy tiles (more than kVtWave kept blocks), listed when they are few
     __shared__ int nheavy;
+    __shared__ int heavy[kVtWaveTiles];
     if (tid == 0) nheavy = 0;
     __syncthreads();
-    int h = 0;
-    for (int v = tid; v < nv; v += 1024) h += vpre[v + 1] - vpre[v] > kVtWave ? 1 : 0;
-    if (h) atomicAdd(&nheavy, h);
+    for (int vb = 0; vb < nv; vb += 1024) {
+      const int v = vb + tid;
+      const bool hv = v < nv && vpre[v + 1] - vpre[v] > kVtWave;
+      const uint64_t m = __ballot(hv);
+      int base = 0;
+      if (lane == 0 && m != 0ull) base = atomicAdd(&nheavy, __builtin_popcountll(m));
+      base = __shfl(base, 0);
+      const int k = base + __builtin_popcountll(m & below);
+      if (hv && k < kVtWaveTiles) heavy[k] = v;
+    }
     __syncthreads();
-    const int wave_min = nheavy <= kVtWaveTiles ? kVtWave : 0x7fffffff;  // kept blocks that make a wave's tile
+    const int nh = nheavy;
+    const int wave_min = nh <= kVtWaveTiles ? kVtWave : 0x7fffffff;  // kept blocks that make a wave's tile
     for (int v = tid; v < nv; v += 1024) {
       vt_start[v] = vpre[v];
       if (vpre[v + 1] - vpre[v] > wave_min) continue;
@@ -861,6 +889,7 @@ __global__ __launch_bounds__(1024) void bwd_compact_kernel(BwdArgs a, int chunk)
       for (int r0 = 0; r0 < nrb; r0 += 64) {  // the tile's column of the bitmap, 64 blocks at a time
         const int nr = min(64, nrb - r0);
         uint64_t col = 0;
+#pragma unroll 16
         for (int r = 0; r < nr; ++r) col |= (uint64_t)((bm[(r0 + r) * cwd + wl] >> bit) & 1u) << r;
         while (col) {
           const int rb = r0 + __builtin_ctzll(col);
@@ -870,10 +899,8 @@ __global__ __launch_bounds__(1024) void bwd_compact_kernel(BwdArgs a, int chunk)
         }
       }
     }
-    const int lane = tid & 63, wv = tid >> 6;
-    const uint64_t below = (1ull << lane) - 1ull;
-    for (int v = wv; v < nv; v += 16) {
-      if (vpre[v + 1] - vpre[v] <= wave_min) continue;
+    for (int i = wv; i < (nh <= kVtWaveTiles ? nh : 0); i += 16) {
+      const int v = heavy[i];
       const int p = pass_of(v);
       const int wl = v >> 5, bit = v & 31;
       int q = vpre[v];
@@ -1193,11 +1220,6 @@ constexpr int dc_steps_per_tile(bool split) {
   return kBwdVocab / (split ? 32 : 128 / (int)sizeof(T));
 }
 
-__device__ __forceinline__ int wave_sum(int v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
-  return v;
-}
 __device__ __forceinline__ int wave_min(int v) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) v = min(v, __shfl_xor(v, o));

@@ -44,12 +44,58 @@ def token_order(tt, d_nll, V, ignore_index=-100):
     return perm
 
 
+def lifting_search(r, f, nrb, maxr, top=None):
+    """The kernel's block search: binary lifting over the steps top = 4 MAXR, ..., 1
+    (every candidate c <= 8 MAXR - 1 reads the table at min(c, nrb))."""
+    lo, step = 0, 4 * maxr if top is None else top
+    while step >= 1:
+        c = lo + step
+        if c < nrb and f(min(c, nrb)) <= r:
+            lo = c
+        step >>= 1
+    return lo
+
+
+def bisection_search(r, f, nrb):
+    lo, hi = 0, nrb - 1
+    while lo < hi:
+        mid = (lo + hi + 1) >> 1
+        if f(mid) <= r:
+            lo = mid
+        else:
+            hi = mid - 1
+    return lo
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_block_search_lifting_equals_bisection(seed):
+    """For every non-decreasing table from 0 (the head and tail rows before each block)
+    and every rank, the lifting search finds the bisection's block; starting one step
+    short (2 MAXR) misses the last blocks once nrb > 4 MAXR."""
+    rng = np.random.default_rng(seed)
+    for maxr in (8, 16):
+        for nrb in (1, 2, 3, 31, 32, 33, 4 * maxr, 4 * maxr + 1, 8 * maxr - 1, 8 * maxr):
+            steps = rng.integers(0, 130, nrb + 1)
+            steps[0] = 0
+            tab = np.cumsum(steps)
+            f = lambda b: int(tab[b])
+            for r in range(0, int(tab[nrb]) + 2, max(1, int(tab[nrb]) // 300)):
+                assert lifting_search(r, f, nrb, maxr) == bisection_search(r, f, nrb)
+    tab = np.arange(0, 128 * 65, 128)  # 64 blocks of 128 rows
+    f = lambda b: int(tab[b])
+    r = int(tab[63]) + 5
+    assert bisection_search(r, f, 64) == 63
+    assert lifting_search(r, f, 64, 8) == 63
+    assert lifting_search(r, f, 64, 8, top=16) != 63  # the short-step mutant
+
+
 def csort_restated(tt, d_nll, V, ignore_index=-100, maxr=16, nkeys=2048, wave_prefix=True):
     """csort_rows: wave w holds rows [w S, (w+1) S), S = ceil(N / 16), 64 per round;
     per round a lane's rank is its wave's running count of its key plus the lower lanes
     with that key (the highest of them advances the 16-bit counter); per key the 16
     counters become a prefix over the waves; head / tail starts come from scans over
-    the keys; the block placement is a bisection over the per-block head / tail counts."""
+    the keys; the block placement searches the per-block head / tail counts by binary
+    lifting over the steps 4 MAXR, ..., 2, 1 (MAXR 8 up to N = 8192, else 16)."""
     N = len(tt)
     nvt = (V + BLOCK - 1) // BLOCK
     assert nvt < nkeys and N <= 1024 * maxr
@@ -87,15 +133,8 @@ def csort_restated(tt, d_nll, V, ignore_index=-100, maxr=16, nkeys=2048, wave_pr
     nT, nrb = N - nH, (N + BLOCK - 1) // BLOCK
     tbl = [min(b * BLOCK, N) * nT // N for b in range(nrb + 1)]
 
-    def last_block(r, before):  # the last block b with before(b) <= r
-        lo, hi = 0, nrb - 1
-        while lo < hi:
-            mid = (lo + hi + 1) >> 1
-            if before(mid) <= r:
-                lo = mid
-            else:
-                hi = mid - 1
-        return lo
+    def last_block(r, before):  # the last block b < nrb with before(b) <= r
+        return lifting_search(r, before, nrb, 8 if N <= 8192 else 16)
 
     perm = np.full(N, -1, dtype=np.int64)
     for row in range(N):
