@@ -849,6 +849,7 @@ __global__ __launch_bounds__(1024) void bwd_compact_kernel(BwdArgs a, int chunk)
       }
     }
   }
+  __shared__ int ntiles;  // the chunk's tiles that keep a pair
   // per vocab tile: its kept token blocks, ascending, as slots.  A tile with few kept
   // blocks takes one thread; when only a few tiles keep many (the tiles of popular
   // targets), each of those takes a wave, a lane per token block, so that no thread
@@ -865,12 +866,17 @@ __global__ __launch_bounds__(1024) void bwd_compact_kernel(BwdArgs a, int chunk)
     // the heavy tiles (more than kVtWave kept blocks), listed when they are few
     __shared__ int nheavy;
     __shared__ int heavy[kVtWaveTiles];
-    if (tid == 0) nheavy = 0;
+    if (tid == 0) {
+      nheavy = 0;
+      ntiles = 0;
+    }
     __syncthreads();
     for (int vb = 0; vb < nv; vb += 1024) {
       const int v = vb + tid;
       const bool hv = v < nv && vpre[v + 1] - vpre[v] > kVtWave;
       const uint64_t m = __ballot(hv);
+      const uint64_t mt = __ballot(v < nv && vpre[v + 1] > vpre[v]);
+      if (lane == 0 && mt != 0ull) atomicAdd(&ntiles, __builtin_popcountll(mt));
       int base = 0;
       if (lane == 0 && m != 0ull) base = atomicAdd(&nheavy, __builtin_popcountll(m));
       base = __shfl(base, 0);
@@ -915,15 +921,18 @@ __global__ __launch_bounds__(1024) void bwd_compact_kernel(BwdArgs a, int chunk)
   }
   if (tid == 0) a.vt_start[nv] = kept;
 
-  // G tasks: runs of at most R consecutive slots of one (pass, token block), ordered by
-  // pass, then run index, then token block.  Tasks that run at the same time then read
-  // the same vocabulary tiles when the lists are dense, and every block's first run
-  // (its lowest, most shared tiles) is taken early.  R is the shortest run (1 to 4)
-  // whose tasks all fit one round of the G kernel's persistent grid, else 4: a task
-  // streams only its own tiles' rows, and the task's time is the kernel's.  Item
-  // (p, k) -- run index k of pass p, k < ceil(most kept tiles of a block in the pass /
-  // R), at least one item per pass -- counts the blocks with more than k runs; the
-  // counts are scanned and every item writes its column.
+  // G tasks: runs of at most R consecutive slots of one (pass, token block).  When the
+  // tiles keep more than two blocks each on average, they are ordered by pass, then run
+  // index, then token block: tasks that run at the same time then read the same
+  // vocabulary tiles, and every block's first run (its lowest, most shared tiles) is
+  // taken early.  Otherwise (each tile read by few tasks) by pass, then token block,
+  // then run index: the tasks an XCD takes at once (a contiguous range) then share few
+  // token blocks, whose rows its L2 fetches once.  R is the shortest run (1 to 4) whose
+  // tasks all fit one round of the G kernel's persistent grid, else 4: a task streams
+  // only its own tiles' rows, and the task's time is the kernel's.  In the first order,
+  // item (p, k) -- run index k of pass p, k < ceil(most kept tiles of a block in the
+  // pass / R), at least one item per pass -- counts the blocks with more than k runs;
+  // the counts are scanned and every item writes its column.
   const int gwg = (a.num_cus > 0 ? a.num_cus + 7 : 256 + 7) / 8 * 8;  // the G kernel's grid
   const int R = ntr[0] <= gwg ? 1 : ntr[1] <= gwg ? 2 : ntr[2] <= gwg ? 3 : 4;
   {
@@ -956,7 +965,28 @@ __global__ __launch_bounds__(1024) void bwd_compact_kernel(BwdArgs a, int chunk)
     return lo;
   };
   int ntask;
-  {
+  if (kept <= 2 * ntiles) {
+    // (pass, token block) pairs in order, a contiguous run of them per thread, each
+    // listing its runs
+    const int per = (I + 1023) >> 10;
+    const int i0 = min(I, tid * per), i1 = min(I, i0 + per);
+    int cnt = 0;
+    for (int i = i0; i < i1; ++i) cnt += (rbs(i + 1) - rbs(i) + R - 1) / R;
+    int tb = block_excl_scan(cnt, wsum, ntask);
+    for (int i = i0; i < i1; ++i) {
+      const int p = i / nrb, rb = i - p * nrb;
+      if (rb == 0) {  // the pass's first pair: its tasks start here
+        a.pinfo[p * kPassInts + kPiTask0] = tb;
+        a.pinfo[p * kPassInts + kPiRun] = R;
+        if (p > 0) a.pinfo[(p - 1) * kPassInts + kPiTask1] = tb;
+      }
+      const int b0 = rbs(i), c = rbs(i + 1) - b0;
+      for (int k4 = 0; k4 < c; k4 += R, ++tb) {
+        a.g_task[tb] = b0 + k4;
+        a.g_task_rb[tb] = rb;
+      }
+    }
+  } else {
     // (item, token block) pairs in task order, a contiguous run of them per thread:
     // pair f = j nrb + rb holds a task when block rb keeps more than R k tiles in the
     // item's pass (k its run index).

@@ -11,7 +11,9 @@ row, an index past its array, two writers of one slot -- fails here, on the CPU:
 - the dC block tasks (the compaction's lists, `bwd_compact_kernel`, and the walk of the
   narrow dC sums, `bwd_sum_narrow_kernel`) against the set of one-tile owners and slices;
 - the 16-bit epilogue's transpose through LDS (`bwd_sum_narrow_kernel`): a bijection from
-  the MFMA register layout to whole 128-byte row pieces, free of LDS bank conflicts.
+  the MFMA register layout to whole 128-byte row pieces, free of LDS bank conflicts;
+- the G task lists (`bwd_compact_kernel`) in both orders, against the slots they must
+  cover: every kept pair once, in runs of at most R slots of one (pass, token block).
 """
 import numpy as np
 import pytest
@@ -283,3 +285,84 @@ def test_epilogue_transpose_is_a_conflict_free_bijection():
             addrs = [(8 * t + (l >> 3)) * 128 + (((l & 7) ^ (((8 * t + (l >> 3)) >> 1) & 7)) << 4)
                      for l in range(8 * g, 8 * g + 8)]
             assert len(groups(addrs)) == 8
+
+
+def g_tasks_restated(bits, cap, maxp, gwg, order=None):
+    """bwd_compact_kernel's slots and G tasks for one chunk: bits[rb, v] the kept pairs;
+    passes cut by the prefix P[v] of kept pairs per tile (tile v in pass P[v] // (cap -
+    nrb) when maxp > 1); slots by pass, block, tile; runs of R slots of one (pass, block),
+    R the shortest run whose tasks fit gwg, else 4; listed by (pass, run index, block)
+    when kept > 2 * (tiles keeping a pair), else by (pass, block, run index).  Returns
+    (rb_start, tasks as (first slot, block), per-pass [task0, task1), R, order)."""
+    nrb, nv = bits.shape
+    kept_v = bits.sum(0)
+    vpre = np.concatenate([[0], np.cumsum(kept_v)])
+    kept = int(vpre[nv])
+    cp = cap - nrb if maxp > 1 else 1 << 62
+    pass_of = vpre[:nv] // cp
+    npass = int(pass_of[nv - 1]) + 1
+    assert npass <= maxp
+    pcnt = np.zeros((npass, nrb), dtype=np.int64)
+    for p in range(npass):
+        pcnt[p] = bits[:, pass_of == p].sum(1)
+    rb_start = np.concatenate([[0], np.cumsum(pcnt.reshape(-1))])
+    ntr = [int(((pcnt + r) // (r + 1)).sum()) for r in range(4)]
+    R = 1 if ntr[0] <= gwg else 2 if ntr[1] <= gwg else 3 if ntr[2] <= gwg else 4
+    ntiles = int((kept_v > 0).sum())
+    if order is None:
+        order = "block" if kept <= 2 * ntiles else "run"
+    tasks, t0 = [], []
+    if order == "block":
+        for p in range(npass):
+            t0.append(len(tasks))
+            for rb in range(nrb):
+                i = p * nrb + rb
+                b0, c = int(rb_start[i]), int(rb_start[i + 1] - rb_start[i])
+                for k4 in range(0, c, R):
+                    tasks.append((b0 + k4, rb))
+    else:
+        for p in range(npass):
+            t0.append(len(tasks))
+            kmax = max(1, -(-int(pcnt[p].max()) // R))
+            for k in range(kmax):
+                for rb in range(nrb):
+                    i = p * nrb + rb
+                    b0, c = int(rb_start[i]), int(rb_start[i + 1] - rb_start[i])
+                    if c > R * k:
+                        tasks.append((b0 + R * k, rb))
+    ranges = [(t0[p], t0[p + 1] if p + 1 < npass else len(tasks)) for p in range(npass)]
+    return rb_start, tasks, ranges, R, order, npass
+
+
+@pytest.mark.parametrize("seed", range(30))
+def test_g_tasks_cover_every_kept_pair_once(seed):
+    """Both task orders: each task is a run of min(R, the rest of its block's slots in
+    the pass) slots inside one (pass, block); the runs of a pass's tasks cover exactly
+    the pass's slots; the orders list the same runs."""
+    rng = np.random.default_rng(seed)
+    nrb = int(rng.choice([1, 3, 32, 64]))
+    nv = int(rng.choice([1, 5, 33, 200, 1002]))
+    dens = float(rng.choice([0.01, 0.05, 0.2, 1.0]))
+    bits = rng.random((nrb, nv)) < dens
+    if seed % 5 == 0:  # one popular tile
+        bits[:, nv // 2] = True
+    if not bits.any():
+        bits[0, 0] = True
+    kept = int(bits.sum())
+    maxp = int(rng.choice([1, 2, 8]))
+    cap = max(2 * nrb, -(-kept // maxp) + nrb + 1) if maxp > 1 else kept
+    gwg = 256
+    runs = {}
+    for order in ("block", "run", None):
+        rb_start, tasks, ranges, R, got, npass = g_tasks_restated(bits, cap, maxp, gwg, order)
+        cover = np.zeros(kept, dtype=np.int64)
+        for p, (a0, a1) in enumerate(ranges):
+            for s0, rb in tasks[a0:a1]:
+                i = p * nrb + rb
+                lo, hi = int(rb_start[i]), int(rb_start[i + 1])
+                assert lo <= s0 < hi  # inside its own (pass, block)
+                cnt = min(R, hi - s0)  # the G kernel's count
+                cover[s0:s0 + cnt] += 1
+        assert (cover == 1).all()
+        runs[order] = sorted(tasks)
+    assert runs["block"] == runs["run"]
