@@ -1899,6 +1899,41 @@ struct SumGeo {
 // with the hi / lo pair) (the dC sums: many owners with one or two kept tiles, where
 // a deeper pipeline and shorter epilogues pay more than the wide slice's halved G
 // traffic).
+// 16-bit output of a 64-row x 128-column wave block straight from the MFMA
+// accumulators: lane (n, h) holds columns 8 q + 4 h + 0..3 of row n of each 32 x 32
+// block (i, jj); one lane swap between the halves per q pair gives it columns 16 pq +
+// 8 h + 0..7, stored as 16 bytes at rowoff[jj] + 2 (d0 + 32 i + 16 pq) (d0: the
+// block's first column + 8 h; columns past D and rows with a dropped offset store
+// nothing).
+template <typename T>
+__device__ __forceinline__ void store_direct16(const f32x16 (&acc)[4][2], const __amdgpu_buffer_rsrc_t rs,
+                                               const uint32_t (&rowoff)[2], int64_t d0, int64_t D) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      uint32_t pk[4][2];
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int k = 0; k < 2; ++k) pk[q][k] = pack2<T>(acc[i][jj][4 * q + 2 * k], acc[i][jj][4 * q + 2 * k + 1]);
+#pragma unroll
+      for (int pq = 0; pq < 2; ++pq) {
+        u32x4 v;
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+          const auto sw = __builtin_amdgcn_permlane32_swap(pk[2 * pq][k], pk[2 * pq + 1][k], false, false);
+          v[k] = sw[0];
+          v[2 + k] = sw[1];
+        }
+        const int64_t d = d0 + 32 * i + 16 * pq;
+        const uint32_t off = d < D ? rowoff[jj] + (uint32_t)(d * (int64_t)sizeof(T)) : 0x80000000u;
+        __builtin_amdgcn_raw_buffer_store_b128(v, rs, off, 0, 0);
+      }
+    }
+  }
+}
+
 template <typename T, bool SPLIT>
 struct SumGeoNarrow {
   static constexpr int NT = 256;
@@ -2748,32 +2783,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_narrow_kernel(BwdArgs a, 
           }
         }
       } else if constexpr (kDirect16) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-#pragma unroll
-          for (int jj = 0; jj < 2; ++jj) {
-            // lane (n, h) holds columns 8 q + 4 h + 0..3 of its row; one lane swap between
-            // the halves per q pair gives it columns 16 pq + 8 h + 0..7, stored as 16 bytes
-            uint32_t pk[4][2];
-#pragma unroll
-            for (int q = 0; q < 4; ++q)
-#pragma unroll
-              for (int k = 0; k < 2; ++k) pk[q][k] = pack2<T>(acc[i][jj][4 * q + 2 * k], acc[i][jj][4 * q + 2 * k + 1]);
-#pragma unroll
-            for (int pq = 0; pq < 2; ++pq) {
-              u32x4 v;
-#pragma unroll
-              for (int k = 0; k < 2; ++k) {
-                const auto sw = __builtin_amdgcn_permlane32_swap(pk[2 * pq][k], pk[2 * pq + 1][k], false, false);
-                v[k] = sw[0];
-                v[2 + k] = sw[1];
-              }
-              const int64_t d = d00 - h * 4 + 32 * i + 16 * pq + 8 * h;
-              const uint32_t off = d < D ? rowoff[jj] + (uint32_t)(d * ES) : 0x80000000u;
-              __builtin_amdgcn_raw_buffer_store_b128(v, rs, off, 0, 0);
-            }
-          }
-        }
+        store_direct16<T>(acc, rs, rowoff, d00 - h * 4 + 8 * h, D);
       } else {
         // 16-bit output through the wave's 4 KiB of LDS past the stages, one 32-row x
         // 64-column unit (jj, ip) at a time: lane (n, h) holds 16 bytes (8 columns) of
