@@ -208,6 +208,12 @@ int cce_backward(int dtype, const void* e, const void* c, const void* bias,
  * the G tiles of its one-tile owners are streamed through it.  This runs every owner
  * as its own task instead (the results are the same bit for bit). */
 #define CCE_BWD_DC_OWNER_TASKS 2048
+/* With the filter on and the kept tiles shared by three or more token blocks on
+ * average, the G kernel's tasks are a vocabulary tile with up to 4 of its kept blocks
+ * (the tile's C rows read once for them), not a token block with up to 4 of its kept
+ * tiles.  This keeps the token-block tasks (the G values can differ in the last bits:
+ * the contraction's slices are summed in another order). */
+#define CCE_BWD_G_TASKS_BY_BLOCK 4096
 
 /* As cce_backward, with flags (CCE_BWD_*) and vocabulary chunks of at most
  * max_chunk_tiles tiles (0: the library's choice; else a multiple of 32; the workspace

@@ -369,6 +369,7 @@ int backward_impl(int dtype, const void* e, const void* c, const void* bias, con
   a.g_split = es == 2 && !(flags & CCE_BWD_G_SINGLE) && ((flags & CCE_BWD_G_PAIR) || !(filter_log_eps > -INFINITY));
   // one-tile dC owners by token block: 16-bit inputs with G rounded once
   a.dc_blk = es == 2 && !a.g_split && dC != nullptr && P.nrb <= cce::kDcBlkMaxRb && !(flags & CCE_BWD_DC_OWNER_TASKS);
+  a.g_tiles_ok = (flags & CCE_BWD_G_TASKS_BY_BLOCK) ? 0 : 1;
   a.plan = P;
   a.num_cus = cus;
   if (q) {
@@ -405,7 +406,7 @@ int cce_backward_ex(int dtype, const void* e, const void* c, const void* bias, c
   constexpr int kKnown = CCE_BWD_DC_ZEROED | CCE_BWD_TOKENS_INPUT | CCE_BWD_TOKENS_SORTED | CCE_BWD_DE_SUMS_WIDE |
                          CCE_BWD_DE_SUMS_NARROW | CCE_BWD_DC_SUMS_WIDE | CCE_BWD_DC_SUMS_NARROW |
                          CCE_BWD_REF_STATS | CCE_BWD_DEVICE_PASSES | CCE_BWD_G_PAIR | CCE_BWD_G_SINGLE |
-                         CCE_BWD_DC_OWNER_TASKS;
+                         CCE_BWD_DC_OWNER_TASKS | CCE_BWD_G_TASKS_BY_BLOCK;
   if (flags & ~kKnown) return fail(CCE_ERR_INVALID_ARGUMENT, "[cce_backward] unknown flags 0x%x", flags);
   if ((flags & CCE_BWD_TOKENS_INPUT) && (flags & CCE_BWD_TOKENS_SORTED))
     return fail(CCE_ERR_INVALID_ARGUMENT, "[cce_backward] CCE_BWD_TOKENS_INPUT and CCE_BWD_TOKENS_SORTED exclude each other");
@@ -467,7 +468,7 @@ int cce_backward_noalloc(int dtype, const void* e, const void* c, const void* bi
   constexpr int kKnown = CCE_BWD_DC_ZEROED | CCE_BWD_TOKENS_INPUT | CCE_BWD_TOKENS_SORTED | CCE_BWD_DE_SUMS_WIDE |
                          CCE_BWD_DE_SUMS_NARROW | CCE_BWD_DC_SUMS_WIDE | CCE_BWD_DC_SUMS_NARROW |
                          CCE_BWD_REF_STATS | CCE_BWD_DEVICE_PASSES | CCE_BWD_G_PAIR | CCE_BWD_G_SINGLE |
-                         CCE_BWD_DC_OWNER_TASKS;
+                         CCE_BWD_DC_OWNER_TASKS | CCE_BWD_G_TASKS_BY_BLOCK;
   if (flags & ~kKnown)
     return fail(CCE_ERR_INVALID_ARGUMENT, "[cce_backward_noalloc] unknown flags 0x%x", flags);
   if (((flags & CCE_BWD_TOKENS_INPUT) && (flags & CCE_BWD_TOKENS_SORTED)) ||

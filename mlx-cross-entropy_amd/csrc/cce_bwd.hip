@@ -965,7 +965,29 @@ __global__ __launch_bounds__(1024) void bwd_compact_kernel(BwdArgs a, int chunk)
     return lo;
   };
   int ntask;
-  if (kept <= 2 * ntiles) {
+  // vocabulary-tile tasks: filtered, each tile kept by three or more blocks on average
+  const bool gvt = a.g_tiles_ok && a.filter_log_eps > -INFINITY && kept >= 3 * ntiles;
+  if (gvt) {
+    // per tile of the chunk (a contiguous run of tiles per thread), runs of up to 4 of
+    // its vt_slot entries (its kept blocks, ascending)
+    const int pv = (nv + 1023) >> 10;
+    const int v0 = min(nv, tid * pv), v1 = min(nv, v0 + pv);
+    int cnt = 0;
+    for (int v = v0; v < v1; ++v) cnt += (vpre[v + 1] - vpre[v] + 3) >> 2;
+    int tb = block_excl_scan(cnt, wsum, ntask);
+    for (int v = v0; v < v1; ++v) {
+      const int p = pass_of(v);
+      if (v == pvt[p]) {  // the pass's first tile: its tasks start here
+        a.pinfo[p * kPassInts + kPiTask0] = tb;
+        a.pinfo[p * kPassInts + kPiRun] = 4;
+        if (p > 0) a.pinfo[(p - 1) * kPassInts + kPiTask1] = tb;
+      }
+      for (int q = vpre[v]; q < vpre[v + 1]; q += 4, ++tb) {
+        a.g_task[tb] = q;
+        a.g_task_rb[tb] = v;
+      }
+    }
+  } else if (kept <= 2 * ntiles) {
     // (pass, token block) pairs in order, a contiguous run of them per thread, each
     // listing its runs
     const int per = (I + 1023) >> 10;
@@ -1128,6 +1150,7 @@ __global__ __launch_bounds__(1024) void bwd_compact_kernel(BwdArgs a, int chunk)
     int* pi = a.pinfo + p * kPassInts;
     pi[kPiTail] = 0;
     pi[kPiDcQueue] = 0;
+    pi[kPiGVt] = gvt ? 1 : 0;
     if (p < npass) {
       pi[kPiVt0] = pvt[p];
       pi[kPiVt1] = pvt[p + 1];
@@ -1390,6 +1413,8 @@ __device__ void dc_schedule(const BwdArgs& a, int pass, int nbins, int spt, char
 constexpr int kGSlice = CCE_G_SLICE, kGStages = CCE_G_STAGES;
 template <typename T>
 using GLoop = NTMainLoop<T, 4 * kBwdVocab, kBwdTokens, 4, 2, kGSlice, kGStages>;  // A = 4 x 128 C rows, B = 128 E rows
+template <typename T>  // vocabulary-tile tasks: A = 4 x 128 E rows, B = 128 C rows, MFMAs swapped
+using GTLoop = NTMainLoop<T, 4 * kBwdTokens, kBwdVocab, 8, 1, kGSlice, kGStages, true>;
 constexpr int kGThreads = GLoop<__bf16>::NTHREADS;
 
 // G of one wave's 128 x 64 block of a tile from its logits w: w[i][j][r] is the logit
@@ -1565,16 +1590,22 @@ __device__ __forceinline__ void g_block_epilogue(const BwdArgs& a, const RowData
   }
 }
 
-template <typename T, bool HAS_BIAS, bool WANT_G, bool WANT_DB, bool RAGGED>
-__global__ __launch_bounds__(kGThreads, 1) void bwd_g_kernel(BwdArgs a, int chunk, int pass) {
-  using Loop = GLoop<T>;
-  static_assert(Loop::NTHREADS == kGThreads, "one launch shape for every dtype");
-  constexpr int TI = Loop::TI, TJ = Loop::TJ;
-  static_assert(TI == 4 && TJ == 2, "wave tile: one vocab tile x 64 tokens");
-  __shared__ __attribute__((aligned(16))) char smem[Loop::SMEM_BYTES];
+// The G kernel's loop over its workgroup's tasks (t = its XCD-major number, then on
+// by the grid size).  VT false: a task is a token block with up to 4 kept tiles
+// (consecutive slots), A = the tiles' C rows, B = the block's E rows, and wave (wa,
+// wb) forms G of tile wa for tokens 64 wb ..; VT true: a task is a vocabulary tile
+// with up to 4 of its kept blocks (consecutive vt_slot entries), A = the blocks' E
+// rows, B = the tile's C rows, the MFMAs swapped so the accumulators hold the same
+// [vocabulary][token] block, and wave w forms G of block w / 2 for tokens 64 (w % 2)
+// ..: the tile's C rows are read once for its blocks.  Either way a wave's G block is
+// 128 columns x 64 tokens of one slot, formed by g_block_epilogue.
+template <typename T, bool HAS_BIAS, bool WANT_G, bool WANT_DB, bool RAGGED, bool VT>
+__device__ __forceinline__ void g_task_loop(const BwdArgs& a, int chunk, int pass, char* smem) {
+  using Loop = typename std::conditional<VT, GTLoop<T>, GLoop<T>>::type;
+  static_assert(Loop::NTHREADS == kGThreads, "one launch shape for every dtype and task kind");
+  static_assert(Loop::SMEM_BYTES == GLoop<T>::SMEM_BYTES, "one LDS size for both task kinds");
   constexpr int ES = sizeof(T);
   const int* pi = a.pinfo + pass * kPassInts;
-  if (ldu(pi, kPiDeMode) < 0) return;  // past the passes the data needs
   const int task0 = ldu(pi, kPiTask0);
   const int ntask = ldu(pi, kPiTask1) - task0;
   const int s0 = ldu(pi, kPiS0);  // the scratch holds slot s at s - s0
@@ -1583,15 +1614,14 @@ __global__ __launch_bounds__(kGThreads, 1) void bwd_g_kernel(BwdArgs a, int chun
   const int xcd = (int)(blockIdx.x & 7), lidx = (int)(blockIdx.x >> 3), nper = (int)(gridDim.x >> 3);
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int wa = wave & 3, wb = wave >> 2;
-  const int n = lane & 31;
-  const int h = lane >> 5;
   const int64_t pitch = a.D * (int64_t)ES;
-  const T* bias = reinterpret_cast<const T*>(a.bias);
   const RowData rd = row_data(a);
   const char* E = rd.e;
   const char* C = reinterpret_cast<const char*>(a.c);
+  (void)lane;
 
+  // VT false: s0 the first slot, rb the block, seg the tiles' first C rows; VT true:
+  // s0 the first vt_slot entry, rb the chunk-local tile, seg the blocks' first E rows
   struct Task {
     int s0, rb, cnt;
     int64_t seg[4];
@@ -1599,65 +1629,45 @@ __global__ __launch_bounds__(kGThreads, 1) void bwd_g_kernel(BwdArgs a, int chun
   auto load_task = [&](int t, Task& k) {
     k.s0 = ldu(a.g_task, task0 + t);
     k.rb = ldu(a.g_task_rb, task0 + t);
-    k.cnt = min(ldu(pi, kPiRun), ldu(rb_start, k.rb + 1) - k.s0);
+    if constexpr (VT) {
+      k.cnt = min(ldu(pi, kPiRun), ldu(a.vt_start, k.rb + 1) - k.s0);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) k.seg[i] = (int64_t)(vlo + ldu(a.slot_vt, k.s0 + (i < k.cnt ? i : k.cnt - 1))) * kBwdVocab;
+      for (int i = 0; i < 4; ++i)
+        k.seg[i] = (int64_t)ldu(a.slot_rb, ldu(a.vt_slot, k.s0 + (i < k.cnt ? i : k.cnt - 1))) * kBwdTokens;
+    } else {
+      k.cnt = min(ldu(pi, kPiRun), ldu(rb_start, k.rb + 1) - k.s0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        k.seg[i] = (int64_t)(vlo + ldu(a.slot_vt, k.s0 + (i < k.cnt ? i : k.cnt - 1))) * kBwdVocab;
+    }
   };
-  // the C rows of vocabulary tiles past the task's count are not loaded (their waves
-  // compute on stale bytes and store nothing)
-  static_assert(Loop::RPL * Loop::NW * 2 == kBwdVocab, "two load rounds per vocabulary tile");
+  // the rows of A segments past the task's count are not loaded (their waves compute
+  // on stale bytes and store nothing)
+  static_assert(Loop::RPL * Loop::NW * 2 == kBwdVocab && kBwdVocab == kBwdTokens, "two load rounds per A segment");
   static_assert(kGStages == 2, "skipped loads rely on the vmcnt(0) stage waits of two stages");
   auto sources = [&](const Task& k) {
-    auto src = Loop::template make_src<kBwdVocab>(C, a.V, k.seg, E, a.N, (int64_t)k.rb * kBwdTokens, pitch, pitch, xcd);
+    auto src = VT ? Loop::template make_src<kBwdTokens>(E, a.N, k.seg, C, a.V, (int64_t)(vlo + k.rb) * kBwdVocab,
+                                                         pitch, pitch, xcd)
+                  : Loop::template make_src<kBwdVocab>(C, a.V, k.seg, E, a.N, (int64_t)k.rb * kBwdTokens, pitch,
+                                                       pitch, xcd);
     src.skip = (0xffu << (2 * k.cnt)) & 0xffu;
     return src;
   };
   auto prefetch = [&](const typename Loop::template Src<4>& src) { Loop::template prefetch<RAGGED>(src, smem); };
 
-  // Once out of tasks, the workgroup takes items from the pass's counter, which the
-  // compaction kernel reset (only when dE or dC is wanted): first the dC schedule
-  // (when dC is wanted), then the owners without kept tiles in the pass, whose rows it
-  // zeroes or finishes (dC rows only when dC did not come zeroed).
-  auto tail = [&]() {
-    if constexpr (WANT_G) {
-      const int sched = a.dC != nullptr ? 1 : 0;
-      // dC rows of vocab tiles without kept tiles need zeros unless dC came zeroed
-      const int nitems = sched + (int)a.plan.nrb + (a.dc_zeroed ? 0 : ldu(pi, kPiVt1) - ldu(pi, kPiVt0));
-      int* box = reinterpret_cast<int*>(smem);
-      for (;;) {
-        __syncthreads();  // box (and smem) free
-        if (threadIdx.x == 0) box[0] = atomicAdd(&a.pinfo[pass * kPassInts + kPiTail], 1);
-        __syncthreads();
-        const int o = box[0];
-        if (o >= nitems) break;
-        if (o < sched) {
-          const int nds = (int)((a.D + kDcSliceCols - 1) / kDcSliceCols);
-          const int nb = dc_bins((int)gridDim.x, nds);
-          dc_schedule<kGThreads>(a, pass, nb > 0 ? nb : 1, dc_steps_per_tile<T>(a.g_split != 0),
-                                 smem + 256);  // its tables start past box
-        } else {
-          empty_owner<T, kGThreads>(a, chunk, pass, o - sched);
-        }
-      }
-    }
-  };
-
   int t = xcd * nper + lidx;  // logical task of this workgroup; advances by the grid size
-  if (t >= ntask) {
-    tail();
-    return;
-  }
+  if (t >= ntask) return;
   Task cur;
   load_task(t, cur);
   auto src = sources(cur);
   prefetch(src);
 
   for (;;) {
-    f32x16 w[TI][TJ];
+    f32x16 w[4][2];
 #pragma unroll
-    for (int i = 0; i < TI; ++i)
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int j = 0; j < TJ; ++j) w[i][j] = zero16();
+      for (int j = 0; j < 2; ++j) w[i][j] = zero16();
     Loop::template consume<RAGGED>(src, smem, w);
 
     const int tn = t + (int)gridDim.x;
@@ -1668,30 +1678,31 @@ __global__ __launch_bounds__(kGThreads, 1) void bwd_g_kernel(BwdArgs a, int chun
       prefetch(src);  // all stages but the last; the epilogue below uses the last one's bytes
     }
 
-    // w[i][j][r]: vocab v0 + 32 i + 8 (r/4) + 4 h + r%4, token t0 + 64 wb + 32 j + n.
-    // Per token: g (0 for masked / out-of-range rows), lz = lse log2(e), or +inf
-    // when g == 0 so that p = 0 and G = 0 without a select, and the target's place
-    // in the tile as tl - 4 h, which register (i, r) holds iff it equals
-    // 32 i + 8 (r/4) + r%4 (a compile-time constant).
-    const bool active = wa < cur.cnt;  // uniform per wave
-    const int slot = cur.s0 + wa;
-    int64_t v0 = cur.seg[0];
+    // This wave's G block: A segment (tile or block) ia of the task, token half ih.
+    const int ia = VT ? wave >> 1 : wave & 3, ih = VT ? wave & 1 : wave >> 2;
+    const bool active = ia < cur.cnt;  // uniform per wave
+    int64_t sg = cur.seg[0];
 #pragma unroll
-    for (int k = 1; k < 4; ++k) v0 = wa == k ? cur.seg[k] : v0;
-    const int64_t t0 = (int64_t)cur.rb * kBwdTokens;
-    float* red = reinterpret_cast<float*>(smem + (Loop::SMEM_BYTES - Loop::STAGE_BYTES));  // [2 wb][4 wa][128] column sums
+    for (int k = 1; k < 4; ++k) sg = ia == k ? cur.seg[k] : sg;
+    const int slot = VT ? (active ? ldu(a.vt_slot, cur.s0 + ia) : s0) : cur.s0 + ia;
+    const int64_t v0 = VT ? (int64_t)(vlo + cur.rb) * kBwdVocab : sg;
+    const int64_t t0 = VT ? sg : (int64_t)cur.rb * kBwdTokens;
+    float* red = reinterpret_cast<float*>(smem + (Loop::SMEM_BYTES - Loop::STAGE_BYTES));  // [8 waves][128] column sums
     static_assert(8 * kBwdVocab * sizeof(float) <= Loop::STAGE_BYTES, "column sums fit one stage");
+    // red: the two token halves of segment ia at red[(2 ia + ih) 128] (VT) or red[(4 ih + ia) 128]
+    const int rw = VT ? 2 * ia + ih : 4 * ih + ia;
     if (active)
-      g_block_epilogue<T, HAS_BIAS, WANT_G, WANT_DB>(a, rd, w, v0, t0 + 64 * wb, 64 * wb,
+      g_block_epilogue<T, HAS_BIAS, WANT_G, WANT_DB>(a, rd, w, v0, t0 + 64 * ih, 64 * ih,
                                                      a.gtile + (size_t)(slot - s0) * a.plan.g_bytes,
-                                                     red + (wb * 4 + wa) * kBwdVocab);
+                                                     red + rw * kBwdVocab);
     if constexpr (WANT_DB) {
       // the two token halves' column sums meet in LDS (the last stage, which no DMA
       // fills until the next task's main loop has passed its first barrier)
       __syncthreads();
-      if (active && wb == 0) {
+      if (active && ih == 0) {
         float* cs = a.colsum + (size_t)(slot - s0) * kBwdVocab;
-        for (int c = lane; c < kBwdVocab; c += 64) cs[c] = red[wa * kBwdVocab + c] + red[(4 + wa) * kBwdVocab + c];
+        const int r0 = VT ? 2 * ia : ia, r1 = VT ? 2 * ia + 1 : 4 + ia;
+        for (int c = lane; c < kBwdVocab; c += 64) cs[c] = red[r0 * kBwdVocab + c] + red[r1 * kBwdVocab + c];
       }
       __syncthreads();
     }
@@ -1699,7 +1710,43 @@ __global__ __launch_bounds__(kGThreads, 1) void bwd_g_kernel(BwdArgs a, int chun
     t = tn;
     cur = nxt;
   }
-  tail();
+}
+
+template <typename T, bool HAS_BIAS, bool WANT_G, bool WANT_DB, bool RAGGED>
+__global__ __launch_bounds__(kGThreads, 1) void bwd_g_kernel(BwdArgs a, int chunk, int pass) {
+  __shared__ __attribute__((aligned(16))) char smem[GLoop<T>::SMEM_BYTES];
+  const int* pi = a.pinfo + pass * kPassInts;
+  if (ldu(pi, kPiDeMode) < 0) return;  // past the passes the data needs
+  if (ldu(pi, kPiGVt))
+    g_task_loop<T, HAS_BIAS, WANT_G, WANT_DB, RAGGED, true>(a, chunk, pass, smem);
+  else
+    g_task_loop<T, HAS_BIAS, WANT_G, WANT_DB, RAGGED, false>(a, chunk, pass, smem);
+
+  // Once out of tasks, the workgroup takes items from the pass's counter, which the
+  // compaction kernel reset (only when dE or dC is wanted): first the dC schedule
+  // (when dC is wanted), then the owners without kept tiles in the pass, whose rows it
+  // zeroes or finishes (dC rows only when dC did not come zeroed).
+  if constexpr (WANT_G) {
+    const int sched = a.dC != nullptr ? 1 : 0;
+    // dC rows of vocab tiles without kept tiles need zeros unless dC came zeroed
+    const int nitems = sched + (int)a.plan.nrb + (a.dc_zeroed ? 0 : ldu(pi, kPiVt1) - ldu(pi, kPiVt0));
+    int* box = reinterpret_cast<int*>(smem);
+    for (;;) {
+      __syncthreads();  // box (and smem) free
+      if (threadIdx.x == 0) box[0] = atomicAdd(&a.pinfo[pass * kPassInts + kPiTail], 1);
+      __syncthreads();
+      const int o = box[0];
+      if (o >= nitems) break;
+      if (o < sched) {
+        const int nds = (int)((a.D + kDcSliceCols - 1) / kDcSliceCols);
+        const int nb = dc_bins((int)gridDim.x, nds);
+        dc_schedule<kGThreads>(a, pass, nb > 0 ? nb : 1, dc_steps_per_tile<T>(a.g_split != 0),
+                               smem + 256);  // its tables start past box
+      } else {
+        empty_owner<T, kGThreads>(a, chunk, pass, o - sched);
+      }
+    }
+  }
 }
 
 // ---------------------------------------------------------------- 4b. G tiles, filter off

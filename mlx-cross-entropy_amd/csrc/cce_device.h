@@ -201,7 +201,11 @@ __device__ __forceinline__ void stage_barrier() {
 // pipeline fill and consume() runs the contraction; run() / run_gather() do all
 // three.  The phase rotation of the slices (make_src) measured 5% faster in the
 // forward than all XCDs streaming the same slice.
-template <typename T, int ROWS_A, int ROWS_B, int WA, int WB, int SLICE = kSliceBytes, int STAGES = kStages>
+//
+// SWAP: the MFMAs take the B fragment as their first operand, so acc holds the block
+// transposed: acc[TJ][TI], rows of B by columns of A (same reads, same products).
+template <typename T, int ROWS_A, int ROWS_B, int WA, int WB, int SLICE = kSliceBytes, int STAGES = kStages,
+          bool SWAP = false>
 struct NTMainLoop {
   static constexpr int kChunks = SLICE / 16;
   static constexpr int TI = ROWS_A / WA / 32;
@@ -214,6 +218,7 @@ struct NTMainLoop {
   static constexpr int KSTEPS = SLICE / 32;                // 32-byte MFMA steps per slice
   static constexpr uint32_t STAGE_BYTES = ROWS * SLICE;
   static constexpr uint32_t SMEM_BYTES = STAGES * STAGE_BYTES;
+  using Acc = f32x16[SWAP ? TJ : TI][SWAP ? TI : TJ];
   static_assert(LPW * RPL * NW == ROWS, "stage must split evenly over the waves");
   static_assert(ROWS_A % 32 == 0 && ROWS_B % 32 == 0, "rows must be multiples of 32");
   static_assert((STAGES - 1) * LPW < 64, "in-flight loads must fit vmcnt");
@@ -344,7 +349,7 @@ struct NTMainLoop {
     __device__ void operator()() const {}
   };
   template <bool RAGGED, int NSEG, typename Hook = NoHook, int FIRST_STORES = 0>
-  static __device__ __forceinline__ void consume(const Src<NSEG>& src, char* smem, f32x16 (&acc)[TI][TJ],
+  static __device__ __forceinline__ void consume(const Src<NSEG>& src, char* smem, Acc& acc,
                                                  Hook hook = Hook(), bool stores_pending = false) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -364,7 +369,12 @@ struct NTMainLoop {
 #pragma unroll
       for (int ti = 0; ti < TI; ++ti)
 #pragma unroll
-        for (int tj = 0; tj < TJ; ++tj) acc[ti][tj] = Traits<T>::mfma(af[ti], bf[tj], acc[ti][tj]);
+        for (int tj = 0; tj < TJ; ++tj) {
+          if constexpr (SWAP)
+            acc[tj][ti] = Traits<T>::mfma(bf[tj], af[ti], acc[tj][ti]);
+          else
+            acc[ti][tj] = Traits<T>::mfma(af[ti], bf[tj], acc[ti][tj]);
+        }
     };
     static_assert(KSTEPS % 2 == 0, "fragments alternate between two register sets");
     constexpr int MF = TI * TJ * Traits<T>::kInstrPerStep;
@@ -419,7 +429,7 @@ struct NTMainLoop {
   static __device__ __forceinline__ void run(const char* __restrict__ A, int64_t a_rows, int64_t a_row0,
                                              const char* __restrict__ B, int64_t b_rows, int64_t b_row0,
                                              int64_t pitch, int64_t kbytes, char* smem,
-                                             f32x16 (&acc)[TI][TJ], int phase8 = 0) {
+                                             Acc& acc, int phase8 = 0) {
     const int64_t seg[1] = {a_row0};
     run_gather<ROWS_A>(A, a_rows, seg, B, b_rows, b_row0, pitch, kbytes, smem, acc, phase8);
   }
@@ -430,7 +440,7 @@ struct NTMainLoop {
                                                     const int64_t (&a_seg0)[ROWS_A / A_SEG],
                                                     const char* __restrict__ B, int64_t b_rows, int64_t b_row0,
                                                     int64_t pitch, int64_t kbytes, char* smem,
-                                                    f32x16 (&acc)[TI][TJ], int phase8 = 0) {
+                                                    Acc& acc, int phase8 = 0) {
     const auto src = make_src<A_SEG>(A, a_rows, a_seg0, B, b_rows, b_row0, pitch, kbytes, phase8);
     if (kbytes % SLICE == 0) {
       prefetch<false>(src, smem);

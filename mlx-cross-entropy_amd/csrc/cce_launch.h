@@ -131,6 +131,7 @@ enum PassField {
   kPiDcBlk = 12,   // dC block tasks per D slice: dc_blk_task[vt0 + i], i < this count
   kPiDcQueue = 13, // dC block tasks: counter of the tasks taken (zeroed by the compaction)
   kPiDcDeal = 14,  // dC owners dealt to the schedule's bins: own_vt[vt0 + i], i < this count (the rest: block tasks)
+  kPiGVt = 15,     // 1: G tasks are runs of a vocabulary tile's vt_slot entries (g_task: the first, g_task_rb: the tile)
 };
 // dE write mode of a pass: one pass over everything writes dE directly; with more
 // passes (or chunks) dE is summed in an fp32 carry: the first pass stores it, the
@@ -357,6 +358,7 @@ struct BwdArgs {
   int g_scaled;         // fp16: G tiles hold G * 2^counts[kGScaleExp] (else unscaled)
   int g_split;          // 16-bit: G tiles hold the hi / lo pair (else G rounded once)
   int dc_blk;           // the narrow dC sums run owners with one kept tile as tasks per (token block, D slice)
+  int g_tiles_ok;       // the compaction may list G tasks by vocabulary tile
   // Pinned host memory of 1 + max_passes ints, or null.  The compaction writes the
   // chunk's pass count to [0] and each pass's kPiDcWide to [1 + p]; the host then
   // launches only those passes and only the dC geometry picked (launch_backward's

@@ -1049,6 +1049,50 @@ def test_backward_captured_in_a_graph(m, cuda, filtered):
             assert torch.equal(x.view(torch.int16), y.view(torch.int16)), rep
 
 
+@pytest.mark.parametrize("case", ["plain", "ragged_bias", "passes"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_g_tile_tasks_match_block_tasks(m, cuda, case, dtype):
+    """Uniform targets over 1002 vocabulary tiles with c2's logit spread keep each tile
+    for ~6 token blocks, so the G kernel takes a tile with up to 4 of its blocks per
+    task (the tile's C rows read once).  dE / dC / dBias agree with the token-block
+    tasks (CCE_BWD_G_TASKS_BY_BLOCK) to the rounding of reordered fp32 sums and repeat
+    bit for bit.  Cases: aligned shapes; ragged N, V and D with a bias (the column sums
+    of dBias); several passes of a small G scratch."""
+    N, D, V = (4096, 512, 128256) if case != "ragged_bias" else (4000, 520, 128000 - 77)
+    e, c, t = normal_case(N, D, V, dtype, cuda, seed=41, std=0.04)
+    t[9] = -100
+    gb = torch.Generator(device=cuda).manual_seed(3)
+    b = (torch.randn(V, generator=gb, device=cuda) * 0.1).to(dtype) if case == "ragged_bias" else None
+    lse_tm = m._ext.forward(e, c, t, b, -100)
+    tm, lse = lse_tm[0], lse_tm[3]
+    d_nll = torch.linspace(0.5, 1.5, N, device=cuda) / N
+    stats = torch.zeros(3, dtype=torch.int64, device=cuda)
+    opts = {"max_g_tiles": 2048} if case == "passes" else {}
+    want_db = b is not None
+    run_bwd = lambda: m._ext.backward(e, c, t, lse, tm, d_nll, b, -100, m.FILTER_LOG_EPS, True, True, want_db,
+                                      tile_stats=stats)
+    with m._ext.backward_options(**opts):
+        g1 = run_bwd()
+        g2 = run_bwd()
+    with m._ext.backward_options(g_tasks="blocks", **opts):
+        gb_ = run_bwd()
+    torch.cuda.synchronize()
+    kept = int(stats[0])
+    ntiles = (V + 127) // 128
+    print(f"{case} {dtype}: kept tiles {kept} over {ntiles} vocabulary tiles")
+    assert kept >= 3 * ntiles  # the tile tasks' condition
+    bits = torch.int32 if dtype == torch.float32 else torch.int16
+    tol = 1e-5 if dtype == torch.float32 else 2e-3
+    for x, y, z, name in zip(g1, g2, gb_, ("dE", "dC", "dBias")):
+        if x is None:
+            continue
+        assert torch.equal(x.view(bits), y.view(bits)), name
+        err = O.rel_fro(f64(x), f64(z))
+        print(f"  {name}: tile tasks vs block tasks {err:.2e}")
+        assert err < tol, (name, err)
+        assert float(x.float().abs().sum()) > 0
+
+
 @pytest.mark.parametrize("case", ["peaked", "uniform", "passes"])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_dc_block_tasks_match_owner_tasks(m, cuda, case, dtype):

@@ -12,8 +12,9 @@ row, an index past its array, two writers of one slot -- fails here, on the CPU:
   narrow dC sums, `bwd_sum_narrow_kernel`) against the set of one-tile owners and slices;
 - the 16-bit epilogue's transpose through LDS (`bwd_sum_narrow_kernel`): a bijection from
   the MFMA register layout to whole 128-byte row pieces, free of LDS bank conflicts;
-- the G task lists (`bwd_compact_kernel`) in both orders, against the slots they must
-  cover: every kept pair once, in runs of at most R slots of one (pass, token block).
+- the G task lists (`bwd_compact_kernel`) in their three kinds, against the slots they
+  must cover: every kept pair once, in runs of at most R slots of one (pass, token block),
+  or of at most 4 vt_slot entries of one vocabulary tile.
 """
 import numpy as np
 import pytest
@@ -366,3 +367,70 @@ def test_g_tasks_cover_every_kept_pair_once(seed):
         assert (cover == 1).all()
         runs[order] = sorted(tasks)
     assert runs["block"] == runs["run"]
+
+
+def g_tile_tasks_restated(bits, cap, maxp):
+    """bwd_compact_kernel's vocabulary-tile G tasks: per tile (in order), runs of up to 4
+    of its vt_slot entries (its kept blocks ascending, as slots); the pass's tasks start
+    at its first tile.  Returns (vt_slot, vt_start, slot_rb, tasks (q, tile),
+    per-pass [task0, task1), rb_start)."""
+    nrb, nv = bits.shape
+    kept_v = bits.sum(0)
+    vpre = np.concatenate([[0], np.cumsum(kept_v)])
+    cp = cap - nrb if maxp > 1 else 1 << 62
+    pass_of = vpre[:nv] // cp
+    npass = int(pass_of[nv - 1]) + 1
+    # slots by (pass, block, tile)
+    slot_of, slot_rb, s = {}, [], 0
+    rb_start = []
+    for p in range(npass):
+        for rb in range(nrb):
+            rb_start.append(s)
+            for v in range(nv):
+                if pass_of[v] == p and bits[rb, v]:
+                    slot_of[(rb, v)] = s
+                    slot_rb.append(rb)
+                    s += 1
+    rb_start.append(s)
+    vt_slot = [slot_of[(rb, v)] for v in range(nv) for rb in range(nrb) if bits[rb, v]]
+    tasks, t0 = [], {}
+    for v in range(nv):
+        p = int(pass_of[v])
+        if p not in t0:
+            t0[p] = len(tasks)
+        for q in range(int(vpre[v]), int(vpre[v + 1]), 4):
+            tasks.append((q, v))
+    ranges = [(t0[p], t0[p + 1] if p + 1 < npass else len(tasks)) for p in range(npass)]
+    return vt_slot, vpre, slot_rb, tasks, ranges, rb_start, npass
+
+
+@pytest.mark.parametrize("seed", range(30))
+def test_g_tile_tasks_cover_every_kept_pair_once(seed):
+    """The G kernel's tile tasks: task (q, v) takes cnt = min(4, vt_start[v + 1] - q)
+    entries, all of tile v, each a slot of the task's pass whose block is slot_rb of it;
+    a pass's tasks cover exactly its slots (every kept pair's G tile is formed once)."""
+    rng = np.random.default_rng(seed)
+    nrb = int(rng.choice([1, 3, 32, 64]))
+    nv = int(rng.choice([1, 5, 33, 200]))
+    bits = rng.random((nrb, nv)) < float(rng.choice([0.05, 0.2, 0.6, 1.0]))
+    if not bits.any():
+        bits[0, 0] = True
+    kept = int(bits.sum())
+    maxp = int(rng.choice([1, 2, 8]))
+    cap = max(2 * nrb, -(-kept // maxp) + nrb + 1) if maxp > 1 else kept
+    vt_slot, vt_start, slot_rb, tasks, ranges, rb_start, npass = g_tile_tasks_restated(bits, cap, maxp)
+    cover = np.zeros(kept, dtype=np.int64)
+    for p, (a0, a1) in enumerate(ranges):
+        s_lo, s_hi = rb_start[p * nrb], rb_start[(p + 1) * nrb]
+        for q, v in tasks[a0:a1]:
+            cnt = min(4, int(vt_start[v + 1]) - q)
+            assert cnt >= 1
+            for i in range(cnt):
+                sl = vt_slot[q + i]
+                assert s_lo <= sl < s_hi  # the pass's G scratch
+                assert bits[slot_rb[sl], v]  # a kept pair of this tile
+                cover[sl] += 1
+            # the segments of the task's loads: the blocks of its first cnt entries
+            blocks = [slot_rb[vt_slot[q + min(i, cnt - 1)]] for i in range(4)]
+            assert blocks[:cnt] == sorted(blocks[:cnt])
+    assert (cover == 1).all()
