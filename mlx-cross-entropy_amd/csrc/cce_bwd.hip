@@ -33,10 +33,11 @@
 //                          zeros (and the fp32 dE carry is started / finished);
 //                          done by the G kernel's workgroups once out of tasks,
 //                          after the first of them deals the dC schedule.
-//   4. bwd_g_kernel        per task (one token block, up to 4 of its kept vocab
-//                          tiles): recompute the 512 x 128 logits on MFMA, form G,
-//                          store each 128 x 128 G tile token-major in the input
-//                          dtype, plus fp32 column sums for dBias.
+//   4. bwd_g_kernel        per task (one token block with up to 4 of its kept vocab
+//                          tiles, or one vocab tile with up to 4 of its kept blocks):
+//                          recompute the 512 x 128 logits on MFMA, form G, store
+//                          each 128 x 128 G tile token-major in the input dtype, plus
+//                          fp32 column sums for dBias.
 //   5. bwd_sum_kernel<0>   dE = sum over a token block's kept tiles of G_j . C_j;
 //      (or the narrow      written to the dE rows of the block (through the sorted
 //      geometry)           order's permutation when it is used);
@@ -626,7 +627,8 @@ __device__ __forceinline__ int order_by_size(int n, F size, int* out, int base, 
 // by pass, then token block, then vocab tile: slot(rb, v) = first slot of (pass,
 // rb) + the kept tiles of row rb in the pass before v.  Per vocab tile the kept token
 // blocks are listed in vt_slot (ascending), the G tasks cut every (pass, token block)
-// run of slots into runs of at most 4, and per pass the owners of the dE and dC sums
+// run of slots, or every tile's vt_slot run, into runs of at most 4, and per pass the
+// owners of the dE and dC sums
 // (token blocks, vocab tiles) that hold kept tiles are listed by descending tile
 // count.  The pass table gets every pass's ranges, counts and dE write mode; passes
 // past the last one the data needs are marked empty.  The token blocks are those of
@@ -921,7 +923,10 @@ __global__ __launch_bounds__(1024) void bwd_compact_kernel(BwdArgs a, int chunk)
   }
   if (tid == 0) a.vt_start[nv] = kept;
 
-  // G tasks: runs of at most R consecutive slots of one (pass, token block).  When the
+  // G tasks.  With the filter on and the tiles keeping three or more blocks each on
+  // average: runs of up to 4 of one vocabulary tile's vt_slot entries, tiles in order
+  // (the G kernel then reads the tile's C rows once for its blocks; below).  Otherwise
+  // runs of at most R consecutive slots of one (pass, token block).  When the
   // tiles keep more than two blocks each on average, they are ordered by pass, then run
   // index, then token block: tasks that run at the same time then read the same
   // vocabulary tiles, and every block's first run (its lowest, most shared tiles) is
