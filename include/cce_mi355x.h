@@ -123,8 +123,10 @@ int cce_forward_ref(int dtype, const void* e, const void* c, const void* bias,
 /*
  * Bytes of the default device workspace of cce_backward for these sizes and outputs.
  * The backward holds the G tiles of the kept (128-row, 128-column) pairs in passes of
- * a bounded size (a 512 MiB budget of G tiles by default, at least 2 tiles per 128-row
- * block): the workspace is O(budget + N*D + V), never O(N*V).  Reference interface
+ * a bounded size (8192 tiles by default, at least 2 tiles per 128-row block; a tile
+ * takes 64 KiB, 512 MiB in all): the workspace is O(budget + N*D + V), never O(N*V).
+ * The size is enough for every filter and flag; cce_backward_workspace_size_flags
+ * gives the smaller one of a 16-bit backward with the filter on.  Reference interface
  * replaced: the output-sized accumulators of cce.cpp:315-340 (zero_alloc dE / dC).
  */
 size_t cce_backward_workspace_size(int dtype, int64_t N, int64_t D, int64_t V,
@@ -136,11 +138,25 @@ size_t cce_backward_workspace_size(int dtype, int64_t N, int64_t D, int64_t V,
  * above the default are lowered to it) and vocabulary chunks of at most
  * max_chunk_tiles 128-column tiles (0: the library's choice; else a multiple of 32).
  * A cce_backward_ex given a workspace of this size and the same max_chunk_tiles runs
- * exactly these passes.  Same reference interface as above.
+ * exactly these passes when its G tiles take 64 KiB (fp32, or the filter off), larger
+ * ones when they take 32 KiB.  Same reference interface as above.
  */
 size_t cce_backward_workspace_size_ex(int dtype, int64_t N, int64_t D, int64_t V,
                                       int want_dE, int want_dC, int want_dBias, int64_t max_g_tiles,
                                       int64_t max_chunk_tiles);
+
+/*
+ * As cce_backward_workspace_size_ex, for a cce_backward_ex with this filter_log_eps
+ * and these flags.  They fix the G tiles' layout: 16-bit G rounded once (the filter
+ * on, or CCE_BWD_G_SINGLE) takes 32 KiB a tile instead of the hi / lo pair's 64 KiB,
+ * so the same passes need half the G bytes (256 MiB by default).  A cce_backward_ex
+ * given a workspace of this size and the same filter_log_eps, flags and
+ * max_chunk_tiles runs exactly these passes.  0 for a NaN filter_log_eps or invalid
+ * flags.  Same reference interface as above.
+ */
+size_t cce_backward_workspace_size_flags(int dtype, int64_t N, int64_t D, int64_t V,
+                                         int want_dE, int want_dC, int want_dBias, int64_t max_g_tiles,
+                                         int64_t max_chunk_tiles, float filter_log_eps, int flags);
 
 /*
  * Backward pass.  Replaces cce_backward_raw (csrc/bindings.cpp:71-86, cce.cpp:152-179),
@@ -158,9 +174,11 @@ size_t cce_backward_workspace_size_ex(int dtype, int64_t N, int64_t D, int64_t V
  * once (dE through an fp32 carry in the workspace when the kept tiles take more than
  * one pass).  Every output element is written, so the outputs need no zero-fill.
  * Rows of dE/dC/dBias that no kept tile touches are 0.
- * The plan depends only on the sizes, the outputs asked for and workspace_bytes: the
- * default plan when the workspace holds cce_backward_workspace_size() bytes, else
- * smaller passes (CCE_ERR_WORKSPACE below the least size).
+ * The plan depends only on the sizes, the outputs asked for, the G tiles' layout
+ * (filter_log_eps and the G flags) and workspace_bytes: the default plan when the
+ * workspace holds cce_backward_workspace_size_flags() bytes (which
+ * cce_backward_workspace_size() always covers), else smaller passes
+ * (CCE_ERR_WORKSPACE below the least size).
  * The workspace must stay untouched until the backward's work on the stream ends.
  * tile_stats (nullable, device int64[3]) receives {kept tiles, total tiles, kept tiles
  * of the input-order token blocks}.  The backward may form its 128-row token blocks

@@ -36,6 +36,28 @@ int fail(int code, const char* fmt, ...) {
 
 size_t elem_size(int dtype) { return dtype == CCE_DTYPE_F32 ? 4 : 2; }
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+// Every CCE_BWD_* flag.
+constexpr int kBwdFlags = CCE_BWD_DC_ZEROED | CCE_BWD_TOKENS_INPUT | CCE_BWD_TOKENS_SORTED | CCE_BWD_DE_SUMS_WIDE |
+                          CCE_BWD_DE_SUMS_NARROW | CCE_BWD_DC_SUMS_WIDE | CCE_BWD_DC_SUMS_NARROW | CCE_BWD_REF_STATS |
+                          CCE_BWD_DEVICE_PASSES | CCE_BWD_G_PAIR | CCE_BWD_G_SINGLE | CCE_BWD_DC_OWNER_TASKS |
+                          CCE_BWD_G_TASKS_BY_BLOCK;
+// Flags of which at most one may be set.
+constexpr int kBwdFlagPairs[4][2] = {{CCE_BWD_TOKENS_INPUT, CCE_BWD_TOKENS_SORTED},
+                                     {CCE_BWD_DE_SUMS_WIDE, CCE_BWD_DE_SUMS_NARROW},
+                                     {CCE_BWD_DC_SUMS_WIDE, CCE_BWD_DC_SUMS_NARROW},
+                                     {CCE_BWD_G_PAIR, CCE_BWD_G_SINGLE}};
+bool bwd_flags_valid(int flags) {
+  if (flags & ~kBwdFlags) return false;
+  for (const auto& pr : kBwdFlagPairs)
+    if ((flags & pr[0]) && (flags & pr[1])) return false;
+  return true;
+}
+// The G tiles' layout: 16-bit G as the hi / lo pair with the filter off (the 1e-3
+// bar), rounded once with it on, unless CCE_BWD_G_PAIR / CCE_BWD_G_SINGLE says.
+bool g_split_for(size_t es, int flags, float filter_log_eps) {
+  return es == 2 && !(flags & CCE_BWD_G_SINGLE) && ((flags & CCE_BWD_G_PAIR) || !(filter_log_eps > -INFINITY));
+}
 bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
 const char* dtype_name(int dtype) {
@@ -212,10 +234,20 @@ size_t cce_backward_workspace_size(int dtype, int64_t N, int64_t D, int64_t V, i
 
 size_t cce_backward_workspace_size_ex(int dtype, int64_t N, int64_t D, int64_t V, int want_dE, int want_dC,
                                       int want_dBias, int64_t max_g_tiles, int64_t max_chunk_tiles) {
+  // the hi / lo pair's 64 KiB slots: enough for either layout
+  return cce_backward_workspace_size_flags(dtype, N, D, V, want_dE, want_dC, want_dBias, max_g_tiles,
+                                           max_chunk_tiles, -INFINITY, CCE_BWD_G_PAIR);
+}
+
+size_t cce_backward_workspace_size_flags(int dtype, int64_t N, int64_t D, int64_t V, int want_dE, int want_dC,
+                                         int want_dBias, int64_t max_g_tiles, int64_t max_chunk_tiles,
+                                         float filter_log_eps, int flags) {
   if (N <= 0 || D <= 0 || V <= 0 || max_g_tiles < 0 || max_chunk_tiles < 0 || max_chunk_tiles % 32 != 0) return 0;
   if (dtype != CCE_DTYPE_F32 && dtype != CCE_DTYPE_F16 && dtype != CCE_DTYPE_BF16) return 0;
-  return cce::make_bwd_plan(elem_size(dtype), N, D, V, want_dE != 0, want_dC != 0, want_dBias != 0,
-                            max_chunk_tiles, false, max_g_tiles)
+  if (std::isnan(filter_log_eps) || !bwd_flags_valid(flags)) return 0;
+  const size_t es = elem_size(dtype);
+  return cce::make_bwd_plan(es, N, D, V, want_dE != 0, want_dC != 0, want_dBias != 0, max_chunk_tiles, false,
+                            max_g_tiles, g_split_for(es, flags, filter_log_eps))
       .total_bytes;
 }
 
@@ -290,17 +322,19 @@ int backward_impl(int dtype, const void* e, const void* c, const void* bias, con
     return fail(CCE_ERR_INVALID_ARGUMENT, "[cce_backward] gradient outputs must be 16-byte aligned");
   if (std::isnan(filter_log_eps))
     return fail(CCE_ERR_INVALID_ARGUMENT, "[cce_backward] filter_log_eps must not be NaN");
-  // The plan is a function of the sizes, the wanted outputs and the workspace size
-  // only: the default plan when the workspace holds it, else smaller passes.
+  // The plan is a function of the sizes, the wanted outputs, the G tiles' layout (the
+  // filter and the G flags) and the workspace size only: the default plan when the
+  // workspace holds it, else smaller passes.
   const size_t es = elem_size(dtype);
+  const bool g_split = g_split_for(es, flags, filter_log_eps);
   int64_t qcv = q ? q->chunk_rows / cce::kBwdVocab : 0;
   if (max_chunk_tiles > 0 && (qcv == 0 || max_chunk_tiles < qcv)) qcv = max_chunk_tiles;
   bool fits = false;
   const cce::BwdPlan P = cce::plan_for_workspace(es, N, D, V, dE != nullptr, dC != nullptr, dBias != nullptr, qcv,
-                                                 q != nullptr, workspace ? workspace_bytes : 0, fits);
+                                                 q != nullptr, g_split, workspace ? workspace_bytes : 0, fits);
   if (!workspace || !fits) {
     const size_t least = cce::make_bwd_plan_cap(es, N, D, V, dE != nullptr, dC != nullptr, dBias != nullptr, 1, false,
-                                                qcv, q != nullptr)
+                                                qcv, q != nullptr, g_split)
                              .total_bytes;
     return fail(CCE_ERR_WORKSPACE, "[cce_backward] workspace of %zu bytes required (at least %zu), %zu given",
                 P.total_bytes, least, workspace ? workspace_bytes : (size_t)0);
@@ -365,8 +399,7 @@ int backward_impl(int dtype, const void* e, const void* c, const void* bias, con
   a.dc_zeroed = (flags & CCE_BWD_DC_ZEROED) ? 1 : 0;
   a.stats32 = (flags & CCE_BWD_REF_STATS) ? 1 : 0;
   a.g_scaled = dtype == CCE_DTYPE_F16 ? 1 : 0;  // fp16 G tiles are scaled into fp16's normal range
-  // 16-bit G as the hi / lo pair with the filter off (the 1e-3 bar), rounded once with it on
-  a.g_split = es == 2 && !(flags & CCE_BWD_G_SINGLE) && ((flags & CCE_BWD_G_PAIR) || !(filter_log_eps > -INFINITY));
+  a.g_split = P.g_split ? 1 : 0;  // the layout the plan's slots are sized for
   // one-tile dC owners by token block: 16-bit inputs with G rounded once
   a.dc_blk = es == 2 && !a.g_split && dC != nullptr && P.nrb <= cce::kDcBlkMaxRb && !(flags & CCE_BWD_DC_OWNER_TASKS);
   a.g_tiles_ok = (flags & CCE_BWD_G_TASKS_BY_BLOCK) ? 0 : 1;
@@ -403,11 +436,7 @@ int cce_backward_ex(int dtype, const void* e, const void* c, const void* bias, c
                     void* dBias, void* workspace, size_t workspace_bytes, int64_t* tile_stats, int flags,
                     int64_t max_chunk_tiles, void* hip_stream) {
   g_err[0] = 0;
-  constexpr int kKnown = CCE_BWD_DC_ZEROED | CCE_BWD_TOKENS_INPUT | CCE_BWD_TOKENS_SORTED | CCE_BWD_DE_SUMS_WIDE |
-                         CCE_BWD_DE_SUMS_NARROW | CCE_BWD_DC_SUMS_WIDE | CCE_BWD_DC_SUMS_NARROW |
-                         CCE_BWD_REF_STATS | CCE_BWD_DEVICE_PASSES | CCE_BWD_G_PAIR | CCE_BWD_G_SINGLE |
-                         CCE_BWD_DC_OWNER_TASKS | CCE_BWD_G_TASKS_BY_BLOCK;
-  if (flags & ~kKnown) return fail(CCE_ERR_INVALID_ARGUMENT, "[cce_backward] unknown flags 0x%x", flags);
+  if (flags & ~kBwdFlags) return fail(CCE_ERR_INVALID_ARGUMENT, "[cce_backward] unknown flags 0x%x", flags);
   if ((flags & CCE_BWD_TOKENS_INPUT) && (flags & CCE_BWD_TOKENS_SORTED))
     return fail(CCE_ERR_INVALID_ARGUMENT, "[cce_backward] CCE_BWD_TOKENS_INPUT and CCE_BWD_TOKENS_SORTED exclude each other");
   if (((flags & CCE_BWD_DE_SUMS_WIDE) && (flags & CCE_BWD_DE_SUMS_NARROW)) ||
@@ -465,27 +494,21 @@ int cce_backward_noalloc(int dtype, const void* e, const void* c, const void* bi
                          const float* tile_max, const float* d_nll, float filter_log_eps, void* dE, void* dC,
                          void* dBias, int64_t* tile_stats, int flags, void* hip_stream) {
   g_err[0] = 0;
-  constexpr int kKnown = CCE_BWD_DC_ZEROED | CCE_BWD_TOKENS_INPUT | CCE_BWD_TOKENS_SORTED | CCE_BWD_DE_SUMS_WIDE |
-                         CCE_BWD_DE_SUMS_NARROW | CCE_BWD_DC_SUMS_WIDE | CCE_BWD_DC_SUMS_NARROW |
-                         CCE_BWD_REF_STATS | CCE_BWD_DEVICE_PASSES | CCE_BWD_G_PAIR | CCE_BWD_G_SINGLE |
-                         CCE_BWD_DC_OWNER_TASKS | CCE_BWD_G_TASKS_BY_BLOCK;
-  if (flags & ~kKnown)
+  if (flags & ~kBwdFlags)
     return fail(CCE_ERR_INVALID_ARGUMENT, "[cce_backward_noalloc] unknown flags 0x%x", flags);
-  if (((flags & CCE_BWD_TOKENS_INPUT) && (flags & CCE_BWD_TOKENS_SORTED)) ||
-      ((flags & CCE_BWD_DE_SUMS_WIDE) && (flags & CCE_BWD_DE_SUMS_NARROW)) ||
-      ((flags & CCE_BWD_DC_SUMS_WIDE) && (flags & CCE_BWD_DC_SUMS_NARROW)) ||
-      ((flags & CCE_BWD_G_PAIR) && (flags & CCE_BWD_G_SINGLE)))
+  if (!bwd_flags_valid(flags))
     return fail(CCE_ERR_INVALID_ARGUMENT, "[cce_backward_noalloc] a pair of flags excludes each other");
   int rc = check_common("cce_backward_noalloc", dtype, e, c, targets, N, D, V);
   if (rc != CCE_OK) return rc;
   // Sizes beyond what the static scratch holds are refused before any device work.
   const size_t es = elem_size(dtype);
+  const bool g_split = g_split_for(es, flags, filter_log_eps);
   bool fits = false;
-  cce::plan_for_workspace(es, N, D, V, dE != nullptr, dC != nullptr, dBias != nullptr, 0, false,
+  cce::plan_for_workspace(es, N, D, V, dE != nullptr, dC != nullptr, dBias != nullptr, 0, false, g_split,
                           (size_t)CCE_NOALLOC_SCRATCH_BYTES, fits);
   if (!fits) {
     const size_t least =
-        cce::make_bwd_plan_cap(es, N, D, V, dE != nullptr, dC != nullptr, dBias != nullptr, 1, false, 0, false)
+        cce::make_bwd_plan_cap(es, N, D, V, dE != nullptr, dC != nullptr, dBias != nullptr, 1, false, 0, false, g_split)
             .total_bytes;
     return fail(CCE_ERR_WORKSPACE,
                 "[cce_backward_noalloc] N=%lld D=%lld V=%lld needs at least %zu bytes of workspace; the static scratch "
@@ -576,8 +599,9 @@ size_t cce_backward_q_workspace_size(int dtype, int64_t N, int64_t D, int64_t V,
                                      int64_t chunk_rows) {
   if (N <= 0 || D <= 0 || V <= 0 || chunk_rows < 0 || chunk_rows % cce::kQuantChunkAlign != 0) return 0;
   if (dtype != CCE_DTYPE_F32 && dtype != CCE_DTYPE_F16 && dtype != CCE_DTYPE_BF16) return 0;
+  // the hi / lo pair's 64 KiB slots: enough for either layout
   return cce::make_bwd_plan(elem_size(dtype), N, D, V, want_dE != 0, false, want_dBias != 0,
-                            quant_chunk_rows(chunk_rows) / cce::kBwdVocab, true)
+                            quant_chunk_rows(chunk_rows) / cce::kBwdVocab, true, 0, true)
       .total_bytes;
 }
 

@@ -82,15 +82,17 @@ constexpr int64_t kQuantDefaultChunkRows = 32768;  // 256 MiB of bf16 scratch at
 // keeps the softmax weight in fp32 through both products.  A tile row of the pair is
 // 256 16-bit values: columns 32 q + i go to elements 64 q + i (hi) and 64 q + 32 + i
 // (lo), so that a 128-byte slice of a row holds 32 columns' hi and lo (the dE sums'
-// contraction slice).  A tile slot is 64 KiB either way.
-constexpr size_t g_tile_bytes(size_t esize) {
-  return (size_t)kBwdTokens * kBwdVocab * (esize == 2 ? 2 * esize : esize);
+// contraction slice).  A tile slot is 64 KiB for fp32 and for the pair, 32 KiB for a
+// 16-bit G rounded once.
+constexpr size_t g_tile_bytes(size_t esize, bool split) {
+  return (size_t)kBwdTokens * kBwdVocab * (esize == 2 && split ? 2 * esize : esize);
 }
-// G-tile budget of one pass, in MiB (the default workspace; a smaller workspace
-// gives smaller passes, down to 2 tiles per token block).  512 MiB holds 8192 tiles, an
-// eighth of the Llama-3 8B head's (N = 8192, V = 128256: 4.2 GB of G when nothing is
-// skipped), so a dense backward takes 8 passes there; a filtered one keeps a few
-// hundred tiles and takes one.
+// G-tile budget of one pass, in MiB of 64 KiB slots (the default workspace; a smaller
+// workspace gives smaller passes, down to 2 tiles per token block).  512 MiB holds 8192
+// tiles, an eighth of the Llama-3 8B head's (N = 8192, V = 128256: 4.2 GB of G when
+// nothing is skipped), so a dense backward takes 8 passes there; a filtered one keeps a
+// few hundred tiles and takes one.  A 16-bit G rounded once holds the same tiles in
+// half the bytes.
 #ifndef CCE_G_SCRATCH_MIB
 #define CCE_G_SCRATCH_MIB 512
 #endif
@@ -146,7 +148,8 @@ struct BwdPlan {
   int64_t chunk_pairs;      // nrb * chunk_nvt: the most pairs one chunk may keep
   int64_t cap;              // G tiles per pass: chunk_pairs, or at least 2 nrb
   int64_t max_passes;       // passes launched per chunk
-  size_t g_bytes;           // bytes of one G tile (g_tile_bytes: hi and lo halves for 16-bit types)
+  size_t g_bytes;           // bytes of one G tile slot (g_tile_bytes of the layout)
+  bool g_split;             // 16-bit G slots hold the hi / lo pair (else G rounded once)
   int esize;                // bytes of one input element
   bool perm_ok;             // the sorted token order is available (N and tile count in range)
   bool carry;               // the fp32 dE carry is reserved (more than one pass or chunk may run)
@@ -175,15 +178,18 @@ inline int64_t plan_chunk_nvt(int64_t nvt, int64_t nrb, int64_t max_chunk_nvt) {
 
 // The plan for passes of at most `cap` G tiles (clamped to [min(2 nrb, chunk_pairs),
 // chunk_pairs]); perm: reserve the sorted token order when it is available; quant
-// reserves the scratch of one chunk's dequantized classifier rows.
+// reserves the scratch of one chunk's dequantized classifier rows; g_split: the G
+// tiles' layout (the hi / lo pair of 16-bit types, else G rounded once).
 inline BwdPlan make_bwd_plan_cap(size_t esize, int64_t N, int64_t D, int64_t V, bool want_de, bool want_dc,
-                                 bool want_db, int64_t cap, bool perm, int64_t max_chunk_nvt, bool quant) {
+                                 bool want_db, int64_t cap, bool perm, int64_t max_chunk_nvt, bool quant,
+                                 bool g_split) {
   BwdPlan P{};
   P.nvt = (V + kBwdVocab - 1) / kBwdVocab;
   P.nrb = (N + kBwdTokens - 1) / kBwdTokens;
   P.total = P.nvt * P.nrb;
   P.nwords = (P.nvt + 31) / 32;
-  P.g_bytes = g_tile_bytes(esize);
+  P.g_split = esize == 2 && g_split;
+  P.g_bytes = g_tile_bytes(esize, P.g_split);
   P.esize = (int)esize;
   const bool want_g = want_de || want_dc;
   const int64_t cw = plan_chunk_nvt(P.nvt, P.nrb, max_chunk_nvt);
@@ -240,28 +246,30 @@ inline BwdPlan make_bwd_plan_cap(size_t esize, int64_t N, int64_t D, int64_t V, 
   return P;
 }
 
-// G tiles of a pass in the default workspace: the budget, at least 2 per token block.
-inline int64_t default_cap(size_t esize, int64_t N) {
+// G tiles of a pass in the default workspace: the budget's 64 KiB slots (whatever
+// the layout), at least 2 per token block.
+inline int64_t default_cap(int64_t N) {
   const int64_t nrb = (N + kBwdTokens - 1) / kBwdTokens;
-  const int64_t by_budget = (int64_t)(kGScratchBudget / g_tile_bytes(esize));
+  const int64_t by_budget = (int64_t)(kGScratchBudget / g_tile_bytes(4, true));
   return by_budget > 2 * nrb ? by_budget : 2 * nrb;
 }
 
 // The plan of the default workspace (max_g_tiles <= 0), or of passes of at most
 // max_g_tiles G tiles.
 inline BwdPlan make_bwd_plan(size_t esize, int64_t N, int64_t D, int64_t V, bool want_de, bool want_dc,
-                             bool want_db, int64_t max_chunk_nvt = 0, bool quant = false, int64_t max_g_tiles = 0) {
-  const int64_t dcap = default_cap(esize, N);
+                             bool want_db, int64_t max_chunk_nvt, bool quant, int64_t max_g_tiles, bool g_split) {
+  const int64_t dcap = default_cap(N);
   const int64_t cap = max_g_tiles > 0 && max_g_tiles < dcap ? max_g_tiles : dcap;
-  return make_bwd_plan_cap(esize, N, D, V, want_de, want_dc, want_db, cap, true, max_chunk_nvt, quant);
+  return make_bwd_plan_cap(esize, N, D, V, want_de, want_dc, want_db, cap, true, max_chunk_nvt, quant, g_split);
 }
 
 // The plan a workspace of ws_bytes runs: the default plan when it fits, else the
 // largest pass capacity that fits (the sorted token order is dropped when even the
 // smallest passes do not fit with it).  ok = false when nothing fits.
 inline BwdPlan plan_for_workspace(size_t esize, int64_t N, int64_t D, int64_t V, bool want_de, bool want_dc,
-                                  bool want_db, int64_t max_chunk_nvt, bool quant, size_t ws_bytes, bool& ok) {
-  BwdPlan P = make_bwd_plan(esize, N, D, V, want_de, want_dc, want_db, max_chunk_nvt, quant);
+                                  bool want_db, int64_t max_chunk_nvt, bool quant, bool g_split, size_t ws_bytes,
+                                  bool& ok) {
+  BwdPlan P = make_bwd_plan(esize, N, D, V, want_de, want_dc, want_db, max_chunk_nvt, quant, 0, g_split);
   ok = P.total_bytes <= ws_bytes;
   if (ok) return P;
   const int64_t dcap = P.cap;
@@ -271,7 +279,8 @@ inline BwdPlan plan_for_workspace(size_t esize, int64_t N, int64_t D, int64_t V,
     BwdPlan best{};
     bool found = false;
     if (hi >= 1) {
-      BwdPlan m = make_bwd_plan_cap(esize, N, D, V, want_de, want_dc, want_db, lo, perm != 0, max_chunk_nvt, quant);
+      BwdPlan m =
+          make_bwd_plan_cap(esize, N, D, V, want_de, want_dc, want_db, lo, perm != 0, max_chunk_nvt, quant, g_split);
       if (m.total_bytes <= ws_bytes) {
         best = m;
         found = true;
@@ -279,7 +288,7 @@ inline BwdPlan plan_for_workspace(size_t esize, int64_t N, int64_t D, int64_t V,
         while (lo < hi) {
           const int64_t mid = lo + (hi - lo + 1) / 2;
           BwdPlan t = make_bwd_plan_cap(esize, N, D, V, want_de, want_dc, want_db, mid, perm != 0, max_chunk_nvt,
-                                        quant);
+                                        quant, g_split);
           if (t.total_bytes <= ws_bytes) {
             best = t;
             lo = mid;

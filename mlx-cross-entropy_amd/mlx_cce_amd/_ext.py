@@ -42,6 +42,8 @@ SIGNATURES = {
     "cce_forward": (_INT, [_INT, _P, _P, _P, _P, _I64, _INT, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P]),
     "cce_backward_workspace_size": (ctypes.c_size_t, [_INT, _I64, _I64, _I64, _INT, _INT, _INT]),
     "cce_backward_workspace_size_ex": (ctypes.c_size_t, [_INT, _I64, _I64, _I64, _INT, _INT, _INT, _I64, _I64]),
+    "cce_backward_workspace_size_flags": (ctypes.c_size_t, [_INT, _I64, _I64, _I64, _INT, _INT, _INT, _I64, _I64,
+                                                            ctypes.c_float, _INT]),
     "cce_backward": (_INT, [_INT, _P, _P, _P, _P, _I64, _INT, _I64, _I64, _I64, _P, _P, _P, ctypes.c_float,
                             _P, _P, _P, _P, ctypes.c_size_t, _P, _P]),
     "cce_forward_ex": (_INT, [_INT, _P, _P, _P, _P, _I64, _INT, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _I64,
@@ -281,15 +283,28 @@ def forward(e, c, targets, bias=None, ignore_index=-100, zero_out=None, ref_stat
     return tile_max, tile_sum_exp, neg_tl, lse, nll
 
 
-def workspace_size(e, c, want_de, want_dc, want_db, max_g_tiles=None, max_chunk_tiles=None):
-    """Bytes of the backward's workspace (cce_backward_workspace_size_ex); the
-    backward_options in force unless given."""
+_ANY_FILTER = object()
+
+
+def workspace_size(e, c, want_de, want_dc, want_db, max_g_tiles=None, max_chunk_tiles=None,
+                   filter_eps=_ANY_FILTER, flags=None):
+    """Bytes of the backward's workspace; the backward_options in force unless given.
+    Without filter_eps: enough for any filter (cce_backward_workspace_size_ex); with
+    it (None: the filter off), the size of a backward with that filter and flags
+    (cce_backward_workspace_size_flags: 16-bit G rounded once takes half the G
+    bytes)."""
     N, D = e.shape
     V = c.shape[0]
     g = _bwd_opts["max_g_tiles"] if max_g_tiles is None else int(max_g_tiles)
     ch = _bwd_opts["max_chunk_tiles"] if max_chunk_tiles is None else int(max_chunk_tiles)
-    return int(lib().cce_backward_workspace_size_ex(DTYPE_CODES.get(e.dtype, -1), N, D, V,
-                                                    int(want_de), int(want_dc), int(want_db), g, ch))
+    code = DTYPE_CODES.get(e.dtype, -1)
+    if filter_eps is _ANY_FILTER:
+        return int(lib().cce_backward_workspace_size_ex(code, N, D, V, int(want_de), int(want_dc), int(want_db),
+                                                        g, ch))
+    eps = -math.inf if filter_eps is None else float(filter_eps)
+    fl = _bwd_opts["flags"] if flags is None else int(flags)
+    return int(lib().cce_backward_workspace_size_flags(code, N, D, V, int(want_de), int(want_dc), int(want_db),
+                                                       g, ch, ctypes.c_float(eps), fl))
 
 
 def _ref_stats_layout(tile_max, N, V, fn):
@@ -341,11 +356,11 @@ def backward(e, c, targets, lse, tile_max, d_nll, bias=None, ignore_index=-100,
         dc_zeroed = None
         dC = torch.empty_like(c) if want_dc else None
     dB = torch.empty_like(bias) if want_db else None
-    ws_bytes = workspace_size(e, c, want_de, want_dc, want_db)
-    ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=e.device)
     eps = -math.inf if filter_eps is None else float(filter_eps)
     has_ignore = ignore_index is not None
     flags = _bwd_opts["flags"] | (CCE_BWD_DC_ZEROED if dc_zeroed is not None else 0) | (CCE_BWD_REF_STATS if ref else 0)
+    ws_bytes = workspace_size(e, c, want_de, want_dc, want_db, filter_eps=eps, flags=flags)
+    ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=e.device)
     with torch.cuda.device(e.device):
         stream = torch.cuda.current_stream(e.device).cuda_stream
         ev = _event_pair("backward")

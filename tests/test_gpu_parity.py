@@ -630,6 +630,64 @@ def test_vocabulary_chunks(m, cuda, dtype, filtered, de_sums, split):
         assert err < tol, (name, err)
 
 
+@pytest.mark.parametrize("sizing", ["exact", "pair", "least"])
+def test_rounded_once_g_workspace_sizes(m, cuda, sizing):
+    """A bf16 backward with the filter on keeps G rounded once in 32 KiB tile slots.
+    Given a workspace of exactly cce_backward_workspace_size_flags's size for the
+    smallest passes, the larger one of the hi / lo pair's 64 KiB slots for the same
+    passes (cce_backward_workspace_size_ex: the plan then takes larger passes), or the
+    least size the call accepts (named by its error), the backward keeps the same tiles
+    and its gradients equal the default workspace's to the passes' fp32 reassociation
+    (2.3e-5, 7.8e-6 and 3.2e-5 relative for dE; dC and dBias, final per pass, bit for
+    bit)."""
+    import ctypes
+    import re
+    ext = m._ext
+    lib = ext.lib()
+    N, D, V = 300, 264, 9000
+    e, c, t = _peaked(cuda, N=N, D=D, V=V, seed=11)
+    t = t.to(torch.int64).contiguous()
+    gb = torch.Generator(device=cuda).manual_seed(12)
+    b = (torch.randn(V, generator=gb, device=cuda) * 0.1).to(torch.bfloat16)
+    tm, _, _, lse, _ = ext.forward(e, c, t, b, -100)
+    d_nll = torch.full((N,), 1.0 / N, device=cuda)
+    eps = m.FILTER_LOG_EPS
+    st0 = torch.zeros(3, dtype=torch.int64, device=cuda)
+    # the least workspace has no room for the sorted token order: its reference keeps
+    # the tiles of the input order's token blocks
+    with ext.backward_options(token_order="input" if sizing == "least" else None):
+        ref = ext.backward(e, c, t, lse, tm, d_nll, b, -100, eps, True, True, True, tile_stats=st0)
+    exact = lib.cce_backward_workspace_size_flags(2, N, D, V, 1, 1, 1, 1, 0, ctypes.c_float(eps), 0)
+    pair = lib.cce_backward_workspace_size_ex(2, N, D, V, 1, 1, 1, 1, 0)
+    assert 0 < exact < pair
+    dE, dC, dB = torch.empty_like(e), torch.empty_like(c), torch.empty_like(b)
+    st = torch.zeros(3, dtype=torch.int64, device=cuda)
+    stream = torch.cuda.current_stream(cuda).cuda_stream
+
+    def call(ws, nbytes):
+        return lib.cce_backward_ex(2, ext._ptr(e), ext._ptr(c), ext._ptr(b), ext._ptr(t), -100, 1, N, D, V,
+                                   ext._ptr(lse), ext._ptr(tm), ext._ptr(d_nll), ctypes.c_float(eps), ext._ptr(dE),
+                                   ext._ptr(dC), ext._ptr(dB), ext._ptr(ws), ctypes.c_size_t(nbytes), ext._ptr(st),
+                                   0, 0, ctypes.c_void_p(stream))
+
+    if sizing == "least":
+        small = torch.empty((256,), dtype=torch.uint8, device=cuda)
+        assert call(small, 256) == ext.CCE_ERR_WORKSPACE  # refused before any device work
+        nbytes = int(re.search(rb"at least (\d+)", lib.cce_last_error()).group(1))
+        assert 0 < nbytes <= exact
+    else:
+        nbytes = exact if sizing == "exact" else pair
+    ws = torch.empty((nbytes,), dtype=torch.uint8, device=cuda)
+    assert call(ws, nbytes) == ext.CCE_OK, lib.cce_last_error()
+    torch.cuda.synchronize()
+    print(f"{sizing}: workspace {nbytes} bytes, tiles {st.tolist()} (default {st0.tolist()})")
+    assert torch.equal(st, st0)
+    for x, y, name in zip((dE, dC, dB), ref, ("dE", "dC", "dBias")):
+        err = O.rel_fro(f64(x), f64(y))
+        print(f"{sizing} vs default {name}: {err:.2e}")
+        assert err < 1e-3, (name, err)
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("case", ["skewed", "uniform"])
 def test_dc_geometry_chosen_per_pass(m, cuda, case, dtype):

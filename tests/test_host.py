@@ -110,6 +110,36 @@ def test_backward_workspace_small_problems_fit_one_pass(ext):
     assert lib.cce_backward_workspace_size_ex(2, N, D, V, 1, 1, 1, 0, -32) == 0
 
 
+@pytest.mark.parametrize("N,D,V", [(8192, 4096, 128256), (1000, 64, 3000)], ids=["c3", "small"])
+def test_workspace_size_follows_the_g_layout(ext, N, D, V):
+    """A 16-bit G rounded once (the filter on, or CCE_BWD_G_SINGLE) takes 32 KiB a
+    tile slot, the hi / lo pair (the filter off, or CCE_BWD_G_PAIR) and fp32 64 KiB:
+    the same passes, so the sizes differ by exactly half the G slots' bytes, and the
+    layout-free size is the pair's."""
+    lib = ext.lib()
+    nrb, nvt = -(-N // 128), -(-V // 128)
+    cap = min(max(8192, 2 * nrb), nrb * nvt)  # G tiles of one pass (the default plan)
+    eps, off = ctypes.c_float(-8.3), ctypes.c_float(float("-inf"))
+
+    def size(dtype, e, flags=0, g=0):
+        return lib.cce_backward_workspace_size_flags(dtype, N, D, V, 1, 1, 1, g, 0, e, flags)
+
+    pair, single = size(2, off), size(2, eps)
+    assert pair == lib.cce_backward_workspace_size(2, N, D, V, 1, 1, 1) == size(2, eps, ext.CCE_BWD_G_PAIR)
+    assert single == size(2, off, ext.CCE_BWD_G_SINGLE) == size(1, eps)
+    assert pair - single == cap * 128 * 128 * 2
+    assert size(0, eps) == size(0, off) == lib.cce_backward_workspace_size(0, N, D, V, 1, 1, 1)
+    # passes of 2 tiles per token block: the same halving of their (fewer) slots
+    small = min(2 * nrb, nrb * nvt)
+    assert size(2, off, 0, 1) - size(2, eps, 0, 1) == small * 128 * 128 * 2
+    assert size(2, off, 0, 1) == lib.cce_backward_workspace_size_ex(2, N, D, V, 1, 1, 1, 1, 0)
+    # invalid filter or flags: 0
+    assert size(2, ctypes.c_float(float("nan"))) == 0
+    assert size(2, eps, 1 << 13) == 0
+    assert size(2, eps, ext.CCE_BWD_G_PAIR | ext.CCE_BWD_G_SINGLE) == 0
+    assert size(2, eps, ext.CCE_BWD_TOKENS_INPUT | ext.CCE_BWD_TOKENS_SORTED) == 0
+
+
 FAKE = 1 << 20  # 16-byte aligned, never dereferenced: validation fails first
 
 
