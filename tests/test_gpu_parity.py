@@ -320,6 +320,34 @@ def test_ragged_shapes(m, cuda, N, D, V):
         assert O.rel_fro(f64(got), r) < 1e-4 or np.abs(f64(got) - r).max() < 1e-6
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("V", [2048, 2000, 1001])
+def test_forward_bias_staged_in_lds(m, cuda, dtype, V):
+    """The forward adds a 16-byte aligned bias whose V * element size is a multiple of
+    16 from LDS (one LDS-DMA copy per tile, zeros past V: V = 2000 ends in a partial
+    vocabulary block), any other bias from global memory.  An unaligned view of the
+    same values takes the global path: the statistics, lse and loss are equal bit for
+    bit, and the loss matches the oracle."""
+    ext = m._ext
+    N, D = 300, 96
+    e, c, t = normal_case(N, D, V, dtype, cuda, seed=V, std=0.1)
+    g = torch.Generator(device=cuda).manual_seed(V + 1)
+    store = (torch.randn(V + 8, generator=g, device=cuda) * 0.5).to(dtype)
+    b_al = store[:V]
+    off = torch.empty(V + 8, dtype=dtype, device=cuda)
+    off[1:V + 1] = b_al
+    b_un = off[1:V + 1]  # the same values, 2 or 4 bytes past a 16-byte boundary
+    assert b_al.data_ptr() % 16 == 0 and b_un.data_ptr() % 16 != 0
+    lds = ext.forward(e, c, t, b_al, -100)
+    glob = ext.forward(e, c, t, b_un, -100)
+    torch.cuda.synchronize()
+    for k, name in ((0, "tile_max"), (1, "tile_sum_exp"), (3, "lse"), (4, "nll")):
+        assert torch.equal(lds[k], glob[k]), name
+    ref = O.linear_cross_entropy(f64(e), f64(c), t.cpu().numpy(), f64(b_al), "none")
+    tol = 1e-5 if dtype == torch.float32 else 2e-3
+    np.testing.assert_allclose(f64(lds[4]), ref, rtol=tol, atol=tol)
+
+
 def test_all_rows_ignored(m, cuda):
     e, c, t = normal_case(64, 32, 300, torch.bfloat16, cuda)
     t[:] = -100
