@@ -124,11 +124,18 @@ __device__ __forceinline__ void fwd_add_bias(const FwdArgs& a, f32x16 (&acc)[TI]
 // only after every wave has passed the stage barriers of the tile in between.
 constexpr int kBiasLdsBytes = 1024;
 static_assert(kFwdVocab * 4 <= kBiasLdsBytes, "one LDS-DMA load holds a block's bias");
+// The lane index, formed where it is used: a value the compiler cannot hoist out of the
+// tile loop, where it would hold a register through every main loop.
+__device__ __forceinline__ int lane_here() {
+  int l;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+  return l;
+}
 template <typename T>
 __device__ __forceinline__ void fwd_stage_bias(const FwdArgs& a, int vb, char* buf) {
   if (__builtin_amdgcn_readfirstlane(threadIdx.x >> 6) != 0) return;  // wave 0 (a uniform branch)
   constexpr int chunks = kFwdVocab * (int)sizeof(T) / 16;  // 16-byte pieces of a block's bias
-  const int lane = threadIdx.x & 63;
+  const int lane = lane_here();
   // lanes past the block's pieces load the first ones again (into bytes nobody reads)
   const int64_t off = ((int64_t)vb * kFwdVocab * (int64_t)sizeof(T)) + (lane % chunks) * 16;
   const char* g = off < a.V * (int64_t)sizeof(T) ? reinterpret_cast<const char*>(a.bias) + off
@@ -137,8 +144,8 @@ __device__ __forceinline__ void fwd_stage_bias(const FwdArgs& a, int vb, char* b
 }
 template <typename T, int TI, int TJ>
 __device__ __forceinline__ void fwd_add_bias_lds(const char* buf, f32x16 (&acc)[TI][TJ]) {
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int lane = lane_here();
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int c0 = (wave & 1) * 128 + (lane >> 5) * 4;
 #pragma unroll
   for (int i = 0; i < TI; ++i) {
