@@ -84,12 +84,12 @@ REF_STAT_TILE = 32
 # Overrides of choices the backward otherwise makes itself, for tests and tuning
 # (results agree to rounding either way).  They travel explicitly with every
 # cce_backward_ex call and its workspace-size query, so the two always agree.
-_bwd_opts = {"flags": 0, "max_g_tiles": 0, "max_chunk_tiles": 0}
+_bwd_opts = {"flags": 0, "max_g_tiles": 0, "max_chunk_tiles": 0, "dc_zero_fill": "backward"}
 
 
 @contextlib.contextmanager
 def backward_options(token_order=None, de_sums=None, dc_sums=None, max_g_tiles=0, max_chunk_tiles=0,
-                     passes=None, g_precision=None, dc_tasks=None, g_tasks=None):
+                     passes=None, g_precision=None, dc_tasks=None, g_tasks=None, dc_zero_fill=None):
     """Within the block, backward() calls run with these overrides:
     token_order "input" | "sorted" (128-row token blocks of the input order, or of the
     rows grouped by target tile); de_sums / dc_sums "wide" | "narrow" (512- or
@@ -102,7 +102,10 @@ def backward_options(token_order=None, de_sums=None, dc_sums=None, max_g_tiles=0
     with the filter off and a single rounding with it on); dc_tasks "owners" (the
     narrow dC sums run one-tile owners as owner tasks, not grouped by token block);
     g_tasks "blocks" (the G kernel's tasks are token blocks with up to 4 kept tiles,
-    never vocabulary tiles with up to 4 kept blocks)."""
+    never vocabulary tiles with up to 4 kept blocks); dc_zero_fill "forward" (the
+    autograd op has the forward's tile kernel zero dC, cce_forward_ex, and the backward
+    write only the rows of kept tiles, CCE_BWD_DC_ZEROED) | "backward" (the default:
+    the backward zeroes the rows no kept tile touches)."""
     flags = 0
     flags |= {None: 0, "pair": CCE_BWD_G_PAIR, "single": CCE_BWD_G_SINGLE}[g_precision]
     flags |= {None: 0, "host": 0, "device": CCE_BWD_DEVICE_PASSES}[passes]
@@ -111,8 +114,11 @@ def backward_options(token_order=None, de_sums=None, dc_sums=None, max_g_tiles=0
     flags |= {None: 0, "input": CCE_BWD_TOKENS_INPUT, "sorted": CCE_BWD_TOKENS_SORTED}[token_order]
     flags |= {None: 0, "wide": CCE_BWD_DE_SUMS_WIDE, "narrow": CCE_BWD_DE_SUMS_NARROW}[de_sums]
     flags |= {None: 0, "wide": CCE_BWD_DC_SUMS_WIDE, "narrow": CCE_BWD_DC_SUMS_NARROW}[dc_sums]
+    if dc_zero_fill not in (None, "forward", "backward"):
+        raise ValueError(f"dc_zero_fill must be 'forward' or 'backward', got {dc_zero_fill!r}")
     saved = dict(_bwd_opts)
-    _bwd_opts.update(flags=flags, max_g_tiles=int(max_g_tiles), max_chunk_tiles=int(max_chunk_tiles))
+    _bwd_opts.update(flags=flags, max_g_tiles=int(max_g_tiles), max_chunk_tiles=int(max_chunk_tiles),
+                     dc_zero_fill=dc_zero_fill or "backward")
     try:
         yield
     finally:

@@ -559,12 +559,13 @@ def test_forward_zero_fill_and_backward_into_zeroed_dc(m, cuda, split):
     the forward's outputs unchanged; cce_backward_ex with CCE_BWD_DC_ZEROED writes only the
     kept vocabulary tiles' dC rows into it, and the result equals the ordinary backward's
     dC bit for bit (filtered, so that most rows are left untouched); in one pass, in
-    vocabulary chunks of 32 tiles, or in passes of the smallest G scratch."""
+    vocabulary chunks of 32 tiles, or in passes of the smallest G scratch.  The autograd
+    op gives the same dC with the fill in its forward (opt-in) and without it."""
     with m._ext.backward_options(**SPLITS[split]):
-        _zero_fill_case(m, cuda)
+        _zero_fill_case(m, cuda, split)
 
 
-def _zero_fill_case(m, cuda):
+def _zero_fill_case(m, cuda, split):
     e, c, t = _peaked(cuda, N=384, D=256, V=9000, seed=13)
     plain = m._ext.forward(e, c, t, None, -100)
     buf = torch.full_like(c, float("nan"))
@@ -584,11 +585,14 @@ def _zero_fill_case(m, cuda):
     kept, total, _ = stats.tolist()
     assert 0 < kept < total
     assert torch.equal(dC.view(torch.int16), dC_ref.view(torch.int16))
-    # the autograd path uses it: same gradients as through the ordinary backward
-    e2 = e.detach().clone().requires_grad_(True)
-    c2 = c.detach().clone().requires_grad_(True)
-    m.linear_cross_entropy(e2, c2, t).backward()
-    assert torch.equal(c2.grad.view(torch.int16), dC_ref.view(torch.int16))
+    # the autograd path, with the fill in the forward (opt-in) or not (the default):
+    # the same gradients as through the ordinary backward
+    for fill in ("forward", "backward"):
+        e2 = e.detach().clone().requires_grad_(True)
+        c2 = c.detach().clone().requires_grad_(True)
+        with m._ext.backward_options(**SPLITS[split], dc_zero_fill=fill):
+            m.linear_cross_entropy(e2, c2, t).backward()
+        assert torch.equal(c2.grad.view(torch.int16), dC_ref.view(torch.int16)), fill
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])

@@ -282,3 +282,20 @@ def test_package_exports_reference_api(ext):
                  "LinearCrossEntropy", "FILTER_LOG_EPS"):
         assert hasattr(m, name), name
     assert abs(m.FILTER_LOG_EPS - math.log(2.0 ** -12)) < 1e-9
+
+
+def test_backward_options_are_scoped_and_validated(ext):
+    """backward_options sets the overrides inside its block only (the dC zero fill in
+    the backward by default) and refuses unknown values before anything runs."""
+    assert ext._bwd_opts["dc_zero_fill"] == "backward" and ext._bwd_opts["flags"] == 0
+    with ext.backward_options(dc_zero_fill="forward", g_tasks="blocks", max_g_tiles=7):
+        assert ext._bwd_opts["dc_zero_fill"] == "forward"
+        assert ext._bwd_opts["flags"] == ext.CCE_BWD_G_TASKS_BY_BLOCK and ext._bwd_opts["max_g_tiles"] == 7
+    assert ext._bwd_opts == {"flags": 0, "max_g_tiles": 0, "max_chunk_tiles": 0, "dc_zero_fill": "backward"}
+    with pytest.raises(ValueError, match="dc_zero_fill"):
+        with ext.backward_options(dc_zero_fill="sometimes"):
+            pass
+    with pytest.raises(KeyError):
+        with ext.backward_options(g_precision="triple"):
+            pass
+    assert ext._bwd_opts["dc_zero_fill"] == "backward"
