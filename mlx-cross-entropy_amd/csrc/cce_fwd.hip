@@ -87,10 +87,11 @@ __device__ __forceinline__ void fwd_store_pending(const FwdArgs& a, const FwdPen
   }
 }
 
-// How a tile kernel adds the bias: none; from global memory (fwd_add_bias); or
-// staged through LDS (fwd_stage_bias / fwd_add_bias_lds), when the bias is 16-byte
-// aligned and V * sizeof(T) is a multiple of 16 (no 16-byte piece of the bias then
-// straddles its end).
+// How a tile kernel adds the bias: none; from global memory after the contraction
+// (fwd_add_bias); or as the accumulators' starting value, staged through LDS
+// (fwd_stage_bias / fwd_init_bias_lds), when the bias is 16-byte aligned and
+// V * sizeof(T) is a multiple of 16 (no 16-byte piece of the bias then straddles its
+// end).  The two orders of the fp32 sums differ in the last bits.
 enum FwdBias { kBiasNone = 0, kBiasGlobal = 1, kBiasLds = 2 };
 
 // The bias of the wave's 128 vocabulary rows added to a tile's logits.  The tile
@@ -116,12 +117,14 @@ __device__ __forceinline__ void fwd_add_bias(const FwdArgs& a, f32x16 (&acc)[TI]
 }
 
 // The bias through LDS (kBiasLds).  Per tile the block's kFwdVocab bias values (1
-// KiB at most; zeros past V) are copied into one of two LDS buffers by one LDS-DMA
-// load of wave 0, issued ahead of the tile's pipeline fill, so that the first stage
-// barrier, which waits for all of a wave's loads, covers it.  The epilogue then reads
-// them from LDS instead of waiting on 64 global loads per lane (2.5% of the forward
-// at N = 4096, D = 2304, V = 256000).  The buffers alternate by tile: one is rewritten
-// only after every wave has passed the stage barriers of the tile in between.
+// KiB at most; zeros past V) are copied into an LDS buffer by one LDS-DMA load of
+// wave 0, issued ahead of the tile's pipeline fill, so that the tile's first stage
+// barrier, which waits for all of a wave's loads, covers it.  Right after that barrier
+// the accumulators are set to the bias (fwd_init_bias_lds), and the MFMAs add the
+// products to it: no bias work is left in the epilogue, where 64 global loads per
+// lane cost 7% of the forward at N = 4096, D = 2304, V = 256000 (adding from LDS
+// there still 4%: the added registers spilled).  The buffer is rewritten at the end
+// of the tile that read it, after every wave has passed the tile's stage barriers.
 constexpr int kBiasLdsBytes = 1024;
 static_assert(kFwdVocab * 4 <= kBiasLdsBytes, "one LDS-DMA load holds a block's bias");
 // The lane index, formed where it is used: a value the compiler cannot hoist out of the
@@ -142,8 +145,9 @@ __device__ __forceinline__ void fwd_stage_bias(const FwdArgs& a, int vb, char* b
                                                   : reinterpret_cast<const char*>(g_zero16);
   dma16(g, __builtin_amdgcn_readfirstlane(lds_addr(buf)));
 }
+// acc[i][j][r] = the bias of the register's vocabulary column (see fwd_epilogue's layout).
 template <typename T, int TI, int TJ>
-__device__ __forceinline__ void fwd_add_bias_lds(const char* buf, f32x16 (&acc)[TI][TJ]) {
+__device__ __forceinline__ void fwd_init_bias_lds(const char* buf, f32x16 (&acc)[TI][TJ]) {
   const int lane = lane_here();
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int c0 = (wave & 1) * 128 + (lane >> 5) * 4;
@@ -167,7 +171,7 @@ __device__ __forceinline__ void fwd_add_bias_lds(const char* buf, f32x16 (&acc)[
 #pragma unroll
       for (int k = 0; k < 4; ++k)
 #pragma unroll
-        for (int j = 0; j < TJ; ++j) acc[i][j][4 * q + k] += add[k];
+        for (int j = 0; j < TJ; ++j) acc[i][j][4 * q + k] = add[k];
     }
   }
 }
@@ -276,7 +280,7 @@ __global__ __launch_bounds__(FwdLoop<T>::NTHREADS, 1) void fwd_tile_kernel(FwdAr
   using Loop = FwdLoop<T>;
   constexpr int TI = Loop::TI, TJ = Loop::TJ;
   __shared__ __attribute__((aligned(16))) char smem[Loop::SMEM_BYTES];
-  __shared__ __attribute__((aligned(16))) char bias_lds[BIAS == kBiasLds ? 2 * kBiasLdsBytes : 16];
+  __shared__ __attribute__((aligned(16))) char bias_lds[BIAS == kBiasLds ? kBiasLdsBytes : 16];
 
   const int xcd = blockIdx.x & 7;
   const int member = blockIdx.x >> 3;
@@ -330,7 +334,6 @@ __global__ __launch_bounds__(FwdLoop<T>::NTHREADS, 1) void fwd_tile_kernel(FwdAr
     zero_upto(z1);
     return;
   }
-  int bias_buf = 0;  // the LDS bias buffer of the current tile
   if constexpr (BIAS == kBiasLds) fwd_stage_bias<T>(a, vb, bias_lds);
   auto src = sources(tb, vb);
   Loop::template prefetch<RAGGED>(src, smem);
@@ -346,10 +349,16 @@ __global__ __launch_bounds__(FwdLoop<T>::NTHREADS, 1) void fwd_tile_kernel(FwdAr
     for (int i = 0; i < TI; ++i)
 #pragma unroll
       for (int j = 0; j < TJ; ++j) acc[i][j] = zero16();
+    // kBiasLds: the accumulators start from the tile's bias (in LDS after the first stage barrier)
     if constexpr (S32) {
-      Loop::template consume<RAGGED>(src, smem, acc);
+      Loop::template consume<RAGGED>(src, smem, acc, [&]() {
+        if constexpr (BIAS == kBiasLds) fwd_init_bias_lds<T>(bias_lds, acc);
+      });
     } else {
-      Loop::template consume<RAGGED>(src, smem, acc, [&]() { fwd_store_pending(a, pend, ptb, pvb); });
+      Loop::template consume<RAGGED>(src, smem, acc, [&]() {
+        if constexpr (BIAS == kBiasLds) fwd_init_bias_lds<T>(bias_lds, acc);
+        fwd_store_pending(a, pend, ptb, pvb);
+      });
     }
 
     // Start the next tile's pipeline fill and target reads, then reduce this
@@ -358,12 +367,8 @@ __global__ __launch_bounds__(FwdLoop<T>::NTHREADS, 1) void fwd_tile_kernel(FwdAr
     const int rn = next_round(r + 1, tbn, vbn);
     int64_t tgn[TJ];
     if constexpr (BIAS == kBiasGlobal) fwd_add_bias<T>(a, acc, vb);
-    if constexpr (BIAS == kBiasLds) {
-      fwd_add_bias_lds<T>(bias_lds + bias_buf * kBiasLdsBytes, acc);
-      bias_buf ^= 1;
-    }
     if (rn < r_end) {
-      if constexpr (BIAS == kBiasLds) fwd_stage_bias<T>(a, vbn, bias_lds + bias_buf * kBiasLdsBytes);
+      if constexpr (BIAS == kBiasLds) fwd_stage_bias<T>(a, vbn, bias_lds);
       src = sources(tbn, vbn);
       Loop::template prefetch<RAGGED>(src, smem);
       targets(tbn, tgn);

@@ -323,11 +323,13 @@ def test_ragged_shapes(m, cuda, N, D, V):
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("V", [2048, 2000, 1001])
 def test_forward_bias_staged_in_lds(m, cuda, dtype, V):
-    """The forward adds a 16-byte aligned bias whose V * element size is a multiple of
-    16 from LDS (one LDS-DMA copy per tile, zeros past V: V = 2000 ends in a partial
-    vocabulary block), any other bias from global memory.  An unaligned view of the
-    same values takes the global path: the statistics, lse and loss are equal bit for
-    bit, and the loss matches the oracle."""
+    """The forward starts the accumulators from a 16-byte aligned bias whose V * element
+    size is a multiple of 16, staged in LDS (one LDS-DMA copy per tile, zeros past V:
+    V = 2000 ends in a partial vocabulary block); any other bias it adds after the
+    contraction, from global memory.  An unaligned view of the same values takes the
+    global path: the two orders of the fp32 sums agree to a few ulps (measured at c4:
+    lse within 1.9e-6), each path is deterministic, and the loss matches the oracle.
+    With V = 1001 (2002 bytes) both views take the global path: bit for bit."""
     ext = m._ext
     N, D = 300, 96
     e, c, t = normal_case(N, D, V, dtype, cuda, seed=V, std=0.1)
@@ -339,10 +341,18 @@ def test_forward_bias_staged_in_lds(m, cuda, dtype, V):
     b_un = off[1:V + 1]  # the same values, 2 or 4 bytes past a 16-byte boundary
     assert b_al.data_ptr() % 16 == 0 and b_un.data_ptr() % 16 != 0
     lds = ext.forward(e, c, t, b_al, -100)
+    lds2 = ext.forward(e, c, t, b_al, -100)
     glob = ext.forward(e, c, t, b_un, -100)
     torch.cuda.synchronize()
+    same_path = V * b_al.element_size() % 16 != 0
     for k, name in ((0, "tile_max"), (1, "tile_sum_exp"), (3, "lse"), (4, "nll")):
-        assert torch.equal(lds[k], glob[k]), name
+        assert torch.equal(lds[k], lds2[k]), name
+        if same_path:
+            assert torch.equal(lds[k], glob[k]), name
+        else:
+            err = (lds[k] - glob[k]).abs().max().item()
+            print(f"V={V} {dtype}: {name} LDS vs global path max diff {err:.2e}")
+            torch.testing.assert_close(lds[k], glob[k], rtol=1e-5, atol=1e-5)
     ref = O.linear_cross_entropy(f64(e), f64(c), t.cpu().numpy(), f64(b_al), "none")
     tol = 1e-5 if dtype == torch.float32 else 2e-3
     np.testing.assert_allclose(f64(lds[4]), ref, rtol=tol, atol=tol)
