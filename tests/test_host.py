@@ -299,3 +299,25 @@ def test_backward_options_are_scoped_and_validated(ext):
         with ext.backward_options(g_precision="triple"):
             pass
     assert ext._bwd_opts["dc_zero_fill"] == "backward"
+
+
+def test_python_workspace_size_follows_the_filter(ext):
+    """_ext.workspace_size: without a filter argument the size any filter needs (the hi /
+    lo pair's slots); with filter_eps (None: the filter off) the exact size of that
+    backward, which is what backward() allocates."""
+    N, D, V = 8192, 4096, 128256
+    e = torch.empty((N, D), dtype=torch.bfloat16)
+    c = torch.empty((V, D), dtype=torch.bfloat16)
+    lib = ext.lib()
+    anyf = ext.workspace_size(e, c, True, True, False)
+    assert anyf == lib.cce_backward_workspace_size(2, N, D, V, 1, 1, 0)
+    assert ext.workspace_size(e, c, True, True, False, filter_eps=None) == anyf
+    on = ext.workspace_size(e, c, True, True, False, filter_eps=ext.FILTER_LOG_EPS)
+    assert on == anyf - 8192 * 128 * 128 * 2  # 8192 slots of 32 KiB instead of 64
+    with ext.backward_options(g_precision="pair"):
+        assert ext.workspace_size(e, c, True, True, False, filter_eps=ext.FILTER_LOG_EPS) == anyf
+    with ext.backward_options(g_precision="single"):
+        assert ext.workspace_size(e, c, True, True, False, filter_eps=None) == on
+    f32 = torch.empty((N, D), dtype=torch.float32), torch.empty((V, D), dtype=torch.float32)
+    assert ext.workspace_size(*f32, True, True, False, filter_eps=ext.FILTER_LOG_EPS) == \
+        ext.workspace_size(*f32, True, True, False)
