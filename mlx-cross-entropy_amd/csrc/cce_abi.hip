@@ -41,7 +41,7 @@ size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 constexpr int kBwdFlags = CCE_BWD_DC_ZEROED | CCE_BWD_TOKENS_INPUT | CCE_BWD_TOKENS_SORTED | CCE_BWD_DE_SUMS_WIDE |
                           CCE_BWD_DE_SUMS_NARROW | CCE_BWD_DC_SUMS_WIDE | CCE_BWD_DC_SUMS_NARROW | CCE_BWD_REF_STATS |
                           CCE_BWD_DEVICE_PASSES | CCE_BWD_G_PAIR | CCE_BWD_G_SINGLE | CCE_BWD_DC_OWNER_TASKS |
-                          CCE_BWD_G_TASKS_BY_BLOCK;
+                          CCE_BWD_G_TASKS_BY_BLOCK | CCE_BWD_DE_WHOLE_TASKS;
 // Flags of which at most one may be set.
 constexpr int kBwdFlagPairs[4][2] = {{CCE_BWD_TOKENS_INPUT, CCE_BWD_TOKENS_SORTED},
                                      {CCE_BWD_DE_SUMS_WIDE, CCE_BWD_DE_SUMS_NARROW},
@@ -382,6 +382,7 @@ int backward_impl(int dtype, const void* e, const void* c, const void* bias, con
   a.gtile = (dE || dC) ? ws + P.gtile : nullptr;
   a.colsum = dBias ? reinterpret_cast<float*>(ws + P.colsum) : nullptr;
   a.de_acc = P.carry ? reinterpret_cast<float*>(ws + P.de_acc) : nullptr;
+  a.de_part = P.de_pieces && !(flags & CCE_BWD_DE_WHOLE_TASKS) ? reinterpret_cast<float*>(ws + P.de_part) : nullptr;
   if (P.perm_ok) {
     a.perm = reinterpret_cast<int*>(ws + P.perm);
     a.sort_buf = reinterpret_cast<uint32_t*>(ws + P.sort_buf);

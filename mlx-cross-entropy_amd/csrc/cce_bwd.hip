@@ -2560,6 +2560,10 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_narrow_kernel(BwdArgs a, 
   if (PHASE == 1 && a.dc_geo == 0 && a.filter_log_eps > -INFINITY && ldu(pi, kPiDcWide) != 0) return;
   const int s0 = ldu(pi, kPiS0);  // the G scratch holds slot s at s - s0
   const int ntasks = ldu(pi, PHASE == 0 ? kPiOwnRb : kPiOwnVt) * nds;
+  // dE pieces: P per task when there are few tasks (items ntasks * npc <= kDePartSlots)
+  const int pcap = (int)gridDim.x < kDePartSlots ? (int)gridDim.x : kDePartSlots;
+  const int npc = PHASE == 0 && a.de_part != nullptr && ntasks > 0 && 4 * ntasks <= pcap ? pcap / ntasks : 1;
+  const int nitems = ntasks * npc;
   const int* own = PHASE == 0 ? a.own_rb + pass * nrb : a.own_vt + ldu(pi, kPiVt0);
   const int* ostart = PHASE == 0 ? a.rb_start + pass * nrb : a.vt_start;  // an owner's slots / vt_slot entries
   const int vwg = xcd * nper + lidx, nwg = (int)gridDim.x;  // workgroups numbered XCD-major
@@ -2577,7 +2581,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_narrow_kernel(BwdArgs a, 
   const RowData rd = row_data(a);
   const char* X = PHASE == 0 ? reinterpret_cast<const char*>(a.c) : rd.e;
   const int64_t xrows = PHASE == 0 ? a.V : a.N;
-  const int mode = PHASE == 0 ? pmode : kWriteT;
+  const int mode = PHASE == 0 ? (npc > 1 ? kPartF32 : pmode) : kWriteT;
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -2635,13 +2639,25 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_narrow_kernel(BwdArgs a, 
     int q, owner, ds, b, cnt, j, h, slot;
     int64_t xrow;
   };
+  // dE pieces (npc > 1): items number at most the workgroups, so workgroup vwg has item
+  // vwg alone, piece k = vwg % npc of task vwg / npc: its tiles [j0, j1) of the task's
+  // (none when the task has fewer tiles than pieces)
+  int pc_j0 = 0, pc_j1 = 0;
+  if (PHASE == 0 && npc > 1 && vwg < nitems) {
+    const int task = vwg / npc, k = vwg - task * npc;
+    const int ow = ldu(own, task / nds);
+    const int cnt = ldu(ostart, ow + 1) - ldu(ostart, ow);
+    pc_j0 = k * cnt / npc;
+    pc_j1 = (k + 1) * cnt / npc;
+  }
   auto seek = [&](int q, Cur& c) -> bool {
     int owner, ds;
     if constexpr (PHASE == 0) {
       const int p = q * nwg + ((q & 1) ? nwg - 1 - vwg : vwg);
-      if (p >= ntasks) return false;
-      owner = ldu(own, p / nds);
-      ds = p - (p / nds) * nds;
+      if (p >= nitems || (npc > 1 && pc_j0 == pc_j1)) return false;
+      const int task = p / npc;
+      owner = ldu(own, task / nds);
+      ds = task - (task / nds) * nds;
     } else {  // the q-th owner of this workgroup's bin (then the same again at slice ds0 + nwg, ...)
       if (bcnt == 0) return false;
       const int t = q / bcnt;
@@ -2653,8 +2669,8 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_narrow_kernel(BwdArgs a, 
     c.q = q;
     c.owner = owner;
     c.ds = ds;
-    c.b = b;
-    c.cnt = ldu(ostart, owner + 1) - b;
+    c.b = b + pc_j0;
+    c.cnt = npc > 1 ? pc_j1 - pc_j0 : ldu(ostart, owner + 1) - b;
     c.j = 0;
     c.h = 0;
     return true;
@@ -2796,6 +2812,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_narrow_kernel(BwdArgs a, 
 #pragma unroll
         for (int jj = 0; jj < 2; ++jj) acc[i][jj] *= gdiv;
     }
+
     const int64_t orow0 = (int64_t)(PHASE == 0 ? c.owner : vlo + c.owner) * 128;
     const int64_t orows = PHASE == 0 ? a.N : a.V;
     const int64_t nrows = orows - orow0 < 128 ? orows - orow0 : 128;
@@ -2889,7 +2906,11 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_narrow_kernel(BwdArgs a, 
         }
       }
     } else {
-      float* carry = a.de_acc + orow0 * D;
+      // the fp32 carry rows of the owner, or (kPartF32) the piece's slot: 128 rows of
+      // the D slice's kDePartCols columns, stored like kStoreF32
+      float* carry = mode == kPartF32 ? a.de_part + (size_t)vwg * (kBwdTokens * kDePartCols) - (int64_t)c.ds * kDePartCols
+                                      : a.de_acc + orow0 * D;
+      const int64_t cstride = mode == kPartF32 ? kDePartCols : D;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
 #pragma unroll
@@ -2901,8 +2922,8 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_narrow_kernel(BwdArgs a, 
             const int64_t d = d00 + 32 * i + 8 * q;
             if (d >= D) continue;
             f32x4 v{acc[i][jj][4 * q], acc[i][jj][4 * q + 1], acc[i][jj][4 * q + 2], acc[i][jj][4 * q + 3]};
-            f32x4* cp = reinterpret_cast<f32x4*>(carry + m * D + d);
-            if (mode == kStoreF32) {
+            f32x4* cp = reinterpret_cast<f32x4*>(carry + m * cstride + d);
+            if (mode == kStoreF32 || mode == kPartF32) {
               *cp = v;
             } else if (mode == kAddF32) {
               *cp = *cp + v;
@@ -3098,6 +3119,65 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_narrow_kernel(BwdArgs a, 
   }
 }
 
+// ---------------------------------------------------------------- 5b. dE pieces
+// The narrow dE sums cut each of a pass's few tasks (token block, D slice) into npc
+// pieces along its kept tiles (kPartF32): here the pieces' fp32 sums are added in piece
+// order and dE is written in the pass's mode, as the sums' epilogue writes a whole
+// task.  Four workgroups per task, 32 of its rows each; a thread takes 4 columns of
+// 8 rows.
+template <typename T>
+__global__ __launch_bounds__(256) void bwd_de_pieces_kernel(BwdArgs a, int chunk, int pass, int nwg) {
+  (void)chunk;
+  const int* pi = a.pinfo + pass * kPassInts;
+  const int mode = ldu(pi, kPiDeMode);
+  if (mode < 0 || a.de_part == nullptr) return;
+  const int nrb = (int)a.plan.nrb;
+  const int nds = (int)((a.D + kDePartCols - 1) / kDePartCols);
+  const int ntasks = ldu(pi, kPiOwnRb) * nds;
+  const int pcap = nwg < kDePartSlots ? nwg : kDePartSlots;
+  if (ntasks == 0 || 4 * ntasks > pcap) return;  // the sums ran whole tasks
+  const int npc = pcap / ntasks;
+  const int task = (int)(blockIdx.x >> 2);
+  if (task >= ntasks) return;
+  const int owner = ldu(a.own_rb + pass * nrb, task / nds);
+  const int ds = task - (task / nds) * nds;
+  const int* rbs = a.rb_start + pass * nrb;
+  const int cnt = ldu(rbs, owner + 1) - ldu(rbs, owner);
+  const RowData rd = row_data(a);
+  const int64_t D = a.D;
+  const int64_t orow0 = (int64_t)owner * kBwdTokens;
+  const int64_t nrows = a.N - orow0 < kBwdTokens ? a.N - orow0 : kBwdTokens;
+  const int col = (int)(threadIdx.x & 63) * 4;
+  const int64_t d = (int64_t)ds * kDePartCols + col;
+  if (d >= D) return;  // D is a multiple of 4: the 4 columns are inside
+  T* dE = reinterpret_cast<T*>(a.dE);
+  for (int rr = 0; rr < 8; ++rr) {
+    const int m = (int)(blockIdx.x & 3) * 32 + rr * 4 + (int)(threadIdx.x >> 6);
+    if (m >= nrows) break;
+    f32x4 sum{0.f, 0.f, 0.f, 0.f};
+    for (int k = 0; k < npc; ++k) {
+      if (k * cnt / npc == (k + 1) * cnt / npc) continue;  // an empty piece (never written)
+      sum += *reinterpret_cast<const f32x4*>(a.de_part + ((size_t)(task * npc + k) * kBwdTokens + m) * kDePartCols + col);
+    }
+    const int64_t orow = rd.map ? (int64_t)rd.map[orow0 + m] : orow0 + m;
+    if (mode != kWriteT) {
+      f32x4* cp = reinterpret_cast<f32x4*>(a.de_acc + (orow0 + m) * D + d);
+      if (mode == kStoreF32) {
+        *cp = sum;
+        continue;
+      }
+      if (mode == kAddF32) {
+        *cp = *cp + sum;
+        continue;
+      }
+      sum = *cp + sum;  // kFinishT
+    }
+    T* o = dE + orow * D + d;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) o[k] = (T)sum[k];
+  }
+}
+
 // ---------------------------------------------------------------- 6. dBias
 // One workgroup per vocab tile of the pass: the sum of its slots' column sums.
 template <typename T>
@@ -3279,6 +3359,11 @@ static hipError_t backward_typed(const BwdArgs& a, hipStream_t s, hipEvent_t pas
       if (want_de) {
         launch_sum<T, 0>(ac, wide_de, chunk, pass, gp, s);
         if ((e2 = hipGetLastError()) != hipSuccess) return e2;
+        if (!wide_de && a.de_part != nullptr) {  // the pieces of a pass with few dE tasks
+          hipLaunchKernelGGL((bwd_de_pieces_kernel<T>), dim3((unsigned)kDePartSlots), dim3(256), 0, s, a, chunk,
+                             pass, gp);
+          if ((e2 = hipGetLastError()) != hipSuccess) return e2;
+        }
       }
       if (want_dc) {
         const bool narrow = auto_dc ? dc_pick != 1 : !wide_dc;

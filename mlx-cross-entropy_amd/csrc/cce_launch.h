@@ -138,7 +138,14 @@ enum PassField {
 // dE write mode of a pass: one pass over everything writes dE directly; with more
 // passes (or chunks) dE is summed in an fp32 carry: the first pass stores it, the
 // middle ones add to it, the last one adds and writes dE.
-enum WriteMode { kWriteT = 0, kStoreF32 = 1, kAddF32 = 2, kFinishT = 3 };
+enum WriteMode { kWriteT = 0, kStoreF32 = 1, kAddF32 = 2, kFinishT = 3, kPartF32 = 4 };
+// dE pieces: when a pass has at most a quarter as many (token block, D slice) tasks as
+// workgroups (or kDePartSlots), the narrow dE sums cut each task along its kept tiles
+// into P pieces; a piece's fp32 sums go to its own slot of the de_part scratch (mode
+// kPartF32) and bwd_de_pieces_kernel adds a task's pieces in order and writes dE in the
+// pass's mode.
+constexpr int kDePartSlots = 256;  // pieces at most (fp32 slots of 128 x 256 sums)
+constexpr int kDePartCols = 256;   // the narrow sums' D slice
 
 struct BwdPlan {
   int64_t nvt, nrb, total;  // vocab tiles, token blocks, pairs
@@ -153,9 +160,10 @@ struct BwdPlan {
   int esize;                // bytes of one input element
   bool perm_ok;             // the sorted token order is available (N and tile count in range)
   bool carry;               // the fp32 dE carry is reserved (more than one pass or chunk may run)
+  bool de_pieces;           // the dE pieces' slots are reserved (few dE tasks possible)
   // workspace byte offsets
   size_t bits, counts, pinfo, rb_start, slot_vt, slot_rb, vt_start, vt_slot, g_task, g_task_rb, own_rb, own_vt,
-      dc_bin_start, dc_bin_owner, dc_blk_task, dc_blk_own, gtile, colsum, de_acc;
+      dc_bin_start, dc_bin_owner, dc_blk_task, dc_blk_own, gtile, colsum, de_acc, de_part;
   size_t perm, sort_buf, rowbits, bits_p, t_perm, lse_perm, dnll_perm, e_perm;  // sorted order (perm_ok)
   size_t qrows;  // dequantized classifier rows of one chunk (quantized classifier only)
   size_t total_bytes;
@@ -228,6 +236,10 @@ inline BwdPlan make_bwd_plan_cap(size_t esize, int64_t N, int64_t D, int64_t V, 
   P.gtile = want_g ? take((size_t)P.cap * P.g_bytes) : 0;
   P.colsum = want_db ? take((size_t)P.cap * kBwdVocab * sizeof(float)) : 0;
   P.de_acc = P.carry ? take((size_t)N * (size_t)D * sizeof(float)) : 0;
+  // the most dE tasks a pass can have (every token block x the narrow D slices) leave
+  // four workgroups per task or more on a 256-CU part
+  P.de_pieces = want_de && P.nrb * ((D + kDePartCols - 1) / kDePartCols) * 4 <= kDePartSlots;
+  P.de_part = P.de_pieces ? take((size_t)kDePartSlots * kBwdTokens * kDePartCols * sizeof(float)) : 0;
   // (dE rows are then written through the map with one buffer over all of dE: < 2^31 bytes)
   P.perm_ok = perm && N <= kPermMaxN && P.nvt + 1 <= kPermMaxKey && (want_g || want_db) &&
               (double)N * (double)D * (double)esize < 2147483648.0;
@@ -345,6 +357,7 @@ struct BwdArgs {
   char* gtile;        // [cap] G tiles of one pass, token-major (g_tile_bytes each)
   float* colsum;      // [cap][128] per-slot column sums of G (dBias)
   float* de_acc;      // [N, D] fp32, only when the plan reserves the carry
+  float* de_part;     // [kDePartSlots][128][kDePartCols] fp32 sums of the dE pieces, or null (whole tasks)
   int64_t* tile_stats;  // [3] or null: kept pairs, all pairs, kept pairs of the input-order token blocks
   BwdPlan plan;
   int num_cus;

@@ -79,6 +79,7 @@ CCE_BWD_G_PAIR = 512
 CCE_BWD_G_SINGLE = 1024
 CCE_BWD_DC_OWNER_TASKS = 2048
 CCE_BWD_G_TASKS_BY_BLOCK = 4096
+CCE_BWD_DE_WHOLE_TASKS = 8192
 REF_STAT_TILE = 32
 
 # Overrides of choices the backward otherwise makes itself, for tests and tuning
@@ -89,7 +90,8 @@ _bwd_opts = {"flags": 0, "max_g_tiles": 0, "max_chunk_tiles": 0, "dc_zero_fill":
 
 @contextlib.contextmanager
 def backward_options(token_order=None, de_sums=None, dc_sums=None, max_g_tiles=0, max_chunk_tiles=0,
-                     passes=None, g_precision=None, dc_tasks=None, g_tasks=None, dc_zero_fill=None):
+                     passes=None, g_precision=None, dc_tasks=None, g_tasks=None, dc_zero_fill=None,
+                     de_tasks=None):
     """Within the block, backward() calls run with these overrides:
     token_order "input" | "sorted" (128-row token blocks of the input order, or of the
     rows grouped by target tile); de_sums / dc_sums "wide" | "narrow" (512- or
@@ -102,7 +104,8 @@ def backward_options(token_order=None, de_sums=None, dc_sums=None, max_g_tiles=0
     with the filter off and a single rounding with it on); dc_tasks "owners" (the
     narrow dC sums run one-tile owners as owner tasks, not grouped by token block);
     g_tasks "blocks" (the G kernel's tasks are token blocks with up to 4 kept tiles,
-    never vocabulary tiles with up to 4 kept blocks); dc_zero_fill "forward" (the
+    never vocabulary tiles with up to 4 kept blocks); de_tasks "whole" (the dE sums never
+    cut a (token block, D slice) task into pieces); dc_zero_fill "forward" (the
     autograd op has the forward's tile kernel zero dC, cce_forward_ex, and the backward
     write only the rows of kept tiles, CCE_BWD_DC_ZEROED) | "backward" (the default:
     the backward zeroes the rows no kept tile touches)."""
@@ -111,6 +114,7 @@ def backward_options(token_order=None, de_sums=None, dc_sums=None, max_g_tiles=0
     flags |= {None: 0, "host": 0, "device": CCE_BWD_DEVICE_PASSES}[passes]
     flags |= {None: 0, "blocks": 0, "owners": CCE_BWD_DC_OWNER_TASKS}[dc_tasks]
     flags |= {None: 0, "tiles": 0, "blocks": CCE_BWD_G_TASKS_BY_BLOCK}[g_tasks]
+    flags |= {None: 0, "pieces": 0, "whole": CCE_BWD_DE_WHOLE_TASKS}[de_tasks]
     flags |= {None: 0, "input": CCE_BWD_TOKENS_INPUT, "sorted": CCE_BWD_TOKENS_SORTED}[token_order]
     flags |= {None: 0, "wide": CCE_BWD_DE_SUMS_WIDE, "narrow": CCE_BWD_DE_SUMS_NARROW}[de_sums]
     flags |= {None: 0, "wide": CCE_BWD_DC_SUMS_WIDE, "narrow": CCE_BWD_DC_SUMS_NARROW}[dc_sums]

@@ -672,6 +672,38 @@ def test_vocabulary_chunks(m, cuda, dtype, filtered, de_sums, split):
         assert err < tol, (name, err)
 
 
+DE_SPLITS = {"one": {}, "passes": dict(max_g_tiles=1), "chunks": dict(max_chunk_tiles=32)}
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("split", ["one", "passes", "chunks"])
+@pytest.mark.parametrize("order", ["sorted", "input"])
+def test_de_pieces_match_whole_tasks(m, cuda, dtype, split, order):
+    """With few dE tasks (here 3 token blocks x 2 D slices for 256 workgroups) the narrow
+    dE sums cut each task into pieces along its kept tiles, whose fp32 sums a finishing
+    kernel adds in order: dE equals the whole tasks' (CCE_BWD_DE_WHOLE_TASKS) to the
+    fp32 sums' reassociation, in one pass (written directly), in passes and chunks (the
+    fp32 carry's store / add / finish modes), with the rows sorted by target tile or in
+    input order; repeated runs are equal bit for bit, and dC / dBias do not change."""
+    N, D, V = 300, 264, 9000
+    e, c, t = normal_case(N, D, V, dtype, cuda, seed=31, std=0.05)
+    t[5] = -100
+    gb = torch.Generator(device=cuda).manual_seed(32)
+    b = (torch.randn(V, generator=gb, device=cuda) * 0.1).to(dtype)
+    feps = m.FILTER_LOG_EPS
+    with m._ext.backward_options(token_order=order, **DE_SPLITS[split]):
+        pieces = run(m, e, c, t, b, reduction="sum", filter_eps=feps)
+        again = run(m, e, c, t, b, reduction="sum", filter_eps=feps)
+    with m._ext.backward_options(token_order=order, de_tasks="whole", **DE_SPLITS[split]):
+        whole = run(m, e, c, t, b, reduction="sum", filter_eps=feps)
+    for x, y in zip(pieces[1:], again[1:]):
+        assert torch.equal(x, y)
+    err = O.rel_fro(f64(pieces[1]), f64(whole[1]))
+    print(f"{dtype} {split} {order}: dE pieces vs whole {err:.2e}")
+    assert err < (1e-5 if dtype == torch.float32 else 2e-3), err
+    assert torch.equal(pieces[2], whole[2]) and torch.equal(pieces[3], whole[3])
+
+
 @pytest.mark.parametrize("sizing", ["exact", "pair", "least"])
 def test_rounded_once_g_workspace_sizes(m, cuda, sizing):
     """A bf16 backward with the filter on keeps G rounded once in 32 KiB tile slots.

@@ -135,7 +135,7 @@ def test_workspace_size_follows_the_g_layout(ext, N, D, V):
     assert size(2, off, 0, 1) == lib.cce_backward_workspace_size_ex(2, N, D, V, 1, 1, 1, 1, 0)
     # invalid filter or flags: 0
     assert size(2, ctypes.c_float(float("nan"))) == 0
-    assert size(2, eps, 1 << 13) == 0
+    assert size(2, eps, 1 << 14) == 0
     assert size(2, eps, ext.CCE_BWD_G_PAIR | ext.CCE_BWD_G_SINGLE) == 0
     assert size(2, eps, ext.CCE_BWD_TOKENS_INPUT | ext.CCE_BWD_TOKENS_SORTED) == 0
 
@@ -179,7 +179,7 @@ def test_backward_validation_errors(ext):
     assert _bwd(lib, ext, dbias=FAKE) == ext.CCE_ERR_INVALID_ARGUMENT  # dBias without bias
     assert _bwd(lib, ext, eps=float("nan")) == ext.CCE_ERR_INVALID_ARGUMENT
     assert _bwd(lib, ext, dtype=3) == ext.CCE_ERR_UNSUPPORTED_DTYPE
-    assert _bwd_ex(lib, flags=1 << 13) == ext.CCE_ERR_INVALID_ARGUMENT  # unknown flag
+    assert _bwd_ex(lib, flags=1 << 14) == ext.CCE_ERR_INVALID_ARGUMENT  # unknown flag
     assert b"unknown flags" in lib.cce_last_error()
     assert _bwd_ex(lib, flags=ext.CCE_BWD_G_PAIR | ext.CCE_BWD_G_SINGLE) == ext.CCE_ERR_INVALID_ARGUMENT
     assert _bwd_ex(lib, flags=ext.CCE_BWD_TOKENS_INPUT | ext.CCE_BWD_TOKENS_SORTED) == ext.CCE_ERR_INVALID_ARGUMENT
@@ -215,7 +215,7 @@ def test_noalloc_validation(ext):
     assert _noalloc(lib, N=8192, D=4096, V=128256) == ext.CCE_ERR_WORKSPACE
     msg = lib.cce_last_error()
     assert b"static scratch" in msg and b"N=8192" in msg
-    assert _noalloc(lib, flags=1 << 13) == ext.CCE_ERR_INVALID_ARGUMENT
+    assert _noalloc(lib, flags=1 << 14) == ext.CCE_ERR_INVALID_ARGUMENT
     assert _noalloc(lib, N=0) == ext.CCE_ERR_INVALID_ARGUMENT
     if not gpu_available():  # fits: stops at the device lookup
         assert _noalloc(lib) == ext.CCE_ERR_NO_DEVICE

@@ -14,7 +14,10 @@ row, an index past its array, two writers of one slot -- fails here, on the CPU:
   the MFMA register layout to whole 128-byte row pieces, free of LDS bank conflicts;
 - the G task lists (`bwd_compact_kernel`) in their three kinds, against the slots they
   must cover: every kept pair once, in runs of at most R slots of one (pass, token block),
-  or of at most 4 vt_slot entries of one vocabulary tile.
+  or of at most 4 vt_slot entries of one vocabulary tile;
+- the dE sums' pieces (`bwd_sum_narrow_kernel`, `bwd_de_pieces_kernel`): with few tasks
+  each is cut along its kept tiles, every tile summed by one piece, every piece's fp32
+  partial in its own slot and added once, in order, by the finishing kernel.
 """
 import numpy as np
 import pytest
@@ -434,3 +437,78 @@ def test_g_tile_tasks_cover_every_kept_pair_once(seed):
             blocks = [slot_rb[vt_slot[q + min(i, cnt - 1)]] for i in range(4)]
             assert blocks[:cnt] == sorted(blocks[:cnt])
     assert (cover == 1).all()
+
+
+DE_PART_SLOTS = 256  # kDePartSlots: fp32 partial sums of 128 x 256 outputs each
+
+
+def de_pieces_restated(own_cnt, nds, nwg):
+    """The narrow dE sums' work items (bwd_sum_narrow_kernel, PHASE 0): ntasks = owners
+    x D slices; when 4 ntasks <= cap = min(nwg, kDePartSlots) task t is cut into
+    P = cap // ntasks pieces, piece k its kept tiles [k cnt // P, (k + 1) cnt // P), item
+    p = t P + k.  Workgroup v walks q = 0, 1, ... over items p = q nwg + v (q even) or
+    q nwg + nwg - 1 - v (q odd) while p < ntasks P, skipping empty pieces.  Returns
+    (P, {p: (workgroup, task, j0, j1)}), and per task the slots bwd_de_pieces_kernel adds
+    (its pieces with j0 < j1, k ascending)."""
+    ntasks = len(own_cnt) * nds
+    cap = min(nwg, DE_PART_SLOTS)
+    P = cap // ntasks if ntasks and 4 * ntasks <= cap else 1
+    items = ntasks * P
+    work = {}
+    for v in range(nwg):
+        q = 0
+        while True:
+            p = q * nwg + (nwg - 1 - v if q & 1 else v)
+            if p >= items:
+                break
+            task = p // P
+            cnt = own_cnt[task // nds]
+            k = p - task * P
+            j0, j1 = (k * cnt // P, (k + 1) * cnt // P) if P > 1 else (0, cnt)
+            q += 1
+            if j0 == j1:
+                continue
+            assert p not in work
+            work[p] = (v, task, j0, j1)
+    fin = {}
+    if P > 1:
+        for t in range(ntasks):
+            cnt = own_cnt[t // nds]
+            fin[t] = [t * P + k for k in range(P) if k * cnt // P < (k + 1) * cnt // P]
+    return P, work, fin
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_de_pieces_cover_every_task_tile_once(seed):
+    rng = np.random.default_rng(seed)
+    nown = int(rng.choice([1, 2, 3, 4, 8, 16, 32, 64, 65]))
+    nds = int(rng.choice([1, 2, 9, 16]))
+    nwg = int(rng.choice([8, 200, 256, 304]))
+    own_cnt = [int(x) for x in rng.integers(1, 400, nown)]
+    own_cnt[0] = int(rng.choice([1, 2, own_cnt[0]]))  # owners with fewer tiles than pieces
+    P, work, fin = de_pieces_restated(own_cnt, nds, nwg)
+    ntasks = nown * nds
+    if 4 * ntasks <= min(nwg, DE_PART_SLOTS):
+        assert P >= 4 and ntasks * P <= min(nwg, DE_PART_SLOTS)
+    else:
+        assert P == 1
+    cover = {t: np.zeros(own_cnt[t // nds], dtype=np.int64) for t in range(ntasks)}
+    for p, (v, task, j0, j1) in work.items():
+        assert 0 <= v < nwg and 0 <= j0 < j1 <= own_cnt[task // nds]
+        if P > 1:
+            assert p < DE_PART_SLOTS and p // P == task  # the piece's own slot
+        cover[task][j0:j1] += 1
+    for t in range(ntasks):
+        assert (cover[t] == 1).all()
+    if P > 1:  # the finisher adds exactly the slots written, once each
+        assert sorted(sum(fin.values(), [])) == sorted(work)
+
+
+def test_de_pieces_mutant_is_caught():
+    """A piece bound off by one (j1 = (k + 1) cnt // P + 1) sums a tile twice."""
+    own_cnt, nds, P = [10], 1, 4
+    cover = np.zeros(10, dtype=np.int64)
+    for k in range(P):
+        j0, j1 = k * 10 // P, min((k + 1) * 10 // P + 1, 10)
+        cover[j0:j1] += 1
+    assert not (cover == 1).all()
