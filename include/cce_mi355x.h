@@ -232,7 +232,7 @@ int cce_backward(int dtype, const void* e, const void* c, const void* bias,
  * tiles.  This keeps the token-block tasks (the G values can differ in the last bits:
  * the contraction's slices are summed in another order). */
 #define CCE_BWD_G_TASKS_BY_BLOCK 4096
-/* When a pass has at most a quarter as many (128-row block, 256-column D slice) dE tasks
+/* When a pass has at most half as many (128-row block, 256-column D slice) dE tasks
  * as workgroups (small N and D), each task is cut along its kept tiles into pieces
  * summed by different workgroups and added in a fixed order by a finishing kernel.
  * This keeps whole tasks (dE can differ in the last bits: the tiles' fp32 sums are

@@ -2562,7 +2562,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_narrow_kernel(BwdArgs a, 
   const int ntasks = ldu(pi, PHASE == 0 ? kPiOwnRb : kPiOwnVt) * nds;
   // dE pieces: P per task when there are few tasks (items ntasks * npc <= kDePartSlots)
   const int pcap = (int)gridDim.x < kDePartSlots ? (int)gridDim.x : kDePartSlots;
-  const int npc = PHASE == 0 && a.de_part != nullptr && ntasks > 0 && 4 * ntasks <= pcap ? pcap / ntasks : 1;
+  const int npc = PHASE == 0 && a.de_part != nullptr && ntasks > 0 && 2 * ntasks <= pcap ? pcap / ntasks : 1;
   const int nitems = ntasks * npc;
   const int* own = PHASE == 0 ? a.own_rb + pass * nrb : a.own_vt + ldu(pi, kPiVt0);
   const int* ostart = PHASE == 0 ? a.rb_start + pass * nrb : a.vt_start;  // an owner's slots / vt_slot entries
@@ -3124,7 +3124,9 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_narrow_kernel(BwdArgs a, 
 // pieces along its kept tiles (kPartF32): here the pieces' fp32 sums are added in piece
 // order and dE is written in the pass's mode, as the sums' epilogue writes a whole
 // task.  Four workgroups per task, 32 of its rows each; a thread takes 4 columns of
-// 8 rows.
+// 8 rows.  The grid covers the most tasks that are cut (kDePartSlots / 2: two pieces
+// each at least).
+constexpr int kDePiecesGrid = 4 * (kDePartSlots / 2);
 template <typename T>
 __global__ __launch_bounds__(256) void bwd_de_pieces_kernel(BwdArgs a, int chunk, int pass, int nwg) {
   (void)chunk;
@@ -3135,7 +3137,7 @@ __global__ __launch_bounds__(256) void bwd_de_pieces_kernel(BwdArgs a, int chunk
   const int nds = (int)((a.D + kDePartCols - 1) / kDePartCols);
   const int ntasks = ldu(pi, kPiOwnRb) * nds;
   const int pcap = nwg < kDePartSlots ? nwg : kDePartSlots;
-  if (ntasks == 0 || 4 * ntasks > pcap) return;  // the sums ran whole tasks
+  if (ntasks == 0 || 2 * ntasks > pcap) return;  // the sums ran whole tasks
   const int npc = pcap / ntasks;
   const int task = (int)(blockIdx.x >> 2);
   if (task >= ntasks) return;
@@ -3360,7 +3362,7 @@ static hipError_t backward_typed(const BwdArgs& a, hipStream_t s, hipEvent_t pas
         launch_sum<T, 0>(ac, wide_de, chunk, pass, gp, s);
         if ((e2 = hipGetLastError()) != hipSuccess) return e2;
         if (!wide_de && a.de_part != nullptr) {  // the pieces of a pass with few dE tasks
-          hipLaunchKernelGGL((bwd_de_pieces_kernel<T>), dim3((unsigned)kDePartSlots), dim3(256), 0, s, a, chunk,
+          hipLaunchKernelGGL((bwd_de_pieces_kernel<T>), dim3((unsigned)kDePiecesGrid), dim3(256), 0, s, a, chunk,
                              pass, gp);
           if ((e2 = hipGetLastError()) != hipSuccess) return e2;
         }

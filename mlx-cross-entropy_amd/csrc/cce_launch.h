@@ -139,7 +139,7 @@ enum PassField {
 // passes (or chunks) dE is summed in an fp32 carry: the first pass stores it, the
 // middle ones add to it, the last one adds and writes dE.
 enum WriteMode { kWriteT = 0, kStoreF32 = 1, kAddF32 = 2, kFinishT = 3, kPartF32 = 4 };
-// dE pieces: when a pass has at most a quarter as many (token block, D slice) tasks as
+// dE pieces: when a pass has at most half as many (token block, D slice) tasks as
 // workgroups (or kDePartSlots), the narrow dE sums cut each task along its kept tiles
 // into P pieces; a piece's fp32 sums go to its own slot of the de_part scratch (mode
 // kPartF32) and bwd_de_pieces_kernel adds a task's pieces in order and writes dE in the
@@ -237,8 +237,8 @@ inline BwdPlan make_bwd_plan_cap(size_t esize, int64_t N, int64_t D, int64_t V, 
   P.colsum = want_db ? take((size_t)P.cap * kBwdVocab * sizeof(float)) : 0;
   P.de_acc = P.carry ? take((size_t)N * (size_t)D * sizeof(float)) : 0;
   // the most dE tasks a pass can have (every token block x the narrow D slices) leave
-  // four workgroups per task or more on a 256-CU part
-  P.de_pieces = want_de && P.nrb * ((D + kDePartCols - 1) / kDePartCols) * 4 <= kDePartSlots;
+  // two workgroups per task or more on a 256-CU part
+  P.de_pieces = want_de && P.nrb * ((D + kDePartCols - 1) / kDePartCols) * 2 <= kDePartSlots;
   P.de_part = P.de_pieces ? take((size_t)kDePartSlots * kBwdTokens * kDePartCols * sizeof(float)) : 0;
   // (dE rows are then written through the map with one buffer over all of dE: < 2^31 bytes)
   P.perm_ok = perm && N <= kPermMaxN && P.nvt + 1 <= kPermMaxKey && (want_g || want_db) &&

@@ -704,6 +704,25 @@ def test_de_pieces_match_whole_tasks(m, cuda, dtype, split, order):
     assert torch.equal(pieces[2], whole[2]) and torch.equal(pieces[3], whole[3])
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_de_pieces_two_per_task(m, cuda, dtype):
+    """96 dE tasks (32 token blocks x 3 D slices, the last one ragged) for 256 workgroups:
+    each task in 2 pieces, 192 slots, the finishing kernel's grid reaching all 96 tasks.
+    dE equals the whole tasks' to the fp32 sums' reassociation and repeats bit for bit."""
+    N, D, V = 4000, 520, 9000
+    e, c, t = normal_case(N, D, V, dtype, cuda, seed=33, std=0.05)
+    feps = m.FILTER_LOG_EPS
+    pieces = run(m, e, c, t, None, reduction="sum", filter_eps=feps)
+    again = run(m, e, c, t, None, reduction="sum", filter_eps=feps)
+    with m._ext.backward_options(de_tasks="whole"):
+        whole = run(m, e, c, t, None, reduction="sum", filter_eps=feps)
+    assert torch.equal(pieces[1], again[1]) and torch.equal(pieces[2], again[2])
+    err = O.rel_fro(f64(pieces[1]), f64(whole[1]))
+    print(f"{dtype}: dE two pieces vs whole {err:.2e}")
+    assert err < (1e-5 if dtype == torch.float32 else 2e-3), err
+    assert torch.equal(pieces[2], whole[2])
+
+
 @pytest.mark.parametrize("sizing", ["exact", "pair", "least"])
 def test_rounded_once_g_workspace_sizes(m, cuda, sizing):
     """A bf16 backward with the filter on keeps G rounded once in 32 KiB tile slots.

@@ -440,11 +440,12 @@ def test_g_tile_tasks_cover_every_kept_pair_once(seed):
 
 
 DE_PART_SLOTS = 256  # kDePartSlots: fp32 partial sums of 128 x 256 outputs each
+DE_PIECES_GRID = 4 * (DE_PART_SLOTS // 2)  # kDePiecesGrid: bwd_de_pieces_kernel, 4 workgroups per task
 
 
 def de_pieces_restated(own_cnt, nds, nwg):
     """The narrow dE sums' work items (bwd_sum_narrow_kernel, PHASE 0): ntasks = owners
-    x D slices; when 4 ntasks <= cap = min(nwg, kDePartSlots) task t is cut into
+    x D slices; when 2 ntasks <= cap = min(nwg, kDePartSlots) task t is cut into
     P = cap // ntasks pieces, piece k its kept tiles [k cnt // P, (k + 1) cnt // P), item
     p = t P + k.  Workgroup v walks q = 0, 1, ... over items p = q nwg + v (q even) or
     q nwg + nwg - 1 - v (q odd) while p < ntasks P, skipping empty pieces.  Returns
@@ -452,7 +453,7 @@ def de_pieces_restated(own_cnt, nds, nwg):
     (its pieces with j0 < j1, k ascending)."""
     ntasks = len(own_cnt) * nds
     cap = min(nwg, DE_PART_SLOTS)
-    P = cap // ntasks if ntasks and 4 * ntasks <= cap else 1
+    P = cap // ntasks if ntasks and 2 * ntasks <= cap else 1
     items = ntasks * P
     work = {}
     for v in range(nwg):
@@ -481,15 +482,15 @@ def de_pieces_restated(own_cnt, nds, nwg):
 @pytest.mark.parametrize("seed", range(40))
 def test_de_pieces_cover_every_task_tile_once(seed):
     rng = np.random.default_rng(seed)
-    nown = int(rng.choice([1, 2, 3, 4, 8, 16, 32, 64, 65]))
+    nown = int(rng.choice([1, 2, 3, 4, 8, 16, 32, 64, 65, 128]))
     nds = int(rng.choice([1, 2, 9, 16]))
     nwg = int(rng.choice([8, 200, 256, 304]))
     own_cnt = [int(x) for x in rng.integers(1, 400, nown)]
     own_cnt[0] = int(rng.choice([1, 2, own_cnt[0]]))  # owners with fewer tiles than pieces
     P, work, fin = de_pieces_restated(own_cnt, nds, nwg)
     ntasks = nown * nds
-    if 4 * ntasks <= min(nwg, DE_PART_SLOTS):
-        assert P >= 4 and ntasks * P <= min(nwg, DE_PART_SLOTS)
+    if 2 * ntasks <= min(nwg, DE_PART_SLOTS):
+        assert P >= 2 and ntasks * P <= min(nwg, DE_PART_SLOTS)
     else:
         assert P == 1
     cover = {t: np.zeros(own_cnt[t // nds], dtype=np.int64) for t in range(ntasks)}
@@ -502,6 +503,8 @@ def test_de_pieces_cover_every_task_tile_once(seed):
         assert (cover[t] == 1).all()
     if P > 1:  # the finisher adds exactly the slots written, once each
         assert sorted(sum(fin.values(), [])) == sorted(work)
+        # its workgroups (task = block // 4) reach every task that was cut
+        assert {b // 4 for b in range(DE_PIECES_GRID)} >= set(range(ntasks))
 
 
 def test_de_pieces_mutant_is_caught():
