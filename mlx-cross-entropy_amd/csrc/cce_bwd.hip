@@ -2544,6 +2544,28 @@ __global__ __launch_bounds__((SumGeo<T, SPLIT>::NT), 1) void bwd_sum_kernel(BwdA
   wait_vmcnt<0>();
 }
 
+// Which dE tasks of a pass are cut into pieces, for a grid of nwg workgroups: npc
+// pieces each of the ncut tasks [tbase, tbase + ncut), or none (npc 1).  With few
+// tasks (2 ntasks <= cap) all of them, npc = cap / ntasks; with tasks overflowing the
+// grid by at most half of it (2 (ntasks - nwg) <= cap) the ones past the grid, npc =
+// cap / (ntasks - nwg), after a first launch of one whole task per workgroup.  cap =
+// min(nwg, kDePartSlots): piece q of cut task tbase + t has slot t npc + q.
+__device__ __forceinline__ void de_pieces_of(const BwdArgs& a, int ntasks, int nwg, int& tbase, int& ncut, int& npc) {
+  tbase = 0;
+  ncut = 0;
+  npc = 1;
+  if (a.de_part == nullptr || ntasks <= 0) return;
+  const int cap = nwg < kDePartSlots ? nwg : kDePartSlots;
+  if (2 * ntasks <= cap) {
+    ncut = ntasks;
+    npc = cap / ntasks;
+  } else if (ntasks > nwg && 2 * (ntasks - nwg) <= cap) {
+    tbase = nwg;
+    ncut = ntasks - nwg;
+    npc = cap / ncut;
+  }
+}
+
 // As bwd_sum_kernel, in the narrow geometry (one 4-wave pipeline of 48 KiB stages).
 template <typename T, int PHASE, bool SPLIT>
 __global__ __launch_bounds__(kThreads, 1) void bwd_sum_narrow_kernel(BwdArgs a, int chunk, int pass) {
@@ -2560,10 +2582,15 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_narrow_kernel(BwdArgs a, 
   if (PHASE == 1 && a.dc_geo == 0 && a.filter_log_eps > -INFINITY && ldu(pi, kPiDcWide) != 0) return;
   const int s0 = ldu(pi, kPiS0);  // the G scratch holds slot s at s - s0
   const int ntasks = ldu(pi, PHASE == 0 ? kPiOwnRb : kPiOwnVt) * nds;
-  // dE pieces: P per task when there are few tasks (items ntasks * npc <= kDePartSlots)
-  const int pcap = (int)gridDim.x < kDePartSlots ? (int)gridDim.x : kDePartSlots;
-  const int npc = PHASE == 0 && a.de_part != nullptr && ntasks > 0 && 2 * ntasks <= pcap ? pcap / ntasks : 1;
-  const int nitems = ntasks * npc;
+  // dE pieces (de_pieces_of): npc pieces per task of [tbase, tbase + ncut) (items ncut *
+  // npc <= kDePartSlots), or whole tasks (npc 1)
+  int tbase = 0, ncut = 0, npc = 1;
+  if (PHASE == 0) de_pieces_of(a, ntasks, (int)gridDim.x, tbase, ncut, npc);
+  if (PHASE == 0 && a.de_stage == 1 && (npc == 1 || tbase == 0)) return;  // no overflow to cut
+  const int nitems = PHASE == 0 && a.de_stage == 1 ? ncut * npc
+                     : PHASE == 0 && npc > 1 && tbase == 0 ? ntasks * npc
+                     : PHASE == 0 && npc > 1 ? tbase : ntasks;
+  const bool cut = PHASE == 0 && npc > 1 && (a.de_stage == 1 || tbase == 0);  // this launch sums pieces
   const int* own = PHASE == 0 ? a.own_rb + pass * nrb : a.own_vt + ldu(pi, kPiVt0);
   const int* ostart = PHASE == 0 ? a.rb_start + pass * nrb : a.vt_start;  // an owner's slots / vt_slot entries
   const int vwg = xcd * nper + lidx, nwg = (int)gridDim.x;  // workgroups numbered XCD-major
@@ -2581,7 +2608,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_narrow_kernel(BwdArgs a, 
   const RowData rd = row_data(a);
   const char* X = PHASE == 0 ? reinterpret_cast<const char*>(a.c) : rd.e;
   const int64_t xrows = PHASE == 0 ? a.V : a.N;
-  const int mode = PHASE == 0 ? (npc > 1 ? kPartF32 : pmode) : kWriteT;
+  const int mode = PHASE == 0 ? (cut ? kPartF32 : pmode) : kWriteT;
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -2639,12 +2666,12 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_narrow_kernel(BwdArgs a, 
     int q, owner, ds, b, cnt, j, h, slot;
     int64_t xrow;
   };
-  // dE pieces (npc > 1): items number at most the workgroups, so workgroup vwg has item
-  // vwg alone, piece k = vwg % npc of task vwg / npc: its tiles [j0, j1) of the task's
-  // (none when the task has fewer tiles than pieces)
+  // dE pieces (cut): items number at most the workgroups, so workgroup vwg has item vwg
+  // alone, piece k = vwg % npc of task tbase + vwg / npc: its tiles [j0, j1) of the
+  // task's (none when the task has fewer tiles than pieces)
   int pc_j0 = 0, pc_j1 = 0;
-  if (PHASE == 0 && npc > 1 && vwg < nitems) {
-    const int task = vwg / npc, k = vwg - task * npc;
+  if (cut && vwg < nitems) {
+    const int task = tbase + vwg / npc, k = vwg - (vwg / npc) * npc;
     const int ow = ldu(own, task / nds);
     const int cnt = ldu(ostart, ow + 1) - ldu(ostart, ow);
     pc_j0 = k * cnt / npc;
@@ -2654,8 +2681,8 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_narrow_kernel(BwdArgs a, 
     int owner, ds;
     if constexpr (PHASE == 0) {
       const int p = q * nwg + ((q & 1) ? nwg - 1 - vwg : vwg);
-      if (p >= nitems || (npc > 1 && pc_j0 == pc_j1)) return false;
-      const int task = p / npc;
+      if (p >= nitems || (cut && pc_j0 == pc_j1)) return false;
+      const int task = cut ? tbase + p / npc : p;
       owner = ldu(own, task / nds);
       ds = task - (task / nds) * nds;
     } else {  // the q-th owner of this workgroup's bin (then the same again at slice ds0 + nwg, ...)
@@ -2670,7 +2697,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_narrow_kernel(BwdArgs a, 
     c.owner = owner;
     c.ds = ds;
     c.b = b + pc_j0;
-    c.cnt = npc > 1 ? pc_j1 - pc_j0 : ldu(ostart, owner + 1) - b;
+    c.cnt = cut ? pc_j1 - pc_j0 : ldu(ostart, owner + 1) - b;
     c.j = 0;
     c.h = 0;
     return true;
@@ -3120,10 +3147,10 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_narrow_kernel(BwdArgs a, 
 }
 
 // ---------------------------------------------------------------- 5b. dE pieces
-// The narrow dE sums cut each of a pass's few tasks (token block, D slice) into npc
-// pieces along its kept tiles (kPartF32): here the pieces' fp32 sums are added in piece
-// order and dE is written in the pass's mode, as the sums' epilogue writes a whole
-// task.  Four workgroups per task, 32 of its rows each; a thread takes 4 columns of
+// The narrow dE sums cut some of a pass's tasks (token block, D slice) into npc pieces
+// along their kept tiles (kPartF32, de_pieces_of): here the pieces' fp32 sums are added
+// in piece order and dE is written in the pass's mode, as the sums' epilogue writes a
+// whole task.  Four workgroups per task, 32 of its rows each; a thread takes 4 columns of
 // 8 rows.  The grid covers the most tasks that are cut (kDePartSlots / 2: two pieces
 // each at least).
 constexpr int kDePiecesGrid = 4 * (kDePartSlots / 2);
@@ -3136,11 +3163,11 @@ __global__ __launch_bounds__(256) void bwd_de_pieces_kernel(BwdArgs a, int chunk
   const int nrb = (int)a.plan.nrb;
   const int nds = (int)((a.D + kDePartCols - 1) / kDePartCols);
   const int ntasks = ldu(pi, kPiOwnRb) * nds;
-  const int pcap = nwg < kDePartSlots ? nwg : kDePartSlots;
-  if (ntasks == 0 || 2 * ntasks > pcap) return;  // the sums ran whole tasks
-  const int npc = pcap / ntasks;
-  const int task = (int)(blockIdx.x >> 2);
-  if (task >= ntasks) return;
+  int tbase, ncut, npc;
+  de_pieces_of(a, ntasks, nwg, tbase, ncut, npc);
+  const int ti = (int)(blockIdx.x >> 2);  // the cut task's index
+  if (npc == 1 || ti >= ncut) return;     // the sums ran whole tasks
+  const int task = tbase + ti;
   const int owner = ldu(a.own_rb + pass * nrb, task / nds);
   const int ds = task - (task / nds) * nds;
   const int* rbs = a.rb_start + pass * nrb;
@@ -3159,7 +3186,7 @@ __global__ __launch_bounds__(256) void bwd_de_pieces_kernel(BwdArgs a, int chunk
     f32x4 sum{0.f, 0.f, 0.f, 0.f};
     for (int k = 0; k < npc; ++k) {
       if (k * cnt / npc == (k + 1) * cnt / npc) continue;  // an empty piece (never written)
-      sum += *reinterpret_cast<const f32x4*>(a.de_part + ((size_t)(task * npc + k) * kBwdTokens + m) * kDePartCols + col);
+      sum += *reinterpret_cast<const f32x4*>(a.de_part + ((size_t)(ti * npc + k) * kBwdTokens + m) * kDePartCols + col);
     }
     const int64_t orow = rd.map ? (int64_t)rd.map[orow0 + m] : orow0 + m;
     if (mode != kWriteT) {
@@ -3361,7 +3388,13 @@ static hipError_t backward_typed(const BwdArgs& a, hipStream_t s, hipEvent_t pas
       if (want_de) {
         launch_sum<T, 0>(ac, wide_de, chunk, pass, gp, s);
         if ((e2 = hipGetLastError()) != hipSuccess) return e2;
-        if (!wide_de && a.de_part != nullptr) {  // the pieces of a pass with few dE tasks
+        if (!wide_de && a.de_part != nullptr) {  // pieces of dE tasks (de_pieces_of)
+          if (P.nrb * ((a.D + kDePartCols - 1) / kDePartCols) > gp) {  // tasks may overflow the grid
+            BwdArgs a1 = ac;
+            a1.de_stage = 1;
+            launch_sum<T, 0>(a1, false, chunk, pass, gp, s);
+            if ((e2 = hipGetLastError()) != hipSuccess) return e2;
+          }
           hipLaunchKernelGGL((bwd_de_pieces_kernel<T>), dim3((unsigned)kDePiecesGrid), dim3(256), 0, s, a, chunk,
                              pass, gp);
           if ((e2 = hipGetLastError()) != hipSuccess) return e2;

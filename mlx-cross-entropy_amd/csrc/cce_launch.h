@@ -143,7 +143,9 @@ enum WriteMode { kWriteT = 0, kStoreF32 = 1, kAddF32 = 2, kFinishT = 3, kPartF32
 // workgroups (or kDePartSlots), the narrow dE sums cut each task along its kept tiles
 // into P pieces; a piece's fp32 sums go to its own slot of the de_part scratch (mode
 // kPartF32) and bwd_de_pieces_kernel adds a task's pieces in order and writes dE in the
-// pass's mode.
+// pass's mode.  When the tasks overflow the grid by at most half of it, the first
+// launch (de_stage 0) runs one whole task per workgroup and a second (de_stage 1) the
+// pieces of the tasks past the grid.
 constexpr int kDePartSlots = 256;  // pieces at most (fp32 slots of 128 x 256 sums)
 constexpr int kDePartCols = 256;   // the narrow sums' D slice
 
@@ -237,8 +239,10 @@ inline BwdPlan make_bwd_plan_cap(size_t esize, int64_t N, int64_t D, int64_t V, 
   P.colsum = want_db ? take((size_t)P.cap * kBwdVocab * sizeof(float)) : 0;
   P.de_acc = P.carry ? take((size_t)N * (size_t)D * sizeof(float)) : 0;
   // the most dE tasks a pass can have (every token block x the narrow D slices) leave
-  // two workgroups per task or more on a 256-CU part
-  P.de_pieces = want_de && P.nrb * ((D + kDePartCols - 1) / kDePartCols) * 2 <= kDePartSlots;
+  // two workgroups per task or more on a 256-CU part, or overflow a 256-workgroup grid
+  // by at most half of it (the tasks past the grid are then cut)
+  const int64_t de_tasks = P.nrb * ((D + kDePartCols - 1) / kDePartCols);
+  P.de_pieces = want_de && (de_tasks * 2 <= kDePartSlots || (de_tasks > kDePartSlots && de_tasks * 2 <= 3 * kDePartSlots));
   P.de_part = P.de_pieces ? take((size_t)kDePartSlots * kBwdTokens * kDePartCols * sizeof(float)) : 0;
   // (dE rows are then written through the map with one buffer over all of dE: < 2^31 bytes)
   P.perm_ok = perm && N <= kPermMaxN && P.nvt + 1 <= kPermMaxKey && (want_g || want_db) &&
@@ -358,6 +362,7 @@ struct BwdArgs {
   float* colsum;      // [cap][128] per-slot column sums of G (dBias)
   float* de_acc;      // [N, D] fp32, only when the plan reserves the carry
   float* de_part;     // [kDePartSlots][128][kDePartCols] fp32 sums of the dE pieces, or null (whole tasks)
+  int de_stage;       // narrow dE sums launch: 0 the tasks (overflow: the first grid's worth), 1 the overflow's pieces
   int64_t* tile_stats;  // [3] or null: kept pairs, all pairs, kept pairs of the input-order token blocks
   BwdPlan plan;
   int num_cus;

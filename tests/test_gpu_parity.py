@@ -723,6 +723,29 @@ def test_de_pieces_two_per_task(m, cuda, dtype):
     assert torch.equal(pieces[2], whole[2])
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_de_pieces_of_tasks_past_the_grid(m, cuda, dtype):
+    """288 dE tasks (32 token blocks x 9 D slices) for 256 workgroups: one launch runs a
+    whole task per workgroup, a second the 32 tasks past the grid cut into 8 pieces each
+    (the last owners, with the fewest kept tiles), and the finishing kernel adds those.
+    dE equals the whole tasks' (two rounds on some workgroups) to the fp32 sums'
+    reassociation and repeats bit for bit; dC is unchanged."""
+    if torch.cuda.get_device_properties(cuda).multi_processor_count != 256:
+        pytest.skip("the task counts are laid out for a 256-workgroup grid")
+    N, D, V = 4096, 2304, 9000
+    e, c, t = normal_case(N, D, V, dtype, cuda, seed=35, std=0.05)
+    feps = m.FILTER_LOG_EPS
+    pieces = run(m, e, c, t, None, reduction="sum", filter_eps=feps)
+    again = run(m, e, c, t, None, reduction="sum", filter_eps=feps)
+    with m._ext.backward_options(de_tasks="whole"):
+        whole = run(m, e, c, t, None, reduction="sum", filter_eps=feps)
+    assert torch.equal(pieces[1], again[1]) and torch.equal(pieces[2], again[2])
+    err = O.rel_fro(f64(pieces[1]), f64(whole[1]))
+    print(f"{dtype}: dE overflow pieces vs whole {err:.2e}")
+    assert err < (1e-5 if dtype == torch.float32 else 2e-3), err
+    assert torch.equal(pieces[2], whole[2])
+
+
 @pytest.mark.parametrize("sizing", ["exact", "pair", "least"])
 def test_rounded_once_g_workspace_sizes(m, cuda, sizing):
     """A bf16 backward with the filter on keeps G rounded once in 32 KiB tile slots.

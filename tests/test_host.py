@@ -86,7 +86,8 @@ def test_backward_workspace_is_bounded(ext, N, D, V):
         bound = (g_slots * (tile + 512)  # G tiles + their column sums
                  + N * D * (4 + es)                # fp32 dE carry + the sorted copy of E
                  + N * nwords * 4 + 2 * nrb * nwords * 4  # keep bits per row / per block
-                 + 40 * chunk_pairs + 64 * N + (4 << 20))
+                 + 40 * chunk_pairs + 64 * N + (4 << 20)
+                 + (32 << 20))  # the dE pieces' slots (few dE tasks, or up to 1.5 grids of them)
         print(f"N={N} D={D} V={V} dtype {dtype}: workspace {ws / 2**30:.3f} GiB (bound {bound / 2**30:.3f}, "
               f"logits {N * V * es / 2**30:.2f})")
         assert 0 < ws <= bound

@@ -443,68 +443,96 @@ DE_PART_SLOTS = 256  # kDePartSlots: fp32 partial sums of 128 x 256 outputs each
 DE_PIECES_GRID = 4 * (DE_PART_SLOTS // 2)  # kDePiecesGrid: bwd_de_pieces_kernel, 4 workgroups per task
 
 
-def de_pieces_restated(own_cnt, nds, nwg):
-    """The narrow dE sums' work items (bwd_sum_narrow_kernel, PHASE 0): ntasks = owners
-    x D slices; when 2 ntasks <= cap = min(nwg, kDePartSlots) task t is cut into
-    P = cap // ntasks pieces, piece k its kept tiles [k cnt // P, (k + 1) cnt // P), item
-    p = t P + k.  Workgroup v walks q = 0, 1, ... over items p = q nwg + v (q even) or
-    q nwg + nwg - 1 - v (q odd) while p < ntasks P, skipping empty pieces.  Returns
-    (P, {p: (workgroup, task, j0, j1)}), and per task the slots bwd_de_pieces_kernel adds
-    (its pieces with j0 < j1, k ascending)."""
-    ntasks = len(own_cnt) * nds
+def de_pieces_of(ntasks, nwg):
+    """de_pieces_of (cce_bwd.hip): (tbase, ncut, npc) -- npc pieces each of the cut tasks
+    [tbase, tbase + ncut); all of few tasks (2 ntasks <= cap), or the ones past the grid
+    when they overflow it by at most half (2 (ntasks - nwg) <= cap); cap = min(nwg, 256)."""
     cap = min(nwg, DE_PART_SLOTS)
-    P = cap // ntasks if ntasks and 2 * ntasks <= cap else 1
-    items = ntasks * P
-    work = {}
-    for v in range(nwg):
-        q = 0
-        while True:
-            p = q * nwg + (nwg - 1 - v if q & 1 else v)
-            if p >= items:
-                break
-            task = p // P
-            cnt = own_cnt[task // nds]
-            k = p - task * P
-            j0, j1 = (k * cnt // P, (k + 1) * cnt // P) if P > 1 else (0, cnt)
-            q += 1
-            if j0 == j1:
-                continue
-            assert p not in work
-            work[p] = (v, task, j0, j1)
+    if ntasks <= 0:
+        return 0, 0, 1
+    if 2 * ntasks <= cap:
+        return 0, ntasks, cap // ntasks
+    if ntasks > nwg and 2 * (ntasks - nwg) <= cap:
+        return nwg, ntasks - nwg, cap // (ntasks - nwg)
+    return 0, 0, 1
+
+
+def de_pieces_restated(own_cnt, nds, nwg):
+    """The narrow dE sums' work items (bwd_sum_narrow_kernel, PHASE 0), over its one or
+    two launches (de_stage 0, and 1 when tasks overflow the grid).  Stage 0 runs the
+    whole tasks (all of them; with an overflow the first nwg) or, when all are cut,
+    their pieces; stage 1 the overflow's pieces.  A launch's items: workgroup v walks
+    q = 0, 1, ... over p = q nwg + v (q even) or q nwg + nwg - 1 - v (q odd) while
+    p < nitems; a cut item p is piece p % npc, tiles [k cnt // npc, (k + 1) cnt // npc),
+    of task tbase + p // npc (skipped when empty), with slot p.  Returns (npc, pieces
+    {slot: (v, task, j0, j1)}, whole [(v, task)], and per cut task the slots
+    bwd_de_pieces_kernel adds)."""
+    ntasks = len(own_cnt) * nds
+    tbase, ncut, npc = de_pieces_of(ntasks, nwg)
+    pieces, whole = {}, []
+    stages = [0, 1] if (npc > 1 and tbase > 0) else [0]
+    for stage in stages:
+        cut = npc > 1 and (stage == 1 or tbase == 0)
+        nitems = ncut * npc if stage == 1 else (ntasks * npc if cut else (tbase if npc > 1 else ntasks))
+        for v in range(nwg):
+            q = 0
+            while True:
+                p = q * nwg + (nwg - 1 - v if q & 1 else v)
+                if p >= nitems:
+                    break
+                q += 1
+                if not cut:
+                    whole.append((v, p))
+                    continue
+                task = tbase + p // npc
+                cnt = own_cnt[task // nds]
+                k = p - (p // npc) * npc
+                j0, j1 = k * cnt // npc, (k + 1) * cnt // npc
+                if j0 == j1:
+                    continue
+                assert p not in pieces
+                pieces[p] = (v, task, j0, j1)
     fin = {}
-    if P > 1:
-        for t in range(ntasks):
-            cnt = own_cnt[t // nds]
-            fin[t] = [t * P + k for k in range(P) if k * cnt // P < (k + 1) * cnt // P]
-    return P, work, fin
+    if npc > 1:
+        for ti in range(ncut):
+            cnt = own_cnt[(tbase + ti) // nds]
+            fin[tbase + ti] = [ti * npc + k for k in range(npc) if k * cnt // npc < (k + 1) * cnt // npc]
+    return npc, pieces, whole, fin
 
 
-@pytest.mark.parametrize("seed", range(40))
+@pytest.mark.parametrize("seed", range(60))
 def test_de_pieces_cover_every_task_tile_once(seed):
     rng = np.random.default_rng(seed)
-    nown = int(rng.choice([1, 2, 3, 4, 8, 16, 32, 64, 65, 128]))
-    nds = int(rng.choice([1, 2, 9, 16]))
+    nown = int(rng.choice([1, 2, 3, 4, 8, 16, 32, 64, 65, 128, 288, 300, 384, 400]))
+    nds = int(rng.choice([1, 1, 2, 9, 16]))
     nwg = int(rng.choice([8, 200, 256, 304]))
     own_cnt = [int(x) for x in rng.integers(1, 400, nown)]
-    own_cnt[0] = int(rng.choice([1, 2, own_cnt[0]]))  # owners with fewer tiles than pieces
-    P, work, fin = de_pieces_restated(own_cnt, nds, nwg)
+    own_cnt[-1] = int(rng.choice([1, 2, own_cnt[-1]]))  # owners with fewer tiles than pieces
+    npc, pieces, whole, fin = de_pieces_restated(own_cnt, nds, nwg)
     ntasks = nown * nds
-    if 2 * ntasks <= min(nwg, DE_PART_SLOTS):
-        assert P >= 2 and ntasks * P <= min(nwg, DE_PART_SLOTS)
+    tbase, ncut, _ = de_pieces_of(ntasks, nwg)
+    cap = min(nwg, DE_PART_SLOTS)
+    if 2 * ntasks <= cap or (ntasks > nwg and 2 * (ntasks - nwg) <= cap):
+        assert npc >= 2 and ncut * npc <= cap
     else:
-        assert P == 1
+        assert npc == 1
     cover = {t: np.zeros(own_cnt[t // nds], dtype=np.int64) for t in range(ntasks)}
-    for p, (v, task, j0, j1) in work.items():
+    for v, task in whole:
+        assert 0 <= v < nwg and not (tbase <= task < tbase + ncut and npc > 1)
+        cover[task][:] += 1
+    for p, (v, task, j0, j1) in pieces.items():
         assert 0 <= v < nwg and 0 <= j0 < j1 <= own_cnt[task // nds]
-        if P > 1:
-            assert p < DE_PART_SLOTS and p // P == task  # the piece's own slot
+        assert p < DE_PART_SLOTS and tbase + p // npc == task  # the piece's own slot
         cover[task][j0:j1] += 1
     for t in range(ntasks):
         assert (cover[t] == 1).all()
-    if P > 1:  # the finisher adds exactly the slots written, once each
-        assert sorted(sum(fin.values(), [])) == sorted(work)
-        # its workgroups (task = block // 4) reach every task that was cut
-        assert {b // 4 for b in range(DE_PIECES_GRID)} >= set(range(ntasks))
+    if npc > 1:  # the finisher adds exactly the slots written, once each
+        assert sorted(sum(fin.values(), [])) == sorted(pieces)
+        # its workgroups (cut task index = block // 4) reach every cut task
+        assert {b // 4 for b in range(DE_PIECES_GRID)} >= set(range(ncut))
+    # each workgroup runs at most one item per launch when anything is cut
+    if npc > 1:
+        assert len({v for v, _ in whole}) == len(whole)
 
 
 def test_de_pieces_mutant_is_caught():
