@@ -235,7 +235,7 @@ int cce_backward(int dtype, const void* e, const void* c, const void* bias,
 /* When a pass has at most half as many (128-row block, 256-column D slice) dE tasks
  * as workgroups (small N and D), each task is cut along its kept tiles into pieces
  * summed by different workgroups and added in a fixed order by a finishing kernel;
- * when the tasks overflow the grid by at most half of it, the tasks past the grid are
+ * when the tasks overflow the grid by at most half of it, the tasks past the grid are cut
  * (after a launch of one whole task per workgroup).
  * This keeps whole tasks (dE can differ in the last bits: the tiles' fp32 sums are
  * added in another order). */
