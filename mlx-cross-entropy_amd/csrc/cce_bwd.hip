@@ -3150,10 +3150,11 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_sum_narrow_kernel(BwdArgs a, 
 // The narrow dE sums cut some of a pass's tasks (token block, D slice) into npc pieces
 // along their kept tiles (kPartF32, de_pieces_of): here the pieces' fp32 sums are added
 // in piece order and dE is written in the pass's mode, as the sums' epilogue writes a
-// whole task.  Four workgroups per task, 32 of its rows each; a thread takes 4 columns of
-// 8 rows.  The grid covers the most tasks that are cut (kDePartSlots / 2: two pieces
-// each at least).
-constexpr int kDePiecesGrid = 4 * (kDePartSlots / 2);
+// whole task.  32 workgroups per task, 4 of its rows each; a thread takes 4 columns of
+// one row and adds the npc pieces' values with four sums in flight.  The grid covers
+// the most tasks that are cut (kDePartSlots / 2: two pieces each at least).
+constexpr int kDePiecesPerTask = kBwdTokens / 4;
+constexpr int kDePiecesGrid = kDePiecesPerTask * (kDePartSlots / 2);
 template <typename T>
 __global__ __launch_bounds__(256) void bwd_de_pieces_kernel(BwdArgs a, int chunk, int pass, int nwg) {
   (void)chunk;
@@ -3165,8 +3166,8 @@ __global__ __launch_bounds__(256) void bwd_de_pieces_kernel(BwdArgs a, int chunk
   const int ntasks = ldu(pi, kPiOwnRb) * nds;
   int tbase, ncut, npc;
   de_pieces_of(a, ntasks, nwg, tbase, ncut, npc);
-  const int ti = (int)(blockIdx.x >> 2);  // the cut task's index
-  if (npc == 1 || ti >= ncut) return;     // the sums ran whole tasks
+  const int ti = (int)(blockIdx.x / kDePiecesPerTask);  // the cut task's index
+  if (npc == 1 || ti >= ncut) return;                    // the sums ran whole tasks
   const int task = tbase + ti;
   const int owner = ldu(a.own_rb + pass * nrb, task / nds);
   const int ds = task - (task / nds) * nds;
@@ -3180,24 +3181,36 @@ __global__ __launch_bounds__(256) void bwd_de_pieces_kernel(BwdArgs a, int chunk
   const int64_t d = (int64_t)ds * kDePartCols + col;
   if (d >= D) return;  // D is a multiple of 4: the 4 columns are inside
   T* dE = reinterpret_cast<T*>(a.dE);
-  for (int rr = 0; rr < 8; ++rr) {
-    const int m = (int)(blockIdx.x & 3) * 32 + rr * 4 + (int)(threadIdx.x >> 6);
-    if (m >= nrows) break;
+  {
+    const int m = (int)(blockIdx.x % kDePiecesPerTask) * 4 + (int)(threadIdx.x >> 6);
+    if (m >= nrows) return;
+    const float* src = a.de_part + ((size_t)ti * npc * kBwdTokens + m) * kDePartCols + col;
+    constexpr size_t kSlot = (size_t)kBwdTokens * kDePartCols;
+    // pieces k ascending; an empty piece (never written) adds nothing
+    auto piece = [&](int k) -> f32x4 {
+      return k * cnt / npc == (k + 1) * cnt / npc ? f32x4{0.f, 0.f, 0.f, 0.f}
+                                                  : *reinterpret_cast<const f32x4*>(src + (size_t)k * kSlot);
+    };
     f32x4 sum{0.f, 0.f, 0.f, 0.f};
-    for (int k = 0; k < npc; ++k) {
-      if (k * cnt / npc == (k + 1) * cnt / npc) continue;  // an empty piece (never written)
-      sum += *reinterpret_cast<const f32x4*>(a.de_part + ((size_t)(ti * npc + k) * kBwdTokens + m) * kDePartCols + col);
+    int k = 0;
+    for (; k + 4 <= npc; k += 4) {
+      const f32x4 p0 = piece(k), p1 = piece(k + 1), p2 = piece(k + 2), p3 = piece(k + 3);
+      sum += p0;
+      sum += p1;
+      sum += p2;
+      sum += p3;
     }
+    for (; k < npc; ++k) sum += piece(k);
     const int64_t orow = rd.map ? (int64_t)rd.map[orow0 + m] : orow0 + m;
     if (mode != kWriteT) {
       f32x4* cp = reinterpret_cast<f32x4*>(a.de_acc + (orow0 + m) * D + d);
       if (mode == kStoreF32) {
         *cp = sum;
-        continue;
+        return;
       }
       if (mode == kAddF32) {
         *cp = *cp + sum;
-        continue;
+        return;
       }
       sum = *cp + sum;  // kFinishT
     }

@@ -440,7 +440,8 @@ def test_g_tile_tasks_cover_every_kept_pair_once(seed):
 
 
 DE_PART_SLOTS = 256  # kDePartSlots: fp32 partial sums of 128 x 256 outputs each
-DE_PIECES_GRID = 4 * (DE_PART_SLOTS // 2)  # kDePiecesGrid: bwd_de_pieces_kernel, 4 workgroups per task
+DE_PIECES_PER_TASK = 128 // 4  # kDePiecesPerTask: 4 of a task's 128 rows per workgroup
+DE_PIECES_GRID = DE_PIECES_PER_TASK * (DE_PART_SLOTS // 2)  # kDePiecesGrid: bwd_de_pieces_kernel
 
 
 def de_pieces_of(ntasks, nwg):
@@ -528,8 +529,10 @@ def test_de_pieces_cover_every_task_tile_once(seed):
         assert (cover[t] == 1).all()
     if npc > 1:  # the finisher adds exactly the slots written, once each
         assert sorted(sum(fin.values(), [])) == sorted(pieces)
-        # its workgroups (cut task index = block // 4) reach every cut task
-        assert {b // 4 for b in range(DE_PIECES_GRID)} >= set(range(ncut))
+        # its workgroups (cut task index = block // 32, rows 4 (block % 32) + wave) reach
+        # every row of every cut task
+        rows = {(b // DE_PIECES_PER_TASK, 4 * (b % DE_PIECES_PER_TASK) + w) for b in range(DE_PIECES_GRID) for w in range(4)}
+        assert rows >= {(ti, m) for ti in range(ncut) for m in range(128)}
     # each workgroup runs at most one item per launch when anything is cut
     if npc > 1:
         assert len({v for v, _ in whole}) == len(whole)
